@@ -1,0 +1,164 @@
+/*
+ * llmtoy_hip.h -- C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * Stands in for llmtoy-zig's src/gpu Vulkan backend on the batch-1 decode
+ * path: GGUF block-quantised matvec (Q8_0, Q4_K, Q6_K, F32) and the MoE layer
+ * around it.  Plain C types only; one context per device; a context is not
+ * thread-safe and launches everything on one HIP stream.
+ *
+ * Pointers passed to compute calls are device pointers unless LT_HOST_IO is
+ * set, in which case they are host pointers, the call stages them through
+ * context-owned device buffers and returns after the results are copied back.
+ * Without LT_HOST_IO a call returns once the work is enqueued on the
+ * context's stream (lt_sync waits for it).
+ *
+ * Reference citations are paths in the llmtoy-zig tree.
+ */
+#ifndef LLMTOY_HIP_H
+#define LLMTOY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The reference reports these conditions through Zig error
+ * unions and null sessions that send the caller to its CPU path
+ * (gemma4/forward.zig:434-480, gpu/matvec.zig:564-577). */
+typedef enum {
+    LT_OK = 0,
+    LT_ERR_UNSUPPORTED = 1, /* type or shape the device path does not cover: use the CPU path */
+    LT_ERR_INVALID = 2,     /* bad argument (null pointer, size mismatch, k out of range) */
+    LT_ERR_DEVICE = 3,      /* HIP runtime error or no device */
+    LT_ERR_OOM = 4          /* device allocation failed */
+} lt_status;
+
+/* GgmlType ids, gguf/types.zig:23-53 */
+enum {
+    LT_TYPE_F32 = 0,
+    LT_TYPE_F16 = 1,
+    LT_TYPE_Q8_0 = 8,
+    LT_TYPE_Q4_K = 12,
+    LT_TYPE_Q6_K = 14
+};
+
+/* Gated-FFN activation: SiLU (ops/math.zig:37-40) or GELU-tanh (math.zig:84-88). */
+enum { LT_ACT_SILU = 0, LT_ACT_GELU_TANH = 1 };
+
+enum {
+    LT_HOST_IO = 1u << 0,       /* pointers are host memory; the call is synchronous */
+    LT_MOE_NORM_TOPK = 1u << 1, /* renormalise the k selected weights to sum to 1 */
+    LT_MOE_ACCUMULATE = 1u << 2 /* out += result (moeForward's contract, ops/moe.zig:17) */
+};
+
+typedef struct lt_ctx lt_ctx;
+typedef struct lt_tensor lt_tensor;
+
+/* Replaces GpuContext.init / deinit (gpu/context.zig:270-) and
+ * GpuWeights.init / deinit (gemma4/gpu_weights.zig:373, 1065).
+ * Environment: LT_FORCE_NO_DEVICE=1 makes lt_init fail with LT_ERR_DEVICE,
+ * which callers treat like the reference's failed GpuContext.init
+ * (main.zig:1889-1892): fall back to the CPU path. */
+int lt_init(int device, lt_ctx **out_ctx);
+void lt_destroy(lt_ctx *ctx);
+/* Text of the last error on this context ("" if none). */
+const char *lt_last_error(const lt_ctx *ctx);
+/* Wait for all work enqueued on the context's stream. */
+int lt_sync(lt_ctx *ctx);
+/* The hipStream_t the context launches on (for events and interop). */
+void *lt_stream(lt_ctx *ctx);
+
+/* Upload one GGUF tensor (raw block bytes) into device memory the context
+ * owns.  Replaces MatvecSession.initFromRaw (gpu/matvec.zig:564-577) and the
+ * expert uploads of GpuWeights (gemma4/gpu_weights.zig:3660-3777).
+ *   rows, cols : per-expert matrix shape (RawMatrix.rows/cols,
+ *                model/model_weights.zig:17-22); cols is the GGUF row length.
+ *   n_experts  : 1 for a 2-D tensor; E for the flattened 3-D expert tensors
+ *                (gemma4/loader.zig:277-292): expert e's rows start at byte
+ *                e * rows * rowBytes(type, cols).
+ *   nbytes     : must equal n_experts * rows * rowBytes(type, cols)
+ *                (ops/math.zig:194-208).
+ * cols must be a multiple of the block size (32 for Q8_0, 256 for K-quants);
+ * pad shorter rows with zero blocks.  The host buffer may be freed after the
+ * call returns.  The device copy is repacked into a planar layout with the
+ * same byte count. */
+int lt_tensor_upload(lt_ctx *ctx, const void *host_bytes, size_t nbytes, uint32_t ggml_type, size_t rows,
+                     size_t cols, size_t n_experts, lt_tensor **out_tensor);
+/* Copy an uploaded tensor (same layout) to a new device allocation; used to
+ * rotate weight copies so that timing is not served from the 256 MB cache. */
+int lt_tensor_clone(lt_ctx *ctx, const lt_tensor *src, lt_tensor **out_tensor);
+int lt_tensor_free(lt_ctx *ctx, lt_tensor *t);
+/* Device bytes held by the tensor (equal to the GGUF byte count). */
+size_t lt_tensor_bytes(const lt_tensor *t);
+
+/* out[rows] = W[rows x cols] * x[cols], fp32 activations and accumulation.
+ * Replaces quantMatvec / quantMatvecPar (ops/math.zig:133-171, 277-320) and
+ * MatvecSession.run / runQ8_1Mv (gpu/matvec.zig:497-647,
+ * gemma4/gpu_weights.zig:1573-1607).  W must be a 2-D tensor. */
+int lt_matvec(lt_ctx *ctx, float *out, const lt_tensor *W, const float *x, uint32_t flags);
+
+/* Dense gated FFN: out[d_model] = Wd * (act(Wg x) * (Wu x)).
+ * Replaces the dense-FFN matvec chain (model/forward.zig:301-308,
+ * gemma4/forward.zig:392-397; GPU: runLayerDenseFfnQ8_1, gpu_weights.zig). */
+int lt_ffn_dense(lt_ctx *ctx, float *out, const lt_tensor *Wg, const lt_tensor *Wu, const lt_tensor *Wd,
+                 const float *x, uint32_t act, uint32_t flags);
+
+/* Router logits, softmax and top-k (selection on the logits: strict '>', the
+ * lowest index wins ties).  ids[k], weights[k] in selection order.
+ * scores (may be NULL) receives n_experts values as routerTopKSoftmax leaves
+ * its scores buffer: the logit of every unselected expert, the (unnormalised)
+ * softmax probability of every selected one.
+ * weights = exp(l - max) / sum_all exp(l - max), or renormalised over the
+ * selection with LT_MOE_NORM_TOPK.  bias (may be NULL) is added to each logit.
+ * F32 routers reproduce dotf32's accumulation order bit for bit
+ * (ops/math.zig:96-116); Q8_0 routers reproduce dotQ8_0's
+ * (quant/dequant.zig:59-78).  Replaces routerTopKSoftmax / softmaxTopK
+ * (gemma4/forward.zig:637-668) and MoeRouterTopKPipeline
+ * (gpu/matvec.zig:2630-2721). */
+int lt_moe_router_topk(lt_ctx *ctx, const lt_tensor *router, const float *x, const float *bias, uint32_t k,
+                       uint32_t flags, uint32_t *ids, float *weights, float *scores);
+
+/* Expert-indexed gate/up: h[s][j] = act(G_e x)[j] * (U_e x)[j] for slot s,
+ * e = ids[s], j < d_expert; h rows are padded with zeros to down_cols.
+ * gate_up is the flattened [E, 2*d_expert, d_model] tensor (gate rows then
+ * up rows per expert, ops/moe.zig:55-73).  h is [k, down_cols] fp32.
+ * Replaces ExpertGateUpIdPipeline (gpu/matvec.zig:1348-1460). */
+int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const float *x, const uint32_t *ids, uint32_t k,
+                         uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, uint32_t flags);
+
+/* Expert-indexed down with the weighted combine fused:
+ * out[i] = sum_{s<k, in slot order} weights[s] * (D_{ids[s]} h[s])[i]
+ * (plus the previous out[i] with LT_MOE_ACCUMULATE).
+ * Replaces ExpertDownIdPipeline + AccumPipeline (gpu/matvec.zig:1465-1610,
+ * 833-1008). */
+int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float *h, const uint32_t *ids,
+                      const float *weights, uint32_t k, float *out, uint32_t flags);
+
+/* One MoE layer for one token: router -> top-k -> expert gate/up -> down ->
+ * weighted combine, optionally plus a shared dense FFN (sh_* non-NULL):
+ * out = shared_ffn(x) + sum_s w_s * expert_s(x).
+ * Replaces moeForward (ops/moe.zig:18-77) and GpuWeights.runExpertBatch
+ * (gemma4/gpu_weights.zig:2748-3149).  out_ids / out_w (may be NULL)
+ * receive the routing.  d_expert is the expert FFN width; down's cols may be
+ * larger (zero-padded K). */
+int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_tensor *router, const float *router_bias,
+                   const lt_tensor *gate_up, const lt_tensor *down, const lt_tensor *sh_gate,
+                   const lt_tensor *sh_up, const lt_tensor *sh_down, uint32_t k, uint32_t d_expert, uint32_t act,
+                   uint32_t flags, uint32_t *out_ids, float *out_w);
+
+/* Batched prefill of one MoE layer over T tokens (X, out: [T, d_model]):
+ * per-token routing as lt_moe_router_topk, tokens sorted per expert, grouped
+ * expert GEMM with bf16 MFMA (fp32 accumulation) over Q4_K weights
+ * dequantised in LDS, then a combine in slot order.  The reference prefills
+ * one token at a time through the decode path (main.zig:1916-1922); results
+ * match per-token lt_moe_forward to bf16 tolerance. */
+int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt_tensor *router,
+                   const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
+                   uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLMTOY_HIP_H */

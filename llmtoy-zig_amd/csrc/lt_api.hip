@@ -1,0 +1,653 @@
+// lt_api.hip -- the C ABI (include/llmtoy_hip.h): contexts, tensor upload
+// into the planar device layout, argument validation, and kernel dispatch.
+#include "llmtoy_hip.h"
+#include "lt_internal.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+#include <vector>
+
+using lt::DevTensor;
+
+struct lt_tensor {
+    DevTensor t;
+};
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+}  // namespace
+
+struct lt_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // context-owned device scratch, grown on demand
+    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh;
+};
+
+namespace {
+
+int fail(lt_ctx *ctx, int code, const char *fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return code;
+}
+
+int hip_fail(lt_ctx *ctx, hipError_t e, const char *what) {
+    return fail(ctx, e == hipErrorOutOfMemory ? LT_ERR_OOM : LT_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define LT_HIP(ctx, call)                                     \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+    } while (0)
+
+int ensure(lt_ctx *ctx, DevBuf &b, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (b.cap >= bytes) return LT_OK;
+    if (b.p) {
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        LT_HIP(ctx, hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    size_t cap = (bytes + 4095) & ~(size_t)4095;
+    LT_HIP(ctx, hipMalloc(&b.p, cap));
+    b.cap = cap;
+    return LT_OK;
+}
+
+size_t block_elems(uint32_t type) {
+    switch (type) {
+    case LT_TYPE_F32: return 1;
+    case LT_TYPE_Q8_0: return 32;
+    case LT_TYPE_Q4_K:
+    case LT_TYPE_Q6_K: return 256;
+    default: return 0;
+    }
+}
+
+size_t block_bytes(uint32_t type) {
+    switch (type) {
+    case LT_TYPE_F32: return 4;
+    case LT_TYPE_Q8_0: return 34;
+    case LT_TYPE_Q4_K: return 144;
+    case LT_TYPE_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
+// Largest row length the LDS-staged kernels take (x is staged as fp32).
+constexpr size_t kMaxQuantCols = 16384;
+
+// Planar repack of GGUF rows (see lt_internal.h).
+void repack(const uint8_t *src, uint8_t *dst, const DevTensor &t) {
+    const size_t R = t.total_rows, nb = t.blocks_per_row;
+    const size_t nblk = R * nb;
+    switch (t.type) {
+    case LT_TYPE_F32: memcpy(dst, src, t.bytes); break;
+    case LT_TYPE_Q8_0: {
+        uint8_t *qs = dst, *d = dst + nblk * 32;
+        for (size_t b = 0; b < nblk; b++) {
+            const uint8_t *blk = src + b * 34;
+            d[2 * b] = blk[0];
+            d[2 * b + 1] = blk[1];
+            memcpy(qs + b * 32, blk + 2, 32);
+        }
+        break;
+    }
+    case LT_TYPE_Q4_K: {
+        uint8_t *hdr = dst, *qs = dst + nblk * 16;
+        for (size_t b = 0; b < nblk; b++) {
+            const uint8_t *blk = src + b * 144;
+            memcpy(hdr + b * 16, blk, 16);
+            memcpy(qs + b * 128, blk + 16, 128);
+        }
+        break;
+    }
+    case LT_TYPE_Q6_K: {
+        uint8_t *ql = dst, *qh = dst + nblk * 128, *sc = qh + nblk * 64, *d = sc + nblk * 16;
+        for (size_t b = 0; b < nblk; b++) {
+            const uint8_t *blk = src + b * 210;
+            memcpy(ql + b * 128, blk, 128);
+            memcpy(qh + b * 64, blk + 128, 64);
+            memcpy(sc + b * 16, blk + 192, 16);
+            d[2 * b] = blk[208];
+            d[2 * b + 1] = blk[209];
+        }
+        break;
+    }
+    }
+}
+
+void set_planes(DevTensor &t) {
+    const size_t nblk = t.total_rows * t.blocks_per_row;
+    uint8_t *b = t.base;
+    t.p0 = b;
+    t.p1 = t.p2 = t.p3 = nullptr;
+    switch (t.type) {
+    case LT_TYPE_Q8_0: t.p1 = b + nblk * 32; break;
+    case LT_TYPE_Q4_K: t.p1 = b + nblk * 16; break;
+    case LT_TYPE_Q6_K:
+        t.p1 = b + nblk * 128;
+        t.p2 = t.p1 + nblk * 64;
+        t.p3 = t.p2 + nblk * 16;
+        break;
+    default: break;
+    }
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Input staging for LT_HOST_IO: copies host data into a context buffer.
+int stage_in(lt_ctx *ctx, DevBuf &buf, const void *host, size_t bytes, const void **dev) {
+    int rc = ensure(ctx, buf, bytes);
+    if (rc) return rc;
+    LT_HIP(ctx, hipMemcpyAsync(buf.p, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    *dev = buf.p;
+    return LT_OK;
+}
+
+int launch_rc(lt_ctx *ctx, hipError_t e, const char *what) {
+    if (e == hipSuccess) return LT_OK;
+    return fail(ctx, LT_ERR_DEVICE, "%s launch failed: %s", what, hipGetErrorString(e));
+}
+
+int matvec_dev(lt_ctx *ctx, const DevTensor &W, const float *x, float *y) {
+    hipError_t e;
+    switch (W.type) {
+    case LT_TYPE_Q4_K: e = lt::launch_matvec_q4k(W, 0, W.total_rows, x, y, ctx->stream); break;
+    case LT_TYPE_Q8_0: e = lt::launch_matvec_q8_0(W, x, y, ctx->stream); break;
+    case LT_TYPE_Q6_K: e = lt::launch_matvec_q6k(W, x, y, ctx->stream); break;
+    case LT_TYPE_F32: e = lt::launch_matvec_f32(W, x, y, ctx->stream); break;
+    default: return fail(ctx, LT_ERR_UNSUPPORTED, "matvec: unsupported type %u", W.type);
+    }
+    return launch_rc(ctx, e, "matvec");
+}
+
+int check_matvec_tensor(lt_ctx *ctx, const lt_tensor *W) {
+    if (!W) return fail(ctx, LT_ERR_INVALID, "null tensor");
+    if (W->t.type != LT_TYPE_F32 && W->t.cols > kMaxQuantCols)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "row length %zu exceeds %zu", W->t.cols, kMaxQuantCols);
+    return LT_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ lifecycle
+extern "C" int lt_init(int device, lt_ctx **out_ctx) {
+    if (!out_ctx) return LT_ERR_INVALID;
+    *out_ctx = nullptr;
+    const char *force = getenv("LT_FORCE_NO_DEVICE");
+    if (force && force[0] == '1') return LT_ERR_DEVICE;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || device < 0 || device >= n) return LT_ERR_DEVICE;
+    if (hipSetDevice(device) != hipSuccess) return LT_ERR_DEVICE;
+    lt_ctx *ctx = new (std::nothrow) lt_ctx();
+    if (!ctx) return LT_ERR_OOM;
+    ctx->device = device;
+    if (hipStreamCreate(&ctx->stream) != hipSuccess) {
+        delete ctx;
+        return LT_ERR_DEVICE;
+    }
+    *out_ctx = ctx;
+    return LT_OK;
+}
+
+extern "C" void lt_destroy(lt_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    DevBuf *bufs[] = {&ctx->x, &ctx->out, &ctx->logits, &ctx->h, &ctx->ids, &ctx->w,
+                      &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh};
+    for (DevBuf *b : bufs)
+        if (b->p) (void)hipFree(b->p);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+extern "C" const char *lt_last_error(const lt_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+extern "C" int lt_sync(lt_ctx *ctx) {
+    if (!ctx) return LT_ERR_INVALID;
+    LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return LT_OK;
+}
+
+extern "C" void *lt_stream(lt_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+// ------------------------------------------------------------------ tensors
+extern "C" int lt_tensor_upload(lt_ctx *ctx, const void *host_bytes, size_t nbytes, uint32_t type, size_t rows,
+                                size_t cols, size_t n_experts, lt_tensor **out_tensor) {
+    if (!ctx || !host_bytes || !out_tensor) return fail(ctx, LT_ERR_INVALID, "null argument");
+    *out_tensor = nullptr;
+    const size_t be = block_elems(type), bb = block_bytes(type);
+    if (!be) return fail(ctx, LT_ERR_UNSUPPORTED, "tensor type %u not supported by the device path", type);
+    if (rows == 0 || cols == 0 || n_experts == 0) return fail(ctx, LT_ERR_INVALID, "empty shape");
+    if (cols % be) return fail(ctx, LT_ERR_UNSUPPORTED, "cols %zu not a multiple of the %zu-element block", cols, be);
+    const size_t total_rows = rows * n_experts;
+    const size_t want = total_rows * (cols / be) * bb;
+    if (nbytes != want) return fail(ctx, LT_ERR_INVALID, "nbytes %zu != expected %zu", nbytes, want);
+    lt_tensor *t = new (std::nothrow) lt_tensor();
+    if (!t) return fail(ctx, LT_ERR_OOM, "host allocation failed");
+    t->t.type = type;
+    t->t.rows = rows;
+    t->t.cols = cols;
+    t->t.n_experts = n_experts;
+    t->t.total_rows = total_rows;
+    t->t.bytes = nbytes;
+    t->t.blocks_per_row = cols / be;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc((void **)&t->t.base, nbytes);
+    if (e != hipSuccess) {
+        delete t;
+        return hip_fail(ctx, e, "hipMalloc(tensor)");
+    }
+    std::vector<uint8_t> planar;
+    const uint8_t *src = (const uint8_t *)host_bytes;
+    if (type != LT_TYPE_F32) {
+        try {
+            planar.resize(nbytes);
+        } catch (...) {
+            (void)hipFree(t->t.base);
+            delete t;
+            return fail(ctx, LT_ERR_OOM, "host repack buffer");
+        }
+        repack(src, planar.data(), t->t);
+        src = planar.data();
+    }
+    e = hipMemcpy(t->t.base, src, nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(t->t.base);
+        delete t;
+        return hip_fail(ctx, e, "hipMemcpy(tensor)");
+    }
+    set_planes(t->t);
+    *out_tensor = t;
+    return LT_OK;
+}
+
+extern "C" int lt_tensor_clone(lt_ctx *ctx, const lt_tensor *src, lt_tensor **out_tensor) {
+    if (!ctx || !src || !out_tensor) return fail(ctx, LT_ERR_INVALID, "null argument");
+    lt_tensor *t = new (std::nothrow) lt_tensor(*src);
+    if (!t) return fail(ctx, LT_ERR_OOM, "host allocation failed");
+    hipError_t e = hipMalloc((void **)&t->t.base, src->t.bytes);
+    if (e == hipSuccess) e = hipMemcpy(t->t.base, src->t.base, src->t.bytes, hipMemcpyDeviceToDevice);
+    if (e != hipSuccess) {
+        if (t->t.base != src->t.base) (void)hipFree(t->t.base);
+        delete t;
+        return hip_fail(ctx, e, "tensor clone");
+    }
+    set_planes(t->t);
+    *out_tensor = t;
+    return LT_OK;
+}
+
+extern "C" int lt_tensor_free(lt_ctx *ctx, lt_tensor *t) {
+    if (!t) return LT_OK;
+    if (ctx) (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(t->t.base);
+    delete t;
+    return LT_OK;
+}
+
+extern "C" size_t lt_tensor_bytes(const lt_tensor *t) { return t ? t->t.bytes : 0; }
+
+// ------------------------------------------------------------------ compute
+extern "C" int lt_matvec(lt_ctx *ctx, float *out, const lt_tensor *W, const float *x, uint32_t flags) {
+    if (!ctx || !out || !x) return fail(ctx, LT_ERR_INVALID, "null argument");
+    int rc = check_matvec_tensor(ctx, W);
+    if (rc) return rc;
+    const DevTensor &T = W->t;
+    const bool host = flags & LT_HOST_IO;
+    const float *dx = x;
+    float *dy = out;
+    if (host) {
+        if ((rc = stage_in(ctx, ctx->x, x, T.cols * 4, (const void **)&dx))) return rc;
+        if ((rc = ensure(ctx, ctx->out, T.total_rows * 4))) return rc;
+        dy = (float *)ctx->out.p;
+    } else if (!aligned16(x)) {
+        return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
+    }
+    if ((rc = matvec_dev(ctx, T, dx, dy))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(out, dy, T.total_rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+namespace {
+
+// act(g) * u elementwise, zero tail to n_out (generic dense-FFN path).
+__global__ void k_act_mul(const float *g, const float *u, int n, int n_out, uint32_t act, float *h) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = lt::act_apply(act, g[i]) * u[i];
+    else if (i < n_out) h[i] = 0.f;
+}
+
+// out = Wd * (act(Wg x) * (Wu x)), all device pointers.
+int ffn_dense_dev(lt_ctx *ctx, const DevTensor &G, const DevTensor &U, const DevTensor &D, const float *x,
+                  uint32_t act, float *out) {
+    const size_t F = G.total_rows, Kd = D.cols;
+    int rc = ensure(ctx, ctx->h, Kd * 4);
+    if (rc) return rc;
+    float *h = (float *)ctx->h.p;
+    if (G.type == LT_TYPE_Q8_0 && U.type == LT_TYPE_Q8_0 && Kd == F) {
+        if ((rc = launch_rc(ctx, lt::launch_gate_up_q8_0(G, U, x, act, h, ctx->stream), "gate_up_q8_0")))
+            return rc;
+    } else {
+        if ((rc = ensure(ctx, ctx->g, F * 4)) || (rc = ensure(ctx, ctx->u, F * 4))) return rc;
+        if ((rc = matvec_dev(ctx, G, x, (float *)ctx->g.p))) return rc;
+        if ((rc = matvec_dev(ctx, U, x, (float *)ctx->u.p))) return rc;
+        hipLaunchKernelGGL(k_act_mul, dim3((Kd + 255) / 256), dim3(256), 0, ctx->stream, (const float *)ctx->g.p,
+                           (const float *)ctx->u.p, (int)F, (int)Kd, act, h);
+        if ((rc = launch_rc(ctx, hipGetLastError(), "act_mul"))) return rc;
+    }
+    return matvec_dev(ctx, D, h, out);
+}
+
+int check_ffn(lt_ctx *ctx, const lt_tensor *Wg, const lt_tensor *Wu, const lt_tensor *Wd, size_t d_model) {
+    int rc;
+    if ((rc = check_matvec_tensor(ctx, Wg)) || (rc = check_matvec_tensor(ctx, Wu)) ||
+        (rc = check_matvec_tensor(ctx, Wd)))
+        return rc;
+    const DevTensor &G = Wg->t, &U = Wu->t, &D = Wd->t;
+    if (G.total_rows != U.total_rows || G.cols != U.cols || G.cols != d_model || D.total_rows != d_model ||
+        D.cols < G.total_rows)
+        return fail(ctx, LT_ERR_INVALID, "dense FFN shapes do not match (gate %zux%zu, up %zux%zu, down %zux%zu)",
+                    G.total_rows, G.cols, U.total_rows, U.cols, D.total_rows, D.cols);
+    return LT_OK;
+}
+
+}  // namespace
+
+extern "C" int lt_ffn_dense(lt_ctx *ctx, float *out, const lt_tensor *Wg, const lt_tensor *Wu,
+                            const lt_tensor *Wd, const float *x, uint32_t act, uint32_t flags) {
+    if (!ctx || !out || !x || !Wg || !Wu || !Wd) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
+    const size_t D = Wg->t.cols;
+    int rc = check_ffn(ctx, Wg, Wu, Wd, D);
+    if (rc) return rc;
+    const bool host = flags & LT_HOST_IO;
+    const float *dx = x;
+    float *dy = out;
+    if (host) {
+        if ((rc = stage_in(ctx, ctx->x, x, D * 4, (const void **)&dx))) return rc;
+        if ((rc = ensure(ctx, ctx->out, D * 4))) return rc;
+        dy = (float *)ctx->out.p;
+    } else if (!aligned16(x)) {
+        return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
+    }
+    if ((rc = ffn_dense_dev(ctx, Wg->t, Wu->t, Wd->t, dx, act, dy))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(out, dy, D * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+namespace {
+
+constexpr uint32_t kMaxK = 16;
+constexpr size_t kMaxExperts = 1024;
+
+int check_router(lt_ctx *ctx, const lt_tensor *router, size_t d_model, uint32_t k) {
+    if (!router) return fail(ctx, LT_ERR_INVALID, "null router");
+    const DevTensor &R = router->t;
+    if (R.type != LT_TYPE_F32 && R.type != LT_TYPE_Q8_0)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "router type %u (device path: F32, Q8_0)", R.type);
+    if (R.cols != d_model) return fail(ctx, LT_ERR_INVALID, "router cols %zu != d_model %zu", R.cols, d_model);
+    if (R.total_rows > kMaxExperts) return fail(ctx, LT_ERR_UNSUPPORTED, "more than %zu experts", kMaxExperts);
+    if (k == 0 || k > kMaxK || k > R.total_rows)
+        return fail(ctx, LT_ERR_INVALID, "k=%u out of range (1..%u, <= n_experts)", k, kMaxK);
+    return LT_OK;
+}
+
+// logits -> ids/w in context buffers (and scores, if non-NULL); x, bias,
+// scores device pointers.
+int router_dev(lt_ctx *ctx, const DevTensor &R, const float *x, const float *bias, uint32_t k, uint32_t flags,
+               float *scores = nullptr) {
+    int rc;
+    if ((rc = ensure(ctx, ctx->logits, R.total_rows * 4)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
+        (rc = ensure(ctx, ctx->w, kMaxK * 4)))
+        return rc;
+    float *logits = (float *)ctx->logits.p;
+    hipError_t e = R.type == LT_TYPE_F32 ? lt::launch_router_f32(R, x, bias, logits, ctx->stream)
+                                         : lt::launch_router_q8_0(R, x, bias, logits, ctx->stream);
+    if ((rc = launch_rc(ctx, e, "router"))) return rc;
+    e = lt::launch_topk_softmax(logits, (uint32_t)R.total_rows, k, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u,
+                                (uint32_t *)ctx->ids.p, (float *)ctx->w.p, scores, ctx->stream);
+    return launch_rc(ctx, e, "topk_softmax");
+}
+
+int stage_bias(lt_ctx *ctx, const float *bias, size_t n, bool host, const float **dbias) {
+    *dbias = bias;
+    if (bias && host) return stage_in(ctx, ctx->bias, bias, n * 4, (const void **)dbias);
+    return LT_OK;
+}
+
+int copy_routing_out(lt_ctx *ctx, uint32_t k, uint32_t *ids, float *w, bool host) {
+    const hipMemcpyKind kind = host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    if (ids) LT_HIP(ctx, hipMemcpyAsync(ids, ctx->ids.p, k * 4, kind, ctx->stream));
+    if (w) LT_HIP(ctx, hipMemcpyAsync(w, ctx->w.p, k * 4, kind, ctx->stream));
+    return LT_OK;
+}
+
+int check_experts(lt_ctx *ctx, const lt_tensor *gate_up, const lt_tensor *down, size_t d_model, uint32_t d_expert,
+                  size_t n_experts) {
+    if (!gate_up || !down) return fail(ctx, LT_ERR_INVALID, "null expert tensor");
+    const DevTensor &GU = gate_up->t, &D = down->t;
+    if (GU.type != LT_TYPE_Q4_K || D.type != LT_TYPE_Q4_K)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "expert types %u/%u: the device expert path takes Q4_K", GU.type,
+                    D.type);
+    if (GU.cols != d_model || GU.rows != 2 * (size_t)d_expert)
+        return fail(ctx, LT_ERR_INVALID, "gate_up per-expert shape %zux%zu != %ux%zu", GU.rows, GU.cols,
+                    2 * d_expert, d_model);
+    if (D.rows != d_model || D.cols < d_expert)
+        return fail(ctx, LT_ERR_INVALID, "down per-expert shape %zux%zu (need %zu rows, >= %u cols)", D.rows, D.cols,
+                    d_model, d_expert);
+    if (GU.n_experts != D.n_experts || (n_experts && GU.n_experts != n_experts))
+        return fail(ctx, LT_ERR_INVALID, "expert counts differ (gate_up %zu, down %zu, router %zu)", GU.n_experts,
+                    D.n_experts, n_experts);
+    if (GU.cols > 8192) return fail(ctx, LT_ERR_UNSUPPORTED, "d_model %zu > 8192", GU.cols);
+    if (D.blocks_per_row > 16) return fail(ctx, LT_ERR_UNSUPPORTED, "down row length %zu > 4096", D.cols);
+    return LT_OK;
+}
+
+}  // namespace
+
+extern "C" int lt_moe_router_topk(lt_ctx *ctx, const lt_tensor *router, const float *x, const float *bias,
+                                  uint32_t k, uint32_t flags, uint32_t *ids, float *weights, float *scores) {
+    if (!ctx || !x || !router || !ids || !weights) return fail(ctx, LT_ERR_INVALID, "null argument");
+    int rc = check_router(ctx, router, router->t.cols, k);
+    if (rc) return rc;
+    const DevTensor &R = router->t;
+    const bool host = flags & LT_HOST_IO;
+    const float *dx = x, *dbias = bias;
+    float *dscores = scores;
+    if (host) {
+        if ((rc = stage_in(ctx, ctx->x, x, R.cols * 4, (const void **)&dx))) return rc;
+        if (scores) {
+            if ((rc = ensure(ctx, ctx->out, R.total_rows * 4))) return rc;
+            dscores = (float *)ctx->out.p;
+        }
+    }
+    if ((rc = stage_bias(ctx, bias, R.total_rows, host, &dbias))) return rc;
+    if ((rc = router_dev(ctx, R, dx, dbias, k, flags, dscores))) return rc;
+    if ((rc = copy_routing_out(ctx, k, ids, weights, host))) return rc;
+    if (host) {
+        if (scores)
+            LT_HIP(ctx, hipMemcpyAsync(scores, dscores, R.total_rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+extern "C" int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const float *x, const uint32_t *ids,
+                                    uint32_t k, uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
+                                    uint32_t flags) {
+    if (!ctx || !gate_up || !x || !ids || !h) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (k == 0 || k > kMaxK) return fail(ctx, LT_ERR_INVALID, "k=%u out of range", k);
+    if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
+    const DevTensor &GU = gate_up->t;
+    if (GU.type != LT_TYPE_Q4_K) return fail(ctx, LT_ERR_UNSUPPORTED, "gate_up type %u: device path takes Q4_K", GU.type);
+    if (GU.rows != 2 * (size_t)d_expert) return fail(ctx, LT_ERR_INVALID, "gate_up rows %zu != 2*d_expert", GU.rows);
+    if (down_cols < d_expert || down_cols % 256) return fail(ctx, LT_ERR_INVALID, "down_cols %u", down_cols);
+    if (GU.cols > 8192) return fail(ctx, LT_ERR_UNSUPPORTED, "d_model %zu > 8192", GU.cols);
+    const bool host = flags & LT_HOST_IO;
+    const float *dx = x;
+    const uint32_t *dids = ids;
+    float *dh = h;
+    int rc;
+    if (host) {
+        for (uint32_t s = 0; s < k; s++)
+            if (ids[s] >= GU.n_experts) return fail(ctx, LT_ERR_INVALID, "ids[%u]=%u >= n_experts", s, ids[s]);
+        if ((rc = stage_in(ctx, ctx->x, x, GU.cols * 4, (const void **)&dx))) return rc;
+        if ((rc = stage_in(ctx, ctx->ids_io, ids, k * 4, (const void **)&dids))) return rc;
+        if ((rc = ensure(ctx, ctx->out, (size_t)k * down_cols * 4))) return rc;
+        dh = (float *)ctx->out.p;
+    }
+    rc = launch_rc(ctx, lt::launch_expert_gate_up_q4k(GU, dx, dids, k, d_expert, down_cols, act, dh, ctx->stream),
+                   "expert_gate_up");
+    if (rc) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(h, dh, (size_t)k * down_cols * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float *h, const uint32_t *ids,
+                                 const float *weights, uint32_t k, float *out, uint32_t flags) {
+    if (!ctx || !down || !h || !ids || !weights || !out) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (k == 0 || k > kMaxK) return fail(ctx, LT_ERR_INVALID, "k=%u out of range", k);
+    const DevTensor &D = down->t;
+    if (D.type != LT_TYPE_Q4_K) return fail(ctx, LT_ERR_UNSUPPORTED, "down type %u: device path takes Q4_K", D.type);
+    if (D.blocks_per_row > 16) return fail(ctx, LT_ERR_UNSUPPORTED, "down row length %zu > 4096", D.cols);
+    const bool host = flags & LT_HOST_IO;
+    const float *dh = h, *dw = weights;
+    const uint32_t *dids = ids;
+    float *dout = out;
+    int rc;
+    if (host) {
+        for (uint32_t s = 0; s < k; s++)
+            if (ids[s] >= D.n_experts) return fail(ctx, LT_ERR_INVALID, "ids[%u]=%u >= n_experts", s, ids[s]);
+        if ((rc = stage_in(ctx, ctx->h, h, (size_t)k * D.cols * 4, (const void **)&dh))) return rc;
+        if ((rc = stage_in(ctx, ctx->ids_io, ids, k * 4, (const void **)&dids))) return rc;
+        if ((rc = stage_in(ctx, ctx->w_io, weights, k * 4, (const void **)&dw))) return rc;
+        if (flags & LT_MOE_ACCUMULATE) {
+            if ((rc = stage_in(ctx, ctx->out, out, D.rows * 4, (const void **)&dout))) return rc;
+        } else if ((rc = ensure(ctx, ctx->out, D.rows * 4))) {
+            return rc;
+        }
+        dout = (float *)ctx->out.p;
+    }
+    rc = launch_rc(ctx,
+                   lt::launch_expert_down_q4k(D, dh, dids, dw, k, nullptr, (flags & LT_MOE_ACCUMULATE) ? 1 : 0, dout,
+                                              ctx->stream),
+                   "expert_down");
+    if (rc) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(out, dout, D.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+namespace {
+
+// The decode MoE layer on device pointers.
+int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const float *bias, const DevTensor &GU,
+            const DevTensor &D, const lt_tensor *sh_gate, const lt_tensor *sh_up, const lt_tensor *sh_down,
+            uint32_t k, uint32_t d_expert, uint32_t act, uint32_t flags) {
+    int rc;
+    const float *base = nullptr;
+    if (sh_gate) {
+        if ((rc = ensure(ctx, ctx->shared, D.rows * 4))) return rc;
+        if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p))) return rc;
+        base = (const float *)ctx->shared.p;
+    }
+    if ((rc = router_dev(ctx, R, x, bias, k, flags))) return rc;
+    const size_t Kd = D.cols;
+    if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
+    float *h = (float *)ctx->eh.p;
+    rc = launch_rc(ctx,
+                   lt::launch_expert_gate_up_q4k(GU, x, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act,
+                                                 h, ctx->stream),
+                   "expert_gate_up");
+    if (rc) return rc;
+    return launch_rc(ctx,
+                     lt::launch_expert_down_q4k(D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k, base,
+                                                (flags & LT_MOE_ACCUMULATE) ? 1 : 0, out, ctx->stream),
+                     "expert_down");
+}
+
+}  // namespace
+
+extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_tensor *router,
+                              const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down,
+                              const lt_tensor *sh_gate, const lt_tensor *sh_up, const lt_tensor *sh_down, uint32_t k,
+                              uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w) {
+    if (!ctx || !out || !x) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
+    if (!router || !gate_up || !down) return fail(ctx, LT_ERR_INVALID, "null tensor");
+    const size_t d_model = gate_up->t.cols;
+    int rc;
+    if ((rc = check_router(ctx, router, d_model, k))) return rc;
+    if ((rc = check_experts(ctx, gate_up, down, d_model, d_expert, router->t.total_rows))) return rc;
+    const bool shared = sh_gate || sh_up || sh_down;
+    if (shared) {
+        if (!sh_gate || !sh_up || !sh_down) return fail(ctx, LT_ERR_INVALID, "shared FFN needs gate, up and down");
+        if ((rc = check_ffn(ctx, sh_gate, sh_up, sh_down, d_model))) return rc;
+    }
+    const bool host = flags & LT_HOST_IO;
+    const float *dx = x, *dbias = router_bias;
+    float *dout = out;
+    if (host) {
+        if ((rc = stage_in(ctx, ctx->x, x, d_model * 4, (const void **)&dx))) return rc;
+        if (flags & LT_MOE_ACCUMULATE) {
+            if ((rc = stage_in(ctx, ctx->out, out, d_model * 4, (const void **)&dout))) return rc;
+        } else if ((rc = ensure(ctx, ctx->out, d_model * 4))) {
+            return rc;
+        }
+        dout = (float *)ctx->out.p;
+    } else if (!aligned16(x)) {
+        return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
+    }
+    if ((rc = stage_bias(ctx, router_bias, router->t.total_rows, host, &dbias))) return rc;
+    rc = moe_dev(ctx, dout, dx, router->t, dbias, gate_up->t, down->t, shared ? sh_gate : nullptr, sh_up, sh_down, k,
+                 d_expert, act, flags);
+    if (rc) return rc;
+    if ((rc = copy_routing_out(ctx, k, out_ids, out_w, host))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(out, dout, d_model * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt_tensor *router,
+                              const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
+                              uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w) {
+    (void)out; (void)X; (void)T; (void)router; (void)router_bias; (void)gate_up; (void)down; (void)k;
+    (void)d_expert; (void)act; (void)flags; (void)out_ids; (void)out_w;
+    return fail(ctx, LT_ERR_UNSUPPORTED, "lt_moe_prefill: not built yet");
+}

@@ -1,0 +1,345 @@
+// lt_q4k.hip -- Q4_K decode kernels for gfx950 (wave64).
+//
+// Q4_K super-block (quant/dequant.zig:136-187): 256 elements, d, dmin (f16),
+// 12 bytes of packed 6-bit (scale, min) for 8 sub-blocks of 32, and 128 bytes
+// of nibbles: qs[32p + i] holds element 64p + i (low nibble, sub-block 2p)
+// and 64p + 32 + i (high nibble, sub-block 2p + 1).
+//
+// Work unit of one lane: a 16-byte "chunk" cc (0..7) of a super-block's qs
+// plane, i.e. 32 elements: bytes qs[32p + h + t] (p = cc/2, h = 16*(cc%2),
+// t < 16) give elements 64p + h + t (low nibbles) and 64p + 32 + h + t (high
+// nibbles).  With the planar layout the 8 chunks of a super-block, and the
+// super-blocks of a row, are consecutive 16-byte vectors, so a wavefront's
+// qs loads are one contiguous stream.  Each lane also loads its super-block's
+// 16-byte header (d, dmin, scales); the 8 lanes of a super-block load the
+// same header in the same instruction.
+//
+// The element value is (d*sc)*q - (dmin*mn); the kernels use
+// (d*sc)*sum(q*x) - (dmin*mn)*sum(x) per 16-element half, which is the same
+// sum reassociated (fp32 accumulation, checked to 1e-3 rel-L2 against the
+// oracle's element-wise dequant then dotf32).
+#include "lt_internal.h"
+
+namespace lt {
+
+namespace {
+
+// x values of chunk cc of super-block sb: 16 low-nibble partners and 16
+// high-nibble partners.
+struct XChunk {
+    float lo[16];
+    float hi[16];
+    float slo, shi;  // sums, for the min term
+};
+
+__device__ __forceinline__ void load_xchunk(const float *xs, int sb, int cc, XChunk &xc) {
+    const float *p = xs + sb * 256 + 64 * (cc >> 1) + 16 * (cc & 1);
+    float slo = 0.f, shi = 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; t += 4) {
+        float4 a = *reinterpret_cast<const float4 *>(p + t);
+        float4 b = *reinterpret_cast<const float4 *>(p + 32 + t);
+        xc.lo[t] = a.x; xc.lo[t + 1] = a.y; xc.lo[t + 2] = a.z; xc.lo[t + 3] = a.w;
+        xc.hi[t] = b.x; xc.hi[t + 1] = b.y; xc.hi[t + 2] = b.z; xc.hi[t + 3] = b.w;
+        slo += (a.x + a.y) + (a.z + a.w);
+        shi += (b.x + b.y) + (b.z + b.w);
+    }
+    xc.slo = slo;
+    xc.shi = shi;
+}
+
+// Dot of one 16-byte qs chunk with its x values.
+__device__ __forceinline__ float q4k_chunk_dot(uint4 hdr, uint4 q, int cc, const XChunk &xc) {
+    const float d = f16_bits_to_f32(hdr.x);
+    const float dmin = f16_bits_to_f32(hdr.x >> 16);
+    const int j = (cc >> 1) * 2;
+    float sc0, mn0, sc1, mn1;
+    // branch-free get_scale_min_k4 for the pair (j, j+1)
+    {
+        const int i0 = j & 3, i1 = (j + 1) & 3;
+        const bool low = j < 4;
+        uint32_t a0 = (hdr.y >> (8 * i0)) & 0xffu, b0 = (hdr.z >> (8 * i0)) & 0xffu,
+                 c0 = (hdr.w >> (8 * i0)) & 0xffu;
+        uint32_t a1 = (hdr.y >> (8 * i1)) & 0xffu, b1 = (hdr.z >> (8 * i1)) & 0xffu,
+                 c1 = (hdr.w >> (8 * i1)) & 0xffu;
+        sc0 = (float)(low ? (a0 & 63u) : ((c0 & 15u) | ((a0 >> 6) << 4)));
+        mn0 = (float)(low ? (b0 & 63u) : ((c0 >> 4) | ((b0 >> 6) << 4)));
+        sc1 = (float)(low ? (a1 & 63u) : ((c1 & 15u) | ((a1 >> 6) << 4)));
+        mn1 = (float)(low ? (b1 & 63u) : ((c1 >> 4) | ((b1 >> 6) << 4)));
+    }
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float dl = 0.f, dh = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t lo = w[t] & 0x0f0f0f0fu;
+        const uint32_t hi = (w[t] >> 4) & 0x0f0f0f0fu;
+        dl += (float)(lo & 0xffu) * xc.lo[4 * t + 0];
+        dl += (float)((lo >> 8) & 0xffu) * xc.lo[4 * t + 1];
+        dl += (float)((lo >> 16) & 0xffu) * xc.lo[4 * t + 2];
+        dl += (float)(lo >> 24) * xc.lo[4 * t + 3];
+        dh += (float)(hi & 0xffu) * xc.hi[4 * t + 0];
+        dh += (float)((hi >> 8) & 0xffu) * xc.hi[4 * t + 1];
+        dh += (float)((hi >> 16) & 0xffu) * xc.hi[4 * t + 2];
+        dh += (float)(hi >> 24) * xc.hi[4 * t + 3];
+    }
+    return ((d * sc0) * dl - (dmin * mn0) * xc.slo) + ((d * sc1) * dh - (dmin * mn1) * xc.shi);
+}
+
+// Stage x[0..n) into LDS with 16-byte loads (n % 4 == 0).
+__device__ __forceinline__ void stage_x(float *xs, const float *x, int n) {
+    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4)
+        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + i);
+    __syncthreads();
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------
+// Generic matvec y[r] = W[row0 + r] . x for r < nrows.
+// G lanes per row (power of two), CPL chunks per lane, R rows per lane group.
+// Block: 256 threads = 256/G groups.  Grid: ceil(nrows / (groups * R)).
+template <int G, int CPL, int R>
+__global__ void __launch_bounds__(256) k_matvec_q4k(const uint8_t *__restrict__ hdr,
+                                                    const uint8_t *__restrict__ qs,
+                                                    const float *__restrict__ x, float *__restrict__ y,
+                                                    int row0, int nrows, int nsb) {
+    extern __shared__ float xs[];
+    stage_x(xs, x, nsb * 256);
+    const int groups = 256 / G;
+    const int g = threadIdx.x / G, lane = threadIdx.x % G;
+    const int rbase = (blockIdx.x * groups + g) * R;
+    const int nch = nsb * 8;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = lane + G * i;
+        if (c < nch) {
+            const int sb = c >> 3, cc = c & 7;
+            uint4 hv[R], qv[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int row = rbase + r;
+                if (row < nrows) {
+                    size_t blk = (size_t)(row0 + row) * nsb + sb;
+                    hv[r] = ldg16(hdr + blk * 16);
+                    qv[r] = ldg16(qs + blk * 128 + cc * 16);
+                }
+            }
+            XChunk xc;
+            load_xchunk(xs, sb, cc, xc);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rbase + r < nrows) acc[r] += q4k_chunk_dot(hv[r], qv[r], cc, xc);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float v = group_sum<G>(acc[r]);
+        if (lane == 0 && rbase + r < nrows) y[rbase + r] = v;
+    }
+}
+
+template <int G, int CPL>
+static hipError_t launch_mv_q4k_t(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
+                                  hipStream_t s) {
+    constexpr int R = 4;
+    const int groups = 256 / G;
+    const int nblk = (int)((nrows + (size_t)groups * R - 1) / ((size_t)groups * R));
+    const int nsb = (int)W.blocks_per_row;
+    hipLaunchKernelGGL((k_matvec_q4k<G, CPL, R>), dim3(nblk), dim3(256), nsb * 256 * sizeof(float), s, W.p0, W.p1,
+                       x, y, (int)row0, (int)nrows, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_q4k(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
+                             hipStream_t s) {
+    const int nch = (int)W.blocks_per_row * 8;
+    if (nch <= 8) return launch_mv_q4k_t<8, 1>(W, row0, nrows, x, y, s);
+    if (nch <= 16) return launch_mv_q4k_t<16, 1>(W, row0, nrows, x, y, s);
+    if (nch <= 32) return launch_mv_q4k_t<32, 1>(W, row0, nrows, x, y, s);
+    switch ((nch + 63) / 64) {
+    case 1: return launch_mv_q4k_t<64, 1>(W, row0, nrows, x, y, s);
+    case 2: return launch_mv_q4k_t<64, 2>(W, row0, nrows, x, y, s);
+    case 3: return launch_mv_q4k_t<64, 3>(W, row0, nrows, x, y, s);
+    case 4: return launch_mv_q4k_t<64, 4>(W, row0, nrows, x, y, s);
+    case 5: return launch_mv_q4k_t<64, 5>(W, row0, nrows, x, y, s);
+    case 6: return launch_mv_q4k_t<64, 6>(W, row0, nrows, x, y, s);
+    case 7: return launch_mv_q4k_t<64, 7>(W, row0, nrows, x, y, s);
+    case 8: return launch_mv_q4k_t<64, 8>(W, row0, nrows, x, y, s);
+    default: return hipErrorInvalidValue;  // K > 16384: rejected by the API layer
+    }
+}
+
+// ------------------------------------------------------------------------
+// Expert-indexed gate/up with the activation fused.
+// Slot s = blockIdx.y selects expert e = ids[s]; its gate rows are
+// [e*2F, e*2F+F) and its up rows [e*2F+F, e*2F+2F) of the flattened tensor
+// (ops/moe.zig:55-73).  h[s][j] = act(gate_j . x) * (up_j . x) for j < F;
+// h[s][F..down_cols) = 0 (zero K padding of the down product).
+// One wavefront (G = 64) per row pair, CPL chunks per lane, R row pairs.
+template <int CPL, int R>
+__global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__restrict__ hdr,
+                                                            const uint8_t *__restrict__ qs,
+                                                            const float *__restrict__ x,
+                                                            const uint32_t *__restrict__ ids, int n_experts,
+                                                            int nsb, int F, int down_cols, uint32_t act,
+                                                            float *__restrict__ h) {
+    extern __shared__ float xs[];
+    const int s = blockIdx.y;
+    const uint32_t e = ids[s];
+    float *hs = h + (size_t)s * down_cols;
+    if (blockIdx.x == 0)
+        for (int j = F + threadIdx.x; j < down_cols; j += blockDim.x) hs[j] = 0.f;
+    if (e >= (uint32_t)n_experts) {  // invalid id from the caller: the slot contributes zeros
+        for (int j = blockIdx.x * 4 * R + threadIdx.x; j < F && j < (int)(blockIdx.x + 1) * 4 * R;
+             j += blockDim.x)
+            hs[j] = 0.f;
+        return;
+    }
+    stage_x(xs, x, nsb * 256);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int jbase = (blockIdx.x * 4 + wave) * R;
+    const int nch = nsb * 8;
+    const size_t gate0 = (size_t)e * 2 * F, up0 = gate0 + F;
+    float ag[R], au[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) ag[r] = au[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = lane + kWave * i;
+        if (c < nch) {
+            const int sb = c >> 3, cc = c & 7;
+            uint4 hg[R], qg[R], hu[R], qu[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int j = jbase + r;
+                if (j < F) {
+                    size_t bg = (gate0 + j) * nsb + sb, bu = (up0 + j) * nsb + sb;
+                    hg[r] = ldg16(hdr + bg * 16);
+                    qg[r] = ldg16(qs + bg * 128 + cc * 16);
+                    hu[r] = ldg16(hdr + bu * 16);
+                    qu[r] = ldg16(qs + bu * 128 + cc * 16);
+                }
+            }
+            XChunk xc;
+            load_xchunk(xs, sb, cc, xc);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (jbase + r < F) {
+                    ag[r] += q4k_chunk_dot(hg[r], qg[r], cc, xc);
+                    au[r] += q4k_chunk_dot(hu[r], qu[r], cc, xc);
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float g = group_sum<kWave>(ag[r]);
+        const float u = group_sum<kWave>(au[r]);
+        if (lane == 0 && jbase + r < F) hs[jbase + r] = act_apply(act, g) * u;
+    }
+}
+
+template <int CPL>
+static hipError_t launch_gu_t(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k, uint32_t F,
+                              uint32_t down_cols, uint32_t act, float *h, hipStream_t s) {
+    constexpr int R = 4;
+    const int nsb = (int)GU.blocks_per_row;
+    dim3 grid((F + 4 * R - 1) / (4 * R), k);
+    hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R>), grid, dim3(256), nsb * 256 * sizeof(float), s, GU.p0,
+                       GU.p1, x, ids, (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
+                                     uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
+                                     hipStream_t s) {
+    const int nch = (int)GU.blocks_per_row * 8;
+    switch ((nch + 63) / 64) {
+    case 1: return launch_gu_t<1>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 2: return launch_gu_t<2>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 3: return launch_gu_t<3>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 4: return launch_gu_t<4>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    default: return hipErrorInvalidValue;  // d_model > 8192: rejected by the API layer
+    }
+}
+
+// ------------------------------------------------------------------------
+// Expert-indexed down with the weighted combine fused:
+//   out[i] = base[i] + sum_{s in slot order} w[s] * (D_{ids[s]} row i) . h[s]
+// (base = previous out with accumulate, the shared-FFN output, or 0).
+// Block: 4 waves x RD output rows.  Wave w handles super-blocks w, w+4, ...
+// of the K = down_cols dimension; lane = (slot within an 8-slot pass, chunk
+// cc).  Per-(row, slot, super-block) partial sums go through LDS and are
+// combined in a fixed order, so the result does not depend on scheduling.
+template <int RD>
+__global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restrict__ hdr,
+                                                         const uint8_t *__restrict__ qs,
+                                                         const float *__restrict__ h,
+                                                         const uint32_t *__restrict__ ids,
+                                                         const float *__restrict__ wts, int k, int n_experts,
+                                                         int rows_per_expert, int nsb, const float *base,
+                                                         int accumulate, float *out) {
+    __shared__ float part[RD][16][16];  // [row][slot][super-block]
+    const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int sl = lane >> 3, cc = lane & 7;
+    const int row0 = blockIdx.x * RD;
+    const int K = nsb * 256;
+    for (int pass = 0; pass * 8 < k; pass++) {
+        const int s = pass * 8 + sl;
+        const bool active = s < k;
+        const uint32_t e = active ? ids[s] : 0u;
+        const bool valid = active && e < (uint32_t)n_experts;
+        const float *hs = h + (size_t)(valid ? s : 0) * K;
+        for (int sb = w; sb < nsb; sb += 4) {
+            uint4 hv[RD], qv[RD];
+#pragma unroll
+            for (int r = 0; r < RD; r++) {
+                const int row = row0 + r;
+                if (valid && row < rows_per_expert) {
+                    size_t blk = ((size_t)e * rows_per_expert + row) * nsb + sb;
+                    hv[r] = ldg16(hdr + blk * 16);
+                    qv[r] = ldg16(qs + blk * 128 + cc * 16);
+                }
+            }
+            XChunk xc;
+            load_xchunk(hs, sb, cc, xc);
+#pragma unroll
+            for (int r = 0; r < RD; r++) {
+                float v = 0.f;
+                if (valid && row0 + r < rows_per_expert) v = q4k_chunk_dot(hv[r], qv[r], cc, xc);
+                v = group_sum<8>(v);
+                if (cc == 0 && active) part[r][s][sb] = v;
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < RD) {
+        const int r = threadIdx.x, row = row0 + r;
+        if (row < rows_per_expert) {
+            float acc = accumulate ? out[row] : 0.f;
+            for (int s = 0; s < k; s++) {
+                float t = part[r][s][0];
+                for (int b = 1; b < nsb; b++) t += part[r][s][b];
+                const uint32_t e = ids[s];
+                if (e < (uint32_t)n_experts) acc += wts[s] * t;
+            }
+            if (base) acc = base[row] + acc;
+            out[row] = acc;
+        }
+    }
+}
+
+hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
+                                  uint32_t k, const float *base, int accumulate, float *out, hipStream_t s) {
+    constexpr int RD = 8;
+    const int nsb = (int)D.blocks_per_row;  // <= 16, k <= 16: checked by the API layer
+    const int rows = (int)D.rows;
+    dim3 grid((rows + RD - 1) / RD);
+    hipLaunchKernelGGL((k_expert_down_q4k<RD>), grid, dim3(256), 0, s, D.p0, D.p1, h, ids, w, (int)k,
+                       (int)D.n_experts, rows, nsb, base, accumulate, out);
+    return hipGetLastError();
+}
+
+}  // namespace lt

@@ -1,0 +1,379 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Bars: expert ids bit-exact; outputs within 1e-3
+relative L2 of the oracle (fp32 accumulation); router logits bit-exact.
+Matvec fuzz cases also hold the reference's own fuzz bound,
+max|d| / max|ref| < 1e-4 for fp32 activations (gpu/matvec.zig:4618).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import llmtoy_amd as lt
+import pyoracle as orc
+from llmtoy_amd import ggml, synth
+from llmtoy_amd.lib import InvalidError, UnsupportedError
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+import make_golden  # noqa: E402
+
+REL_L2 = 1e-3
+FUZZ_MAX_REL = 1e-4
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def max_rel(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / (np.max(np.abs(b)) + 1e-6))
+
+
+def gpu_matvec(ctx, w, gtype, rows, cols, x, n_experts=1):
+    t = ctx.upload(w, gtype, rows, cols, n_experts)
+    y = np.zeros(rows * n_experts, np.float32)
+    ctx.quant_matvec(y, t, x)
+    t.free()
+    return y
+
+
+# ------------------------------------------------------------------ KATs
+def test_gpu_matvec_q8_0_identity_rows(ctx):
+    # gpu/matvec.zig:3728-3767
+    mat = np.zeros((32, 34), np.uint8)
+    mat[:, 1] = 0x3C
+    for r in range(32):
+        mat[r, 2 + r] = 1
+    y = gpu_matvec(ctx, mat, ggml.Q8_0, 32, 32, np.arange(1, 33, dtype=np.float32))
+    assert y.tolist() == [float(i + 1) for i in range(32)]
+
+
+def test_gpu_matvec_q4k_scale(ctx):
+    # gpu/matvec.zig:3877-3908
+    blk = np.zeros(144, np.uint8)
+    blk[1], blk[4] = 0x3C, 1
+    blk[16:48] = 0x11
+    assert gpu_matvec(ctx, blk, ggml.Q4_K, 1, 256, np.ones(256, np.float32))[0] == pytest.approx(32.0, abs=1e-4)
+
+
+def test_gpu_matvec_q4k_min(ctx):
+    # gpu/matvec.zig:3910-3939
+    blk = np.zeros(144, np.uint8)
+    blk[3], blk[8] = 0x3C, 2
+    assert gpu_matvec(ctx, blk, ggml.Q4_K, 1, 256, np.ones(256, np.float32))[0] == pytest.approx(-64.0, abs=1e-4)
+
+
+def test_gpu_f16_subnormal_scales(ctx):
+    # f16 subnormals are kept (quant/dequant.zig:302-305); a flush-to-zero
+    # conversion would return 0 here.
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = [0x01, 0x00]  # d = 2^-24
+    blk[2:4] = [0xFF, 0x03]  # dmin = 1023 * 2^-24
+    blk[4:16] = ggml.pack_q4k_scales(np.full(8, 63, np.uint8), np.full(8, 1, np.uint8))
+    blk[16:] = 0xFF
+    x = np.ones(256, np.float32)
+    y = gpu_matvec(ctx, blk, ggml.Q4_K, 1, 256, x)[0]
+    ref = orc.quant_matvec(blk, orc.Q4_K, x, 1, 256)[0]
+    assert ref != 0 and abs(y - ref) <= 1e-6 * abs(ref)
+    q8 = np.zeros(34, np.uint8)
+    q8[0:2] = [0x00, 0x02]  # 512 * 2^-24
+    q8[2:] = 100
+    y8 = gpu_matvec(ctx, q8, ggml.Q8_0, 1, 32, np.ones(32, np.float32))[0]
+    assert y8 == np.float32(orc.quant_matvec(q8, orc.Q8_0, np.ones(32, np.float32), 1, 32)[0]) != 0
+
+
+def test_gpu_router_kat(ctx):
+    # gpu/matvec.zig:3582-3656 (no norm): logits [0, 8, 4, 8] -> ids [1, 3]
+    w = np.zeros((4, 8), np.float32)
+    w[1], w[2], w[3] = 1.0, 0.5, 1.0
+    r = ctx.upload(w, ggml.F32, 4, 8)
+    ids = np.zeros(2, np.uint32)
+    wt = np.zeros(2, np.float32)
+    ctx.router_topk(r, np.ones(8, np.float32), 2, ids, wt)
+    assert ids.tolist() == [1, 3]
+    p = np.exp(8.0) / (2 * np.exp(8.0) + np.exp(4.0) + 1)
+    assert np.allclose(wt, [p, p], atol=1e-6)
+
+
+def test_gpu_topk_tie_kat(ctx):
+    # gemma4/forward.zig:823-829 ties: {1,4,4,-2,3.5,4,0} -> [1,2,5,4]
+    logits = np.array([1.0, 4.0, 4.0, -2.0, 3.5, 4.0, 0.0], np.float32)
+    r = ctx.upload(np.diag(logits).astype(np.float32), ggml.F32, 7, 7)
+    ids = np.zeros(4, np.uint32)
+    ctx.router_topk(r, np.ones(7, np.float32), 4, ids, np.zeros(4, np.float32))
+    assert ids.tolist() == [1, 2, 5, 4]
+
+
+# ------------------------------------------------------------------ fuzz (reference style)
+@pytest.mark.parametrize("gtype,rows,cols,seed", [
+    (ggml.Q8_0, 32, 256, 1), (ggml.Q4_K, 32, 256, 3), (ggml.Q4_K, 64, 2048, 11), (ggml.Q4_K, 19, 4096, 13),
+    (ggml.Q6_K, 32, 256, 5), (ggml.Q6_K, 37, 1024, 17), (ggml.Q8_0, 33, 4864, 19), (ggml.Q4_K, 70, 768, 23)])
+def test_gpu_matvec_fuzz(ctx, gtype, rows, cols, seed):
+    # gpu/matvec.zig:4543-4619: random bytes with every f16 super-scale stamped
+    # to 0x21CD (~0.012), x ~ U(-1, 1), max|d|/max|ref| < 1e-4.
+    g = np.random.default_rng(seed)
+    rb = ggml.row_bytes(gtype, cols)
+    mat = g.integers(0, 256, (rows, rb), dtype=np.uint8)
+    bb = ggml.BLOCK_BYTES[gtype]
+    blk = mat.reshape(rows, -1, bb)
+    if gtype == ggml.Q6_K:
+        blk[..., 208], blk[..., 209] = 0xCD, 0x21
+    else:
+        blk[..., 0], blk[..., 1] = 0xCD, 0x21
+        if gtype == ggml.Q4_K:
+            blk[..., 2], blk[..., 3] = 0xCD, 0x21
+    x = ((g.random(cols, dtype=np.float32) - 0.5) * 2).astype(np.float32)
+    y = gpu_matvec(ctx, mat, gtype, rows, cols, x)
+    ref = orc.quant_matvec(mat, gtype, x, rows, cols)
+    assert max_rel(y, ref) < FUZZ_MAX_REL
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 33), (128, 2048), (5, 4), (200, 2816)])
+def test_gpu_matvec_f32_bit_exact(ctx, rows, cols):
+    # fp32 rows follow dotf32's order exactly (ops/math.zig:96-116)
+    g = np.random.default_rng(rows * cols)
+    w = g.standard_normal((rows, cols)).astype(np.float32)
+    x = g.standard_normal(cols).astype(np.float32)
+    y = gpu_matvec(ctx, w, ggml.F32, rows, cols, x)
+    ref = orc.quant_matvec(w, orc.F32, x, rows, cols)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ golden fixtures
+@pytest.mark.parametrize("name", ["mv_f32", "mv_q8_0", "mv_q4_k", "mv_q4_k_pad", "mv_q6_k_pad"])
+def test_gpu_golden_matvec(ctx, name):
+    gold = np.load(os.path.join(HERE, "golden", "golden.npz"))
+    w, x, y = gold[f"{name}.w"], gold[f"{name}.x"], gold[f"{name}.y"]
+    gtype = {"mv_f32": ggml.F32, "mv_q8_0": ggml.Q8_0, "mv_q6_k_pad": ggml.Q6_K}.get(name, ggml.Q4_K)
+    rows = w.shape[0]
+    cols = x.shape[0]
+    got = gpu_matvec(ctx, np.ascontiguousarray(w), gtype, rows, cols, x)
+    if gtype == ggml.F32:
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32))
+    else:
+        assert rel_l2(got, y) <= REL_L2
+
+
+@pytest.mark.parametrize("name", ["moe_small", "moe_small_norm_bias_gelu"])
+def test_gpu_golden_moe(ctx, name):
+    gold = np.load(os.path.join(HERE, "golden", "golden.npz"))
+    builder, _ = make_golden.cases()[name]
+    d = builder()
+    w = d["w"]
+    k = gold[f"{name}.ids"].size
+    act = lt.ACT_GELU_TANH if "gelu" in name else lt.ACT_SILU
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    out = np.zeros(w.d_model, np.float32)
+    ids = np.zeros(k, np.uint32)
+    wt = np.zeros(k, np.float32)
+    ctx.moe_forward(out, d["x"], router, gate_up, down, k, w.d_expert, act=act, norm_topk="norm" in name,
+                    bias=d["bias"], out_ids=ids, out_w=wt)
+    assert np.array_equal(ids, gold[f"{name}.ids"])
+    assert np.allclose(wt, gold[f"{name}.wt"], rtol=1e-5)
+    assert rel_l2(out, gold[f"{name}.out"]) <= REL_L2
+    for t in (router, gate_up, down):
+        t.free()
+
+
+# ------------------------------------------------------------------ BASELINE configs
+def test_gpu_config2_q4k_4096(ctx):
+    c = synth.config2()
+    y = gpu_matvec(ctx, c["w"], ggml.Q4_K, 4096, 4096, c["x"])
+    with orc.Pool(16) as p:
+        ref = orc.quant_matvec(c["w"], orc.Q4_K, c["x"], 4096, 4096, pool=p)
+    assert rel_l2(y, ref) <= REL_L2
+    assert max_rel(y, ref) < FUZZ_MAX_REL
+
+
+def test_gpu_config2_q6k_151936(ctx):
+    c = synth.config2_q6k()
+    y = gpu_matvec(ctx, c["w"], ggml.Q6_K, c["rows"], c["cols"], c["x"])
+    with orc.Pool(16) as p:
+        ref = orc.quant_matvec(c["w"], orc.Q6_K, c["x"], c["rows"], c["cols"], pool=p)
+    assert rel_l2(y, ref) <= REL_L2
+    assert max_rel(y, ref) < FUZZ_MAX_REL
+
+
+def test_gpu_config1_dense_ffn_q8_0(ctx):
+    c = synth.config1()
+    D, F = c["d_model"], c["d_ffn"]
+    wg = ctx.upload(c["w_gate"], ggml.Q8_0, F, D)
+    wu = ctx.upload(c["w_up"], ggml.Q8_0, F, D)
+    wd = ctx.upload(c["w_down"], ggml.Q8_0, D, F)
+    out = np.zeros(D, np.float32)
+    ctx.ffn_dense(out, wg, wu, wd, c["x"], act=lt.ACT_SILU)
+    with orc.Pool(16) as p:
+        ref = orc.ffn_dense(c["w_gate"], c["w_up"], c["w_down"], orc.Q8_0, c["x"], D, F, pool=p)
+    assert rel_l2(out, ref) <= REL_L2
+    for t in (wg, wu, wd):
+        t.free()
+
+
+@pytest.fixture(scope="module")
+def cfg3(ctx):
+    c = synth.config3()
+    tens = lt.upload_moe(ctx, c["weights"])
+    yield c, tens
+    for t in tens:
+        t.free()
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_gpu_config3_qwen3_moe(ctx, cfg3, pool, norm):
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    for i in range(6):
+        x = c["x"] if i == 0 else synth.config3_x(i)
+        out = np.zeros(w.d_model, np.float32)
+        ids = np.zeros(8, np.uint32)
+        wt = np.zeros(8, np.float32)
+        ctx.moe_forward(out, x, router, gate_up, down, 8, w.d_expert, norm_topk=norm, out_ids=ids, out_w=wt)
+        ref, rids, rw, agree = orc.moe_forward(w, x, 8, norm_topk=norm, pool=pool)
+        assert agree, "probability tie changes the reference selection for this input"
+        assert np.array_equal(ids, rids), (i, ids, rids)
+        assert np.allclose(wt, rw, rtol=1e-5, atol=0), (i, wt, rw)
+        assert rel_l2(out, ref) <= REL_L2, i
+
+
+def test_gpu_config3_router_logits_bit_exact(ctx, cfg3):
+    c, (router, _, _) = cfg3
+    w = c["weights"]
+    for i in range(4):
+        x = synth.config3_x(50 + i)
+        ids = np.zeros(8, np.uint32)
+        scores = np.zeros(w.n_experts, np.float32)
+        ctx.router_topk(router, x, 8, ids, np.zeros(8, np.float32), scores=scores)
+        logits = orc.quant_matvec(w.router, orc.F32, x, w.n_experts, w.d_model)
+        rest = np.setdiff1d(np.arange(w.n_experts), ids)
+        assert np.array_equal(scores[rest].view(np.uint32), logits[rest].view(np.uint32))
+        assert ids.tolist() == orc.topk_softmax_stats(logits, 8)[0].tolist()
+
+
+def test_gpu_config3_expert_stages_compose(ctx, cfg3, pool):
+    # runExpertBatch-style: caller-provided routing through the two expert stages
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    x = c["x"]
+    ids = np.zeros(8, np.uint32)
+    wt = np.zeros(8, np.float32)
+    ctx.router_topk(router, x, 8, ids, wt, norm_topk=True)
+    h = np.zeros((8, w.down_cols), np.float32)
+    ctx.expert_gate_up_id(gate_up, x, ids, 8, w.d_expert, w.down_cols, h)
+    out = np.full(w.d_model, 0.5, np.float32)
+    ctx.expert_down_id(down, h, ids, wt, 8, out, accumulate=True)
+    ref, *_ = orc.moe_forward(w, x, 8, norm_topk=True, pool=pool, out=np.full(w.d_model, 0.5, np.float32))
+    assert rel_l2(out, ref) <= REL_L2
+
+
+def test_gpu_config4_gemma_like(ctx, pool):
+    c = synth.config4()
+    w = c["weights"]
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    D, S = w.d_model, c["d_shared"]
+    sg = ctx.upload(c["sh_gate"], ggml.Q8_0, S, D)
+    su = ctx.upload(c["sh_up"], ggml.Q8_0, S, D)
+    sd = ctx.upload(c["sh_down"], ggml.Q8_0, D, S)
+    for i in range(3):
+        x = c["x"] if i == 0 else synth.normal(synth.stream(4, 300 + i), (D,))
+        out = np.zeros(D, np.float32)
+        ids = np.zeros(8, np.uint32)
+        wt = np.zeros(8, np.float32)
+        ctx.moe_forward(out, x, router, gate_up, down, 8, w.d_expert, act=lt.ACT_GELU_TANH, shared=(sg, su, sd),
+                        out_ids=ids, out_w=wt)
+        ref, rids, rw = orc.moe_layer_shared(w, x, 8, c["sh_gate"], c["sh_up"], c["sh_down"], S, pool=pool)
+        assert np.array_equal(ids, rids), (i, ids, rids)
+        assert np.allclose(wt, rw, rtol=1e-5)
+        assert rel_l2(out, ref) <= REL_L2
+        # Q8_0 router logits follow dotQ8_0's order bit for bit
+        scores = np.zeros(w.n_experts, np.float32)
+        ctx.router_topk(router, x, 8, ids, wt, scores=scores)
+        logits = orc.quant_matvec(w.router, orc.Q8_0, x, w.n_experts, D)
+        rest = np.setdiff1d(np.arange(w.n_experts), ids)
+        assert np.array_equal(scores[rest].view(np.uint32), logits[rest].view(np.uint32))
+    for t in (router, gate_up, down, sg, su, sd):
+        t.free()
+
+
+# ------------------------------------------------------------------ edge cases
+@pytest.mark.parametrize("E,k", [(128, 1), (128, 16), (100, 8), (1000, 4), (16, 16)])
+def test_gpu_moe_expert_counts_and_k(ctx, pool, E, k):
+    w = synth.moe_weights(60 + E % 7, 512, E, 256)
+    x = synth.normal(synth.stream(60, E + k), (512,))
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    out = np.zeros(512, np.float32)
+    ids = np.zeros(k, np.uint32)
+    ctx.moe_forward(out, x, router, gate_up, down, k, 256, out_ids=ids)
+    ref, rids, _, agree = orc.moe_forward(w, x, k, pool=pool)
+    assert agree and np.array_equal(ids, rids)
+    assert rel_l2(out, ref) <= REL_L2
+    for t in (router, gate_up, down):
+        t.free()
+
+
+def test_gpu_router_duplicate_rows_lowest_index_wins(ctx):
+    g = np.random.default_rng(4)
+    w = g.standard_normal((64, 256)).astype(np.float32) * 0.02
+    w[40] = w[7]
+    w[9] = w[7]
+    x = g.standard_normal(256).astype(np.float32)
+    w[7] = np.sign(x) * 0.5  # make row 7 (and its copies) the clear maximum
+    w[9] = w[7]
+    w[40] = w[7]
+    r = ctx.upload(w, ggml.F32, 64, 256)
+    ids = np.zeros(3, np.uint32)
+    ctx.router_topk(r, x, 3, ids, np.zeros(3, np.float32))
+    assert ids.tolist() == [7, 9, 40]
+
+
+def test_gpu_deterministic_repeat(ctx, cfg3):
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    outs = []
+    for _ in range(3):
+        out = np.zeros(w.d_model, np.float32)
+        ctx.moe_forward(out, c["x"], router, gate_up, down, 8, w.d_expert, norm_topk=True)
+        outs.append(out)
+    assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])
+
+
+def test_gpu_device_pointer_path_matches_host(ctx, cfg3):
+    torch = pytest.importorskip("torch")
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    host = np.zeros(w.d_model, np.float32)
+    ctx.moe_forward(host, c["x"], router, gate_up, down, 8, w.d_expert, norm_topk=True)
+    xd = torch.from_numpy(c["x"]).cuda()
+    od = torch.zeros(w.d_model, dtype=torch.float32, device="cuda")
+    idd = torch.zeros(8, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.moe_forward(od, xd, router, gate_up, down, 8, w.d_expert, norm_topk=True, out_ids=idd)
+    ctx.sync()
+    assert np.array_equal(od.cpu().numpy().view(np.uint32), host.view(np.uint32))
+
+
+def test_gpu_errors(ctx):
+    with pytest.raises(UnsupportedError):
+        ctx.upload(np.zeros(64, np.uint8), ggml.F16, 1, 32)
+    with pytest.raises(UnsupportedError):
+        ctx.upload(np.zeros(144, np.uint8), ggml.Q4_K, 1, 200)
+    with pytest.raises(InvalidError):
+        ctx.upload(np.zeros(100, np.uint8), ggml.Q4_K, 1, 256)
+    w = synth.moe_weights(61, 256, 4, 256)
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    out = np.zeros(256, np.float32)
+    with pytest.raises(InvalidError):
+        ctx.moe_forward(out, np.zeros(256, np.float32), router, gate_up, down, 0, 256)
+    with pytest.raises(InvalidError):
+        ctx.moe_forward(out, np.zeros(256, np.float32), router, gate_up, down, 5, 256)
+    with pytest.raises(InvalidError):
+        ctx.expert_gate_up_id(gate_up, np.zeros(256, np.float32), np.array([0, 9], np.uint32), 2, 256, 256,
+                              np.zeros((2, 256), np.float32))
+    for t in (router, gate_up, down):
+        t.free()
