@@ -1,0 +1,289 @@
+#!/usr/bin/env python3
+"""MoE-layer decode benchmark on one MI355X.
+
+Workload: the Qwen3-style MoE layer at batch 1 -- d_model 2048, 128 experts,
+expert d_ffn 768, top-8, fp32 router, Q4_K expert weights, SiLU, renormalised
+top-k weights.  One step = one token through the layer (router -> softmax /
+top-k -> expert gate/up -> down -> weighted combine), inputs resident in HBM.
+
+Measurement:
+  * 8 device copies of the expert and router tensors (8 x 340 MB) are
+    rotated, and the input x cycles through a pool of 64 vectors, so weights
+    come from HBM, not from the 256 MB Infinity Cache, and the selected
+    experts change from step to step.
+  * The timed steps replay a hipGraph of 64 captured steps (no host launch
+    cost per kernel); the eager (one API call per step) rate is reported too.
+  * roofline: the dominant kernel (expert gate/up) launched alone, one HIP
+    event pair per launch on the library's stream; achieved = algorithmic
+    bytes per launch / mean launch duration.  traffic = HBM bytes per launch
+    from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/*_pmc.json), scaled by
+    the counters' reading on a copy kernel of known size.
+  * cpu_baseline: the oracle's restatement of the reference CPU path
+    (quantMatvecPar row split over a persistent pool + moeForward), timed on
+    this host on a bounded sample of the same inputs.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "llmtoy-zig_amd"), os.path.join(ROOT, "oracle")]
+
+METRIC = "MoE-layer decode µs/token + achieved HBM GB/s (% of 8 TB/s) at batch 1"
+PEAK_GBPS = 8000.0
+D, E, F, K = 2048, 128, 768, 8
+Q4K_ROW_D = (D // 256) * 144          # 1152 B: one gate or up row
+Q4K_ROW_F = (F // 256) * 144          # 432 B: one down row
+EXPERT_BYTES = 2 * F * Q4K_ROW_D + D * Q4K_ROW_F      # 2,654,208 B per expert
+SELECTED_BYTES = K * EXPERT_BYTES                      # 21,233,664 B (metric denominator)
+LAYER_BYTES = SELECTED_BYTES + E * D * 4 + 4 * D * 4   # + fp32 router + x/out/h traffic -> 22,347,776 B
+GATE_UP_WEIGHT_BYTES = K * 2 * F * Q4K_ROW_D           # 14,155,776 B
+GATE_UP_BYTES = GATE_UP_WEIGHT_BYTES + D * 4 + K * F * 4   # + x read + h write = 14,188,544 B
+DOWN_BYTES = K * D * Q4K_ROW_F + K * F * 4 + D * 4          # 7,077,888 + h + out
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def pmc_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", f"{name}_pmc.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        p = json.load(f)
+    try:
+        fetch = p["kernels"][p["dominant"]]["FETCH_SIZE_kib"] / p["copy_calibration"]["fetch_factor"]
+        write = p["kernels"][p["dominant"]]["WRITE_SIZE_kib"] / p["copy_calibration"]["write_factor"]
+        return (fetch + write) * 1024.0, path
+    except (KeyError, ZeroDivisionError):
+        return None, path
+
+
+def cpu_baseline(w, xs, seconds: float, threads: int):
+    import numpy as np
+    import pyoracle as orc
+    res = {}
+    for nt, budget in ((threads, seconds), (1, max(2.0, seconds / 4))):
+        with orc.Pool(nt) as pool:
+            orc.moe_forward(w, xs[0], K, norm_topk=True, pool=pool)  # warm
+            ts = []
+            t_end = time.perf_counter() + budget
+            i = 0
+            while (time.perf_counter() < t_end or len(ts) < 50) and len(ts) < 5000:
+                x = xs[i % len(xs)]
+                t0 = time.perf_counter()
+                orc.moe_forward(w, x, K, norm_topk=True, pool=pool)
+                ts.append(time.perf_counter() - t0)
+                i += 1
+        res[nt] = (statistics.median(ts) * 1e6, len(ts))
+        log(f"cpu baseline {nt} thread(s): {res[nt][0]:.1f} us/token over {len(ts)} tokens")
+        if nt == 1:
+            break
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4096)
+    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--xpool", type=int, default=64)
+    ap.add_argument("--kernel-iters", type=int, default=512)
+    ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
+              "sharding of this path is described in DESIGN.md and not run", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import llmtoy_amd as lt
+    import pyoracle as orc
+    from llmtoy_amd import synth
+    from llmtoy_amd.hip import DeviceArray, Event, Graph, sync_stream
+
+    t0 = time.time()
+    log("generating config-3 weights (128 experts, Q4_K) ...")
+    c = synth.config3()
+    w = c["weights"]
+    xs = [c["x"]] + [synth.config3_x(i) for i in range(1, args.xpool)]
+    log(f"generated in {time.time() - t0:.1f}s; uploading {args.copies} copies")
+
+    ctx = lt.Context(0)
+    stream = ctx.stream
+    base = lt.upload_moe(ctx, w)
+    copies = [base] + [tuple(t.clone() for t in base) for _ in range(args.copies - 1)]
+    dev_bytes = sum(t.nbytes for cp in copies for t in cp)
+    log(f"{args.copies} weight copies resident: {dev_bytes / 2**30:.2f} GiB")
+
+    # parity check of the benchmarked configuration against the oracle
+    out_h = np.zeros(D, np.float32)
+    ids_h = np.zeros(K, np.uint32)
+    ctx.moe_forward(out_h, xs[0], *base, K, F, norm_topk=True, out_ids=ids_h)
+    with orc.Pool(min(16, os.cpu_count() or 1)) as p:
+        ref, rids, _, _ = orc.moe_forward(w, xs[0], K, norm_topk=True, pool=p)
+    parity = {"ids_bit_exact": bool(np.array_equal(ids_h, rids)),
+              "rel_l2": float(np.linalg.norm(out_h - ref) / np.linalg.norm(ref))}
+    log(f"parity: {parity}")
+
+    X = DeviceArray.from_numpy(np.stack(xs))
+    out = DeviceArray((D,), np.float32)
+
+    def step(i):
+        r, g, d = copies[i % args.copies]
+        ctx.moe_forward(out, X.row(i % args.xpool), r, g, d, K, F, norm_topk=True)
+
+    # ---- eager warmup + eager rate
+    for i in range(args.warmup):
+        step(i)
+    sync_stream(stream)
+    n_eager = min(args.steps, 1024)
+    t = time.perf_counter()
+    for i in range(n_eager):
+        step(i)
+    sync_stream(stream)
+    eager_us = (time.perf_counter() - t) / n_eager * 1e6
+    log(f"eager: {eager_us:.2f} us/token")
+
+    # ---- graph replay: one graph holds G consecutive steps (copy and x cycle with period G)
+    G = int(np.lcm(args.copies, args.xpool))
+    while G < 64:
+        G *= 2
+    graph = Graph(stream, lambda: [step(i) for i in range(G)])
+    rem = args.steps % G
+    graph_rem = Graph(stream, lambda: [step(i) for i in range(rem)]) if rem else None
+    for _ in range(max(1, args.warmup // G)):
+        graph.launch()
+    sync_stream(stream)
+    e0, e1 = Event(), Event()
+    t = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps // G):
+        graph.launch()
+    if graph_rem:
+        graph_rem.launch()
+    e1.record(stream)
+    sync_stream(stream)
+    wall = time.perf_counter() - t
+    dev_ms = e0.elapsed_ms(e1)
+    us_per_token = wall / args.steps * 1e6
+    log(f"graph replay: {us_per_token:.3f} us/token wall, {dev_ms * 1e3 / args.steps:.3f} us/token device")
+
+    # ---- per-kernel launch durations (one event pair per launch)
+    ids_pool = []
+    for i in range(args.xpool):
+        ids = np.zeros(K, np.uint32)
+        wt = np.zeros(K, np.float32)
+        ctx.router_topk(base[0], xs[i], K, ids, wt, norm_topk=True)
+        ids_pool.append((ids, wt))
+    IDS = DeviceArray.from_numpy(np.stack([a for a, _ in ids_pool]))
+    WTS = DeviceArray.from_numpy(np.stack([b for _, b in ids_pool]))
+    H = DeviceArray((K, F), np.float32)
+    dids = DeviceArray((K,), np.uint32)
+    dw = DeviceArray((K,), np.float32)
+
+    def time_launches(fn, n):
+        evs = [(Event(), Event()) for _ in range(n)]
+        for i in range(min(n, 32)):
+            fn(i)
+        sync_stream(stream)
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            fn(i)
+            b.record(stream)
+        sync_stream(stream)
+        ms = [a.elapsed_ms(b) for a, b in evs]
+        for a, b in evs:
+            a.destroy()
+            b.destroy()
+        return statistics.mean(ms) * 1e3, statistics.median(ms) * 1e3
+
+    def gu(i):
+        r, g, d = copies[i % args.copies]
+        ctx.expert_gate_up_id(g, X.row(i % args.xpool), IDS.row(i % args.xpool), K, F, F, H)
+
+    def dn(i):
+        r, g, d = copies[i % args.copies]
+        ctx.expert_down_id(d, H, IDS.row(i % args.xpool), WTS.row(i % args.xpool), K, out)
+
+    def rt(i):
+        r, g, d = copies[i % args.copies]
+        ctx.router_topk(r, X.row(i % args.xpool), K, dids, dw, norm_topk=True)
+
+    gu_mean, gu_med = time_launches(gu, args.kernel_iters)
+    dn_mean, dn_med = time_launches(dn, args.kernel_iters)
+    rt_mean, rt_med = time_launches(rt, args.kernel_iters)
+    log(f"gate/up {gu_mean:.2f} us (median {gu_med:.2f}); down {dn_mean:.2f} us; router+topk {rt_mean:.2f} us")
+
+    gu_gbps = GATE_UP_BYTES / (gu_mean * 1e-6) / 1e9
+    traffic, pmc_path = pmc_traffic("expert_gate_up_q4k_cfg3")
+    roofline = {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gu_gbps / PEAK_GBPS, 4), "traffic": None if traffic is None else round(traffic),
+                "kernel": "k_expert_gate_up_q4k", "algorithmic_bytes": GATE_UP_BYTES,
+                "mean_launch_us": round(gu_mean, 3), "median_launch_us": round(gu_med, 3)}
+
+    layer_gbps = SELECTED_BYTES / (us_per_token * 1e-6) / 1e9
+    result = {
+        "metric": METRIC, "value": round(us_per_token, 3), "unit": "us/token", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us_per_token / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded; Q4_K experts per BASELINE value scheme)",
+        "config": {"workload": "qwen3_moe_decode_cfg3", "d_model": D, "n_experts": E, "d_expert": F, "top_k": K,
+                   "expert_quant": "Q4_K", "router": "f32", "act": "silu", "norm_topk": True, "batch": 1,
+                   "weight_copies": args.copies, "x_pool": args.xpool, "graph_steps": G},
+        "achieved_gbps_selected_experts": round(layer_gbps, 1),
+        "hbm_frac_selected_experts": round(layer_gbps / PEAK_GBPS, 4),
+        "achieved_gbps_full_layer": round(LAYER_BYTES / (us_per_token * 1e-6) / 1e9, 1),
+        "device_us_per_token": round(dev_ms * 1e3 / args.steps, 3),
+        "eager_us_per_token": round(eager_us, 3),
+        "kernel_us": {"router_topk": round(rt_mean, 3), "expert_gate_up": round(gu_mean, 3),
+                      "expert_down": round(dn_mean, 3)},
+        "kernel_gbps": {"expert_gate_up": round(gu_gbps, 1),
+                        "expert_down": round(DOWN_BYTES / (dn_mean * 1e-6) / 1e9, 1)},
+        "roofline": roofline,
+        "parity": parity,
+    }
+
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1, 64)
+        res = cpu_baseline(w, xs, args.cpu_seconds, threads)
+        cpu_model = ""
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu_model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+        except (OSError, StopIteration):
+            pass
+        result["cpu_baseline"] = {
+            "value": round(res[threads][0], 1), "unit": "us/token", "cores": threads, "kind": "port",
+            "sample": f"{res[threads][1]} config-3 tokens (x pool of {args.xpool}), median; oracle/lt_oracle.c "
+                      f"quantMatvecPar + moeForward, --threads {threads}",
+            "value_1_thread": round(res[1][0], 1), "nproc": os.cpu_count(), "cpu_model": cpu_model}
+
+    print(json.dumps(result), flush=True)
+    graph.destroy()
+    if graph_rem:
+        graph_rem.destroy()
+    for a in (X, out, IDS, WTS, H, dids, dw):
+        a.free()
+    for cp in copies:
+        for tns in cp:
+            tns.free()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

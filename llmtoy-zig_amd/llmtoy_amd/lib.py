@@ -11,7 +11,8 @@ or error.ExpertNotOnGpu); InvalidError stands for the reference's shape
 assertions.
 
 Arrays: numpy arrays are host memory (the call is synchronous, LT_HOST_IO);
-torch CUDA tensors are passed as device pointers (the call is enqueued on the
+llmtoy_amd.hip.DeviceArray (or a CUDA tensor of a framework that shares this
+HIP runtime) is passed as a device pointer (the call is enqueued on the
 context's stream; call Context.sync()).  There is no CPU fallback here: the
 library must be built (make -C llmtoy-zig_amd) and a GPU must be present.
 """
@@ -116,6 +117,8 @@ def _ptr(a):
         if not a.flags["C_CONTIGUOUS"]:
             raise InvalidError("array must be C-contiguous")
         return a.ctypes.data, True
+    if hasattr(a, "ptr") and hasattr(a, "dtype"):  # hip.DeviceArray / DeviceView
+        return a.ptr, False
     if _is_torch(a):
         if not a.is_contiguous():
             raise InvalidError("tensor must be contiguous")

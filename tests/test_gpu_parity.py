@@ -344,18 +344,50 @@ def test_gpu_deterministic_repeat(ctx, cfg3):
 
 
 def test_gpu_device_pointer_path_matches_host(ctx, cfg3):
-    torch = pytest.importorskip("torch")
+    from llmtoy_amd.hip import DeviceArray
     c, (router, gate_up, down) = cfg3
     w = c["weights"]
     host = np.zeros(w.d_model, np.float32)
-    ctx.moe_forward(host, c["x"], router, gate_up, down, 8, w.d_expert, norm_topk=True)
-    xd = torch.from_numpy(c["x"]).cuda()
-    od = torch.zeros(w.d_model, dtype=torch.float32, device="cuda")
-    idd = torch.zeros(8, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
+    hids = np.zeros(8, np.uint32)
+    ctx.moe_forward(host, c["x"], router, gate_up, down, 8, w.d_expert, norm_topk=True, out_ids=hids)
+    xd = DeviceArray.from_numpy(c["x"])
+    od = DeviceArray((w.d_model,), np.float32)
+    idd = DeviceArray((8,), np.uint32)
     ctx.moe_forward(od, xd, router, gate_up, down, 8, w.d_expert, norm_topk=True, out_ids=idd)
     ctx.sync()
-    assert np.array_equal(od.cpu().numpy().view(np.uint32), host.view(np.uint32))
+    assert np.array_equal(od.numpy().view(np.uint32), host.view(np.uint32))
+    assert np.array_equal(idd.numpy(), hids)
+    for a in (xd, od, idd):
+        a.free()
+
+
+def test_gpu_graph_replay_matches_eager(ctx, cfg3):
+    # the decode step captured into a hipGraph (no allocation, no memset
+    # inside) replays to the eager result, with eager work between replays
+    from llmtoy_amd.hip import DeviceArray, Graph
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    xs = [c["x"], synth.config3_x(1)]
+    xd = [DeviceArray.from_numpy(x) for x in xs]
+    od = DeviceArray((w.d_model,), np.float32)
+    eager = []
+    for x in xs:
+        o = np.zeros(w.d_model, np.float32)
+        ctx.moe_forward(o, x, router, gate_up, down, 8, w.d_expert, norm_topk=True)
+        eager.append(o)
+    graphs = [Graph(ctx.stream, lambda d=d: ctx.moe_forward(od, d, router, gate_up, down, 8, w.d_expert,
+                                                            norm_topk=True)) for d in xd]
+    for rep in range(3):
+        for gi, g in enumerate(graphs):
+            g.launch()
+            ctx.sync()
+            assert np.array_equal(od.numpy().view(np.uint32), eager[gi].view(np.uint32)), (rep, gi)
+            o = np.zeros(w.d_model, np.float32)  # eager work between replays
+            ctx.moe_forward(o, xs[1 - gi], router, gate_up, down, 8, w.d_expert, norm_topk=True)
+    for g in graphs:
+        g.destroy()
+    for a in xd + [od]:
+        a.free()
 
 
 def test_gpu_errors(ctx):
