@@ -33,6 +33,9 @@ struct lt_ctx {
     std::string err;
     // context-owned device scratch, grown on demand
     DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh;
+    // arrival ticket of the router's last-block top-k; zeroed once at init,
+    // every launch leaves it at zero again
+    unsigned *ticket = nullptr;
 };
 
 namespace {
@@ -207,6 +210,14 @@ extern "C" int lt_init(int device, lt_ctx **out_ctx) {
         delete ctx;
         return LT_ERR_DEVICE;
     }
+    hipError_t e = hipMalloc((void **)&ctx->ticket, 256);
+    if (e == hipSuccess) e = hipMemset(ctx->ticket, 0, 256);
+    if (e != hipSuccess) {
+        if (ctx->ticket) (void)hipFree(ctx->ticket);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return e == hipErrorOutOfMemory ? LT_ERR_OOM : LT_ERR_DEVICE;
+    }
     *out_ctx = ctx;
     return LT_OK;
 }
@@ -219,6 +230,7 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
                       &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
+    if (ctx->ticket) (void)hipFree(ctx->ticket);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -430,12 +442,9 @@ int router_dev(lt_ctx *ctx, const DevTensor &R, const float *x, const float *bia
         (rc = ensure(ctx, ctx->w, kMaxK * 4)))
         return rc;
     float *logits = (float *)ctx->logits.p;
-    hipError_t e = R.type == LT_TYPE_F32 ? lt::launch_router_f32(R, x, bias, logits, ctx->stream)
-                                         : lt::launch_router_q8_0(R, x, bias, logits, ctx->stream);
-    if ((rc = launch_rc(ctx, e, "router"))) return rc;
-    e = lt::launch_topk_softmax(logits, (uint32_t)R.total_rows, k, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u,
-                                (uint32_t *)ctx->ids.p, (float *)ctx->w.p, scores, ctx->stream);
-    return launch_rc(ctx, e, "topk_softmax");
+    hipError_t e = lt::launch_router(R, x, bias, logits, ctx->ticket, k, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u,
+                                     (uint32_t *)ctx->ids.p, (float *)ctx->w.p, scores, ctx->stream);
+    return launch_rc(ctx, e, "router_topk");
 }
 
 int stage_bias(lt_ctx *ctx, const float *bias, size_t n, bool host, const float **dbias) {

@@ -77,6 +77,128 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Hides the known-zero bits of a value from the optimiser, so that byte
+// extractions of a masked word stay single v_cvt_f32_ubyte{0..3} ops
+// instead of being rewritten into v_bfe + v_cvt_f32_ubyte0.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Cross-lane moves.  DPP controls (gfx9 encoding): quad_perm [1,0,3,2] =
+// 0xB1, [2,3,0,1] = 0x4E, row_ror:n = 0x120 + n, row_half_mirror = 0x141.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// lane i <- lane i ^ 16 (within each 32-lane half)
+__device__ __forceinline__ float xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+}
+// v_permlane32_swap exchanges the two 32-lane halves between its operands;
+// with both operands equal, one of its two results holds the value of lane
+// i ^ 32 in every lane.  p32_first(lane) tells which one (computed once).
+__device__ __forceinline__ bool p32_first(int lane) {
+    auto pr = __builtin_amdgcn_permlane32_swap((unsigned)lane, (unsigned)lane, false, false);
+    return (int)pr[0] != lane;
+}
+__device__ __forceinline__ float xor32(float v, bool first) {
+    auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(first ? pr[0] : pr[1]);
+}
+
+// Sums V values (V = 1, 2, 4 or 8) over the 64 lanes of a wavefront with
+// log2(V) exchange steps (each halves the values a lane carries) followed by
+// a plain reduction over the remaining lane bits.  Returns, in every lane,
+// the total of value index lane >> (6 - log2 V).
+template <int V>
+__device__ __forceinline__ float wave_sum_transposed(float (&v)[V], int lane, bool first) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "V");
+    float a[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) a[i] = v[i];
+    int n = V;
+    if (n > 1) {  // lane bit 5
+        const bool hi = lane & 32;
+#pragma unroll
+        for (int i = 0; i < V / 2; i++) {
+            const float send = hi ? a[i] : a[i + V / 2], keep = hi ? a[i + V / 2] : a[i];
+            a[i] = keep + xor32(send, first);
+        }
+        n = V / 2;
+    }
+    if (n > 1) {  // lane bit 4
+        const bool hi = lane & 16;
+#pragma unroll
+        for (int i = 0; i < V / 4; i++) {
+            const float send = hi ? a[i] : a[i + V / 4], keep = hi ? a[i + V / 4] : a[i];
+            a[i] = keep + xor16(send);
+        }
+        n = V / 4;
+    }
+    if (n > 1) {  // lane bit 3 (row_ror:8 pairs i with i ^ 8 inside a 16-lane row)
+        const bool hi = lane & 8;
+        const float send = hi ? a[0] : a[1], keep = hi ? a[1] : a[0];
+        a[0] = keep + dpp<0x128>(send);
+    }
+    float t = a[0];
+    if (V == 8) {  // lane bits 0..2
+        t += dpp<0xB1>(t);
+        t += dpp<0x4E>(t);
+        t += dpp<0x141>(t);
+    } else {  // lane bits 0..3, then 4 and 5 as needed
+        t += dpp<0x128>(t);
+        t += dpp<0x124>(t);
+        t += dpp<0x122>(t);
+        t += dpp<0x121>(t);
+        if (V <= 2) t += xor16(t);
+        if (V == 1) t += xor32(t, first);
+    }
+    return t;
+}
+
+// Sums V values (V = 1, 2, 4 or 8) over each aligned group of 8 lanes.
+// Returns, in lane g*8 + j, the group's total of value index j * V / 8
+// (for V = 8: value j).
+template <int V>
+__device__ __forceinline__ float group8_sum_transposed(float (&v)[V], int lane) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "V");
+    float a[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) a[i] = v[i];
+    int n = V;
+    if (n > 1) {  // lane bit 2: row_half_mirror pairs i with 7 - i
+        const bool hi = lane & 4;
+#pragma unroll
+        for (int i = 0; i < V / 2; i++) {
+            const float send = hi ? a[i] : a[i + V / 2], keep = hi ? a[i + V / 2] : a[i];
+            a[i] = keep + dpp<0x141>(send);
+        }
+        n = V / 2;
+    } else {
+        a[0] += dpp<0x141>(a[0]);
+    }
+    if (n > 1) {  // lane bit 1
+        const bool hi = lane & 2;
+#pragma unroll
+        for (int i = 0; i < V / 4; i++) {
+            const float send = hi ? a[i] : a[i + V / 4], keep = hi ? a[i + V / 4] : a[i];
+            a[i] = keep + dpp<0x4E>(send);
+        }
+        n = V / 4;
+    } else {
+        a[0] += dpp<0x4E>(a[0]);
+    }
+    if (n > 1) {  // lane bit 0
+        const bool hi = lane & 1;
+        const float send = hi ? a[0] : a[1], keep = hi ? a[1] : a[0];
+        a[0] = keep + dpp<0xB1>(send);
+    } else {
+        a[0] += dpp<0xB1>(a[0]);
+    }
+    return a[0];
+}
+
 __device__ __forceinline__ float act_silu(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float act_gelu_tanh(float g) {
@@ -105,12 +227,11 @@ hipError_t launch_matvec_q6k(const DevTensor &W, const float *x, float *y, hipSt
 hipError_t launch_matvec_f32(const DevTensor &W, const float *x, float *y, hipStream_t s);
 hipError_t launch_gate_up_q8_0(const DevTensor &Wg, const DevTensor &Wu, const float *x, uint32_t act,
                                float *h, hipStream_t s);
-hipError_t launch_router_f32(const DevTensor &R, const float *x, const float *bias, float *logits,
-                             hipStream_t s);
-hipError_t launch_router_q8_0(const DevTensor &R, const float *x, const float *bias, float *logits,
-                              hipStream_t s);
-hipError_t launch_topk_softmax(const float *logits, uint32_t n, uint32_t k, uint32_t norm, uint32_t *ids,
-                               float *w, float *scores, hipStream_t s);
+// Router logits (F32 or Q8_0 router, exact reference order) plus softmax /
+// top-k in the same launch.  ticket: a zero-initialised counter owned by the
+// caller, left at zero after every launch.  k = 0 computes logits only.
+hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, float *logits, unsigned *ticket,
+                         uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s);
 hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
                                      hipStream_t s);

@@ -34,15 +34,23 @@ struct XChunk {
 
 __device__ __forceinline__ void load_xchunk(const float *xs, int sb, int cc, XChunk &xc) {
     const float *p = xs + sb * 256 + 64 * (cc >> 1) + 16 * (cc & 1);
-    float slo = 0.f, shi = 0.f;
 #pragma unroll
     for (int t = 0; t < 16; t += 4) {
         float4 a = *reinterpret_cast<const float4 *>(p + t);
         float4 b = *reinterpret_cast<const float4 *>(p + 32 + t);
         xc.lo[t] = a.x; xc.lo[t + 1] = a.y; xc.lo[t + 2] = a.z; xc.lo[t + 3] = a.w;
         xc.hi[t] = b.x; xc.hi[t + 1] = b.y; xc.hi[t + 2] = b.z; xc.hi[t + 3] = b.w;
-        slo += (a.x + a.y) + (a.z + a.w);
-        shi += (b.x + b.y) + (b.z + b.w);
+    }
+}
+
+// The x sums used by the min term; kept apart from load_xchunk so that the
+// adds can be placed after the weight loads are issued.
+__device__ __forceinline__ void sum_xchunk(XChunk &xc) {
+    float slo = 0.f, shi = 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; t += 4) {
+        slo += (xc.lo[t] + xc.lo[t + 1]) + (xc.lo[t + 2] + xc.lo[t + 3]);
+        shi += (xc.hi[t] + xc.hi[t + 1]) + (xc.hi[t + 2] + xc.hi[t + 3]);
     }
     xc.slo = slo;
     xc.shi = shi;
@@ -52,36 +60,32 @@ __device__ __forceinline__ void load_xchunk(const float *xs, int sb, int cc, XCh
 __device__ __forceinline__ float q4k_chunk_dot(uint4 hdr, uint4 q, int cc, const XChunk &xc) {
     const float d = f16_bits_to_f32(hdr.x);
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
-    const int j = (cc >> 1) * 2;
-    float sc0, mn0, sc1, mn1;
-    // branch-free get_scale_min_k4 for the pair (j, j+1)
-    {
-        const int i0 = j & 3, i1 = (j + 1) & 3;
-        const bool low = j < 4;
-        uint32_t a0 = (hdr.y >> (8 * i0)) & 0xffu, b0 = (hdr.z >> (8 * i0)) & 0xffu,
-                 c0 = (hdr.w >> (8 * i0)) & 0xffu;
-        uint32_t a1 = (hdr.y >> (8 * i1)) & 0xffu, b1 = (hdr.z >> (8 * i1)) & 0xffu,
-                 c1 = (hdr.w >> (8 * i1)) & 0xffu;
-        sc0 = (float)(low ? (a0 & 63u) : ((c0 & 15u) | ((a0 >> 6) << 4)));
-        mn0 = (float)(low ? (b0 & 63u) : ((c0 >> 4) | ((b0 >> 6) << 4)));
-        sc1 = (float)(low ? (a1 & 63u) : ((c1 & 15u) | ((a1 >> 6) << 4)));
-        mn1 = (float)(low ? (b1 & 63u) : ((c1 >> 4) | ((b1 >> 6) << 4)));
-    }
+    // get_scale_min_k4 for the sub-block pair (2p, 2p+1) of this chunk, both
+    // fields at once: the pair's bytes sit at byte offset 2*(p&1) of the
+    // scale words (hdr.y = scales[0..3], hdr.z = [4..7], hdr.w = [8..11]).
+    const int p = cc >> 1;
+    const int sh = (p & 1) * 16;
+    const uint32_t ys = hdr.y >> sh, zs = hdr.z >> sh, ws = hdr.w >> sh;
+    const uint32_t scp = opaque(p < 2 ? (ys & 0x3f3fu) : ((ws & 0x0f0fu) | ((ys >> 2) & 0x3030u)));
+    const uint32_t mnp = opaque(p < 2 ? (zs & 0x3f3fu) : (((ws >> 4) & 0x0f0fu) | ((zs >> 2) & 0x3030u)));
+    const float sc0 = (float)(scp & 0xffu), sc1 = (float)((scp >> 8) & 0xffu);
+    const float mn0 = (float)(mnp & 0xffu), mn1 = (float)((mnp >> 8) & 0xffu);
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-    float dl = 0.f, dh = 0.f;
+    float dl0 = 0.f, dl1 = 0.f, dh0 = 0.f, dh1 = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const uint32_t lo = w[t] & 0x0f0f0f0fu;
-        const uint32_t hi = (w[t] >> 4) & 0x0f0f0f0fu;
-        dl += (float)(lo & 0xffu) * xc.lo[4 * t + 0];
-        dl += (float)((lo >> 8) & 0xffu) * xc.lo[4 * t + 1];
-        dl += (float)((lo >> 16) & 0xffu) * xc.lo[4 * t + 2];
-        dl += (float)(lo >> 24) * xc.lo[4 * t + 3];
-        dh += (float)(hi & 0xffu) * xc.hi[4 * t + 0];
-        dh += (float)((hi >> 8) & 0xffu) * xc.hi[4 * t + 1];
-        dh += (float)((hi >> 16) & 0xffu) * xc.hi[4 * t + 2];
-        dh += (float)(hi >> 24) * xc.hi[4 * t + 3];
+        const uint32_t lo = opaque(w[t] & 0x0f0f0f0fu);
+        const uint32_t hi = opaque((w[t] >> 4) & 0x0f0f0f0fu);
+        dl0 = fmaf((float)(lo & 0xffu), xc.lo[4 * t + 0], dl0);
+        dl1 = fmaf((float)((lo >> 8) & 0xffu), xc.lo[4 * t + 1], dl1);
+        dl0 = fmaf((float)((lo >> 16) & 0xffu), xc.lo[4 * t + 2], dl0);
+        dl1 = fmaf((float)(lo >> 24), xc.lo[4 * t + 3], dl1);
+        dh0 = fmaf((float)(hi & 0xffu), xc.hi[4 * t + 0], dh0);
+        dh1 = fmaf((float)((hi >> 8) & 0xffu), xc.hi[4 * t + 1], dh1);
+        dh0 = fmaf((float)((hi >> 16) & 0xffu), xc.hi[4 * t + 2], dh0);
+        dh1 = fmaf((float)(hi >> 24), xc.hi[4 * t + 3], dh1);
     }
+    const float dl = dl0 + dl1, dh = dh0 + dh1;
     return ((d * sc0) * dl - (dmin * mn0) * xc.slo) + ((d * sc1) * dh - (dmin * mn1) * xc.shi);
 }
 
@@ -129,15 +133,24 @@ __global__ void __launch_bounds__(256) k_matvec_q4k(const uint8_t *__restrict__ 
             }
             XChunk xc;
             load_xchunk(xs, sb, cc, xc);
+            sum_xchunk(xc);
 #pragma unroll
             for (int r = 0; r < R; r++)
                 if (rbase + r < nrows) acc[r] += q4k_chunk_dot(hv[r], qv[r], cc, xc);
         }
     }
+    if constexpr (G == 64) {
+        // row r's total lands in lanes [r*64/R, (r+1)*64/R)
+        const float t = wave_sum_transposed<R>(acc, lane, p32_first(lane));
+        constexpr int SH = R == 8 ? 3 : (R == 4 ? 4 : (R == 2 ? 5 : 6));
+        const int r = lane >> SH;
+        if ((lane & ((1 << SH) - 1)) == 0 && rbase + r < nrows) y[rbase + r] = t;
+    } else {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float v = group_sum<G>(acc[r]);
-        if (lane == 0 && rbase + r < nrows) y[rbase + r] = v;
+        for (int r = 0; r < R; r++) {
+            float v = group_sum<G>(acc[r]);
+            if (lane == 0 && rbase + r < nrows) y[rbase + r] = v;
+        }
     }
 }
 
@@ -178,7 +191,10 @@ hipError_t launch_matvec_q4k(const DevTensor &W, size_t row0, size_t nrows, cons
 // [e*2F, e*2F+F) and its up rows [e*2F+F, e*2F+2F) of the flattened tensor
 // (ops/moe.zig:55-73).  h[s][j] = act(gate_j . x) * (up_j . x) for j < F;
 // h[s][F..down_cols) = 0 (zero K padding of the down product).
-// One wavefront (G = 64) per row pair, CPL chunks per lane, R row pairs.
+// One wavefront (64 lanes) per row pair, CPL chunks per lane, R row pairs per
+// wave, 4 waves per block.  Every weight load of the wave is issued before
+// any arithmetic (one HBM round trip per wave); x comes from L2 straight
+// into registers.
 template <int CPL, int R>
 __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__restrict__ hdr,
                                                             const uint8_t *__restrict__ qs,
@@ -186,69 +202,80 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
                                                             const uint32_t *__restrict__ ids, int n_experts,
                                                             int nsb, int F, int down_cols, uint32_t act,
                                                             float *__restrict__ h) {
-    extern __shared__ float xs[];
     const int s = blockIdx.y;
-    const uint32_t e = ids[s];
+    const uint32_t e = __builtin_amdgcn_readfirstlane(ids[s]);
     float *hs = h + (size_t)s * down_cols;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int jbase = (blockIdx.x * 4 + wave) * R;
     if (blockIdx.x == 0)
         for (int j = F + threadIdx.x; j < down_cols; j += blockDim.x) hs[j] = 0.f;
     if (e >= (uint32_t)n_experts) {  // invalid id from the caller: the slot contributes zeros
-        for (int j = blockIdx.x * 4 * R + threadIdx.x; j < F && j < (int)(blockIdx.x + 1) * 4 * R;
-             j += blockDim.x)
-            hs[j] = 0.f;
+        if (lane < R && jbase + lane < F) hs[jbase + lane] = 0.f;
         return;
     }
-    stage_x(xs, x, nsb * 256);
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int jbase = (blockIdx.x * 4 + wave) * R;
     const int nch = nsb * 8;
     const size_t gate0 = (size_t)e * 2 * F, up0 = gate0 + F;
-    float ag[R], au[R];
+    // x first (L2-resident), then the weights row by row, so that rows can
+    // be consumed as their loads land (vmcnt retires in issue order).
+    XChunk xc[CPL];
 #pragma unroll
-    for (int r = 0; r < R; r++) ag[r] = au[r] = 0.f;
+    for (int i = 0; i < CPL; i++)
+        if (lane + kWave * i < nch) load_xchunk(x, (lane + kWave * i) >> 3, (lane + kWave * i) & 7, xc[i]);
+    uint4 hg[R][CPL], qg[R][CPL], hu[R][CPL], qu[R][CPL];
 #pragma unroll
-    for (int i = 0; i < CPL; i++) {
-        const int c = lane + kWave * i;
-        if (c < nch) {
+    for (int r = 0; r < R; r++) {
+        const int j = jbase + r;
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int c = lane + kWave * i;
             const int sb = c >> 3, cc = c & 7;
-            uint4 hg[R], qg[R], hu[R], qu[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int j = jbase + r;
-                if (j < F) {
-                    size_t bg = (gate0 + j) * nsb + sb, bu = (up0 + j) * nsb + sb;
-                    hg[r] = ldg16(hdr + bg * 16);
-                    qg[r] = ldg16(qs + bg * 128 + cc * 16);
-                    hu[r] = ldg16(hdr + bu * 16);
-                    qu[r] = ldg16(qs + bu * 128 + cc * 16);
-                }
+            if (c < nch && j < F) {
+                const size_t bg = (gate0 + j) * nsb + sb, bu = (up0 + j) * nsb + sb;
+                hg[r][i] = ldg16(hdr + bg * 16);
+                qg[r][i] = ldg16(qs + bg * 128 + cc * 16);
+                hu[r][i] = ldg16(hdr + bu * 16);
+                qu[r][i] = ldg16(qs + bu * 128 + cc * 16);
             }
-            XChunk xc;
-            load_xchunk(xs, sb, cc, xc);
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (jbase + r < F) {
-                    ag[r] += q4k_chunk_dot(hg[r], qg[r], cc, xc);
-                    au[r] += q4k_chunk_dot(hu[r], qu[r], cc, xc);
-                }
         }
     }
 #pragma unroll
+    for (int i = 0; i < CPL; i++) sum_xchunk(xc[i]);
+    float ag[R], au[R];
+#pragma unroll
     for (int r = 0; r < R; r++) {
-        const float g = group_sum<kWave>(ag[r]);
-        const float u = group_sum<kWave>(au[r]);
-        if (lane == 0 && jbase + r < F) hs[jbase + r] = act_apply(act, g) * u;
+        ag[r] = au[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int c = lane + kWave * i;
+            if (c < nch && jbase + r < F) {
+                ag[r] += q4k_chunk_dot(hg[r][i], qg[r][i], c & 7, xc[i]);
+                au[r] += q4k_chunk_dot(hu[r][i], qu[r][i], c & 7, xc[i]);
+            }
+        }
     }
+    // 2R partial sums per lane -> one total per 64/(2R) lanes: gate row r in
+    // lanes [r*S, (r+1)*S), up row r in the same lanes + 32 (S = 64/(2R)).
+    float v[2 * R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        v[r] = ag[r];
+        v[R + r] = au[r];
+    }
+    const bool first = p32_first(lane);
+    const float t = wave_sum_transposed<2 * R>(v, lane, first);
+    const float u = xor32(t, first);
+    constexpr int SH = (2 * R == 8) ? 3 : (2 * R == 4 ? 4 : 5);
+    const int r = lane >> SH;
+    if (lane < 32 && (lane & ((1 << SH) - 1)) == 0 && jbase + r < F) hs[jbase + r] = act_apply(act, t) * u;
 }
 
-template <int CPL>
+template <int CPL, int R>
 static hipError_t launch_gu_t(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k, uint32_t F,
                               uint32_t down_cols, uint32_t act, float *h, hipStream_t s) {
-    constexpr int R = 4;
     const int nsb = (int)GU.blocks_per_row;
     dim3 grid((F + 4 * R - 1) / (4 * R), k);
-    hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R>), grid, dim3(256), nsb * 256 * sizeof(float), s, GU.p0,
-                       GU.p1, x, ids, (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h);
+    hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R>), grid, dim3(256), 0, s, GU.p0, GU.p1, x, ids,
+                       (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h);
     return hipGetLastError();
 }
 
@@ -257,10 +284,10 @@ hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const 
                                      hipStream_t s) {
     const int nch = (int)GU.blocks_per_row * 8;
     switch ((nch + 63) / 64) {
-    case 1: return launch_gu_t<1>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    case 2: return launch_gu_t<2>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    case 3: return launch_gu_t<3>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    case 4: return launch_gu_t<4>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 1: return launch_gu_t<1, 4>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 2: return launch_gu_t<2, 2>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 3: return launch_gu_t<3, 2>(GU, x, ids, k, d_expert, down_cols, act, h, s);
+    case 4: return launch_gu_t<4, 1>(GU, x, ids, k, d_expert, down_cols, act, h, s);
     default: return hipErrorInvalidValue;  // d_model > 8192: rejected by the API layer
     }
 }
@@ -269,10 +296,12 @@ hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const 
 // Expert-indexed down with the weighted combine fused:
 //   out[i] = base[i] + sum_{s in slot order} w[s] * (D_{ids[s]} row i) . h[s]
 // (base = previous out with accumulate, the shared-FFN output, or 0).
-// Block: 4 waves x RD output rows.  Wave w handles super-blocks w, w+4, ...
-// of the K = down_cols dimension; lane = (slot within an 8-slot pass, chunk
-// cc).  Per-(row, slot, super-block) partial sums go through LDS and are
-// combined in a fixed order, so the result does not depend on scheduling.
+// Block: NW = min(nsb, 4) waves x RD output rows.  Wave w handles
+// super-blocks w, w+NW, ... of the K = down_cols dimension; lane = (slot
+// within an 8-slot pass, chunk cc), so one load instruction covers the same
+// super-block of 8 experts (8 contiguous 128-byte runs).  Per-(row, slot,
+// super-block) partial sums go through LDS and are combined in a fixed
+// order, so the result does not depend on scheduling.
 template <int RD>
 __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restrict__ hdr,
                                                          const uint8_t *__restrict__ qs,
@@ -282,6 +311,7 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
                                                          int rows_per_expert, int nsb, const float *base,
                                                          int accumulate, float *out) {
     __shared__ float part[RD][16][16];  // [row][slot][super-block]
+    const int NW = blockDim.x / kWave;
     const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int sl = lane >> 3, cc = lane & 7;
     const int row0 = blockIdx.x * RD;
@@ -292,26 +322,27 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
         const uint32_t e = active ? ids[s] : 0u;
         const bool valid = active && e < (uint32_t)n_experts;
         const float *hs = h + (size_t)(valid ? s : 0) * K;
-        for (int sb = w; sb < nsb; sb += 4) {
+        for (int sb = w; sb < nsb; sb += NW) {
+            XChunk xc;
+            load_xchunk(hs, sb, cc, xc);
             uint4 hv[RD], qv[RD];
 #pragma unroll
             for (int r = 0; r < RD; r++) {
                 const int row = row0 + r;
                 if (valid && row < rows_per_expert) {
-                    size_t blk = ((size_t)e * rows_per_expert + row) * nsb + sb;
+                    const size_t blk = ((size_t)e * rows_per_expert + row) * nsb + sb;
                     hv[r] = ldg16(hdr + blk * 16);
                     qv[r] = ldg16(qs + blk * 128 + cc * 16);
                 }
             }
-            XChunk xc;
-            load_xchunk(hs, sb, cc, xc);
+            sum_xchunk(xc);
+            float v[RD];
 #pragma unroll
-            for (int r = 0; r < RD; r++) {
-                float v = 0.f;
-                if (valid && row0 + r < rows_per_expert) v = q4k_chunk_dot(hv[r], qv[r], cc, xc);
-                v = group_sum<8>(v);
-                if (cc == 0 && active) part[r][s][sb] = v;
-            }
+            for (int r = 0; r < RD; r++)
+                v[r] = (valid && row0 + r < rows_per_expert) ? q4k_chunk_dot(hv[r], qv[r], cc, xc) : 0.f;
+            // lane (slot, cc) receives the 8-lane total of row cc
+            const float t = group8_sum_transposed<RD>(v, lane);
+            if (active) part[cc][s][sb] = t;
         }
     }
     __syncthreads();
@@ -335,9 +366,10 @@ hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint
                                   uint32_t k, const float *base, int accumulate, float *out, hipStream_t s) {
     constexpr int RD = 8;
     const int nsb = (int)D.blocks_per_row;  // <= 16, k <= 16: checked by the API layer
+    const int nw = nsb < 4 ? nsb : 4;
     const int rows = (int)D.rows;
     dim3 grid((rows + RD - 1) / RD);
-    hipLaunchKernelGGL((k_expert_down_q4k<RD>), grid, dim3(256), 0, s, D.p0, D.p1, h, ids, w, (int)k,
+    hipLaunchKernelGGL((k_expert_down_q4k<RD>), grid, dim3(64 * nw), 0, s, D.p0, D.p1, h, ids, w, (int)k,
                        (int)D.n_experts, rows, nsb, base, accumulate, out);
     return hipGetLastError();
 }

@@ -1,5 +1,5 @@
 // lt_router.hip -- MoE router: logits with the reference's exact fp32
-// operation order, then softmax + top-k in one wavefront.
+// operation order, then softmax + top-k in the last block to finish.
 //
 // Routing must match the CPU path bit for bit.  Selection depends only on the
 // order of the logits, so the logits are computed with exactly the rounded
@@ -11,28 +11,186 @@
 //   Q8_0 router: dotQ8_0 (quant/dequant.zig:59-78): per block, 8 lane
 //                accumulators over 4 groups, ordered reduce, times d, added
 //                to a running total in block order.
+// The block that finishes last (atomic ticket) runs softmax + top-k over all
+// logits in one wavefront, so routing costs one launch.
 #include "lt_internal.h"
 
 #include <math.h>
 
 namespace lt {
 
-// One thread per (row, chain); 8 rows x 32 chains per 256-thread block.
-__global__ void __launch_bounds__(256) k_router_f32(const float *__restrict__ W, const float *__restrict__ x,
-                                                    const float *__restrict__ bias, float *__restrict__ logits,
-                                                    int rows, int cols) {
+namespace {
+
+// true if (va, ia) ranks before (vb, ib): larger value, then lower index --
+// the strict '>' rule of every reference top-k (ops/moe.zig:87,
+// gemma4/forward.zig:612-625).
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+    return va > vb || (!(va < vb) && ia < ib);
+}
+
+// Softmax + top-k over n <= 64*PER logits, executed by one full wavefront
+// (lane = 0..63; lane owns entries lane + 64*j).  NaN logits rank last.
+// Each of the k rounds takes the lane-local best unselected entry and runs
+// a wave-wide argmax with DPP row rotations and the two half-swaps.
+// w[r] = exp(l - max) / sum_j exp(l_j - max); with norm, divided by the sum
+// of the selected weights taken in selection order.  scores (optional):
+// logits, with the selected entries replaced by their probabilities
+// (routerTopKSoftmax's buffer, gemma4/forward.zig:645-668).
+__device__ __forceinline__ void argmax_merge(float &bv, int &bi, float ov, int oi) {
+    if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+template <int PER>
+__device__ void topk_softmax_wave(const float *logits, int n, int k, int norm, uint32_t *ids, float *w,
+                                  float *scores, int lane) {
+    const bool first = p32_first(lane);
+    float v[PER];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int idx = lane + 64 * j;
+        float t = idx < n ? logits[idx] : -INFINITY;
+        if (t != t) t = -INFINITY;
+        v[j] = t;
+        m = fmaxf(m, t);
+    }
+    m = fmaxf(m, dpp<0x128>(m));
+    m = fmaxf(m, dpp<0x124>(m));
+    m = fmaxf(m, dpp<0x122>(m));
+    m = fmaxf(m, dpp<0x121>(m));
+    m = fmaxf(m, xor16(m));
+    m = fmaxf(m, xor32(m, first));
+    float se = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; j++)
+        if (lane + 64 * j < n) se += expf(v[j] - m);
+    se += dpp<0x128>(se);
+    se += dpp<0x124>(se);
+    se += dpp<0x122>(se);
+    se += dpp<0x121>(se);
+    se += xor16(se);
+    se += xor32(se, first);
+
+    unsigned taken = 0;
+    float my_v = -INFINITY;
+    int my_i = 0;
+    for (int r = 0; r < k; r++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int idx = lane + 64 * j;
+            if (idx < n && !((taken >> j) & 1u) && better(v[j], idx, bv, bi)) {
+                bv = v[j];
+                bi = idx;
+            }
+        }
+        argmax_merge(bv, bi, dpp<0x128>(bv), dpp_i<0x128>(bi));
+        argmax_merge(bv, bi, dpp<0x124>(bv), dpp_i<0x124>(bi));
+        argmax_merge(bv, bi, dpp<0x122>(bv), dpp_i<0x122>(bi));
+        argmax_merge(bv, bi, dpp<0x121>(bv), dpp_i<0x121>(bi));
+        argmax_merge(bv, bi, xor16(bv), __float_as_int(xor16(__int_as_float(bi))));
+        argmax_merge(bv, bi, xor32(bv, first), __float_as_int(xor32(__int_as_float(bi), first)));
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == r) {
+            my_v = bv;
+            my_i = bi;
+        }
+    }
+    const float my_p = lane < k ? expf(my_v - m) / se : 0.0f;
+    float ps = 0.0f;  // sum of the selected weights in selection order
+    if (norm)
+        for (int r = 0; r < k; r++) ps = ps + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), r));
+    if (lane < k) {
+        ids[lane] = (uint32_t)my_i;
+        w[lane] = norm ? my_p / ps : my_p;
+    }
+    if (scores) {
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int idx = lane + 64 * j;
+            if (idx < n) {
+                float val = logits[idx];
+                if ((taken >> j) & 1u)
+                    for (int r = 0; r < k; r++)
+                        if (__builtin_amdgcn_readlane(my_i, r) == idx)
+                            val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), r));
+                scores[idx] = val;
+            }
+        }
+    }
+}
+
+struct TopkArgs {
+    unsigned *ticket;  // zero-initialised; wraps back to 0 after each launch
+    int k;             // 0: logits only
+    int norm;
+    uint32_t *ids;
+    float *w;
+    float *scores;
+};
+
+// After this block's logits are stored: the last block to arrive runs the
+// top-k.  Must be called by every thread of the block.
+__device__ __forceinline__ void last_block_topk(const float *logits, int n, const TopkArgs &a) {
+    if (a.k == 0) return;
+    __shared__ int is_last;
+    __threadfence();  // release this block's logits
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicInc(a.ticket, gridDim.x - 1) == gridDim.x - 1;
+    __syncthreads();
+    if (is_last && threadIdx.x < 64) {
+        __threadfence();  // acquire the other blocks' logits
+        const int lane = threadIdx.x;
+        if (n <= 64)
+            topk_softmax_wave<1>(logits, n, a.k, a.norm, a.ids, a.w, a.scores, lane);
+        else if (n <= 128)
+            topk_softmax_wave<2>(logits, n, a.k, a.norm, a.ids, a.w, a.scores, lane);
+        else if (n <= 256)
+            topk_softmax_wave<4>(logits, n, a.k, a.norm, a.ids, a.w, a.scores, lane);
+        else
+            topk_softmax_wave<16>(logits, n, a.k, a.norm, a.ids, a.w, a.scores, lane);
+    }
+}
+
+}  // namespace
+
+// One wavefront per two rows; lane = (row of the pair, chain c).  All
+// MAXIT loads of a chain are issued before its first add.
+template <int MAXIT>
+__global__ void __launch_bounds__(64) k_router_f32(const float *__restrict__ W, const float *__restrict__ x,
+                                                   const float *__restrict__ bias, float *__restrict__ logits,
+                                                   int rows, int cols, TopkArgs ta) {
 #pragma clang fp contract(off)
-    __shared__ float chain[8][32];
+    __shared__ float chain[2][32];
     const int rl = threadIdx.x >> 5, c = threadIdx.x & 31;
-    const int row = blockIdx.x * 8 + rl;
-    const int n32 = cols & ~31;
-    const float *w = W + (size_t)(row < rows ? row : 0) * cols;
+    const int row = blockIdx.x * 2 + rl;
+    const int nit = cols >> 5, n32 = nit << 5;
+    const float *wr = W + (size_t)(row < rows ? row : 0) * cols;
     float a = 0.0f;
     if (row < rows) {
-#pragma unroll 16
-        for (int i = 0; i < n32; i += 32) {
-            float p = w[i + c] * x[i + c];
-            a = a + p;
+        for (int it0 = 0; it0 < nit; it0 += MAXIT) {
+            float wv[MAXIT], xv[MAXIT];
+#pragma unroll
+            for (int t = 0; t < MAXIT; t++)
+                if (it0 + t < nit) {
+                    wv[t] = wr[(it0 + t) * 32 + c];
+                    xv[t] = x[(it0 + t) * 32 + c];
+                }
+#pragma unroll
+            for (int t = 0; t < MAXIT; t++)
+                if (it0 + t < nit) {
+                    float p = wv[t] * xv[t];
+                    a = a + p;
+                }
         }
     }
     chain[rl][c] = a;
@@ -49,38 +207,27 @@ __global__ void __launch_bounds__(256) k_router_f32(const float *__restrict__ W,
         for (; i + 8 <= cols; i += 8)
 #pragma unroll
             for (int l = 0; l < 8; l++) {
-                float p = w[i + l] * x[i + l];
+                float p = wr[i + l] * x[i + l];
                 acc[l] = acc[l] + p;
             }
         float sum = acc[0];
 #pragma unroll
         for (int l = 1; l < 8; l++) sum = sum + acc[l];
         for (; i < cols; i++) {
-            float p = w[i] * x[i];
+            float p = wr[i] * x[i];
             sum = sum + p;
         }
         if (bias) sum = sum + bias[row];
         logits[row] = sum;
     }
+    last_block_topk(logits, rows, ta);
 }
 
-hipError_t launch_router_f32(const DevTensor &R, const float *x, const float *bias, float *logits,
-                             hipStream_t s) {
-    const int rows = (int)R.total_rows, cols = (int)R.cols;
-    hipLaunchKernelGGL(k_router_f32, dim3((rows + 7) / 8), dim3(256), 0, s, (const float *)R.p0, x, bias, logits,
-                       rows, cols);
-    return hipGetLastError();
-}
-
-hipError_t launch_matvec_f32(const DevTensor &W, const float *x, float *y, hipStream_t s) {
-    return launch_router_f32(W, x, nullptr, y, s);
-}
-
-// One block per row: thread b computes block b's term reduce(acc)*d exactly,
-// then thread 0 adds the terms in block order.
-__global__ void __launch_bounds__(256) k_router_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ dp,
+// One block (2 waves) per row: thread b computes block b's term
+// reduce(acc)*d exactly, then thread 0 adds the terms in block order.
+__global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ dp,
                                                      const float *__restrict__ x, const float *__restrict__ bias,
-                                                     float *__restrict__ logits, int nb) {
+                                                     float *__restrict__ logits, int nb, int rows, TopkArgs ta) {
 #pragma clang fp contract(off)
     extern __shared__ float term[];
     const int row = blockIdx.x;
@@ -110,114 +257,27 @@ __global__ void __launch_bounds__(256) k_router_q8_0(const int8_t *__restrict__ 
         if (bias) total = total + bias[row];
         logits[row] = total;
     }
+    last_block_topk(logits, rows, ta);
 }
 
-hipError_t launch_router_q8_0(const DevTensor &R, const float *x, const float *bias, float *logits,
-                              hipStream_t s) {
-    const int rows = (int)R.total_rows, nb = (int)R.blocks_per_row;
-    hipLaunchKernelGGL(k_router_q8_0, dim3(rows), dim3(128), nb * sizeof(float), s, (const int8_t *)R.p0,
-                       (const uint16_t *)R.p1, x, bias, logits, nb);
+hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, float *logits, unsigned *ticket,
+                         uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s) {
+    const TopkArgs ta{ticket, (int)k, (int)norm, ids, w, scores};
+    const int rows = (int)R.total_rows;
+    if (R.type == 0) {  // F32
+        const int cols = (int)R.cols;
+        hipLaunchKernelGGL(k_router_f32<64>, dim3((rows + 1) / 2), dim3(64), 0, s, (const float *)R.p0, x, bias,
+                           logits, rows, cols, ta);
+    } else {  // Q8_0
+        const int nb = (int)R.blocks_per_row;
+        hipLaunchKernelGGL(k_router_q8_0, dim3(rows), dim3(128), nb * sizeof(float), s, (const int8_t *)R.p0,
+                           (const uint16_t *)R.p1, x, bias, logits, nb, rows, ta);
+    }
     return hipGetLastError();
 }
 
-// ------------------------------------------------------------------------
-// Softmax + top-k in a single wavefront (n <= 1024, k <= 16).
-// Selection is on the logits, descending, the lowest index winning ties --
-// the rule of every top-k in the reference (strict '>': ops/moe.zig:87,
-// gemma4/forward.zig:612-625).  NaN logits never win over a number.
-// w[i] = exp(l_i - max) / sum_j exp(l_j - max); with norm, w[i] is divided by
-// the sum of the selected weights taken in selection order.
-__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-    // true if (va, ia) ranks before (vb, ib)
-    return va > vb || (!(va < vb) && ia < ib);
-}
-
-__global__ void __launch_bounds__(64) k_topk_softmax(const float *__restrict__ logits, int n, int k, int norm,
-                                                     uint32_t *__restrict__ ids, float *__restrict__ w,
-                                                     float *__restrict__ scores) {
-    const int lane = threadIdx.x;
-    constexpr int PER = 16;
-    float v[PER];
-    bool taken[PER];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int idx = lane + 64 * j;
-        float t = idx < n ? logits[idx] : -INFINITY;
-        if (t != t) t = -INFINITY;  // NaN ranks last
-        v[j] = t;
-        taken[j] = idx >= n;
-        m = fmaxf(m, t);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    float se = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PER; j++)
-        if (lane + 64 * j < n) se += expf(v[j] - m);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) se += __shfl_xor(se, off, 64);
-
-    float selv[16];
-    int seli[16];
-    for (int r = 0; r < k; r++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int idx = lane + 64 * j;
-            if (!taken[j] && better(v[j], idx, bv, bi)) {
-                bv = v[j];
-                bi = idx;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            float ov = __shfl_xor(bv, off, 64);
-            int oi = __shfl_xor(bi, off, 64);
-            if (better(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < PER; j++)
-            if (lane + 64 * j == bi) taken[j] = true;
-        selv[r] = bv;
-        seli[r] = bi;
-    }
-    // bv/bi, hence selv/seli, m and se, are identical in every lane here.
-    float p[16];
-    float ps = 0.0f;
-    for (int r = 0; r < k; r++) {
-        p[r] = expf(selv[r] - m) / se;
-        ps = ps + p[r];
-    }
-    if (lane == 0)
-        for (int r = 0; r < k; r++) {
-            ids[r] = (uint32_t)seli[r];
-            w[r] = norm ? p[r] / ps : p[r];
-        }
-    if (scores) {
-        // routerTopKSoftmax's buffer: probabilities at the selected experts,
-        // logits elsewhere.  Each lane writes only its own entries.
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int idx = lane + 64 * j;
-            if (idx < n) {
-                float val = logits[idx];
-                for (int r = 0; r < k; r++)
-                    if (seli[r] == idx) val = p[r];
-                scores[idx] = val;
-            }
-        }
-    }
-}
-
-hipError_t launch_topk_softmax(const float *logits, uint32_t n, uint32_t k, uint32_t norm, uint32_t *ids,
-                               float *w, float *scores, hipStream_t s) {
-    hipLaunchKernelGGL(k_topk_softmax, dim3(1), dim3(64), 0, s, logits, (int)n, (int)k, (int)norm, ids, w, scores);
-    return hipGetLastError();
+hipError_t launch_matvec_f32(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    return launch_router(W, x, nullptr, y, nullptr, 0, 0, nullptr, nullptr, nullptr, s);
 }
 
 }  // namespace lt
