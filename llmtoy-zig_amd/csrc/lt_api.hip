@@ -32,7 +32,7 @@ struct lt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // context-owned device scratch, grown on demand
-    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh;
+    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh, pf;
     // arrival ticket of the router's last-block top-k; zeroed once at init,
     // every launch leaves it at zero again
     unsigned *ticket = nullptr;
@@ -227,7 +227,7 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     DevBuf *bufs[] = {&ctx->x, &ctx->out, &ctx->logits, &ctx->h, &ctx->ids, &ctx->w,
-                      &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh};
+                      &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh, &ctx->pf};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (ctx->ticket) (void)hipFree(ctx->ticket);
@@ -656,7 +656,54 @@ extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_
 extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt_tensor *router,
                               const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
                               uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w) {
-    (void)out; (void)X; (void)T; (void)router; (void)router_bias; (void)gate_up; (void)down; (void)k;
-    (void)d_expert; (void)act; (void)flags; (void)out_ids; (void)out_w;
-    return fail(ctx, LT_ERR_UNSUPPORTED, "lt_moe_prefill: not built yet");
+    if (!ctx || !out || !X) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (T == 0 || T > 65536) return fail(ctx, LT_ERR_INVALID, "T=%u out of range (1..65536)", T);
+    if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
+    if (!router || !gate_up || !down) return fail(ctx, LT_ERR_INVALID, "null tensor");
+    if (flags & LT_MOE_ACCUMULATE) return fail(ctx, LT_ERR_UNSUPPORTED, "prefill does not accumulate");
+    const size_t D = gate_up->t.cols;
+    int rc;
+    if ((rc = check_router(ctx, router, D, k))) return rc;
+    if ((rc = check_experts(ctx, gate_up, down, D, d_expert, router->t.total_rows))) return rc;
+    if (d_expert % 64 || D % 128)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "prefill tiles need d_expert %% 64 == 0 and d_model %% 128 == 0");
+    if ((size_t)T * k > (1u << 20)) return fail(ctx, LT_ERR_UNSUPPORTED, "T*k > 2^20");
+    const int E = (int)router->t.total_rows, Kd = (int)down->t.cols;
+    const bool host = flags & LT_HOST_IO;
+    const float *dX = X, *dbias = router_bias;
+    float *dout = out;
+    uint32_t *dids = out_ids;
+    float *dw = out_w;
+    if (host) {
+        if ((rc = stage_in(ctx, ctx->x, X, (size_t)T * D * 4, (const void **)&dX))) return rc;
+        if ((rc = ensure(ctx, ctx->out, (size_t)T * D * 4))) return rc;
+        dout = (float *)ctx->out.p;
+        dids = nullptr;  // copied from the workspace below
+        dw = nullptr;
+    } else if (!aligned16(X)) {
+        return fail(ctx, LT_ERR_INVALID, "X must be 16-byte aligned");
+    }
+    if ((rc = stage_bias(ctx, router_bias, E, host, &dbias))) return rc;
+    const size_t wsb = lt::prefill_workspace_bytes((int)T, (int)k, E, Kd, (int)D);
+    if ((rc = ensure(ctx, ctx->pf, wsb))) return rc;
+    rc = launch_rc(ctx,
+                   lt::launch_moe_prefill(router->t, gate_up->t, down->t, dX, (int)T, dbias, (int)k, (int)d_expert,
+                                          act, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, ctx->pf.p, dout, dids, dw,
+                                          ctx->stream),
+                   "moe_prefill");
+    if (rc) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(out, dout, (size_t)T * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+        // ids and weights sit right after the logits in the workspace
+        const size_t logits_b = ((size_t)T * E * 4 + 255) & ~(size_t)255;
+        const size_t ids_b = ((size_t)T * k * 4 + 255) & ~(size_t)255;
+        const uint8_t *wsp = (const uint8_t *)ctx->pf.p;
+        if (out_ids)
+            LT_HIP(ctx, hipMemcpyAsync(out_ids, wsp + logits_b, (size_t)T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+        if (out_w)
+            LT_HIP(ctx, hipMemcpyAsync(out_w, wsp + logits_b + ids_b, (size_t)T * k * 4, hipMemcpyDeviceToHost,
+                                       ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
 }

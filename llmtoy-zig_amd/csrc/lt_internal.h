@@ -232,6 +232,16 @@ hipError_t launch_gate_up_q8_0(const DevTensor &Wg, const DevTensor &Wu, const f
 // caller, left at zero after every launch.  k = 0 computes logits only.
 hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, float *logits, unsigned *ticket,
                          uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s);
+// Router logits for T tokens (X [T][cols] -> logits [T][rows]) and per-token
+// softmax + top-k (ids, w: [T][k]).
+hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, const float *bias, float *logits,
+                                 uint32_t k, uint32_t norm, uint32_t *ids, float *w, hipStream_t s);
+// Batched prefill MoE (Q4_K experts), see lt_prefill.hip.  ws: workspace of
+// prefill_workspace_bytes(T, k, E, F, D) bytes.
+size_t prefill_workspace_bytes(int T, int k, int E, int F, int D);
+hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const DevTensor &Dn, const float *X, int T,
+                              const float *bias, int k, int F, uint32_t act, uint32_t norm, void *ws, float *out,
+                              uint32_t *out_ids, float *out_w, hipStream_t s);
 hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
                                      hipStream_t s);

@@ -171,6 +171,8 @@ __global__ void __launch_bounds__(64) k_router_f32(const float *__restrict__ W, 
                                                    int rows, int cols, TopkArgs ta) {
 #pragma clang fp contract(off)
     __shared__ float chain[2][32];
+    x += (size_t)blockIdx.y * cols;  // token blockIdx.y of a batch (decode: 0)
+    logits += (size_t)blockIdx.y * rows;
     const int rl = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int row = blockIdx.x * 2 + rl;
     const int nit = cols >> 5, n32 = nit << 5;
@@ -230,6 +232,8 @@ __global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ 
                                                      float *__restrict__ logits, int nb, int rows, TopkArgs ta) {
 #pragma clang fp contract(off)
     extern __shared__ float term[];
+    x += (size_t)blockIdx.y * nb * 32;  // token blockIdx.y of a batch (decode: 0)
+    logits += (size_t)blockIdx.y * rows;
     const int row = blockIdx.x;
     for (int b = threadIdx.x; b < nb; b += blockDim.x) {
         const int8_t *q = qs + ((size_t)row * nb + b) * 32;
@@ -273,6 +277,38 @@ hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, 
         hipLaunchKernelGGL(k_router_q8_0, dim3(rows), dim3(128), nb * sizeof(float), s, (const int8_t *)R.p0,
                            (const uint16_t *)R.p1, x, bias, logits, nb, rows, ta);
     }
+    return hipGetLastError();
+}
+
+// Softmax + top-k of token blockIdx.x of a batch of logits rows.
+template <int PER>
+__global__ void __launch_bounds__(64) k_topk_rows(const float *__restrict__ logits, int n, int k, int norm,
+                                                  uint32_t *__restrict__ ids, float *__restrict__ w) {
+    const size_t t = blockIdx.x;
+    topk_softmax_wave<PER>(logits + t * n, n, k, norm, ids + t * k, w + t * k, nullptr, threadIdx.x);
+}
+
+hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, const float *bias, float *logits,
+                                 uint32_t k, uint32_t norm, uint32_t *ids, float *w, hipStream_t s) {
+    const TopkArgs none{nullptr, 0, 0, nullptr, nullptr, nullptr};
+    const int rows = (int)R.total_rows;
+    if (R.type == 0)
+        hipLaunchKernelGGL(k_router_f32<64>, dim3((rows + 1) / 2, T), dim3(64), 0, s, (const float *)R.p0, X, bias,
+                           logits, rows, (int)R.cols, none);
+    else
+        hipLaunchKernelGGL(k_router_q8_0, dim3(rows, T), dim3(128), R.blocks_per_row * sizeof(float), s,
+                           (const int8_t *)R.p0, (const uint16_t *)R.p1, X, bias, logits, (int)R.blocks_per_row,
+                           rows, none);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (rows <= 64)
+        hipLaunchKernelGGL(k_topk_rows<1>, dim3(T), dim3(64), 0, s, logits, rows, (int)k, (int)norm, ids, w);
+    else if (rows <= 128)
+        hipLaunchKernelGGL(k_topk_rows<2>, dim3(T), dim3(64), 0, s, logits, rows, (int)k, (int)norm, ids, w);
+    else if (rows <= 256)
+        hipLaunchKernelGGL(k_topk_rows<4>, dim3(T), dim3(64), 0, s, logits, rows, (int)k, (int)norm, ids, w);
+    else
+        hipLaunchKernelGGL(k_topk_rows<16>, dim3(T), dim3(64), 0, s, logits, rows, (int)k, (int)norm, ids, w);
     return hipGetLastError();
 }
 

@@ -409,3 +409,63 @@ def test_gpu_errors(ctx):
                               np.zeros((2, 256), np.float32))
     for t in (router, gate_up, down):
         t.free()
+
+
+# ------------------------------------------------------------------ prefill (config 5)
+PREFILL_REL_L2 = 1e-2  # bf16 MFMA operands, fp32 accumulation
+
+
+def test_gpu_config5_prefill_512(ctx, cfg3, pool):
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    p = synth.config5(512, weights=w)
+    out = np.zeros((512, w.d_model), np.float32)
+    ids = np.zeros((512, 8), np.uint32)
+    wt = np.zeros((512, 8), np.float32)
+    ctx.moe_prefill(out, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"],
+                    out_ids=ids, out_w=wt)
+    ref, rids, rw = orc.moe_prefill(w, p["X"], 8, norm_topk=True, bias=p["bias"], pool=pool)
+    assert np.array_equal(ids, rids)
+    assert np.allclose(wt, rw, rtol=1e-5)
+    assert rel_l2(out, ref) <= PREFILL_REL_L2
+    # Zipf bias skews the load: the busiest expert gets far more than the mean
+    counts = np.bincount(ids.ravel(), minlength=w.n_experts)
+    assert counts.max() > 4 * counts.mean()
+
+
+def test_gpu_prefill_matches_decode_per_token(ctx, cfg3):
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    X = np.stack([synth.config3_x(200 + i) for i in range(7)])
+    out = np.zeros((7, w.d_model), np.float32)
+    ctx.moe_prefill(out, X, router, gate_up, down, 8, w.d_expert, norm_topk=True)
+    for t in range(7):
+        o = np.zeros(w.d_model, np.float32)
+        ctx.moe_forward(o, X[t], router, gate_up, down, 8, w.d_expert, norm_topk=True)
+        assert rel_l2(out[t], o) <= PREFILL_REL_L2
+
+
+def test_gpu_prefill_gelu_padded_k(ctx, pool):
+    # config-4 expert shapes (d_model 2816, d_expert 704 -> down K padded to 768)
+    w = synth.moe_weights(44, 2816, 16, 704, down_cols=768)
+    X = synth.normal(synth.stream(44, 9), (37, 2816))
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    out = np.zeros((37, 2816), np.float32)
+    ids = np.zeros((37, 4), np.uint32)
+    ctx.moe_prefill(out, X, router, gate_up, down, 4, 704, act=lt.ACT_GELU_TANH, out_ids=ids)
+    ref, rids, _ = orc.moe_prefill(w, X, 4, act=orc.ACT_GELU_TANH, pool=pool)
+    assert np.array_equal(ids, rids)
+    assert rel_l2(out, ref) <= PREFILL_REL_L2
+    for t in (router, gate_up, down):
+        t.free()
+
+
+def test_gpu_prefill_deterministic(ctx, cfg3):
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    p = synth.config5(64, weights=w)
+    a = np.zeros((64, w.d_model), np.float32)
+    b = np.zeros((64, w.d_model), np.float32)
+    ctx.moe_prefill(a, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"])
+    ctx.moe_prefill(b, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"])
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
