@@ -91,23 +91,100 @@ def cpu_baseline(w, xs, seconds: float, threads: int):
     return res
 
 
+PREFILL_FLOP = 512 * K * (2 * 2 * F * D + 2 * D * F)  # 38,654,705,664 (gate, up, down)
+
+
+def calibrate_copy(ctx, nbytes=256 << 20):
+    """A device-to-device copy of known size (the runtime's copy kernel), for
+    scaling the FETCH_SIZE / WRITE_SIZE counters in a rocprofv3 --pmc run."""
+    from llmtoy_amd.hip import D2D, DeviceArray, check, hip
+    a, b = DeviceArray((nbytes // 4,), "float32"), DeviceArray((nbytes // 4,), "float32")
+    for _ in range(3):
+        check(hip().hipMemcpy(b.ptr, a.ptr, nbytes, D2D), "hipMemcpy D2D")
+    a.free()
+    b.free()
+    log(f"calibration: 3 x {nbytes >> 20} MiB device copies")
+
+
+def bench_prefill(args):
+    """Config-5 batched prefill (512 tokens): extra workload for the MFMA path."""
+    import numpy as np
+
+    import llmtoy_amd as lt
+    import pyoracle as orc
+    from llmtoy_amd import synth
+    from llmtoy_amd.hip import DeviceArray, Event, sync_stream
+
+    c = synth.config3()
+    w = c["weights"]
+    p = synth.config5(512, weights=w)
+    ctx = lt.Context(0)
+    base = lt.upload_moe(ctx, w)
+    copies = [base] + [tuple(t.clone() for t in base) for _ in range(max(1, args.copies // 2) - 1)]
+    out_h = np.zeros((512, D), np.float32)
+    ctx.moe_prefill(out_h, p["X"], *base, K, F, norm_topk=True, bias=p["bias"])
+    with orc.Pool(min(16, os.cpu_count() or 1)) as pool:
+        ref, _, _ = orc.moe_prefill(w, p["X"], K, norm_topk=True, bias=p["bias"], pool=pool)
+    parity = {"rel_l2": float(np.linalg.norm(out_h - ref) / np.linalg.norm(ref))}
+    X = DeviceArray.from_numpy(p["X"])
+    B = DeviceArray.from_numpy(p["bias"])
+    out = DeviceArray((512, D), np.float32)
+    stream = ctx.stream
+
+    def call(i):
+        ctx.moe_prefill(out, X, *copies[i % len(copies)], K, F, norm_topk=True, bias=B)
+
+    for i in range(args.warmup):
+        call(i)
+    sync_stream(stream)
+    e0, e1 = Event(), Event()
+    t = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        call(i)
+    e1.record(stream)
+    sync_stream(stream)
+    wall = time.perf_counter() - t
+    us = wall / args.steps * 1e6
+    result = {"metric": "MoE-layer batched prefill tokens/s (config 5, 512 tokens)", "value": round(512 / (us * 1e-6)),
+              "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "ms_per_step": round(us / 1e3, 4), "higher_is_better": True, "dtype": "bf16 MFMA, fp32 accumulation",
+              "data": "synthetic", "config": {"workload": "qwen3_moe_prefill_cfg5", "tokens": 512, "d_model": D,
+                                              "n_experts": E, "d_expert": F, "top_k": K, "router_bias": "zipf(1.1)"},
+              "us_per_call": round(us, 2), "device_us_per_call": round(e0.elapsed_ms(e1) * 1e3 / args.steps, 2),
+              "achieved_tflops": round(PREFILL_FLOP / (us * 1e-6) / 1e12, 2), "parity": parity}
+    if args.calibrate:
+        calibrate_copy(ctx)
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4096)
-    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--xpool", type=int, default=64)
     ap.add_argument("--kernel-iters", type=int, default=512)
     ap.add_argument("--cpu-threads", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding of this path is described in DESIGN.md and not run", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "prefill":
+        args.steps = args.steps or 50
+        args.warmup = args.warmup if args.warmup is not None else 5
+        bench_prefill(args)
+        return
+    args.steps = args.steps or 4096
+    args.warmup = args.warmup if args.warmup is not None else 256
 
     import numpy as np
 
@@ -273,6 +350,8 @@ def main():
                       f"quantMatvecPar + moeForward, --threads {threads}",
             "value_1_thread": round(res[1][0], 1), "nproc": os.cpu_count(), "cpu_model": cpu_model}
 
+    if args.calibrate:
+        calibrate_copy(ctx)
     print(json.dumps(result), flush=True)
     graph.destroy()
     if graph_rem:

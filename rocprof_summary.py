@@ -1,0 +1,124 @@
+#!/usr/bin/env python3
+"""Summarise rocprofv3 result databases (rocpd SQLite) into profiles/.
+
+  trace <db> <out.md> "<command>"
+      per-kernel dispatch count and duration statistics (kernel trace).
+  traffic <fetch_db> <write_db> <kernel-substring> <out.json> "<fetch cmd>" "<write cmd>"
+      mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the kernel, and the
+      same counters on the 256 MiB device copies bench.py --calibrate runs,
+      giving the scale factors bench.py applies (counter KiB / true KiB).
+  mfma <db> <out.md> "<command>"
+      MFMA busy % per kernel: SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs).
+"""
+import json
+import sqlite3
+import statistics
+import sys
+
+CALIB_BYTES = 256 << 20
+SIMDS = 256 * 4  # MI355X: 256 CUs x 4 SIMDs
+
+
+def kernel_rows(db):
+    con = sqlite3.connect(db)
+    return con.execute("select name, duration from kernels").fetchall()
+
+
+def short(name):
+    return name.split("(")[0].replace("void ", "")
+
+
+def trace(db, out, cmd):
+    by = {}
+    for name, dur in kernel_rows(db):
+        by.setdefault(short(name), []).append(dur / 1000.0)
+    lines = [f"# Kernel trace: {out.split('/')[-1].rsplit('.', 1)[0]}", "", "Command (GPU box, repo root):", "",
+             "```", cmd, "```", "",
+             "| kernel | dispatches | mean us | median us | min us | max us | total ms |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    stats = {}
+    for k, v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{k}` | {len(v)} | {statistics.mean(v):.3f} | {statistics.median(v):.3f} | {min(v):.3f} | "
+                     f"{max(v):.3f} | {sum(v) / 1000:.3f} |")
+        stats[k] = {"dispatches": len(v), "mean_us": statistics.mean(v), "median_us": statistics.median(v)}
+    open(out, "w").write("\n".join(lines) + "\n")
+    return stats
+
+
+def pmc_values(db, counter):
+    con = sqlite3.connect(db)
+    rows = con.execute("select kernel_name, grid_size, value from counters_collection where counter_name = ?",
+                       (counter,)).fetchall()
+    return rows
+
+
+def traffic(fetch_db, write_db, kernel, out, fetch_cmd, write_cmd):
+    res = {"dominant": kernel, "kernels": {}, "copy_calibration": {}, "commands": [fetch_cmd, write_cmd]}
+    for db, counter in ((fetch_db, "FETCH_SIZE"), (write_db, "WRITE_SIZE")):
+        rows = pmc_values(db, counter)
+        by = {}
+        for name, grid, val in rows:
+            by.setdefault(short(name), []).append(val)
+        for k, v in by.items():
+            res["kernels"].setdefault(k, {})[f"{counter}_kib"] = statistics.mean(v)
+            res["kernels"][k]["dispatches"] = len(v)
+        # calibration: the largest copyBuffer dispatches are the 256 MiB copies
+        copies = sorted((val for name, grid, val in rows if "copyBuffer" in name), reverse=True)[:3]
+        factor = statistics.mean(copies) / (CALIB_BYTES / 1024.0) if copies else None
+        res["copy_calibration"]["fetch_factor" if counter == "FETCH_SIZE" else "write_factor"] = factor
+        res["copy_calibration"][f"{counter}_kib_per_256MiB_copy"] = copies
+    match = [k for k in res["kernels"] if kernel in k]
+    if match:
+        res["dominant"] = match[0]
+    json.dump(res, open(out, "w"), indent=1)
+    md = out.rsplit(".", 1)[0] + ".md"
+    d = res["kernels"].get(res["dominant"], {})
+    cal = res["copy_calibration"]
+    f_kib, w_kib = d.get("FETCH_SIZE_kib"), d.get("WRITE_SIZE_kib")
+    lines = [f"# HBM traffic: {res['dominant']}", "", "Commands (GPU box, repo root):", "", "```", fetch_cmd,
+             write_cmd, "```", "",
+             f"- FETCH_SIZE per dispatch: {f_kib:.1f} KiB (mean of {d.get('dispatches')} dispatches)" if f_kib else
+             "- FETCH_SIZE: n/a",
+             f"- WRITE_SIZE per dispatch: {w_kib:.1f} KiB" if w_kib else "- WRITE_SIZE: n/a",
+             f"- copy calibration (256 MiB device copy): FETCH factor {cal.get('fetch_factor')}, "
+             f"WRITE factor {cal.get('write_factor')}",
+             ]
+    if f_kib and w_kib and cal.get("fetch_factor") and cal.get("write_factor"):
+        tb = (f_kib / cal["fetch_factor"] + w_kib / cal["write_factor"]) * 1024
+        lines.append(f"- HBM bytes per dispatch (scaled): {tb:,.0f} B")
+        res["hbm_bytes_per_dispatch"] = tb
+        json.dump(res, open(out, "w"), indent=1)
+    lines += ["", "| kernel | FETCH KiB/dispatch | WRITE KiB/dispatch |", "|---|---:|---:|"]
+    for k, v in res["kernels"].items():
+        lines.append(f"| `{k}` | {v.get('FETCH_SIZE_kib', float('nan')):.1f} | {v.get('WRITE_SIZE_kib', float('nan')):.1f} |")
+    open(md, "w").write("\n".join(lines) + "\n")
+
+
+def mfma(db, out, cmd):
+    con = sqlite3.connect(db)
+    rows = con.execute("select dispatch_id, kernel_name, counter_name, value from counters_collection").fetchall()
+    per = {}
+    for did, name, cname, val in rows:
+        per.setdefault((did, short(name)), {})[cname] = val
+    by = {}
+    for (did, name), c in per.items():
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in c and c.get("GRBM_GUI_ACTIVE"):
+            by.setdefault(name, []).append(100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * SIMDS))
+    lines = ["# MFMA busy: batched prefill (config 5)", "", "Command (GPU box, repo root):", "", "```", cmd, "```", "",
+             "MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) x 100, per dispatch.", "",
+             "| kernel | dispatches | mean MFMA busy % |", "|---|---:|---:|"]
+    for k, v in sorted(by.items()):
+        lines.append(f"| `{k}` | {len(v)} | {statistics.mean(v):.2f} |")
+    open(out, "w").write("\n".join(lines) + "\n")
+
+
+if __name__ == "__main__":
+    mode = sys.argv[1]
+    if mode == "trace":
+        trace(*sys.argv[2:5])
+    elif mode == "traffic":
+        traffic(*sys.argv[2:8])
+    elif mode == "mfma":
+        mfma(*sys.argv[2:5])
+    else:
+        sys.exit(__doc__)
