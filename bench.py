@@ -236,6 +236,19 @@ def main():
     eager_us = (time.perf_counter() - t) / n_eager * 1e6
     log(f"eager: {eager_us:.2f} us/token")
 
+    # host buffers in and out (LT_HOST_IO: H2D of x, D2H of out, synchronous) -- PCIe-inclusive
+    host_out = np.zeros(D, np.float32)
+    for i in range(16):
+        r, g, d = copies[i % args.copies]
+        ctx.moe_forward(host_out, xs[i % args.xpool], r, g, d, K, F, norm_topk=True)
+    n_host = 256
+    t = time.perf_counter()
+    for i in range(n_host):
+        r, g, d = copies[i % args.copies]
+        ctx.moe_forward(host_out, xs[i % args.xpool], r, g, d, K, F, norm_topk=True)
+    host_io_us = (time.perf_counter() - t) / n_host * 1e6
+    log(f"host-buffer (PCIe-inclusive) calls: {host_io_us:.2f} us/token")
+
     # ---- graph replay: one graph holds G consecutive steps (copy and x cycle with period G)
     G = int(np.lcm(args.copies, args.xpool))
     while G < 64:
@@ -327,6 +340,7 @@ def main():
         "achieved_gbps_full_layer": round(LAYER_BYTES / (us_per_token * 1e-6) / 1e9, 1),
         "device_us_per_token": round(dev_ms * 1e3 / args.steps, 3),
         "eager_us_per_token": round(eager_us, 3),
+        "host_io_us_per_token": round(host_io_us, 3),
         "kernel_us": {"router_topk": round(rt_mean, 3), "expert_gate_up": round(gu_mean, 3),
                       "expert_down": round(dn_mean, 3)},
         "kernel_gbps": {"expert_gate_up": round(gu_gbps, 1),

@@ -51,6 +51,25 @@ def test_force_no_device_reports_device_error():
     assert "DEVICE 3" in out.stdout, out.stdout + out.stderr
 
 
+CPP_TEST = os.path.join(ROOT, "tests", "cpp", "build", "test_host_ops")
+
+
+def test_cpp_host_layer_builds_and_lists_tests():
+    # the C++ mirror of the reference op API (llmtoy-zig_amd/host/llmtoy_ops.hpp)
+    out = subprocess.run([CPP_TEST, "--list"], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0
+    names = out.stdout.splitlines()
+    assert "gpu matvec Q4_K scale" in names and len(names) == 10
+
+
+@pytest.mark.gpu
+def test_gpu_cpp_host_layer_parity():
+    print("running tests/cpp/build/test_host_ops", flush=True)
+    out = subprocess.run([CPP_TEST], capture_output=True, text=True, timeout=120)
+    print(out.stdout[-3000:])
+    assert out.returncode == 0 and "ALL PASSED" in out.stdout, out.stdout + out.stderr
+
+
 def test_null_arguments_are_invalid_without_touching_a_device():
     L = lt.load_library()
     assert L.lt_init(0, None) == ltlib.LT_ERR_INVALID
