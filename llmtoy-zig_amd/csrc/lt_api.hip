@@ -420,6 +420,7 @@ namespace {
 
 constexpr uint32_t kMaxK = 16;
 constexpr size_t kMaxExperts = 1024;
+constexpr size_t kRoutedGateUpMaxExperts = 256;  // top-k inside the gate/up blocks up to here
 
 int check_router(lt_ctx *ctx, const lt_tensor *router, size_t d_model, uint32_t k) {
     if (!router) return fail(ctx, LT_ERR_INVALID, "null router");
@@ -594,14 +595,25 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
         if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p))) return rc;
         base = (const float *)ctx->shared.p;
     }
-    if ((rc = router_dev(ctx, R, x, bias, k, flags))) return rc;
     const size_t Kd = D.cols;
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
-    rc = launch_rc(ctx,
-                   lt::launch_expert_gate_up_q4k(GU, x, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act,
-                                                 h, ctx->stream),
-                   "expert_gate_up");
+    if (R.total_rows <= kRoutedGateUpMaxExperts) {
+        // logits only; each gate/up block selects its expert from them
+        if ((rc = router_dev(ctx, R, x, bias, 0, flags))) return rc;
+        rc = launch_rc(ctx,
+                       lt::launch_expert_gate_up_q4k_routed(GU, x, (const float *)ctx->logits.p, k,
+                                                            (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, d_expert,
+                                                            (uint32_t)Kd, act, h, (uint32_t *)ctx->ids.p,
+                                                            (float *)ctx->w.p, ctx->stream),
+                       "expert_gate_up_routed");
+    } else {
+        if ((rc = router_dev(ctx, R, x, bias, k, flags))) return rc;
+        rc = launch_rc(ctx,
+                       lt::launch_expert_gate_up_q4k(GU, x, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd,
+                                                     act, h, ctx->stream),
+                       "expert_gate_up");
+    }
     if (rc) return rc;
     return launch_rc(ctx,
                      lt::launch_expert_down_q4k(D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k, base,

@@ -245,6 +245,12 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
 hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
                                      hipStream_t s);
+// Gate/up that routes for itself: every block runs softmax + top-k over the
+// router logits (n_experts <= 256) and block (0, 0) writes the selection to
+// ids_out / w_out for the down kernel.
+hipError_t launch_expert_gate_up_q4k_routed(const DevTensor &GU, const float *x, const float *logits, uint32_t k,
+                                            uint32_t norm, uint32_t d_expert, uint32_t down_cols, uint32_t act,
+                                            float *h, uint32_t *ids_out, float *w_out, hipStream_t s);
 hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
                                   uint32_t k, const float *base, int accumulate, float *out, hipStream_t s);
 }  // namespace lt

@@ -19,6 +19,7 @@
 // sum reassociated (fp32 accumulation, checked to 1e-3 rel-L2 against the
 // oracle's element-wise dequant then dotf32).
 #include "lt_internal.h"
+#include "lt_topk.h"
 
 namespace lt {
 
@@ -192,35 +193,60 @@ hipError_t launch_matvec_q4k(const DevTensor &W, size_t row0, size_t nrows, cons
 // (ops/moe.zig:55-73).  h[s][j] = act(gate_j . x) * (up_j . x) for j < F;
 // h[s][F..down_cols) = 0 (zero K padding of the down product).
 // One wavefront (64 lanes) per row pair, CPL chunks per lane, R row pairs per
-// wave, 4 waves per block.  Every weight load of the wave is issued before
-// any arithmetic (one HBM round trip per wave); x comes from L2 straight
-// into registers.
-template <int CPL, int R>
+// wave, WPB waves per block.  Every weight load of the wave is issued before
+// any arithmetic; x comes from L2 straight into registers first.
+// ROUTE = 0: ids come from the caller.  ROUTE = PER > 0: each block routes
+// for itself -- wave 0 runs softmax + top-k over the router logits
+// (PER logits per lane) while the other waves load x; block (0, 0) also
+// publishes the selection (ids, weights) for the down kernel.
+struct RouteArgs {
+    const float *logits;  // [n_experts]
+    int k;
+    int norm;
+    uint32_t *ids_out;    // [k]
+    float *w_out;         // [k]
+};
+
+template <int CPL, int R, int WPB, int ROUTE>
 __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__restrict__ hdr,
                                                             const uint8_t *__restrict__ qs,
                                                             const float *__restrict__ x,
                                                             const uint32_t *__restrict__ ids, int n_experts,
                                                             int nsb, int F, int down_cols, uint32_t act,
-                                                            float *__restrict__ h) {
+                                                            float *__restrict__ h, RouteArgs ra) {
     const int s = blockIdx.y;
-    const uint32_t e = __builtin_amdgcn_readfirstlane(ids[s]);
-    float *hs = h + (size_t)s * down_cols;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int jbase = (blockIdx.x * 4 + wave) * R;
+    const int jbase = (blockIdx.x * WPB + wave) * R;
+    const int nch = nsb * 8;
+    // x first (L2-resident), so its latency overlaps the routing below
+    XChunk xc[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; i++)
+        if (lane + kWave * i < nch) load_xchunk(x, (lane + kWave * i) >> 3, (lane + kWave * i) & 7, xc[i]);
+    uint32_t e;
+    if constexpr (ROUTE > 0) {
+        __shared__ uint32_t s_ids[16];
+        __shared__ float s_w[16];
+        if (wave == 0) topk_softmax_wave<ROUTE>(ra.logits, n_experts, ra.k, ra.norm, s_ids, s_w, nullptr, lane);
+        __syncthreads();
+        if (blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < ra.k) {
+            ra.ids_out[threadIdx.x] = s_ids[threadIdx.x];
+            ra.w_out[threadIdx.x] = s_w[threadIdx.x];
+        }
+        e = __builtin_amdgcn_readfirstlane(s_ids[s]);
+    } else {
+        e = __builtin_amdgcn_readfirstlane(ids[s]);
+    }
+    float *hs = h + (size_t)s * down_cols;
     if (blockIdx.x == 0)
         for (int j = F + threadIdx.x; j < down_cols; j += blockDim.x) hs[j] = 0.f;
     if (e >= (uint32_t)n_experts) {  // invalid id from the caller: the slot contributes zeros
         if (lane < R && jbase + lane < F) hs[jbase + lane] = 0.f;
         return;
     }
-    const int nch = nsb * 8;
     const size_t gate0 = (size_t)e * 2 * F, up0 = gate0 + F;
-    // x first (L2-resident), then the weights row by row, so that rows can
-    // be consumed as their loads land (vmcnt retires in issue order).
-    XChunk xc[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; i++)
-        if (lane + kWave * i < nch) load_xchunk(x, (lane + kWave * i) >> 3, (lane + kWave * i) & 7, xc[i]);
+    // weights row by row, so that rows can be consumed as their loads land
+    // (vmcnt retires in issue order)
     uint4 hg[R][CPL], qg[R][CPL], hu[R][CPL], qu[R][CPL];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -269,27 +295,54 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
     if (lane < 32 && (lane & ((1 << SH) - 1)) == 0 && jbase + r < F) hs[jbase + r] = act_apply(act, t) * u;
 }
 
-template <int CPL, int R>
+template <int CPL, int R, int ROUTE>
 static hipError_t launch_gu_t(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k, uint32_t F,
-                              uint32_t down_cols, uint32_t act, float *h, hipStream_t s) {
+                              uint32_t down_cols, uint32_t act, float *h, const RouteArgs &ra, hipStream_t s) {
     const int nsb = (int)GU.blocks_per_row;
-    dim3 grid((F + 4 * R - 1) / (4 * R), k);
-    hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R>), grid, dim3(256), 0, s, GU.p0, GU.p1, x, ids,
-                       (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h);
+    // 3 waves per block when that splits the rows evenly (F = 768: 512 blocks,
+    // exactly two per CU), else 4
+    if (F % (3 * R) == 0) {
+        dim3 grid(F / (3 * R), k);
+        hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R, 3, ROUTE>), grid, dim3(192), 0, s, GU.p0, GU.p1, x, ids,
+                           (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h, ra);
+    } else {
+        dim3 grid((F + 4 * R - 1) / (4 * R), k);
+        hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R, 4, ROUTE>), grid, dim3(256), 0, s, GU.p0, GU.p1, x, ids,
+                           (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h, ra);
+    }
     return hipGetLastError();
+}
+
+template <int ROUTE>
+static hipError_t launch_gu_route(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
+                                  uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, const RouteArgs &ra,
+                                  hipStream_t s) {
+    const int nch = (int)GU.blocks_per_row * 8;
+    switch ((nch + 63) / 64) {
+    case 1: return launch_gu_t<1, 4, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    case 2: return launch_gu_t<2, 2, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    case 3: return launch_gu_t<3, 2, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    case 4: return launch_gu_t<4, 1, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    default: return hipErrorInvalidValue;  // d_model > 8192: rejected by the API layer
+    }
 }
 
 hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
                                      hipStream_t s) {
-    const int nch = (int)GU.blocks_per_row * 8;
-    switch ((nch + 63) / 64) {
-    case 1: return launch_gu_t<1, 4>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    case 2: return launch_gu_t<2, 2>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    case 3: return launch_gu_t<3, 2>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    case 4: return launch_gu_t<4, 1>(GU, x, ids, k, d_expert, down_cols, act, h, s);
-    default: return hipErrorInvalidValue;  // d_model > 8192: rejected by the API layer
-    }
+    const RouteArgs none{nullptr, 0, 0, nullptr, nullptr};
+    return launch_gu_route<0>(GU, x, ids, k, d_expert, down_cols, act, h, none, s);
+}
+
+hipError_t launch_expert_gate_up_q4k_routed(const DevTensor &GU, const float *x, const float *logits, uint32_t k,
+                                            uint32_t norm, uint32_t d_expert, uint32_t down_cols, uint32_t act,
+                                            float *h, uint32_t *ids_out, float *w_out, hipStream_t s) {
+    const RouteArgs ra{logits, (int)k, (int)norm, ids_out, w_out};
+    const int E = (int)GU.n_experts;
+    if (E <= 64) return launch_gu_route<1>(GU, x, nullptr, k, d_expert, down_cols, act, h, ra, s);
+    if (E <= 128) return launch_gu_route<2>(GU, x, nullptr, k, d_expert, down_cols, act, h, ra, s);
+    if (E <= 256) return launch_gu_route<4>(GU, x, nullptr, k, d_expert, down_cols, act, h, ra, s);
+    return hipErrorInvalidValue;  // more experts: the caller uses the router's top-k
 }
 
 // ------------------------------------------------------------------------

@@ -14,120 +14,13 @@
 // The block that finishes last (atomic ticket) runs softmax + top-k over all
 // logits in one wavefront, so routing costs one launch.
 #include "lt_internal.h"
+#include "lt_topk.h"
 
 #include <math.h>
 
 namespace lt {
 
 namespace {
-
-// true if (va, ia) ranks before (vb, ib): larger value, then lower index --
-// the strict '>' rule of every reference top-k (ops/moe.zig:87,
-// gemma4/forward.zig:612-625).
-__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-    return va > vb || (!(va < vb) && ia < ib);
-}
-
-// Softmax + top-k over n <= 64*PER logits, executed by one full wavefront
-// (lane = 0..63; lane owns entries lane + 64*j).  NaN logits rank last.
-// Each of the k rounds takes the lane-local best unselected entry and runs
-// a wave-wide argmax with DPP row rotations and the two half-swaps.
-// w[r] = exp(l - max) / sum_j exp(l_j - max); with norm, divided by the sum
-// of the selected weights taken in selection order.  scores (optional):
-// logits, with the selected entries replaced by their probabilities
-// (routerTopKSoftmax's buffer, gemma4/forward.zig:645-668).
-__device__ __forceinline__ void argmax_merge(float &bv, int &bi, float ov, int oi) {
-    if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-    }
-}
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
-}
-
-template <int PER>
-__device__ void topk_softmax_wave(const float *logits, int n, int k, int norm, uint32_t *ids, float *w,
-                                  float *scores, int lane) {
-    const bool first = p32_first(lane);
-    float v[PER];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int idx = lane + 64 * j;
-        float t = idx < n ? logits[idx] : -INFINITY;
-        if (t != t) t = -INFINITY;
-        v[j] = t;
-        m = fmaxf(m, t);
-    }
-    m = fmaxf(m, dpp<0x128>(m));
-    m = fmaxf(m, dpp<0x124>(m));
-    m = fmaxf(m, dpp<0x122>(m));
-    m = fmaxf(m, dpp<0x121>(m));
-    m = fmaxf(m, xor16(m));
-    m = fmaxf(m, xor32(m, first));
-    float se = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PER; j++)
-        if (lane + 64 * j < n) se += expf(v[j] - m);
-    se += dpp<0x128>(se);
-    se += dpp<0x124>(se);
-    se += dpp<0x122>(se);
-    se += dpp<0x121>(se);
-    se += xor16(se);
-    se += xor32(se, first);
-
-    unsigned taken = 0;
-    float my_v = -INFINITY;
-    int my_i = 0;
-    for (int r = 0; r < k; r++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int idx = lane + 64 * j;
-            if (idx < n && !((taken >> j) & 1u) && better(v[j], idx, bv, bi)) {
-                bv = v[j];
-                bi = idx;
-            }
-        }
-        argmax_merge(bv, bi, dpp<0x128>(bv), dpp_i<0x128>(bi));
-        argmax_merge(bv, bi, dpp<0x124>(bv), dpp_i<0x124>(bi));
-        argmax_merge(bv, bi, dpp<0x122>(bv), dpp_i<0x122>(bi));
-        argmax_merge(bv, bi, dpp<0x121>(bv), dpp_i<0x121>(bi));
-        argmax_merge(bv, bi, xor16(bv), __float_as_int(xor16(__int_as_float(bi))));
-        argmax_merge(bv, bi, xor32(bv, first), __float_as_int(xor32(__int_as_float(bi), first)));
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == r) {
-            my_v = bv;
-            my_i = bi;
-        }
-    }
-    const float my_p = lane < k ? expf(my_v - m) / se : 0.0f;
-    float ps = 0.0f;  // sum of the selected weights in selection order
-    if (norm)
-        for (int r = 0; r < k; r++) ps = ps + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), r));
-    if (lane < k) {
-        ids[lane] = (uint32_t)my_i;
-        w[lane] = norm ? my_p / ps : my_p;
-    }
-    if (scores) {
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int idx = lane + 64 * j;
-            if (idx < n) {
-                float val = logits[idx];
-                if ((taken >> j) & 1u)
-                    for (int r = 0; r < k; r++)
-                        if (__builtin_amdgcn_readlane(my_i, r) == idx)
-                            val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), r));
-                scores[idx] = val;
-            }
-        }
-    }
-}
 
 struct TopkArgs {
     unsigned *ticket;  // zero-initialised; wraps back to 0 after each launch
