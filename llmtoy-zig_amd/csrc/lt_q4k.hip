@@ -298,30 +298,25 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
 template <int CPL, int R, int ROUTE>
 static hipError_t launch_gu_t(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k, uint32_t F,
                               uint32_t down_cols, uint32_t act, float *h, const RouteArgs &ra, hipStream_t s) {
-    const int nsb = (int)GU.blocks_per_row;
-    // 3 waves per block when that splits the rows evenly (F = 768: 512 blocks,
-    // exactly two per CU), else 4
-    if (F % (3 * R) == 0) {
-        dim3 grid(F / (3 * R), k);
-        hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R, 3, ROUTE>), grid, dim3(192), 0, s, GU.p0, GU.p1, x, ids,
-                           (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h, ra);
-    } else {
-        dim3 grid((F + 4 * R - 1) / (4 * R), k);
-        hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R, 4, ROUTE>), grid, dim3(256), 0, s, GU.p0, GU.p1, x, ids,
-                           (int)GU.n_experts, nsb, (int)F, (int)down_cols, act, h, ra);
-    }
+    constexpr int WPB = 4;
+    dim3 grid((F + WPB * R - 1) / (WPB * R), k);
+    hipLaunchKernelGGL((k_expert_gate_up_q4k<CPL, R, WPB, ROUTE>), grid, dim3(64 * WPB), 0, s, GU.p0, GU.p1, x, ids,
+                       (int)GU.n_experts, (int)GU.blocks_per_row, (int)F, (int)down_cols, act, h, ra);
     return hipGetLastError();
 }
 
+// At most 4 chunk dots per lane (CPL x R row pairs): more, shorter waves
+// keep more loads in flight per CU than fewer, longer ones (config 3:
+// R = 2 takes 5.8 us against 7.0 us for R = 4).
 template <int ROUTE>
 static hipError_t launch_gu_route(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                   uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, const RouteArgs &ra,
                                   hipStream_t s) {
     const int nch = (int)GU.blocks_per_row * 8;
     switch ((nch + 63) / 64) {
-    case 1: return launch_gu_t<1, 4, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
-    case 2: return launch_gu_t<2, 2, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
-    case 3: return launch_gu_t<3, 2, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    case 1: return launch_gu_t<1, 2, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    case 2: return launch_gu_t<2, 1, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
+    case 3: return launch_gu_t<3, 1, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
     case 4: return launch_gu_t<4, 1, ROUTE>(GU, x, ids, k, d_expert, down_cols, act, h, ra, s);
     default: return hipErrorInvalidValue;  // d_model > 8192: rejected by the API layer
     }
@@ -393,9 +388,10 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
 #pragma unroll
             for (int r = 0; r < RD; r++)
                 v[r] = (valid && row0 + r < rows_per_expert) ? q4k_chunk_dot(hv[r], qv[r], cc, xc) : 0.f;
-            // lane (slot, cc) receives the 8-lane total of row cc
+            // lane (slot, cc) receives the 8-lane total of row cc * RD / 8
             const float t = group8_sum_transposed<RD>(v, lane);
-            if (active) part[cc][s][sb] = t;
+            constexpr int SPLIT = 8 / RD;  // lanes per row after the reduction
+            if (active && cc % SPLIT == 0) part[cc / SPLIT][s][sb] = t;
         }
     }
     __syncthreads();
@@ -417,7 +413,7 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
 
 hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
                                   uint32_t k, const float *base, int accumulate, float *out, hipStream_t s) {
-    constexpr int RD = 8;
+    constexpr int RD = 2;  // 2 rows per block: 7.5 -> 6.5 us against 8 rows (config 3)
     const int nsb = (int)D.blocks_per_row;  // <= 16, k <= 16: checked by the API layer
     const int nw = nsb < 4 ? nsb : 4;
     const int rows = (int)D.rows;
