@@ -50,7 +50,9 @@ enum { LT_ACT_SILU = 0, LT_ACT_GELU_TANH = 1 };
 enum {
     LT_HOST_IO = 1u << 0,       /* pointers are host memory; the call is synchronous */
     LT_MOE_NORM_TOPK = 1u << 1, /* renormalise the k selected weights to sum to 1 */
-    LT_MOE_ACCUMULATE = 1u << 2 /* out += result (moeForward's contract, ops/moe.zig:17) */
+    LT_MOE_ACCUMULATE = 1u << 2, /* out += result (moeForward's contract, ops/moe.zig:17) */
+    LT_MOE_UNFUSED = 1u << 3     /* lt_moe_forward: run router, gate/up and down as separate launches
+                                    instead of the single-launch kernel (same results to tolerance) */
 };
 
 typedef struct lt_ctx lt_ctx;

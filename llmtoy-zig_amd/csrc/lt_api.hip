@@ -36,6 +36,11 @@ struct lt_ctx {
     // arrival ticket of the router's last-block top-k; zeroed once at init,
     // every launch leaves it at zero again
     unsigned *ticket = nullptr;
+    // hand-over memory of the fused MoE kernel (allocated on first use) and
+    // its host-mapped error word
+    void *fused = nullptr;
+    uint32_t *fused_err = nullptr;
+    lt::FusedScratch fsc{};
 };
 
 namespace {
@@ -173,6 +178,49 @@ int launch_rc(lt_ctx *ctx, hipError_t e, const char *what) {
     return fail(ctx, LT_ERR_DEVICE, "%s launch failed: %s", what, hipGetErrorString(e));
 }
 
+// Allocates and zeroes the fused kernel's hand-over memory (once).
+int ensure_fused(lt_ctx *ctx) {
+    if (ctx->fused) return LT_OK;
+    const size_t n_cnt = (size_t)lt::kFusedBlocks * 4;
+    const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128;
+    const size_t n_hl = (size_t)lt::kFusedBlocks * 128 * lt::kFusedRecCopies;
+    const size_t n_hc = 2 * 16 * 128;
+    const size_t bytes = n_cnt + n_lg + n_hl + n_hc;
+    void *p = nullptr;
+    LT_HIP(ctx, hipMalloc(&p, bytes));
+    hipError_t e = hipMemset(p, 0, bytes);
+    void *hp = nullptr;
+    if (e == hipSuccess) e = hipHostMalloc(&hp, 64, hipHostMallocMapped);
+    void *dp = nullptr;
+    if (e == hipSuccess) {
+        memset(hp, 0, 64);
+        e = hipHostGetDevicePointer(&dp, hp, 0);
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        if (hp) (void)hipHostFree(hp);
+        return hip_fail(ctx, e, "fused scratch");
+    }
+    uint8_t *b = (uint8_t *)p;
+    ctx->fused = p;
+    ctx->fused_err = (uint32_t *)hp;
+    ctx->fsc.counters = (uint32_t *)b;
+    ctx->fsc.lg = (uint64_t *)(b + n_cnt);
+    ctx->fsc.hl = (uint64_t *)(b + n_cnt + n_lg);
+    ctx->fsc.hcnt = (uint32_t *)(b + n_cnt + n_lg + n_hl);
+    ctx->fsc.err = (uint32_t *)dp;
+    return LT_OK;
+}
+
+// A fused-kernel wait that ran into its time limit (the outputs of that
+// call are NaN); reported, and cleared, by the next synchronising call.
+int check_fused_err(lt_ctx *ctx) {
+    if (!ctx->fused_err) return LT_OK;
+    const uint32_t v = __atomic_exchange_n(ctx->fused_err, 0u, __ATOMIC_SEQ_CST);
+    if (v) return fail(ctx, LT_ERR_DEVICE, "fused MoE kernel: a hand-over wait timed out (code %u)", v);
+    return LT_OK;
+}
+
 int matvec_dev(lt_ctx *ctx, const DevTensor &W, const float *x, float *y) {
     hipError_t e;
     switch (W.type) {
@@ -231,6 +279,8 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (ctx->ticket) (void)hipFree(ctx->ticket);
+    if (ctx->fused) (void)hipFree(ctx->fused);
+    if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -240,7 +290,7 @@ extern "C" const char *lt_last_error(const lt_ctx *ctx) { return ctx ? ctx->err.
 extern "C" int lt_sync(lt_ctx *ctx) {
     if (!ctx) return LT_ERR_INVALID;
     LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return LT_OK;
+    return check_fused_err(ctx);
 }
 
 extern "C" void *lt_stream(lt_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
@@ -596,6 +646,20 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
         base = (const float *)ctx->shared.p;
     }
     const size_t Kd = D.cols;
+    if (!(flags & LT_MOE_UNFUSED) && R.type == LT_TYPE_F32) {
+        const lt::FusedPlan pl = lt::plan_moe_fused((int)R.total_rows, (int)GU.cols, (int)d_expert, (int)Kd, (int)k);
+        if (pl.ok) {
+            if ((rc = ensure_fused(ctx)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
+                (rc = ensure(ctx, ctx->w, kMaxK * 4)))
+                return rc;
+            return launch_rc(ctx,
+                             lt::launch_moe_fused(pl, R, bias, GU, D, x, (int)k, (int)d_expert, act,
+                                                  (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, base,
+                                                  (flags & LT_MOE_ACCUMULATE) ? 1 : 0, out, (uint32_t *)ctx->ids.p,
+                                                  (float *)ctx->w.p, ctx->fsc, ctx->stream),
+                             "moe_fused");
+        }
+    }
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
     if (R.total_rows <= kRoutedGateUpMaxExperts) {
@@ -661,6 +725,7 @@ extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dout, d_model * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return check_fused_err(ctx);
     }
     return LT_OK;
 }

@@ -253,4 +253,32 @@ hipError_t launch_expert_gate_up_q4k_routed(const DevTensor &GU, const float *x,
                                             float *h, uint32_t *ids_out, float *w_out, hipStream_t s);
 hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
                                   uint32_t k, const float *base, int accumulate, float *out, hipStream_t s);
+
+// The whole decode MoE layer in one launch (lt_moe_fused.hip): F32 router,
+// Q4_K gate_up and down.  The grid is always kFusedBlocks workgroups, which
+// keeps the per-block launch counters equal.
+constexpr int kFusedBlocks = 1024;
+constexpr int kFusedMaxRouterBlocks = 64;  // E <= 256, 4 logits per block
+constexpr int kFusedRecCopies = 8;         // copies of each hand-over record
+struct FusedPlan {
+    bool ok;     // the shape fits the fused kernel
+    int per;     // logits per lane in the top-k wavefront (2 or 4)
+    int rpt;     // down rows per thread
+    int NR, NG, ND;  // router, gate/up and down block counts
+    size_t lds;  // dynamic LDS bytes per block
+};
+// Device memory the fused kernel hands results over through; zeroed once
+// when allocated and never cleared again (words carry launch epochs).
+struct FusedScratch {
+    uint32_t *counters;  // [kFusedBlocks]
+    uint64_t *lg;        // [kFusedMaxRouterBlocks][16]
+    uint64_t *hl;        // [kFusedRecCopies][kFusedBlocks][16]
+    uint32_t *hcnt;      // [2][16][32] finished-gate/up counters (launch parity)
+    uint32_t *err;       // host-mapped error word (device address)
+};
+FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k);
+hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
+                            const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,
+                            const float *base, int accumulate, float *out, uint32_t *ids_out, float *w_out,
+                            const FusedScratch &sc, hipStream_t s);
 }  // namespace lt

@@ -1,0 +1,777 @@
+// lt_moe_fused.hip -- one decode MoE layer (batch 1) in a single launch.
+//
+// The layer is three dependent steps: router logits + softmax/top-k
+// (ops/moe.zig:44-52, gemma4/forward.zig:645-668), the selected experts'
+// gate/up products with the gated activation (moe.zig:55-66), and their down
+// products with the weighted combine (moe.zig:67-76).  Three launches cost
+// three launch latencies plus three HBM round trips in series; here one grid
+// of kFusedBlocks workgroups runs all three, each block in one role chosen
+// by its index:
+//
+//   [0, NR)            router: one logit row per wavefront, dotf32 order
+//   [NR, NR+NG)        gate/up: 16 consecutive h values of one slot
+//   [NR+NG, NR+NG+ND)  down: kDownRows output rows for all k slots
+//
+// Results move between blocks as 64-bit words (32-bit payload, 32-bit launch
+// epoch) written and read with relaxed agent-scope atomics (global_store /
+// global_load with sc1, coherent across the XCDs' L2s without cache
+// flushes).  Every 128-byte line of hand-over words has exactly one writing
+// block.  A reader waits until every word it needs carries the current
+// epoch.  The epoch of a launch is the launch count: block b keeps its own
+// counter counters[b] (no contended atomic), and since every launch runs the
+// same kFusedBlocks blocks, all counters stay equal.
+//
+// Blocks only wait for blocks with smaller indices (down -> gate/up ->
+// router), and workgroups are dispatched in index order, so the waits
+// always end even when the grid does not fit on the GPU at once.  Every wait
+// is also bounded by a wall-clock limit; on expiry the block sets the
+// host-visible error word and writes NaN to the outputs it owns.
+//
+// Arithmetic.  Router logits reproduce dotf32 (ops/math.zig:96-116) bit for
+// bit (exact routing).  The expert products multiply 4-bit weights by fp32
+// activations split into two int8 limbs per element over groups of 16:
+// x ~= sp * (256*a + b), a in [-127, 127], b in [-128, 127], sp = max|x| /
+// (127*256); |x - sp*(256a+b)| <= max|x| / 65024.  Weight nibbles and limbs
+// meet in v_dot4 (4 products per instruction, exact int32 sums); the Q4_K
+// scale and min terms are applied per sub-block in fp32
+// (quant/dequant.zig:157-187 reassociated).  Gate/up blocks publish h
+// already in this limb form, so down blocks need no conversion after the
+// hand-over.
+#include "lt_internal.h"
+#include "lt_topk.h"
+
+#include <math.h>
+
+namespace lt {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kDownRows = 8;                // output rows per down block
+constexpr uint64_t kWaitTicks = 20000000;   // 200 ms of the 100 MHz wall clock
+constexpr int kRecWords = 10;               // h record: a[4] b[4] sp xs
+constexpr int kPollGroups = 25;             // h record lines per poll pass of a block (250 threads)
+constexpr int kPollLines = 16;              // h record lines per thread per poll pass
+constexpr int kRecCopies = kFusedRecCopies;  // copies of every h record (readers spread over them)
+constexpr int kCounters = 16;               // finished-gate/up counters per launch parity
+
+struct FusedArgs {
+    const float *router;  // [E][D] fp32
+    const float *bias;    // [E] or null
+    const uint8_t *gu_hdr, *gu_qs;  // gate_up planes, E*2F rows of nsb super-blocks
+    const uint8_t *dn_hdr, *dn_qs;  // down planes, E*D rows of nsbd super-blocks
+    const float *x;
+    const float *base;  // added to the result (shared FFN output) or null
+    float *out;
+    uint32_t *ids_out;
+    float *w_out;
+    uint32_t *counters;  // [kFusedBlocks]
+    uint64_t *lg;        // logit lines [NR][16]
+    uint64_t *hl;        // h record lines [NG][16]
+    uint32_t *hcnt;      // finished gate/up blocks: [2 parities][kCounters], 32 words apart
+    uint32_t *err;       // host-visible error word
+    int E, D, nsb, F, nsbd, k, norm, act, accumulate;
+    int NR, NG, ND, F16;
+};
+
+__device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
+    __hip_atomic_store(p, (uint64_t)v | ((uint64_t)ep << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t hand_get(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t ep) { return (uint32_t)(w >> 32) == ep; }
+
+__device__ __forceinline__ void report_timeout(uint32_t *err, uint32_t code) {
+    __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppw(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+// Activations of one 64-element window (4 groups of 16) as limbs.
+struct Limbs {
+    uint32_t a[4][4];  // a[g][m]: bytes = limb a of elements 16g + 4m + 0..3
+    uint32_t b[4][4];
+    float sp[4];
+    float xs_lo, xs_hi;  // exact sums of groups 0+1 and 2+3
+};
+
+// 16 values -> limbs (a[4], b[4] packed bytes), scale sp and their sum.
+// A non-finite input makes sp NaN so that the dot products come out NaN.
+__device__ __forceinline__ void limbs16(const float (&v)[16], uint32_t (&a)[4], uint32_t (&b)[4], float &sp,
+                                        float &xs) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] = v[2 * i] + v[2 * i + 1];
+    xs = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+    const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+    sp = m * (1.0f / 32512.0f);
+    if (!(fabsf(xs) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        uint32_t pa = 0, pb = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float t = v[4 * w + j] * inv;
+            const float fa = rintf(t);
+            const float fb = fminf(rintf((t - fa) * 256.0f), 127.0f);
+            pa |= ((uint32_t)(int)fa & 0xffu) << (8 * j);
+            pb |= ((uint32_t)(int)fb & 0xffu) << (8 * j);
+        }
+        a[w] = pa;
+        b[w] = pb;
+    }
+}
+
+// Q4_K scale decode of sub-block pair p (2p, 2p+1) from the header words
+// (h0 = d | dmin << 16, h1..h3 = scales[0..11]): get_scale_min_k4,
+// quant/dequant.zig:289-300.  Returns d*sc and dmin*mn of both sub-blocks.
+struct PairScale {
+    float dsc0, dsc1, dmn0, dmn1;
+};
+
+__device__ __forceinline__ PairScale pair_scale(uint32_t h0, uint32_t h1, uint32_t h2, uint32_t h3, int p) {
+    const float d = f16_bits_to_f32(h0);
+    const float dmin = f16_bits_to_f32(h0 >> 16);
+    const int sh = (p & 1) * 16;
+    const uint32_t ys = h1 >> sh, zs = h2 >> sh, ws = h3 >> sh;
+    const uint32_t scp = p < 2 ? (ys & 0x3f3fu) : ((ws & 0x0f0fu) | ((ys >> 2) & 0x3030u));
+    const uint32_t mnp = p < 2 ? (zs & 0x3f3fu) : (((ws >> 4) & 0x0f0fu) | ((zs >> 2) & 0x3030u));
+    PairScale s;
+    s.dsc0 = d * (float)(scp & 0xffu);
+    s.dsc1 = d * (float)((scp >> 8) & 0xffu);
+    s.dmn0 = dmin * (float)(mnp & 0xffu);
+    s.dmn1 = dmin * (float)((mnp >> 8) & 0xffu);
+    return s;
+}
+
+// The four header words of a (row, super-block) from the one word each lane
+// of an aligned quad loaded (lane & 3 = word index).
+__device__ __forceinline__ void quad_header(uint32_t mine, uint32_t &h0, uint32_t &h1, uint32_t &h2,
+                                            uint32_t &h3) {
+    h0 = dppw<0x00>(mine);
+    h1 = dppw<0x55>(mine);
+    h2 = dppw<0xAA>(mine);
+    h3 = dppw<0xFF>(mine);
+}
+
+// Dot of one Q4_K sub-block pair (64 weights: qs bytes 32p..32p+31 of a
+// super-block, w[0..7]) with the limbs of the matching 64 activations.
+__device__ __forceinline__ float q4k_pair_dot(const uint32_t (&w)[8], const PairScale &s, const Limbs &x) {
+    int A[4] = {0, 0, 0, 0}, B[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const uint32_t lo0 = w[m] & 0x0f0f0f0fu, hi0 = (w[m] >> 4) & 0x0f0f0f0fu;
+        const uint32_t lo1 = w[4 + m] & 0x0f0f0f0fu, hi1 = (w[4 + m] >> 4) & 0x0f0f0f0fu;
+        A[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.a[0][m], A[0], false);
+        B[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.b[0][m], B[0], false);
+        A[1] = __builtin_amdgcn_sdot4((int)lo1, (int)x.a[1][m], A[1], false);
+        B[1] = __builtin_amdgcn_sdot4((int)lo1, (int)x.b[1][m], B[1], false);
+        A[2] = __builtin_amdgcn_sdot4((int)hi0, (int)x.a[2][m], A[2], false);
+        B[2] = __builtin_amdgcn_sdot4((int)hi0, (int)x.b[2][m], B[2], false);
+        A[3] = __builtin_amdgcn_sdot4((int)hi1, (int)x.a[3][m], A[3], false);
+        B[3] = __builtin_amdgcn_sdot4((int)hi1, (int)x.b[3][m], B[3], false);
+    }
+    float c[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) c[g] = (float)((A[g] << 8) + B[g]);  // |.| < 2^23: exact
+    const float t_lo = x.sp[0] * c[0] + x.sp[1] * c[1];
+    const float t_hi = x.sp[2] * c[2] + x.sp[3] * c[3];
+    return (s.dsc0 * t_lo - s.dmn0 * x.xs_lo) + (s.dsc1 * t_hi - s.dmn1 * x.xs_hi);
+}
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// One wavefront waits for the E logits (logit r is word r & 3 of line
+// r >> 2) and returns them in v[j] = logit lane + 64j.  False on timeout.
+template <int PER>
+__device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], int lane) {
+    const uint64_t t0 = wall_clock64();
+    while (true) {
+        uint64_t wv[PER];
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int r = lane + 64 * j;
+            wv[j] = r < a.E ? hand_get(a.lg + (r >> 2) * 16 + (r & 3)) : ((uint64_t)ep << 32);
+        }
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            ok = ok && tag_is(wv[j], ep);
+            v[j] = __uint_as_float((uint32_t)wv[j]);
+        }
+        if (__all(ok)) return true;
+        if (wall_clock64() - t0 > kWaitTicks) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Counters of finished gate/up blocks: block g counts in counter g % 16 of
+// the launch's parity (ep & 1); router block 0 zeroes the other parity's
+// counters for launch ep + 1 (the launch before, which used them, has
+// completed).  Each counter has its own 128-byte line.
+__device__ __forceinline__ uint32_t *hcount(const FusedArgs &a, uint32_t ep, int c) {
+    return a.hcnt + 32 * ((int)(ep & 1u) * kCounters + c);
+}
+
+// Bumps this block's launch counter; the new value is the launch epoch.
+__device__ __forceinline__ uint32_t next_epoch(uint32_t *counters, int bid) {
+    const uint32_t c = __hip_atomic_load(counters + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(counters + bid, c + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return c + 1u;
+}
+
+// Sum of 4 values per lane over each 32-lane half, transposed: returns in
+// every lane the half's total of value index (lane >> 3) & 3.
+__device__ __forceinline__ float half_sum4(const float (&v)[4], int lane) {
+    float a0, a1;
+    {
+        const bool hi = lane & 16;  // lane bit 4: keep values {0,1} or {2,3}
+        const float s0 = hi ? v[0] : v[2], k0 = hi ? v[2] : v[0];
+        const float s1 = hi ? v[1] : v[3], k1 = hi ? v[3] : v[1];
+        a0 = k0 + xor16(s0);
+        a1 = k1 + xor16(s1);
+    }
+    float t;
+    {
+        const bool hi = lane & 8;  // lane bit 3 (row_ror:8 pairs i with i ^ 8 in a 16-lane row)
+        const float send = hi ? a0 : a1, keep = hi ? a1 : a0;
+        t = keep + dpp<0x128>(send);
+    }
+    t += dpp<0xB1>(t);   // lane bit 0
+    t += dpp<0x4E>(t);   // lane bit 1
+    t += dpp<0x141>(t);  // lane bit 2 (row_half_mirror)
+    return t;
+}
+
+__device__ __forceinline__ uint32_t swap_halves(uint32_t v, bool first) {
+    return __float_as_uint(xor32(__uint_as_float(v), first));
+}
+
+// ---------------------------------------------------------------- router
+// Wavefront w computes logit row bid*4 + w with dotf32's rounded operations
+// (ops/math.zig:96-116; the same sequence as k_router_f32 in lt_router.hip):
+// one rounding per product, 32 sequential chains over the 32-element
+// strides, (acc0+acc1)+(acc2+acc3) per lane l < 8, the ordered 8-lane
+// reduce, then + bias.  D % 256 == 0 and D <= 2048 (checked by the host).
+__device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int bid, int tid,
+                                            int wave, int lane) {
+#pragma clang fp contract(off)
+    float *prod = reinterpret_cast<float *>(smem) + wave * a.D;
+    float *chain = reinterpret_cast<float *>(smem) + 4 * a.D;  // [4][32]
+    float *s_lg = chain + 4 * 32;                               // [4]
+    const int row = bid * 4 + wave;
+    const bool valid = row < a.E;
+    const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
+    float4 wv[8], xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if (i < a.nsb) {
+            wv[i] = *reinterpret_cast<const float4 *>(wr + i * 256 + 4 * lane);
+            xv[i] = *reinterpret_cast<const float4 *>(a.x + i * 256 + 4 * lane);
+        }
+    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if (i < a.nsb) {
+            float4 pr;
+            pr.x = wv[i].x * xv[i].x;
+            pr.y = wv[i].y * xv[i].y;
+            pr.z = wv[i].z * xv[i].z;
+            pr.w = wv[i].w * xv[i].w;
+            *reinterpret_cast<float4 *>(prod + i * 256 + 4 * lane) = pr;
+        }
+    __syncthreads();
+    if (bid == 0 && tid < kCounters)
+        __hip_atomic_store(hcount(a, *s_ep + 1u, tid), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane < 32) {
+        float acc = 0.0f;
+        const int nit = a.D >> 5;
+        for (int it = 0; it < nit; it++) acc = acc + prod[it * 32 + lane];
+        chain[wave * 32 + lane] = acc;
+    }
+    __syncthreads();
+    if (lane == 0 && valid) {
+        const float *ch = chain + wave * 32;
+        float acc8[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const float s01 = ch[l] + ch[8 + l];
+            const float s23 = ch[16 + l] + ch[24 + l];
+            acc8[l] = s01 + s23;
+        }
+        float sum = acc8[0];
+#pragma unroll
+        for (int l = 1; l < 8; l++) sum = sum + acc8[l];
+        if (a.bias) sum = sum + a.bias[row];
+        s_lg[wave] = sum;
+    }
+    __syncthreads();
+    if (tid < 4 && bid * 4 + tid < a.E) hand_put(a.lg + bid * 16 + tid, __float_as_uint(s_lg[tid]), *s_ep);
+}
+
+// ---------------------------------------------------------------- gate/up
+// Block g: slot s = g / G, h indices j0 = 16 (g % G) + [0, 16) (G = Kd/16
+// groups per slot; indices >= F are the zero padding of the down K).
+// Wavefront w: pairs j0 + 4w + [0, 4).  Lanes 0-31 take the gate row, lanes
+// 32-63 the up row; lane & 31 = (super-block, sub-block pair) position, so
+// a lane reads 32 bytes of quants per row and one header word (the quad's
+// four words are shared over DPP).
+template <int PER>
+__device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
+                                             int *s_fail, int bid, int tid, int wave, int lane) {
+    const int G = a.nsbd * 16;
+    const int g = bid - a.NR;
+    const int s = g / G, j0 = (g - s * G) * 16;
+    const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
+    const bool lane_on = pos < 4 * a.nsb;
+    const bool first = p32_first(lane);
+    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+    // activation limbs of this lane's 64-element window; each half converts
+    // 32 elements and the halves swap
+    Limbs xl;
+    {
+        float v0[16], v1[16];
+        const float *xp = a.x + sb * 256 + 64 * p + 32 * half;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float4 f0 = lane_on ? *reinterpret_cast<const float4 *>(xp + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 f1 = lane_on ? *reinterpret_cast<const float4 *>(xp + 16 + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v0[4 * i] = f0.x; v0[4 * i + 1] = f0.y; v0[4 * i + 2] = f0.z; v0[4 * i + 3] = f0.w;
+            v1[4 * i] = f1.x; v1[4 * i + 1] = f1.y; v1[4 * i + 2] = f1.z; v1[4 * i + 3] = f1.w;
+        }
+        uint32_t a0[4], b0[4], a1[4], b1[4];
+        float sp0, xs0, sp1, xs1;
+        limbs16(v0, a0, b0, sp0, xs0);
+        limbs16(v1, a1, b1, sp1, xs1);
+        const float xs = xs0 + xs1;
+        const float xo = xor32(xs, first);
+        xl.xs_lo = half ? xo : xs;
+        xl.xs_hi = half ? xs : xo;
+        const float spo0 = xor32(sp0, first), spo1 = xor32(sp1, first);
+        xl.sp[0] = half ? spo0 : sp0;
+        xl.sp[1] = half ? spo1 : sp1;
+        xl.sp[2] = half ? sp0 : spo0;
+        xl.sp[3] = half ? sp1 : spo1;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint32_t oa0 = swap_halves(a0[m], first), oa1 = swap_halves(a1[m], first);
+            const uint32_t ob0 = swap_halves(b0[m], first), ob1 = swap_halves(b1[m], first);
+            xl.a[0][m] = half ? oa0 : a0[m];
+            xl.a[1][m] = half ? oa1 : a1[m];
+            xl.a[2][m] = half ? a0[m] : oa0;
+            xl.a[3][m] = half ? a1[m] : oa1;
+            xl.b[0][m] = half ? ob0 : b0[m];
+            xl.b[1][m] = half ? ob1 : b1[m];
+            xl.b[2][m] = half ? b0[m] : ob0;
+            xl.b[3][m] = half ? b1[m] : ob1;
+        }
+    }
+    __syncthreads();  // s_ep
+    const uint32_t ep = *s_ep;
+    if (wave == 0) {  // only this slot's expert: s + 1 selection rounds, no softmax
+        float lv[PER];
+        const bool ok = poll_logits<PER>(a, ep, lv, lane);
+        const int idx = topk_index_at<PER>(lv, a.E, s, lane);
+        if (lane == 0) {
+            s_ids[0] = (uint32_t)idx;
+            if (!ok) *s_fail = 1;
+        }
+    }
+    __syncthreads();  // s_ids[0], s_fail
+    uint32_t e = s_ids[0];
+    if (e >= (uint32_t)a.E) e = 0;
+    const int jb = j0 + wave * 4;
+    uint4 q0[4], q1[4];
+    uint32_t hw[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        q0[r] = q1[r] = make_uint4(0u, 0u, 0u, 0u);
+        hw[r] = 0u;
+        if (lane_on && jb + r < a.F) {
+            const size_t row = (size_t)e * 2 * a.F + (size_t)half * a.F + (jb + r);
+            const size_t blk = row * a.nsb + sb;
+            q0[r] = ld16(a.gu_qs + blk * 128 + 32 * p);
+            q1[r] = ld16(a.gu_qs + blk * 128 + 32 * p + 16);
+            hw[r] = *reinterpret_cast<const uint32_t *>(a.gu_hdr + blk * 16 + 4 * (lane & 3));
+        }
+    }
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        uint32_t h0, h1, h2, h3;
+        quad_header(hw[r], h0, h1, h2, h3);
+        const PairScale ps = pair_scale(h0, h1, h2, h3, p);
+        const uint32_t w8[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+        v[r] = (lane_on && jb + r < a.F) ? q4k_pair_dot(w8, ps, xl) : 0.0f;
+    }
+    const float t = half_sum4(v, lane);
+    const float u = xor32(t, first);  // the up total of the same pair
+    float *s_h = reinterpret_cast<float *>(smem);
+    if (lane < 32 && (lane & 7) == 0) {
+        const int r = lane >> 3;
+        s_h[wave * 4 + r] = (jb + r < a.F) ? act_apply((uint32_t)a.act, t) * u : 0.0f;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // the 16 h values as one limb record: lanes 0..15 own one value each
+        const float hv = lane < 16 ? s_h[lane] : 0.0f;
+        float m = fabsf(hv);
+        m = fmaxf(m, dpp<0x128>(m));
+        m = fmaxf(m, dpp<0x124>(m));
+        m = fmaxf(m, dpp<0x122>(m));
+        m = fmaxf(m, dpp<0x121>(m));
+        float xs = hv;
+        xs += dpp<0x128>(xs);
+        xs += dpp<0x124>(xs);
+        xs += dpp<0x122>(xs);
+        xs += dpp<0x121>(xs);
+        xs = __shfl(xs, 0, 64);
+        m = __shfl(m, 0, 64);
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        float sp = m * (1.0f / 32512.0f);
+        if (!(fabsf(xs) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);
+        const float tt = hv * inv;
+        const float fa = rintf(tt);
+        const float fb = fminf(rintf((tt - fa) * 256.0f), 127.0f);
+        uint32_t pa = ((uint32_t)(int)fa & 0xffu) << (8 * (lane & 3));
+        uint32_t pb = ((uint32_t)(int)fb & 0xffu) << (8 * (lane & 3));
+        pa |= dppw<0xB1>(pa);
+        pa |= dppw<0x4E>(pa);
+        pb |= dppw<0xB1>(pb);
+        pb |= dppw<0x4E>(pb);
+        // record word i: a-words from lanes 0,4,8,12; b-words; sp; xs
+        const int src = lane < 4 ? 4 * lane : (lane < 8 ? 4 * (lane - 4) : 0);
+        const uint32_t ga = (uint32_t)__shfl((int)pa, src, 64);
+        const uint32_t gb = (uint32_t)__shfl((int)pb, src, 64);
+        uint32_t word = lane < 4 ? ga : (lane < 8 ? gb : (lane == 8 ? __float_as_uint(sp) : __float_as_uint(xs)));
+        if (*s_fail) word = lane < 8 ? 0u : 0x7fc00000u;  // routing timed out: NaN record
+        if (lane < kRecWords)
+#pragma unroll
+            for (int c = 0; c < kRecCopies; c++)
+                hand_put(a.hl + ((size_t)c * kFusedBlocks + g) * 16 + lane, word, ep);
+        if (lane == 0)
+            __hip_atomic_fetch_add(hcount(a, ep, g % kCounters), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ---------------------------------------------------------------- down
+// Sums V values per lane over each aligned group of 16 lanes, transposed:
+// returns the group's total of value index (lane & 15) >> log2(16 / V).
+template <int V>
+__device__ __forceinline__ float group16_sum_transposed(const float (&v)[V], int lane) {
+    float a[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) a[i] = v[i];
+    if (V >= 2) {  // lane bit 3: row_ror:8 pairs i with i ^ 8
+        const bool hi = lane & 8;
+#pragma unroll
+        for (int i = 0; i < V / 2; i++) {
+            const float send = hi ? a[i] : a[i + V / 2], keep = hi ? a[i + V / 2] : a[i];
+            a[i] = keep + dpp<0x128>(send);
+        }
+    }
+    if (V >= 4) {  // lane bit 2: row_half_mirror pairs i with 7 - i
+        const bool hi = lane & 4;
+#pragma unroll
+        for (int i = 0; i < V / 4; i++) {
+            const float send = hi ? a[i] : a[i + V / 4], keep = hi ? a[i + V / 4] : a[i];
+            a[i] = keep + dpp<0x141>(send);
+        }
+    }
+    if (V >= 8) {  // lane bit 1: quad_perm [2,3,0,1]
+        const bool hi = lane & 2;
+        const float send = hi ? a[0] : a[1], keep = hi ? a[1] : a[0];
+        a[0] = keep + dpp<0x4E>(send);
+    }
+    float t = a[0];
+    if (V < 8) t += dpp<0x4E>(t);
+    if (V < 4) t += dpp<0x141>(t);
+    if (V < 2) t += dpp<0x128>(t);
+    t += dpp<0xB1>(t);
+    return t;
+}
+
+// Block: output rows row0 + [0, kDownRows) for all k slots.  Threads form
+// groups of 16: group q = tid >> 4 takes slot q % k and rows (q / k) * RPT +
+// [0, RPT) (groups with q / k >= 8 / RPT idle); lane (tid & 15) = (super-
+// block, sub-block pair) position.  Down weights are loaded and their
+// scales decoded while the gate/up blocks run; once every gate/up block has
+// counted itself done, the h records are read into LDS, each group sums its
+// row partials over DPP, and the rows are combined over slots in slot order.
+template <int PER, int RPT>
+__device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, float *s_w,
+                                          uint32_t *s_ep, int *s_fail, int bid, int tid, int wave, int lane) {
+    constexpr int TPD = kDownRows / RPT;  // row sets per block
+    const int G = a.nsbd * 16;
+    const int NL = a.k * G;  // h record lines
+    const int row0 = (bid - a.NR - a.NG) * kDownRows;
+    const int q = tid >> 4, l16 = tid & 15;
+    const int tq = q / a.k, s = q - tq * a.k;
+    const int sb = l16 >> 2, p = l16 & 3;
+    const bool grp_on = tq < TPD;
+    const bool t_on = grp_on && sb < a.nsbd;
+    uint32_t *rec_a = reinterpret_cast<uint32_t *>(smem);
+    uint32_t *rec_b = rec_a + NL * 4;
+    float *rec_sp = reinterpret_cast<float *>(rec_b + NL * 4);
+    float *rec_xs = rec_sp + NL;
+    float *tot = rec_xs + NL;  // [kDownRows][k]
+    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+    __syncthreads();
+    const uint32_t ep = *s_ep;
+    if (wave == 0) {
+        float lv[PER];
+        const bool ok = poll_logits<PER>(a, ep, lv, lane);
+        uint32_t key[PER];
+        int my_i;
+        float my_p;
+        topk_softmax_regs<PER>(lv, a.E, a.k, a.norm, s_ids, s_w, key, my_i, my_p, lane);
+        if (!ok && lane == 0) *s_fail = 1;
+    }
+    __syncthreads();
+    if (bid == a.NR + a.NG && tid < a.k) {  // the routing, for the caller
+        a.ids_out[tid] = s_ids[tid];
+        a.w_out[tid] = s_w[tid];
+    }
+    uint32_t e = grp_on ? s_ids[s] : 0u;
+    if (e >= (uint32_t)a.E) e = 0;
+    uint4 q0[RPT], q1[RPT];
+    uint32_t hw[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int row = row0 + tq * RPT + i;
+        q0[i] = q1[i] = make_uint4(0u, 0u, 0u, 0u);
+        hw[i] = 0u;
+        if (t_on && row < a.D) {
+            const size_t blk = ((size_t)e * a.D + row) * a.nsbd + sb;
+            q0[i] = ld16(a.dn_qs + blk * 128 + 32 * p);
+            q1[i] = ld16(a.dn_qs + blk * 128 + 32 * p + 16);
+            hw[i] = *reinterpret_cast<const uint32_t *>(a.dn_hdr + blk * 16 + 4 * p);
+        }
+    }
+    PairScale ps[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        uint32_t h0, h1, h2, h3;
+        quad_header(hw[i], h0, h1, h2, h3);
+        ps[i] = pair_scale(h0, h1, h2, h3, p);
+    }
+    // wait until every gate/up block has counted itself done
+    if (wave == 0) {
+        const uint32_t want = lane < kCounters ? (uint32_t)((a.NG - lane + kCounters - 1) / kCounters) : 0u;
+        const uint64_t t0 = wall_clock64();
+        while (true) {
+            const uint32_t got = lane < kCounters
+                                     ? __hip_atomic_load(hcount(a, ep, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0u;
+            if (__all(got >= want)) break;
+            if (wall_clock64() - t0 > kWaitTicks) {
+                if (lane == 0) *s_fail = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+    // h records: line L (= slot * G + group) holds words 0..9.  Threads
+    // qq*10 + wl (qq < 25) read word wl of lines qq + 25j: up to kPollLines
+    // lines per thread per pass, all loads in flight at once (normally one
+    // pass: the records were published before the count was taken).
+    bool ok = true;
+    {
+        const int qq = tid / kRecWords, wl = tid - qq * kRecWords;
+        const bool on = tid < kPollGroups * kRecWords;
+        const uint64_t *hrec = a.hl + (size_t)((bid - a.NR - a.NG) % kRecCopies) * kFusedBlocks * 16;
+        const uint64_t t0 = wall_clock64();
+        for (int L0 = qq; L0 < NL; L0 += kPollGroups * kPollLines) {
+            while (true) {
+                uint64_t w[kPollLines];
+                uint32_t off = (uint32_t)(L0 * 16 + wl) * 8u;
+#pragma unroll
+                for (int j = 0; j < kPollLines; j++) {
+                    const bool use = on && L0 + kPollGroups * j < NL;
+                    w[j] = use ? hand_get(reinterpret_cast<const uint64_t *>(reinterpret_cast<const uint8_t *>(hrec) + off))
+                               : ((uint64_t)ep << 32);
+                    off += kPollGroups * 128u;
+                }
+                bool good = true;
+#pragma unroll
+                for (int j = 0; j < kPollLines; j++) good = good && tag_is(w[j], ep);
+                if (__all(good)) {
+#pragma unroll
+                    for (int j = 0; j < kPollLines; j++) {
+                        const int L = L0 + kPollGroups * j;
+                        if (on && L < NL) {
+                            const uint32_t val = (uint32_t)w[j];
+                            if (wl < 4) rec_a[L * 4 + wl] = val;
+                            else if (wl < 8) rec_b[L * 4 + wl - 4] = val;
+                            else if (wl == 8) rec_sp[L] = __uint_as_float(val);
+                            else rec_xs[L] = __uint_as_float(val);
+                        }
+                    }
+                    break;
+                }
+                if (wall_clock64() - t0 > kWaitTicks) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (!ok) break;
+        }
+    }
+    if (!ok) atomicOr(s_fail, 1);
+    __syncthreads();
+    float v[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) v[i] = 0.0f;
+    if (t_on) {
+        const int gi = s * G + sb * 16 + 4 * p;  // first of the window's 4 groups
+        Limbs xl;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint4 va = *reinterpret_cast<const uint4 *>(rec_a + (gi + g) * 4);
+            const uint4 vb = *reinterpret_cast<const uint4 *>(rec_b + (gi + g) * 4);
+            xl.a[g][0] = va.x; xl.a[g][1] = va.y; xl.a[g][2] = va.z; xl.a[g][3] = va.w;
+            xl.b[g][0] = vb.x; xl.b[g][1] = vb.y; xl.b[g][2] = vb.z; xl.b[g][3] = vb.w;
+        }
+        const float4 sp4 = *reinterpret_cast<const float4 *>(rec_sp + gi);
+        const float4 xs4 = *reinterpret_cast<const float4 *>(rec_xs + gi);
+        xl.sp[0] = sp4.x; xl.sp[1] = sp4.y; xl.sp[2] = sp4.z; xl.sp[3] = sp4.w;
+        xl.xs_lo = xs4.x + xs4.y;
+        xl.xs_hi = xs4.z + xs4.w;
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const uint32_t w8[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
+            v[i] = q4k_pair_dot(w8, ps[i], xl);
+        }
+    }
+    const float t = group16_sum_transposed<RPT>(v, lane);
+    constexpr int SH = RPT == 8 ? 1 : (RPT == 4 ? 2 : (RPT == 2 ? 3 : 4));
+    if (grp_on && (l16 & ((1 << SH) - 1)) == 0) tot[(tq * RPT + (l16 >> SH)) * a.k + s] = t;
+    __syncthreads();
+    if (tid < kDownRows) {
+        const int row = row0 + tid;
+        float tv[16], wv[16];
+#pragma unroll
+        for (int sl = 0; sl < 16; sl++) {
+            tv[sl] = sl < a.k ? tot[tid * a.k + sl] : 0.0f;
+            wv[sl] = sl < a.k ? s_w[sl] : 0.0f;
+        }
+        if (row < a.D) {
+            float acc = a.accumulate ? a.out[row] : 0.0f;
+#pragma unroll
+            for (int sl = 0; sl < 16; sl++)
+                if (sl < a.k) acc += wv[sl] * tv[sl];
+            if (a.base) acc = a.base[row] + acc;
+            a.out[row] = *s_fail ? __int_as_float(0x7fc00000) : acc;
+        }
+    }
+}
+
+template <int PER, int RPT>
+__global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t s_ep;
+    __shared__ uint32_t s_ids[16];
+    __shared__ float s_w[16];
+    __shared__ int s_fail;
+    const int bid = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (bid >= a.NR + a.NG + a.ND) {  // no role in this configuration: keep the counter in step
+        if (tid == 0) (void)next_epoch(a.counters, bid);
+        return;
+    }
+    if (tid == 0) s_fail = 0;
+    if (bid < a.NR) {
+        role_router(a, smem, &s_ep, bid, tid, wave, lane);
+    } else if (bid < a.NR + a.NG) {
+        role_gate_up<PER>(a, smem, s_ids, &s_ep, &s_fail, bid, tid, wave, lane);
+    } else {
+        role_down<PER, RPT>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, tid, wave, lane);
+    }
+    if (tid == 0 && s_fail) report_timeout(a.err, 1u);
+}
+
+}  // namespace
+
+FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
+    FusedPlan pl{};
+    pl.ok = false;
+    if (D % 256 != 0 || D > 2048 || D < 256) return pl;
+    if (Kd % 256 != 0 || Kd < F || Kd > 1024) return pl;  // 16 lanes = 4 super-blocks x 4 pairs
+    if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return pl;
+    const int nsbd = Kd / 256;
+    int tpd = 1;  // row sets per down block: 16 groups of 16 threads over k slots
+    while (tpd * 2 <= 16 / k && tpd < kDownRows) tpd *= 2;
+    pl.rpt = kDownRows / tpd;
+    pl.per = E <= 128 ? 2 : 4;
+    pl.NR = (E + 3) / 4;
+    pl.NG = k * nsbd * 16;
+    pl.ND = (D + kDownRows - 1) / kDownRows;
+    if (pl.NR + pl.NG + pl.ND > kFusedBlocks) return pl;
+    const size_t lds_router = (size_t)4 * D * 4 + 4 * 32 * 4 + 16;
+    const size_t NL = (size_t)k * nsbd * 16;
+    const size_t lds_down = NL * 40 + (size_t)kDownRows * k * 4;
+    pl.lds = lds_router > lds_down ? lds_router : lds_down;
+    if (pl.lds < 64) pl.lds = 64;
+    if (pl.lds > 64 * 1024) return pl;
+    pl.ok = true;
+    return pl;
+}
+
+template <int PER, int RPT>
+static hipError_t launch_fused_t(const FusedArgs &fa, size_t lds, hipStream_t s) {
+    hipLaunchKernelGGL((k_moe_fused<PER, RPT>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
+                            const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,
+                            const float *base, int accumulate, float *out, uint32_t *ids_out, float *w_out,
+                            const FusedScratch &sc, hipStream_t s) {
+    FusedArgs fa;
+    fa.router = reinterpret_cast<const float *>(R.p0);
+    fa.bias = bias;
+    fa.gu_hdr = GU.p0;
+    fa.gu_qs = GU.p1;
+    fa.dn_hdr = Dn.p0;
+    fa.dn_qs = Dn.p1;
+    fa.x = x;
+    fa.base = base;
+    fa.out = out;
+    fa.ids_out = ids_out;
+    fa.w_out = w_out;
+    fa.counters = sc.counters;
+    fa.lg = sc.lg;
+    fa.hl = sc.hl;
+    fa.hcnt = sc.hcnt;
+    fa.err = sc.err;
+    fa.E = (int)R.total_rows;
+    fa.D = (int)GU.cols;
+    fa.nsb = (int)GU.blocks_per_row;
+    fa.F = F;
+    fa.nsbd = (int)Dn.blocks_per_row;
+    fa.k = k;
+    fa.norm = (int)norm;
+    fa.act = (int)act;
+    fa.accumulate = accumulate;
+    fa.NR = pl.NR;
+    fa.NG = pl.NG;
+    fa.ND = pl.ND;
+    fa.F16 = (F + 15) / 16;
+    const bool p2 = pl.per == 2;
+    switch (pl.rpt) {
+    case 1: return p2 ? launch_fused_t<2, 1>(fa, pl.lds, s) : launch_fused_t<4, 1>(fa, pl.lds, s);
+    case 2: return p2 ? launch_fused_t<2, 2>(fa, pl.lds, s) : launch_fused_t<4, 2>(fa, pl.lds, s);
+    case 4: return p2 ? launch_fused_t<2, 4>(fa, pl.lds, s) : launch_fused_t<4, 4>(fa, pl.lds, s);
+    default: return p2 ? launch_fused_t<2, 8>(fa, pl.lds, s) : launch_fused_t<4, 8>(fa, pl.lds, s);
+    }
+}
+
+}  // namespace lt

@@ -469,3 +469,67 @@ def test_gpu_prefill_deterministic(ctx, cfg3):
     ctx.moe_prefill(a, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"])
     ctx.moe_prefill(b, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"])
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------------------ single-launch kernel
+# lt_moe_forward runs the whole layer in one launch when the shape fits
+# (F32 router, Q4_K experts, d_model <= 2048); LT_MOE_UNFUSED forces the
+# router / gate-up / down launches.  Both must match the oracle; routing is
+# bit-exact on both.
+@pytest.mark.gpu
+@pytest.mark.parametrize("D,E,F,Kd,k,act,norm,bias", [
+    (2048, 128, 768, 768, 8, 0, True, False),    # config 3
+    (512, 61, 256, 256, 5, 0, False, True),      # E not a multiple of 4, k odd, router bias
+    (1024, 200, 288, 512, 16, 1, True, False),   # E > 128, F % 256 != 0, zero-padded down K, GELU
+    (256, 8, 64, 256, 1, 0, False, False),       # smallest shapes, one expert
+])
+def test_gpu_fused_layer_matches_oracle_and_unfused(ctx, pool, D, E, F, Kd, k, act, norm, bias):
+    w = synth.moe_weights(70 + E % 11, D, E, F, down_cols=Kd)
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    b = synth.normal(synth.stream(71, E), (E,), 0.5) if bias else None
+    for i in range(3):
+        x = synth.normal(synth.stream(72, 100 * E + i), (D,))
+        res = {}
+        for unfused in (False, True):
+            out = np.zeros(D, np.float32)
+            ids = np.zeros(k, np.uint32)
+            wt = np.zeros(k, np.float32)
+            ctx.moe_forward(out, x, router, gate_up, down, k, F, act=act, norm_topk=norm, bias=b, out_ids=ids,
+                            out_w=wt, unfused=unfused)
+            res[unfused] = (out, ids, wt)
+        ref, rids, rw, agree = orc.moe_forward(w, x, k, act=act, norm_topk=norm, bias=b, pool=pool)
+        assert agree
+        for unfused, (out, ids, wt) in res.items():
+            assert np.array_equal(ids, rids), (unfused, i, ids, rids)
+            assert np.allclose(wt, rw, rtol=1e-5, atol=0), (unfused, i)
+            assert rel_l2(out, ref) <= REL_L2, (unfused, i, rel_l2(out, ref))
+        # the two-limb activations (|error| <= max|x| / 65024 per group of
+        # 16) keep the result well inside the bar
+        assert rel_l2(res[False][0], ref) <= 2e-4, rel_l2(res[False][0], ref)
+    for t in (router, gate_up, down):
+        t.free()
+
+
+@pytest.mark.gpu
+def test_gpu_fused_accumulate_and_alternating_shapes(ctx, cfg3, pool):
+    # out += layer (moeForward's contract), and calls of another shape in
+    # between: the hand-over words of one shape must not satisfy the waits of
+    # the next
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    small = synth.moe_weights(73, 512, 16, 256)
+    sr, sg, sd = lt.upload_moe(ctx, small)
+    for i in range(4):
+        x = synth.config3_x(200 + i)
+        base = synth.normal(synth.stream(74, i), (w.d_model,))
+        out = base.copy()
+        ctx.moe_forward(out, x, router, gate_up, down, 8, w.d_expert, norm_topk=True, accumulate=True)
+        ref, *_ = orc.moe_forward(w, x, 8, norm_topk=True, pool=pool, out=base)
+        assert rel_l2(out, ref) <= REL_L2, i
+        xs = synth.normal(synth.stream(75, i), (512,))
+        so = np.zeros(512, np.float32)
+        ctx.moe_forward(so, xs, sr, sg, sd, 4, 256)
+        sref, *_ = orc.moe_forward(small, xs, 4, pool=pool)
+        assert rel_l2(so, sref) <= REL_L2, i
+    for t in (sr, sg, sd):
+        t.free()
