@@ -183,9 +183,9 @@ int ensure_fused(lt_ctx *ctx) {
     if (ctx->fused) return LT_OK;
     const size_t n_cnt = (size_t)lt::kFusedBlocks * 4;
     const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128;
-    const size_t n_hl = (size_t)lt::kFusedBlocks * 128 * lt::kFusedRecCopies;
-    const size_t n_hc = 2 * 16 * 128;
-    const size_t bytes = n_cnt + n_lg + n_hl + n_hc;
+    const size_t n_hl = (size_t)lt::kFusedBlocks * 128;
+    const size_t n_pl = (size_t)lt::kFusedBlocks * 4 * 128;
+    const size_t bytes = n_cnt + n_lg + n_hl + n_pl;
     void *p = nullptr;
     LT_HIP(ctx, hipMalloc(&p, bytes));
     hipError_t e = hipMemset(p, 0, bytes);
@@ -207,7 +207,7 @@ int ensure_fused(lt_ctx *ctx) {
     ctx->fsc.counters = (uint32_t *)b;
     ctx->fsc.lg = (uint64_t *)(b + n_cnt);
     ctx->fsc.hl = (uint64_t *)(b + n_cnt + n_lg);
-    ctx->fsc.hcnt = (uint32_t *)(b + n_cnt + n_lg + n_hl);
+    ctx->fsc.pl = (uint64_t *)(b + n_cnt + n_lg + n_hl);
     ctx->fsc.err = (uint32_t *)dp;
     return LT_OK;
 }

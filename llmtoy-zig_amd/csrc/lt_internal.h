@@ -259,21 +259,23 @@ hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint
 // keeps the per-block launch counters equal.
 constexpr int kFusedBlocks = 1024;
 constexpr int kFusedMaxRouterBlocks = 64;  // E <= 256, 4 logits per block
-constexpr int kFusedRecCopies = 8;         // copies of each hand-over record
 struct FusedPlan {
     bool ok;     // the shape fits the fused kernel
     int per;     // logits per lane in the top-k wavefront (2 or 4)
-    int rpt;     // down rows per thread
-    int NR, NG, ND;  // router, gate/up and down block counts
+    int NRg;     // router blocks per XCD group
+    int SPG;     // slots per XCD group (ceil(k / 8))
+    int G;       // h groups of 16 per slot (down K / 16)
+    int NDg;     // down blocks per slot
+    int NCg;     // combining blocks per XCD group
     size_t lds;  // dynamic LDS bytes per block
 };
 // Device memory the fused kernel hands results over through; zeroed once
 // when allocated and never cleared again (words carry launch epochs).
 struct FusedScratch {
     uint32_t *counters;  // [kFusedBlocks]
-    uint64_t *lg;        // [kFusedMaxRouterBlocks][16]
-    uint64_t *hl;        // [kFusedRecCopies][kFusedBlocks][16]
-    uint32_t *hcnt;      // [2][16][32] finished-gate/up counters (launch parity)
+    uint64_t *lg;        // [kFusedMaxRouterBlocks][16] logit lines
+    uint64_t *hl;        // [kFusedBlocks][16] h record lines
+    uint64_t *pl;        // [4 * kFusedBlocks][16] partial-output lines
     uint32_t *err;       // host-mapped error word (device address)
 };
 FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k);

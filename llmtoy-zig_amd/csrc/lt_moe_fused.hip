@@ -5,27 +5,39 @@
 // gate/up products with the gated activation (moe.zig:55-66), and their down
 // products with the weighted combine (moe.zig:67-76).  Three launches cost
 // three launch latencies plus three HBM round trips in series; here one grid
-// of kFusedBlocks workgroups runs all three, each block in one role chosen
-// by its index:
+// of kFusedBlocks workgroups runs all of it.
 //
-//   [0, NR)            router: one logit row per wavefront, dotf32 order
-//   [NR, NR+NG)        gate/up: 16 consecutive h values of one slot
-//   [NR+NG, NR+NG+ND)  down: kDownRows output rows for all k slots
+// Placement.  Workgroups are dealt to the 8 XCDs round robin, so the blocks
+// with equal bid % 8 ("group" x) share one XCD and its L2.  Slot s (the s-th
+// selected expert) is computed entirely inside group s % 8: its gate/up
+// blocks publish h, its down blocks read that h (traffic stays inside one
+// XCD) and publish their slot's weighted rows; only those small per-slot
+// partial outputs cross XCDs, to the combining blocks.  Within group x the
+// in-group index i = bid / 8 picks the role:
 //
-// Results move between blocks as 64-bit words (32-bit payload, 32-bit launch
+//   i < NRg                 router: logit rows 4*bid + [0, 4), dotf32 order
+//   next SPG*G              gate/up: slot x + 8u, h group jg (16 values)
+//   next SPG*NDg            down: slot x + 8u, rows 64j + [0, 64)
+//   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
+//
+// (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = NCg = ceil(D /
+// 64)).  The placement only affects speed: every hand-over below is coherent
+// across XCDs.
+//
+// Hand-over.  Results move as 64-bit words (32-bit payload, 32-bit launch
 // epoch) written and read with relaxed agent-scope atomics (global_store /
-// global_load with sc1, coherent across the XCDs' L2s without cache
+// global_load with sc1: coherent across the XCDs' L2s without cache
 // flushes).  Every 128-byte line of hand-over words has exactly one writing
-// block.  A reader waits until every word it needs carries the current
+// wavefront.  A reader waits until every word it needs carries the current
 // epoch.  The epoch of a launch is the launch count: block b keeps its own
 // counter counters[b] (no contended atomic), and since every launch runs the
 // same kFusedBlocks blocks, all counters stay equal.
 //
-// Blocks only wait for blocks with smaller indices (down -> gate/up ->
-// router), and workgroups are dispatched in index order, so the waits
-// always end even when the grid does not fit on the GPU at once.  Every wait
-// is also bounded by a wall-clock limit; on expiry the block sets the
-// host-visible error word and writes NaN to the outputs it owns.
+// Blocks only wait for blocks with smaller indices (combine -> down ->
+// gate/up -> router), and workgroups are dispatched in index order, so the
+// waits always end even when the grid does not fit on the GPU at once.
+// Every wait is also bounded by a wall-clock limit; on expiry the block sets
+// the host-visible error word and its outputs become NaN.
 //
 // Arithmetic.  Router logits reproduce dotf32 (ops/math.zig:96-116) bit for
 // bit (exact routing).  The expert products multiply 4-bit weights by fp32
@@ -35,8 +47,7 @@
 // meet in v_dot4 (4 products per instruction, exact int32 sums); the Q4_K
 // scale and min terms are applied per sub-block in fp32
 // (quant/dequant.zig:157-187 reassociated).  Gate/up blocks publish h
-// already in this limb form, so down blocks need no conversion after the
-// hand-over.
+// already in this limb form.
 #include "lt_internal.h"
 #include "lt_topk.h"
 
@@ -47,13 +58,10 @@ namespace lt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kDownRows = 8;                // output rows per down block
+constexpr int kDownRows = 64;               // output rows per down block (16 lane groups x 4)
+constexpr int kCombRows = 8;                // output rows per combining block
 constexpr uint64_t kWaitTicks = 20000000;   // 200 ms of the 100 MHz wall clock
 constexpr int kRecWords = 10;               // h record: a[4] b[4] sp xs
-constexpr int kPollGroups = 25;             // h record lines per poll pass of a block (250 threads)
-constexpr int kPollLines = 16;              // h record lines per thread per poll pass
-constexpr int kRecCopies = kFusedRecCopies;  // copies of every h record (readers spread over them)
-constexpr int kCounters = 16;               // finished-gate/up counters per launch parity
 
 struct FusedArgs {
     const float *router;  // [E][D] fp32
@@ -66,12 +74,12 @@ struct FusedArgs {
     uint32_t *ids_out;
     float *w_out;
     uint32_t *counters;  // [kFusedBlocks]
-    uint64_t *lg;        // logit lines [NR][16]
-    uint64_t *hl;        // h record lines [NG][16]
-    uint32_t *hcnt;      // finished gate/up blocks: [2 parities][kCounters], 32 words apart
+    uint64_t *lg;        // logit lines [8*NRg][16]
+    uint64_t *hl;        // h record lines [k*G][16]
+    uint64_t *pl;        // partial-output lines [k*NDg*4][16]
     uint32_t *err;       // host-visible error word
     int E, D, nsb, F, nsbd, k, norm, act, accumulate;
-    int NR, NG, ND, F16;
+    int NRg, SPG, G, NDg, NCg;
 };
 
 __device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
@@ -91,7 +99,6 @@ __device__ __forceinline__ uint32_t dppw(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 
-// Activations of one 64-element window (4 groups of 16) as limbs.
 struct Limbs {
     uint32_t a[4][4];  // a[g][m]: bytes = limb a of elements 16g + 4m + 0..3
     uint32_t b[4][4];
@@ -212,14 +219,6 @@ __device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], in
     }
 }
 
-// Counters of finished gate/up blocks: block g counts in counter g % 16 of
-// the launch's parity (ep & 1); router block 0 zeroes the other parity's
-// counters for launch ep + 1 (the launch before, which used them, has
-// completed).  Each counter has its own 128-byte line.
-__device__ __forceinline__ uint32_t *hcount(const FusedArgs &a, uint32_t ep, int c) {
-    return a.hcnt + 32 * ((int)(ep & 1u) * kCounters + c);
-}
-
 // Bumps this block's launch counter; the new value is the launch epoch.
 __device__ __forceinline__ uint32_t next_epoch(uint32_t *counters, int bid) {
     const uint32_t c = __hip_atomic_load(counters + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -288,8 +287,6 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
             *reinterpret_cast<float4 *>(prod + i * 256 + 4 * lane) = pr;
         }
     __syncthreads();
-    if (bid == 0 && tid < kCounters)
-        __hip_atomic_store(hcount(a, *s_ep + 1u, tid), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (lane < 32) {
         float acc = 0.0f;
         const int nit = a.D >> 5;
@@ -317,18 +314,18 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
 }
 
 // ---------------------------------------------------------------- gate/up
-// Block g: slot s = g / G, h indices j0 = 16 (g % G) + [0, 16) (G = Kd/16
-// groups per slot; indices >= F are the zero padding of the down K).
+// Block: slot s, h indices j0 = 16 jg + [0, 16), jg < G = Kd/16 (indices
+// >= F are the zero padding of the down K); its record is line s*G + jg.
 // Wavefront w: pairs j0 + 4w + [0, 4).  Lanes 0-31 take the gate row, lanes
 // 32-63 the up row; lane & 31 = (super-block, sub-block pair) position, so
 // a lane reads 32 bytes of quants per row and one header word (the quad's
 // four words are shared over DPP).
 template <int PER>
 __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
-                                             int *s_fail, int bid, int tid, int wave, int lane) {
+                                             int *s_fail, int bid, int s, int jg, int tid, int wave, int lane) {
     const int G = a.nsbd * 16;
-    const int g = bid - a.NR;
-    const int s = g / G, j0 = (g - s * G) * 16;
+    const int g = s * G + jg;  // record line
+    const int j0 = jg * 16;
     const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
     const bool lane_on = pos < 4 * a.nsb;
     const bool first = p32_first(lane);
@@ -452,12 +449,7 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
         const uint32_t gb = (uint32_t)__shfl((int)pb, src, 64);
         uint32_t word = lane < 4 ? ga : (lane < 8 ? gb : (lane == 8 ? __float_as_uint(sp) : __float_as_uint(xs)));
         if (*s_fail) word = lane < 8 ? 0u : 0x7fc00000u;  // routing timed out: NaN record
-        if (lane < kRecWords)
-#pragma unroll
-            for (int c = 0; c < kRecCopies; c++)
-                hand_put(a.hl + ((size_t)c * kFusedBlocks + g) * 16 + lane, word, ep);
-        if (lane == 0)
-            __hip_atomic_fetch_add(hcount(a, ep, g % kCounters), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane < kRecWords) hand_put(a.hl + (size_t)g * 16 + lane, word, ep);
     }
 }
 
@@ -505,23 +497,26 @@ __device__ __forceinline__ float group16_sum_transposed(const float (&v)[V], int
 // scales decoded while the gate/up blocks run; once every gate/up block has
 // counted itself done, the h records are read into LDS, each group sums its
 // row partials over DPP, and the rows are combined over slots in slot order.
-template <int PER, int RPT>
+// Block: slot s, output rows row0 = 64 j + [0, 64).  Thread groups of 16:
+// group rg = tid >> 4 takes rows row0 + 4 rg + [0, 4); lane l16 = tid & 15 =
+// (super-block, sub-block pair) position.  Its down weights are loaded and
+// their scales decoded while the gate/up blocks run; then the block reads
+// the slot's G h records (same XCD), each group sums its row partials over
+// DPP, and wavefront w writes rows 16w + [0, 16), times the slot weight, as
+// one line of partial-output words.
+template <int PER>
 __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, float *s_w,
-                                          uint32_t *s_ep, int *s_fail, int bid, int tid, int wave, int lane) {
-    constexpr int TPD = kDownRows / RPT;  // row sets per block
-    const int G = a.nsbd * 16;
-    const int NL = a.k * G;  // h record lines
-    const int row0 = (bid - a.NR - a.NG) * kDownRows;
-    const int q = tid >> 4, l16 = tid & 15;
-    const int tq = q / a.k, s = q - tq * a.k;
+                                          uint32_t *s_ep, int *s_fail, int bid, int s, int j, int tid, int wave,
+                                          int lane) {
+    const int G = a.G;
+    const int row0 = j * kDownRows;
+    const int rg = tid >> 4, l16 = tid & 15;
     const int sb = l16 >> 2, p = l16 & 3;
-    const bool grp_on = tq < TPD;
-    const bool t_on = grp_on && sb < a.nsbd;
+    const bool t_on = sb < a.nsbd;
     uint32_t *rec_a = reinterpret_cast<uint32_t *>(smem);
-    uint32_t *rec_b = rec_a + NL * 4;
-    float *rec_sp = reinterpret_cast<float *>(rec_b + NL * 4);
-    float *rec_xs = rec_sp + NL;
-    float *tot = rec_xs + NL;  // [kDownRows][k]
+    uint32_t *rec_b = rec_a + G * 4;
+    float *rec_sp = reinterpret_cast<float *>(rec_b + G * 4);
+    float *rec_xs = rec_sp + G;
     if (tid == 0) *s_ep = next_epoch(a.counters, bid);
     __syncthreads();
     const uint32_t ep = *s_ep;
@@ -535,17 +530,18 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         if (!ok && lane == 0) *s_fail = 1;
     }
     __syncthreads();
-    if (bid == a.NR + a.NG && tid < a.k) {  // the routing, for the caller
+    if (s == 0 && j == 0 && tid < a.k) {  // the routing, for the caller
         a.ids_out[tid] = s_ids[tid];
         a.w_out[tid] = s_w[tid];
     }
-    uint32_t e = grp_on ? s_ids[s] : 0u;
+    uint32_t e = s_ids[s];
     if (e >= (uint32_t)a.E) e = 0;
-    uint4 q0[RPT], q1[RPT];
-    uint32_t hw[RPT];
+    const float ws = s_w[s];
+    uint4 q0[4], q1[4];
+    uint32_t hw[4];
 #pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        const int row = row0 + tq * RPT + i;
+    for (int i = 0; i < 4; i++) {
+        const int row = row0 + rg * 4 + i;
         q0[i] = q1[i] = make_uint4(0u, 0u, 0u, 0u);
         hw[i] = 0u;
         if (t_on && row < a.D) {
@@ -555,60 +551,38 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
             hw[i] = *reinterpret_cast<const uint32_t *>(a.dn_hdr + blk * 16 + 4 * p);
         }
     }
-    PairScale ps[RPT];
+    PairScale ps[4];
 #pragma unroll
-    for (int i = 0; i < RPT; i++) {
+    for (int i = 0; i < 4; i++) {
         uint32_t h0, h1, h2, h3;
         quad_header(hw[i], h0, h1, h2, h3);
         ps[i] = pair_scale(h0, h1, h2, h3, p);
     }
-    // wait until every gate/up block has counted itself done
-    if (wave == 0) {
-        const uint32_t want = lane < kCounters ? (uint32_t)((a.NG - lane + kCounters - 1) / kCounters) : 0u;
-        const uint64_t t0 = wall_clock64();
-        while (true) {
-            const uint32_t got = lane < kCounters
-                                     ? __hip_atomic_load(hcount(a, ep, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                     : 0u;
-            if (__all(got >= want)) break;
-            if (wall_clock64() - t0 > kWaitTicks) {
-                if (lane == 0) *s_fail = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-    }
-    __syncthreads();
-    // h records: line L (= slot * G + group) holds words 0..9.  Threads
-    // qq*10 + wl (qq < 25) read word wl of lines qq + 25j: up to kPollLines
-    // lines per thread per pass, all loads in flight at once (normally one
-    // pass: the records were published before the count was taken).
+    // the slot's h records: thread q*10 + wl (q < 25) reads word wl of lines
+    // q + 25 m, all loads of a pass in flight at once
     bool ok = true;
     {
         const int qq = tid / kRecWords, wl = tid - qq * kRecWords;
-        const bool on = tid < kPollGroups * kRecWords;
-        const uint64_t *hrec = a.hl + (size_t)((bid - a.NR - a.NG) % kRecCopies) * kFusedBlocks * 16;
+        const bool on = tid < 25 * kRecWords;
+        const uint64_t *src = a.hl + (size_t)s * G * 16;
         const uint64_t t0 = wall_clock64();
-        for (int L0 = qq; L0 < NL; L0 += kPollGroups * kPollLines) {
+        for (int L0 = qq; L0 < G; L0 += 25 * 4) {
             while (true) {
-                uint64_t w[kPollLines];
-                uint32_t off = (uint32_t)(L0 * 16 + wl) * 8u;
+                uint64_t w[4];
 #pragma unroll
-                for (int j = 0; j < kPollLines; j++) {
-                    const bool use = on && L0 + kPollGroups * j < NL;
-                    w[j] = use ? hand_get(reinterpret_cast<const uint64_t *>(reinterpret_cast<const uint8_t *>(hrec) + off))
-                               : ((uint64_t)ep << 32);
-                    off += kPollGroups * 128u;
+                for (int m = 0; m < 4; m++) {
+                    const int L = L0 + 25 * m;
+                    w[m] = (on && L < G) ? hand_get(src + (size_t)L * 16 + wl) : ((uint64_t)ep << 32);
                 }
                 bool good = true;
 #pragma unroll
-                for (int j = 0; j < kPollLines; j++) good = good && tag_is(w[j], ep);
+                for (int m = 0; m < 4; m++) good = good && tag_is(w[m], ep);
                 if (__all(good)) {
 #pragma unroll
-                    for (int j = 0; j < kPollLines; j++) {
-                        const int L = L0 + kPollGroups * j;
-                        if (on && L < NL) {
-                            const uint32_t val = (uint32_t)w[j];
+                    for (int m = 0; m < 4; m++) {
+                        const int L = L0 + 25 * m;
+                        if (on && L < G) {
+                            const uint32_t val = (uint32_t)w[m];
                             if (wl < 4) rec_a[L * 4 + wl] = val;
                             else if (wl < 8) rec_b[L * 4 + wl - 4] = val;
                             else if (wl == 8) rec_sp[L] = __uint_as_float(val);
@@ -628,11 +602,9 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     }
     if (!ok) atomicOr(s_fail, 1);
     __syncthreads();
-    float v[RPT];
-#pragma unroll
-    for (int i = 0; i < RPT; i++) v[i] = 0.0f;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (t_on) {
-        const int gi = s * G + sb * 16 + 4 * p;  // first of the window's 4 groups
+        const int gi = sb * 16 + 4 * p;  // first of the window's 4 groups
         Limbs xl;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -647,35 +619,68 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         xl.xs_lo = xs4.x + xs4.y;
         xl.xs_hi = xs4.z + xs4.w;
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
+        for (int i = 0; i < 4; i++) {
             const uint32_t w8[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
             v[i] = q4k_pair_dot(w8, ps[i], xl);
         }
     }
-    const float t = group16_sum_transposed<RPT>(v, lane);
-    constexpr int SH = RPT == 8 ? 1 : (RPT == 4 ? 2 : (RPT == 2 ? 3 : 4));
-    if (grp_on && (l16 & ((1 << SH) - 1)) == 0) tot[(tq * RPT + (l16 >> SH)) * a.k + s] = t;
-    __syncthreads();
-    if (tid < kDownRows) {
-        const int row = row0 + tid;
-        float tv[16], wv[16];
-#pragma unroll
-        for (int sl = 0; sl < 16; sl++) {
-            tv[sl] = sl < a.k ? tot[tid * a.k + sl] : 0.0f;
-            wv[sl] = sl < a.k ? s_w[sl] : 0.0f;
-        }
-        if (row < a.D) {
-            float acc = a.accumulate ? a.out[row] : 0.0f;
-#pragma unroll
-            for (int sl = 0; sl < 16; sl++)
-                if (sl < a.k) acc += wv[sl] * tv[sl];
-            if (a.base) acc = a.base[row] + acc;
-            a.out[row] = *s_fail ? __int_as_float(0x7fc00000) : acc;
-        }
+    // row rg*4 + (l16 >> 2) in lanes l16 = 0, 4, 8, 12 of each group; the
+    // wave's 4 groups cover rows 16 wave + [0, 16) = one partial line
+    const float t = group16_sum_transposed<4>(v, lane);
+    if ((l16 & 3) == 0) {
+        const int rr = rg * 4 + (l16 >> 2);  // row within the block
+        const float val = *s_fail ? __int_as_float(0x7fc00000) : ws * t;
+        hand_put(a.pl + ((size_t)(s * a.NDg + j) * 4 + (rr >> 4)) * 16 + (rr & 15), __float_as_uint(val), ep);
     }
 }
 
-template <int PER, int RPT>
+// ---------------------------------------------------------------- combine
+// Rows 8c + [0, 8): out = base + (prev + sum over slots in slot order of the
+// weighted slot rows), the combine of moeForward (ops/moe.zig:67-76).  Lane
+// r < 8 reads row 8c + r of every slot (one word of a partial line each).
+__device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep, int bid, int c, int tid) {
+    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+    __syncthreads();
+    if (tid >= kCombRows) return;
+    const uint32_t ep = *s_ep;
+    const int row = c * kCombRows + tid;
+    if (row >= a.D) return;
+    const int j = row / kDownRows, rr = row % kDownRows;
+    float v[16];
+    bool ok = false;
+    const uint64_t t0 = wall_clock64();
+    while (true) {
+        uint64_t w[16];
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+            w[s] = s < a.k ? hand_get(a.pl + ((size_t)(s * a.NDg + j) * 4 + (rr >> 4)) * 16 + (rr & 15))
+                           : ((uint64_t)ep << 32);
+        bool good = true;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            good = good && tag_is(w[s], ep);
+            v[s] = __uint_as_float((uint32_t)w[s]);
+        }
+        if (good) {
+            ok = true;
+            break;
+        }
+        if (wall_clock64() - t0 > kWaitTicks) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    float acc = a.accumulate ? a.out[row] : 0.0f;
+#pragma unroll
+    for (int s = 0; s < 16; s++)
+        if (s < a.k) acc = acc + v[s];
+    if (a.base) acc = a.base[row] + acc;
+    if (!ok) {
+        acc = __int_as_float(0x7fc00000);
+        report_timeout(a.err, 1u);
+    }
+    a.out[row] = acc;
+}
+
+template <int PER>
 __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_ep;
@@ -683,19 +688,34 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     __shared__ float s_w[16];
     __shared__ int s_fail;
     const int bid = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (bid >= a.NR + a.NG + a.ND) {  // no role in this configuration: keep the counter in step
-        if (tid == 0) (void)next_epoch(a.counters, bid);
+    const int x = bid & 7, i = bid >> 3;
+    if (tid == 0) s_fail = 0;
+    int u = i;
+    if (u < a.NRg) {
+        role_router(a, smem, &s_ep, bid, tid, wave, lane);
         return;
     }
-    if (tid == 0) s_fail = 0;
-    if (bid < a.NR) {
-        role_router(a, smem, &s_ep, bid, tid, wave, lane);
-    } else if (bid < a.NR + a.NG) {
-        role_gate_up<PER>(a, smem, s_ids, &s_ep, &s_fail, bid, tid, wave, lane);
-    } else {
-        role_down<PER, RPT>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, tid, wave, lane);
+    u -= a.NRg;
+    if (u < a.SPG * a.G) {
+        const int s = x + 8 * (u / a.G);
+        if (s < a.k) {
+            role_gate_up<PER>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane);
+            if (tid == 0 && s_fail) report_timeout(a.err, 1u);
+            return;
+        }
+    } else if ((u -= a.SPG * a.G) < a.SPG * a.NDg) {
+        const int s = x + 8 * (u / a.NDg);
+        if (s < a.k) {
+            role_down<PER>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane);
+            if (tid == 0 && s_fail) report_timeout(a.err, 1u);
+            return;
+        }
+    } else if ((u -= a.SPG * a.NDg) < a.NCg) {
+        role_combine(a, &s_ep, bid, 8 * u + x, tid);
+        return;
     }
-    if (tid == 0 && s_fail) report_timeout(a.err, 1u);
+    // no role in this configuration: keep the counter in step
+    if (tid == 0) (void)next_epoch(a.counters, bid);
 }
 
 }  // namespace
@@ -706,18 +726,17 @@ FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
     if (D % 256 != 0 || D > 2048 || D < 256) return pl;
     if (Kd % 256 != 0 || Kd < F || Kd > 1024) return pl;  // 16 lanes = 4 super-blocks x 4 pairs
     if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return pl;
-    const int nsbd = Kd / 256;
-    int tpd = 1;  // row sets per down block: 16 groups of 16 threads over k slots
-    while (tpd * 2 <= 16 / k && tpd < kDownRows) tpd *= 2;
-    pl.rpt = kDownRows / tpd;
     pl.per = E <= 128 ? 2 : 4;
-    pl.NR = (E + 3) / 4;
-    pl.NG = k * nsbd * 16;
-    pl.ND = (D + kDownRows - 1) / kDownRows;
-    if (pl.NR + pl.NG + pl.ND > kFusedBlocks) return pl;
+    pl.NRg = (E + 31) / 32;
+    pl.SPG = (k + 7) / 8;
+    pl.G = Kd / 16;
+    pl.NDg = (D + kDownRows - 1) / kDownRows;
+    pl.NCg = pl.NDg;
+    if (8 * (pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg) > kFusedBlocks) return pl;
+    if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;                 // h record lines
+    if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;       // partial lines
     const size_t lds_router = (size_t)4 * D * 4 + 4 * 32 * 4 + 16;
-    const size_t NL = (size_t)k * nsbd * 16;
-    const size_t lds_down = NL * 40 + (size_t)kDownRows * k * 4;
+    const size_t lds_down = (size_t)pl.G * 40;
     pl.lds = lds_router > lds_down ? lds_router : lds_down;
     if (pl.lds < 64) pl.lds = 64;
     if (pl.lds > 64 * 1024) return pl;
@@ -725,9 +744,9 @@ FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
     return pl;
 }
 
-template <int PER, int RPT>
+template <int PER>
 static hipError_t launch_fused_t(const FusedArgs &fa, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((k_moe_fused<PER, RPT>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
+    hipLaunchKernelGGL((k_moe_fused<PER>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
     return hipGetLastError();
 }
 
@@ -750,7 +769,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     fa.counters = sc.counters;
     fa.lg = sc.lg;
     fa.hl = sc.hl;
-    fa.hcnt = sc.hcnt;
+    fa.pl = sc.pl;
     fa.err = sc.err;
     fa.E = (int)R.total_rows;
     fa.D = (int)GU.cols;
@@ -761,17 +780,12 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     fa.norm = (int)norm;
     fa.act = (int)act;
     fa.accumulate = accumulate;
-    fa.NR = pl.NR;
-    fa.NG = pl.NG;
-    fa.ND = pl.ND;
-    fa.F16 = (F + 15) / 16;
-    const bool p2 = pl.per == 2;
-    switch (pl.rpt) {
-    case 1: return p2 ? launch_fused_t<2, 1>(fa, pl.lds, s) : launch_fused_t<4, 1>(fa, pl.lds, s);
-    case 2: return p2 ? launch_fused_t<2, 2>(fa, pl.lds, s) : launch_fused_t<4, 2>(fa, pl.lds, s);
-    case 4: return p2 ? launch_fused_t<2, 4>(fa, pl.lds, s) : launch_fused_t<4, 4>(fa, pl.lds, s);
-    default: return p2 ? launch_fused_t<2, 8>(fa, pl.lds, s) : launch_fused_t<4, 8>(fa, pl.lds, s);
-    }
+    fa.NRg = pl.NRg;
+    fa.SPG = pl.SPG;
+    fa.G = pl.G;
+    fa.NDg = pl.NDg;
+    fa.NCg = pl.NCg;
+    return pl.per == 2 ? launch_fused_t<2>(fa, pl.lds, s) : launch_fused_t<4>(fa, pl.lds, s);
 }
 
 }  // namespace lt
