@@ -106,36 +106,6 @@ struct Limbs {
     float xs_lo, xs_hi;  // exact sums of groups 0+1 and 2+3
 };
 
-// 16 values -> limbs (a[4], b[4] packed bytes), scale sp and their sum.
-// A non-finite input makes sp NaN so that the dot products come out NaN.
-__device__ __forceinline__ void limbs16(const float (&v)[16], uint32_t (&a)[4], uint32_t (&b)[4], float &sp,
-                                        float &xs) {
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
-    float s[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) s[i] = v[2 * i] + v[2 * i + 1];
-    xs = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
-    const float inv = m > 0.0f ? 127.0f / m : 0.0f;
-    sp = m * (1.0f / 32512.0f);
-    if (!(fabsf(xs) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        uint32_t pa = 0, pb = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float t = v[4 * w + j] * inv;
-            const float fa = rintf(t);
-            const float fb = fminf(rintf((t - fa) * 256.0f), 127.0f);
-            pa |= ((uint32_t)(int)fa & 0xffu) << (8 * j);
-            pb |= ((uint32_t)(int)fb & 0xffu) << (8 * j);
-        }
-        a[w] = pa;
-        b[w] = pb;
-    }
-}
-
 // Q4_K scale decode of sub-block pair p (2p, 2p+1) from the header words
 // (h0 = d | dmin << 16, h1..h3 = scales[0..11]): get_scale_min_k4,
 // quant/dequant.zig:289-300.  Returns d*sc and dmin*mn of both sub-blocks.
@@ -195,11 +165,27 @@ __device__ __forceinline__ float q4k_pair_dot(const uint32_t (&w)[8], const Pair
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
+// Single-lane wait for one hand-over word (the probe), with a short sleep
+// between reads, so that waiting blocks put little load on the memory
+// system; the caller then reads everything it needs once.  False on timeout.
+__device__ __forceinline__ bool probe_wait(const uint64_t *w, uint32_t ep, uint64_t t0) {
+    while (!tag_is(hand_get(w), ep)) {
+        if (wall_clock64() - t0 > kWaitTicks) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return true;
+}
+
 // One wavefront waits for the E logits (logit r is word r & 3 of line
-// r >> 2) and returns them in v[j] = logit lane + 64j.  False on timeout.
+// r >> 2) and returns them in v[j] = logit lane + 64j.  Lane 0 first waits
+// for one line (chosen by block index, spreading the probes over the lines),
+// then the wavefront reads all of them.  False on timeout.
 template <int PER>
 __device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], int lane) {
     const uint64_t t0 = wall_clock64();
+    bool ok = true;
+    if (lane == 0) ok = probe_wait(a.lg + (size_t)(blockIdx.x % ((a.E + 3) >> 2)) * 16, ep, t0);
+    if (!__all(ok)) return false;
     while (true) {
         uint64_t wv[PER];
 #pragma unroll
@@ -207,21 +193,25 @@ __device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], in
             const int r = lane + 64 * j;
             wv[j] = r < a.E ? hand_get(a.lg + (r >> 2) * 16 + (r & 3)) : ((uint64_t)ep << 32);
         }
-        bool ok = true;
+        bool good = true;
 #pragma unroll
         for (int j = 0; j < PER; j++) {
-            ok = ok && tag_is(wv[j], ep);
+            good = good && tag_is(wv[j], ep);
             v[j] = __uint_as_float((uint32_t)wv[j]);
         }
-        if (__all(ok)) return true;
+        if (__all(good)) return true;
         if (wall_clock64() - t0 > kWaitTicks) return false;
         __builtin_amdgcn_s_sleep(1);
     }
 }
 
-// Bumps this block's launch counter; the new value is the launch epoch.
-__device__ __forceinline__ uint32_t next_epoch(uint32_t *counters, int bid) {
-    const uint32_t c = __hip_atomic_load(counters + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The launch counter of block bid: epoch_peek reads it (issued early, its
+// value used late), epoch_commit stores the incremented value; the new value
+// is the launch epoch.
+__device__ __forceinline__ uint32_t epoch_peek(const uint32_t *counters, int bid) {
+    return __hip_atomic_load(counters + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t epoch_commit(uint32_t *counters, int bid, uint32_t c) {
     __hip_atomic_store(counters + bid, c + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return c + 1u;
 }
@@ -249,9 +239,6 @@ __device__ __forceinline__ float half_sum4(const float (&v)[4], int lane) {
     return t;
 }
 
-__device__ __forceinline__ uint32_t swap_halves(uint32_t v, bool first) {
-    return __float_as_uint(xor32(__uint_as_float(v), first));
-}
 
 // ---------------------------------------------------------------- router
 // Wavefront w computes logit row bid*4 + w with dotf32's rounded operations
@@ -275,7 +262,7 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
             wv[i] = *reinterpret_cast<const float4 *>(wr + i * 256 + 4 * lane);
             xv[i] = *reinterpret_cast<const float4 *>(a.x + i * 256 + 4 * lane);
         }
-    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
 #pragma unroll
     for (int i = 0; i < 8; i++)
         if (i < a.nsb) {
@@ -286,11 +273,19 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
             pr.w = wv[i].w * xv[i].w;
             *reinterpret_cast<float4 *>(prod + i * 256 + 4 * lane) = pr;
         }
+    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, c0);
     __syncthreads();
     if (lane < 32) {
+        // chain lane: 8 reads in flight, then the 8 adds in order
         float acc = 0.0f;
-        const int nit = a.D >> 5;
-        for (int it = 0; it < nit; it++) acc = acc + prod[it * 32 + lane];
+        const int nit = a.D >> 5;  // a multiple of 8
+        for (int it0 = 0; it0 < nit; it0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = prod[(it0 + u) * 32 + lane];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = acc + v[u];
+        }
         chain[wave * 32 + lane] = acc;
     }
     __syncthreads();
@@ -329,48 +324,61 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
     const bool lane_on = pos < 4 * a.nsb;
     const bool first = p32_first(lane);
-    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
-    // activation limbs of this lane's 64-element window; each half converts
-    // 32 elements and the halves swap
-    Limbs xl;
-    {
-        float v0[16], v1[16];
-        const float *xp = a.x + sb * 256 + 64 * p + 32 * half;
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    // activation limbs, once per block: thread t converts elements 8t + [0, 8)
+    // (half of group t / 2) into LDS; each lane then reads its window's 4
+    // groups.  LDS: limb-a words [D/4], limb-b words [D/4], sp [D/16], xs [D/16].
+    uint32_t *la = reinterpret_cast<uint32_t *>(smem + 64);
+    uint32_t *lb = la + a.D / 4;
+    float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
+    float *lxs = lsp + a.D / 16;
+    if (tid < a.D / 8) {
+        const float4 f0 = *reinterpret_cast<const float4 *>(a.x + 8 * tid);
+        const float4 f1 = *reinterpret_cast<const float4 *>(a.x + 8 * tid + 4);
+        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        float m = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 f0 = lane_on ? *reinterpret_cast<const float4 *>(xp + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            float4 f1 = lane_on ? *reinterpret_cast<const float4 *>(xp + 16 + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            v0[4 * i] = f0.x; v0[4 * i + 1] = f0.y; v0[4 * i + 2] = f0.z; v0[4 * i + 3] = f0.w;
-            v1[4 * i] = f1.x; v1[4 * i + 1] = f1.y; v1[4 * i + 2] = f1.z; v1[4 * i + 3] = f1.w;
+        for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+        m = fmaxf(m, dpp<0xB1>(m));  // the other half of the group (lane ^ 1)
+        const float h8 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        const float xs = h8 + dpp<0xB1>(h8);
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        float sp = m * (1.0f / 32512.0f);
+        if (!(fabsf(xs) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);
+        uint32_t pa[2] = {0u, 0u}, pb[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float t = v[i] * inv;
+            const float fa = rintf(t);
+            const float fb = fminf(rintf((t - fa) * 256.0f), 127.0f);
+            pa[i >> 2] |= ((uint32_t)(int)fa & 0xffu) << (8 * (i & 3));
+            pb[i >> 2] |= ((uint32_t)(int)fb & 0xffu) << (8 * (i & 3));
         }
-        uint32_t a0[4], b0[4], a1[4], b1[4];
-        float sp0, xs0, sp1, xs1;
-        limbs16(v0, a0, b0, sp0, xs0);
-        limbs16(v1, a1, b1, sp1, xs1);
-        const float xs = xs0 + xs1;
-        const float xo = xor32(xs, first);
-        xl.xs_lo = half ? xo : xs;
-        xl.xs_hi = half ? xs : xo;
-        const float spo0 = xor32(sp0, first), spo1 = xor32(sp1, first);
-        xl.sp[0] = half ? spo0 : sp0;
-        xl.sp[1] = half ? spo1 : sp1;
-        xl.sp[2] = half ? sp0 : spo0;
-        xl.sp[3] = half ? sp1 : spo1;
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const uint32_t oa0 = swap_halves(a0[m], first), oa1 = swap_halves(a1[m], first);
-            const uint32_t ob0 = swap_halves(b0[m], first), ob1 = swap_halves(b1[m], first);
-            xl.a[0][m] = half ? oa0 : a0[m];
-            xl.a[1][m] = half ? oa1 : a1[m];
-            xl.a[2][m] = half ? a0[m] : oa0;
-            xl.a[3][m] = half ? a1[m] : oa1;
-            xl.b[0][m] = half ? ob0 : b0[m];
-            xl.b[1][m] = half ? ob1 : b1[m];
-            xl.b[2][m] = half ? b0[m] : ob0;
-            xl.b[3][m] = half ? b1[m] : ob1;
+        *reinterpret_cast<uint2 *>(la + 2 * tid) = make_uint2(pa[0], pa[1]);
+        *reinterpret_cast<uint2 *>(lb + 2 * tid) = make_uint2(pb[0], pb[1]);
+        if ((tid & 1) == 0) {
+            lsp[tid >> 1] = sp;
+            lxs[tid >> 1] = xs;
         }
     }
-    __syncthreads();  // s_ep
+    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, c0);
+    __syncthreads();  // limbs (and s_ep)
+    Limbs xl;
+    {
+        const int gi = lane_on ? sb * 16 + 4 * p : 0;  // first of the window's 4 groups
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint4 va = *reinterpret_cast<const uint4 *>(la + (gi + g) * 4);
+            const uint4 vb = *reinterpret_cast<const uint4 *>(lb + (gi + g) * 4);
+            xl.a[g][0] = va.x; xl.a[g][1] = va.y; xl.a[g][2] = va.z; xl.a[g][3] = va.w;
+            xl.b[g][0] = vb.x; xl.b[g][1] = vb.y; xl.b[g][2] = vb.z; xl.b[g][3] = vb.w;
+        }
+        const float4 sp4 = *reinterpret_cast<const float4 *>(lsp + gi);
+        const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + gi);
+        xl.sp[0] = sp4.x; xl.sp[1] = sp4.y; xl.sp[2] = sp4.z; xl.sp[3] = sp4.w;
+        xl.xs_lo = xs4.x + xs4.y;
+        xl.xs_hi = xs4.z + xs4.w;
+    }
     const uint32_t ep = *s_ep;
     if (wave == 0) {  // only this slot's expert: s + 1 selection rounds, no softmax
         float lv[PER];
@@ -517,9 +525,11 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     uint32_t *rec_b = rec_a + G * 4;
     float *rec_sp = reinterpret_cast<float *>(rec_b + G * 4);
     float *rec_xs = rec_sp + G;
-    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     __syncthreads();
     const uint32_t ep = *s_ep;
+    // full softmax + top-k before the weight loads: they then start a little
+    // after the gate/up blocks' loads, which are needed first
     if (wave == 0) {
         float lv[PER];
         const bool ok = poll_logits<PER>(a, ep, lv, lane);
@@ -530,13 +540,8 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         if (!ok && lane == 0) *s_fail = 1;
     }
     __syncthreads();
-    if (s == 0 && j == 0 && tid < a.k) {  // the routing, for the caller
-        a.ids_out[tid] = s_ids[tid];
-        a.w_out[tid] = s_w[tid];
-    }
     uint32_t e = s_ids[s];
     if (e >= (uint32_t)a.E) e = 0;
-    const float ws = s_w[s];
     uint4 q0[4], q1[4];
     uint32_t hw[4];
 #pragma unroll
@@ -558,8 +563,11 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         quad_header(hw[i], h0, h1, h2, h3);
         ps[i] = pair_scale(h0, h1, h2, h3, p);
     }
-    // the slot's h records: thread q*10 + wl (q < 25) reads word wl of lines
-    // q + 25 m, all loads of a pass in flight at once
+    // the slot's h records: thread 0 waits for one record line, then thread
+    // q*10 + wl (q < 25) reads word wl of lines q + 25 m, all loads of a
+    // pass in flight at once
+    if (tid == 0 && !probe_wait(a.hl + ((size_t)s * G + (size_t)(j % G)) * 16, ep, wall_clock64())) *s_fail = 1;
+    __syncthreads();
     bool ok = true;
     {
         const int qq = tid / kRecWords, wl = tid - qq * kRecWords;
@@ -601,7 +609,12 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         }
     }
     if (!ok) atomicOr(s_fail, 1);
-    __syncthreads();
+    __syncthreads();  // records, s_ids / s_w
+    if (s == 0 && j == 0 && tid < a.k) {  // the routing, for the caller
+        a.ids_out[tid] = s_ids[tid];
+        a.w_out[tid] = s_w[tid];
+    }
+    const float ws = s_w[s];
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (t_on) {
         const int gi = sb * 16 + 4 * p;  // first of the window's 4 groups
@@ -639,7 +652,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
 // weighted slot rows), the combine of moeForward (ops/moe.zig:67-76).  Lane
 // r < 8 reads row 8c + r of every slot (one word of a partial line each).
 __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep, int bid, int c, int tid) {
-    if (tid == 0) *s_ep = next_epoch(a.counters, bid);
+    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     __syncthreads();
     if (tid >= kCombRows) return;
     const uint32_t ep = *s_ep;
@@ -649,6 +662,7 @@ __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep,
     float v[16];
     bool ok = false;
     const uint64_t t0 = wall_clock64();
+    if (tid == 0) (void)probe_wait(a.pl + ((size_t)j * 4 + (rr >> 4)) * 16 + (rr & 15), ep, t0);
     while (true) {
         uint64_t w[16];
 #pragma unroll
@@ -715,7 +729,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
         return;
     }
     // no role in this configuration: keep the counter in step
-    if (tid == 0) (void)next_epoch(a.counters, bid);
+    if (tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
 }
 
 }  // namespace
@@ -737,7 +751,9 @@ FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
     if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;       // partial lines
     const size_t lds_router = (size_t)4 * D * 4 + 4 * 32 * 4 + 16;
     const size_t lds_down = (size_t)pl.G * 40;
+    const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
     pl.lds = lds_router > lds_down ? lds_router : lds_down;
+    if (lds_gu > pl.lds) pl.lds = lds_gu;
     if (pl.lds < 64) pl.lds = 64;
     if (pl.lds > 64 * 1024) return pl;
     pl.ok = true;
