@@ -13,11 +13,14 @@ Measurement:
     experts change from step to step.
   * The timed steps replay a hipGraph of 64 captured steps (no host launch
     cost per kernel); the eager (one API call per step) rate is reported too.
-  * roofline: the dominant kernel (expert gate/up) launched alone, one HIP
-    event pair per launch on the library's stream; achieved = algorithmic
-    bytes per launch / mean launch duration.  traffic = HBM bytes per launch
-    from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/*_pmc.json), scaled by
-    the counters' reading on a copy kernel of known size.
+  * roofline: the layer runs as one kernel (k_moe_fused); a HIP event pair
+    around back-to-back launches on the library's stream gives its mean
+    launch duration; achieved =
+    algorithmic bytes per launch (selected experts + router + x + out) /
+    mean launch duration.  traffic = HBM bytes per launch from rocprofv3
+    FETCH_SIZE + WRITE_SIZE (profiles/moe_fused_cfg3_pmc.json), scaled by
+    the counters' reading on a copy kernel of known size.  The three-launch
+    path (LT_MOE_UNFUSED) is timed per kernel too, for comparison.
   * cpu_baseline: the oracle's restatement of the reference CPU path
     (quantMatvecPar row split over a persistent pool + moeForward), timed on
     this host on a bounded sample of the same inputs.
@@ -44,6 +47,7 @@ Q4K_ROW_F = (F // 256) * 144          # 432 B: one down row
 EXPERT_BYTES = 2 * F * Q4K_ROW_D + D * Q4K_ROW_F      # 2,654,208 B per expert
 SELECTED_BYTES = K * EXPERT_BYTES                      # 21,233,664 B (metric denominator)
 LAYER_BYTES = SELECTED_BYTES + E * D * 4 + 4 * D * 4   # + fp32 router + x/out/h traffic -> 22,347,776 B
+FUSED_BYTES = SELECTED_BYTES + E * D * 4 + 2 * D * 4    # + router + x + out = 22,298,624 B per launch
 GATE_UP_WEIGHT_BYTES = K * 2 * F * Q4K_ROW_D           # 14,155,776 B
 GATE_UP_BYTES = GATE_UP_WEIGHT_BYTES + D * 4 + K * F * 4   # + x read + h write = 14,188,544 B
 DOWN_BYTES = K * D * Q4K_ROW_F + K * F * 4 + D * 4          # 7,077,888 + h + out
@@ -287,20 +291,22 @@ def main():
     dw = DeviceArray((K,), np.float32)
 
     def time_launches(fn, n):
-        evs = [(Event(), Event()) for _ in range(n)]
+        """Mean launch duration: n back-to-back launches between one HIP event
+        pair on the library's stream (per-launch event pairs would add their
+        own overhead to every launch)."""
         for i in range(min(n, 32)):
             fn(i)
         sync_stream(stream)
-        for i, (a, b) in enumerate(evs):
-            a.record(stream)
+        a, b = Event(), Event()
+        a.record(stream)
+        for i in range(n):
             fn(i)
-            b.record(stream)
+        b.record(stream)
         sync_stream(stream)
-        ms = [a.elapsed_ms(b) for a, b in evs]
-        for a, b in evs:
-            a.destroy()
-            b.destroy()
-        return statistics.mean(ms) * 1e3, statistics.median(ms) * 1e3
+        us = a.elapsed_ms(b) * 1e3 / n
+        a.destroy()
+        b.destroy()
+        return us
 
     def gu(i):
         r, g, d = copies[i % args.copies]
@@ -314,17 +320,20 @@ def main():
         r, g, d = copies[i % args.copies]
         ctx.router_topk(r, X.row(i % args.xpool), K, dids, dw, norm_topk=True)
 
-    gu_mean, gu_med = time_launches(gu, args.kernel_iters)
-    dn_mean, dn_med = time_launches(dn, args.kernel_iters)
-    rt_mean, rt_med = time_launches(rt, args.kernel_iters)
-    log(f"gate/up {gu_mean:.2f} us (median {gu_med:.2f}); down {dn_mean:.2f} us; router+topk {rt_mean:.2f} us")
+    fu_mean = time_launches(step, args.kernel_iters)
+    gu_mean = time_launches(gu, args.kernel_iters)
+    dn_mean = time_launches(dn, args.kernel_iters)
+    rt_mean = time_launches(rt, args.kernel_iters)
+    log(f"fused layer kernel {fu_mean:.2f} us per launch; three-launch path kernels alone: gate/up {gu_mean:.2f} us, "
+        f"down {dn_mean:.2f} us, router+topk {rt_mean:.2f} us")
 
-    gu_gbps = GATE_UP_BYTES / (gu_mean * 1e-6) / 1e9
-    traffic, pmc_path = pmc_traffic("expert_gate_up_q4k_cfg3")
-    roofline = {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                "frac": round(gu_gbps / PEAK_GBPS, 4), "traffic": None if traffic is None else round(traffic),
-                "kernel": "k_expert_gate_up_q4k", "algorithmic_bytes": GATE_UP_BYTES,
-                "mean_launch_us": round(gu_mean, 3), "median_launch_us": round(gu_med, 3)}
+    fu_gbps = FUSED_BYTES / (fu_mean * 1e-6) / 1e9
+    traffic, pmc_path = pmc_traffic("moe_fused_cfg3")
+    roofline = {"bound": "hbm", "achieved": round(fu_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(fu_gbps / PEAK_GBPS, 4), "traffic": None if traffic is None else round(traffic),
+                "kernel": "k_moe_fused", "algorithmic_bytes": FUSED_BYTES,
+                "mean_launch_us": round(fu_mean, 3), "timing": f"{args.kernel_iters} back-to-back launches, one HIP "
+                "event pair on the library stream"}
 
     layer_gbps = SELECTED_BYTES / (us_per_token * 1e-6) / 1e9
     result = {
@@ -341,10 +350,11 @@ def main():
         "device_us_per_token": round(dev_ms * 1e3 / args.steps, 3),
         "eager_us_per_token": round(eager_us, 3),
         "host_io_us_per_token": round(host_io_us, 3),
-        "kernel_us": {"router_topk": round(rt_mean, 3), "expert_gate_up": round(gu_mean, 3),
-                      "expert_down": round(dn_mean, 3)},
-        "kernel_gbps": {"expert_gate_up": round(gu_gbps, 1),
-                        "expert_down": round(DOWN_BYTES / (dn_mean * 1e-6) / 1e9, 1)},
+        "kernel_us": {"moe_fused": round(fu_mean, 3)},
+        "unfused_kernel_us": {"router_topk": round(rt_mean, 3), "expert_gate_up": round(gu_mean, 3),
+                              "expert_down": round(dn_mean, 3)},
+        "unfused_kernel_gbps": {"expert_gate_up": round(GATE_UP_BYTES / (gu_mean * 1e-6) / 1e9, 1),
+                                "expert_down": round(DOWN_BYTES / (dn_mean * 1e-6) / 1e9, 1)},
         "roofline": roofline,
         "parity": parity,
     }

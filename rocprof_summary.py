@@ -25,7 +25,7 @@ def kernel_rows(db):
 
 
 def short(name):
-    return name.split("(")[0].replace("void ", "")
+    return name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
 
 
 def trace(db, out, cmd):
