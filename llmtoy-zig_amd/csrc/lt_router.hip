@@ -173,6 +173,111 @@ hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, 
     return hipGetLastError();
 }
 
+// Batched F32 router (prefill): block = RB router rows x TB tokens.  Thread
+// (c = tid % 32, g = tid / 32) runs dotf32 chain c (elements 32 it + c) of
+// 4 rows x 4 tokens side by side -- the same rounded products and adds in
+// the same order per chain as k_router_f32, so the logits are identical --
+// with K staged through LDS 256 at a time (double-buffered) and each loaded
+// value used by 4 chains.  The 32 chain totals of a (row, token) then meet
+// in LDS for the (acc0+acc1)+(acc2+acc3) and ordered lane reduce.
+// Requires cols % 256 == 0.
+constexpr int RT_RB = 8, RT_TB = 16, RT_KC = 256;
+
+__global__ void __launch_bounds__(256) k_router_f32_tile(const float *__restrict__ W, const float *__restrict__ X,
+                                                         const float *__restrict__ bias, float *__restrict__ logits,
+                                                         int rows, int cols, int T) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float ws[2][RT_RB][RT_KC];
+    __shared__ __attribute__((aligned(16))) float xs[2][RT_TB][RT_KC];
+    __shared__ float ch[RT_RB][RT_TB][33];
+    const int tid = threadIdx.x, c = tid & 31, g = tid >> 5;
+    const int rg = g & 1, tg = g >> 1;  // rows 4 rg + [0, 4), tokens 4 tg + [0, 4)
+    const int r0 = blockIdx.x * RT_RB, t0 = blockIdx.y * RT_TB;
+    // stage loads: W tile 8 x 256 = 512 float4 (2 per thread), X tile
+    // 16 x 256 = 1024 float4 (4 per thread); rows / tokens past the end
+    // re-read the last valid one (never used)
+    const float *wsrc[2], *xsrc[4];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int f = tid + 256 * u, r = f >> 6;
+        wsrc[u] = W + (size_t)min(r0 + r, rows - 1) * cols + (f & 63) * 4;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int f = tid + 256 * u, t = f >> 6;
+        xsrc[u] = X + (size_t)min(t0 + t, T - 1) * cols + (f & 63) * 4;
+    }
+    float4 wr[2], xr[4];
+#pragma unroll
+    for (int u = 0; u < 2; u++) wr[u] = ldg16f(wsrc[u]);
+#pragma unroll
+    for (int u = 0; u < 4; u++) xr[u] = ldg16f(xsrc[u]);
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+    const int nkc = cols / RT_KC;
+    for (int kc = 0; kc < nkc; kc++) {
+        const int b = kc & 1;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int f = tid + 256 * u;
+            *reinterpret_cast<float4 *>(&ws[b][f >> 6][(f & 63) * 4]) = wr[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int f = tid + 256 * u;
+            *reinterpret_cast<float4 *>(&xs[b][f >> 6][(f & 63) * 4]) = xr[u];
+        }
+        __syncthreads();
+        if (kc + 1 < nkc) {  // next chunk's loads in flight during this one
+#pragma unroll
+            for (int u = 0; u < 2; u++) wr[u] = ldg16f(wsrc[u] + (kc + 1) * RT_KC);
+#pragma unroll
+            for (int u = 0; u < 4; u++) xr[u] = ldg16f(xsrc[u] + (kc + 1) * RT_KC);
+        }
+#pragma unroll
+        for (int it = 0; it < RT_KC / 32; it++) {
+            float wv[4], xv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) wv[i] = ws[b][4 * rg + i][it * 32 + c];
+#pragma unroll
+            for (int j = 0; j < 4; j++) xv[j] = xs[b][4 * tg + j][it * 32 + c];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float p = wv[i] * xv[j];
+                    acc[i][j] = acc[i][j] + p;
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) ch[4 * rg + i][4 * tg + j][c] = acc[i][j];
+    __syncthreads();
+    if (tid < RT_RB * RT_TB) {
+        const int r = tid / RT_TB, t = tid % RT_TB, row = r0 + r, tok = t0 + t;
+        if (row < rows && tok < T) {
+            const float *cv = ch[r][t];
+            float a8[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                const float s01 = cv[l] + cv[8 + l];
+                const float s23 = cv[16 + l] + cv[24 + l];
+                a8[l] = s01 + s23;
+            }
+            float sum = a8[0];
+#pragma unroll
+            for (int l = 1; l < 8; l++) sum = sum + a8[l];
+            if (bias) sum = sum + bias[row];
+            logits[(size_t)tok * rows + row] = sum;
+        }
+    }
+}
+
 // Softmax + top-k of token blockIdx.x of a batch of logits rows.
 template <int PER>
 __global__ void __launch_bounds__(64) k_topk_rows(const float *__restrict__ logits, int n, int k, int norm,
@@ -185,7 +290,10 @@ hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, cons
                                  uint32_t k, uint32_t norm, uint32_t *ids, float *w, hipStream_t s) {
     const TopkArgs none{nullptr, 0, 0, nullptr, nullptr, nullptr};
     const int rows = (int)R.total_rows;
-    if (R.type == 0)
+    if (R.type == 0 && R.cols % RT_KC == 0)
+        hipLaunchKernelGGL(k_router_f32_tile, dim3((rows + RT_RB - 1) / RT_RB, (T + RT_TB - 1) / RT_TB), dim3(256), 0,
+                           s, (const float *)R.p0, X, bias, logits, rows, (int)R.cols, T);
+    else if (R.type == 0)
         hipLaunchKernelGGL(k_router_f32<64>, dim3((rows + 1) / 2, T), dim3(64), 0, s, (const float *)R.p0, X, bias,
                            logits, rows, (int)R.cols, none);
     else
