@@ -51,8 +51,12 @@ enum {
     LT_HOST_IO = 1u << 0,       /* pointers are host memory; the call is synchronous */
     LT_MOE_NORM_TOPK = 1u << 1, /* renormalise the k selected weights to sum to 1 */
     LT_MOE_ACCUMULATE = 1u << 2, /* out += result (moeForward's contract, ops/moe.zig:17) */
-    LT_MOE_UNFUSED = 1u << 3     /* lt_moe_forward: run router, gate/up and down as separate launches
+    LT_MOE_UNFUSED = 1u << 3,    /* lt_moe_forward: run router, gate/up and down as separate launches
                                     instead of the single-launch kernel (same results to tolerance) */
+    LT_MOE_DETERMINISTIC = 1u << 4 /* lt_moe_forward: add the k expert outputs in slot order (bit-identical
+                                      results run to run, like the reference's moeForward, ops/moe.zig:67-76);
+                                      without it the single-launch kernel adds them with float atomics in
+                                      arrival order (faster; last bits may vary between runs) */
 };
 
 typedef struct lt_ctx lt_ctx;

@@ -655,7 +655,8 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
             return launch_rc(ctx,
                              lt::launch_moe_fused(pl, R, bias, GU, D, x, (int)k, (int)d_expert, act,
                                                   (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, base,
-                                                  (flags & LT_MOE_ACCUMULATE) ? 1 : 0, out, (uint32_t *)ctx->ids.p,
+                                                  (flags & LT_MOE_ACCUMULATE) ? 1 : 0,
+                                                  (flags & LT_MOE_DETERMINISTIC) ? 1 : 0, out, (uint32_t *)ctx->ids.p,
                                                   (float *)ctx->w.p, ctx->fsc, ctx->stream),
                              "moe_fused");
         }

@@ -281,6 +281,6 @@ struct FusedScratch {
 FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k);
 hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
                             const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,
-                            const float *base, int accumulate, float *out, uint32_t *ids_out, float *w_out,
-                            const FusedScratch &sc, hipStream_t s);
+                            const float *base, int accumulate, int deterministic, float *out, uint32_t *ids_out,
+                            float *w_out, const FusedScratch &sc, hipStream_t s);
 }  // namespace lt

@@ -10,9 +10,7 @@
 // Placement.  Workgroups are dealt to the 8 XCDs round robin, so the blocks
 // with equal bid % 8 ("group" x) share one XCD and its L2.  Slot s (the s-th
 // selected expert) is computed entirely inside group s % 8: its gate/up
-// blocks publish h, its down blocks read that h (traffic stays inside one
-// XCD) and publish their slot's weighted rows; only those small per-slot
-// partial outputs cross XCDs, to the combining blocks.  Within group x the
+// blocks publish h and its down blocks read that h.  Within group x the
 // in-group index i = bid / 8 picks the role:
 //
 //   i < NRg                 router: logit rows 4*bid + [0, 4), dotf32 order
@@ -23,6 +21,17 @@
 // (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = NCg = ceil(D /
 // 64)).  The placement only affects speed: every hand-over below is coherent
 // across XCDs.
+//
+// Combine.  By default the down blocks add their slot's weighted rows
+// straight into out with float atomics (agent scope): the router blocks
+// first set out to its starting value (0, the shared FFN output, or out +
+// that when accumulating) with coherent stores, and every router wavefront
+// waits for their acknowledgement before its block publishes logits, so
+// each add lands after the start value.  The order of the k adds to a row
+// varies, so the result's last bits may differ run to run.  With det set,
+// the down blocks publish per-slot partial rows instead and the combining
+// blocks add them in slot order (moeForward's order, ops/moe.zig:67-76):
+// bit-identical results at the cost of one more hand-over.
 //
 // Hand-over.  Results move as 64-bit words (32-bit payload, 32-bit launch
 // epoch) written and read with relaxed agent-scope atomics (global_store /
@@ -78,7 +87,7 @@ struct FusedArgs {
     uint64_t *hl;        // h record lines [k*G][16]
     uint64_t *pl;        // partial-output lines [k*NDg*4][16]
     uint32_t *err;       // host-visible error word
-    int E, D, nsb, F, nsbd, k, norm, act, accumulate;
+    int E, D, nsb, F, nsbd, k, norm, act, accumulate, det;
     int NRg, SPG, G, NDg, NCg;
 };
 
@@ -262,6 +271,13 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
             wv[i] = *reinterpret_cast<const float4 *>(wr + i * 256 + 4 * lane);
             xv[i] = *reinterpret_cast<const float4 *>(a.x + i * 256 + 4 * lane);
         }
+    // atomic combine: output row bid * 256 + tid starts at base, 0, or out +
+    // base (the router blocks cover 8 * NRg * 256 >= 2048 >= D rows)
+    const int orow = bid * kThreads + tid;
+    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
+        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
+        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const uint32_t c0 = epoch_peek(a.counters, bid);
 #pragma unroll
     for (int i = 0; i < 8; i++)
@@ -304,6 +320,9 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
         if (a.bias) sum = sum + a.bias[row];
         s_lg[wave] = sum;
     }
+    // every wavefront's output-row stores are acknowledged (memory-side)
+    // before the logits that let down blocks start adding
+    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid < 4 && bid * 4 + tid < a.E) hand_put(a.lg + bid * 16 + tid, __float_as_uint(s_lg[tid]), *s_ep);
 }
@@ -643,7 +662,10 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     if ((l16 & 3) == 0) {
         const int rr = rg * 4 + (l16 >> 2);  // row within the block
         const float val = *s_fail ? __int_as_float(0x7fc00000) : ws * t;
-        hand_put(a.pl + ((size_t)(s * a.NDg + j) * 4 + (rr >> 4)) * 16 + (rr & 15), __float_as_uint(val), ep);
+        if (a.det)
+            hand_put(a.pl + ((size_t)(s * a.NDg + j) * 4 + (rr >> 4)) * 16 + (rr & 15), __float_as_uint(val), ep);
+        else if (row0 + rr < a.D)
+            (void)__hip_atomic_fetch_add(a.out + row0 + rr, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -653,6 +675,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
 // r < 8 reads row 8c + r of every slot (one word of a partial line each).
 __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep, int bid, int c, int tid) {
     if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
+    if (!a.det) return;  // the down blocks added into out themselves
     __syncthreads();
     if (tid >= kCombRows) return;
     const uint32_t ep = *s_ep;
@@ -768,8 +791,8 @@ static hipError_t launch_fused_t(const FusedArgs &fa, size_t lds, hipStream_t s)
 
 hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
                             const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,
-                            const float *base, int accumulate, float *out, uint32_t *ids_out, float *w_out,
-                            const FusedScratch &sc, hipStream_t s) {
+                            const float *base, int accumulate, int deterministic, float *out, uint32_t *ids_out,
+                            float *w_out, const FusedScratch &sc, hipStream_t s) {
     FusedArgs fa;
     fa.router = reinterpret_cast<const float *>(R.p0);
     fa.bias = bias;
@@ -796,6 +819,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     fa.norm = (int)norm;
     fa.act = (int)act;
     fa.accumulate = accumulate;
+    fa.det = deterministic;
     fa.NRg = pl.NRg;
     fa.SPG = pl.SPG;
     fa.G = pl.G;

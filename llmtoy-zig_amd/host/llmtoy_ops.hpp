@@ -155,8 +155,11 @@ inline void quantMatvec(GpuContext &g, float *out, const RawMatrix &mat, const f
 // accumulate the weighted expert outputs into out (the caller zeroes it).
 // Same semantics as the reference: softmax over all router logits, top-k
 // with the lowest index winning ties, weights not renormalised, SiLU.
+// deterministic: add the expert outputs in slot order (bit-identical run to
+// run); otherwise the device adds them in arrival order.
 inline void moeForward(GpuContext &g, float *out, const RawMatrix &router_w, const RawMatrix &gate_up,
-                       const RawMatrix &down, const float *x, size_t n_experts_used, size_t d_expert) {
+                       const RawMatrix &down, const float *x, size_t n_experts_used, size_t d_expert,
+                       bool deterministic = false) {
     const size_t n_experts = router_w.rows;
     if (gate_up.rows != n_experts * 2 * d_expert || down.rows % n_experts)
         throw Exception(Error::Invalid, LT_ERR_INVALID, "moeForward: expert tensor shapes do not match the router");
@@ -164,7 +167,9 @@ inline void moeForward(GpuContext &g, float *out, const RawMatrix &router_w, con
     const lt_tensor *gu = g.tensor(gate_up, n_experts);
     const lt_tensor *dn = g.tensor(down, n_experts);
     g.check(lt_moe_forward(g.raw(), out, x, r, nullptr, gu, dn, nullptr, nullptr, nullptr, (uint32_t)n_experts_used,
-                           (uint32_t)d_expert, LT_ACT_SILU, LT_HOST_IO | LT_MOE_ACCUMULATE, nullptr, nullptr));
+                           (uint32_t)d_expert, LT_ACT_SILU,
+                           LT_HOST_IO | LT_MOE_ACCUMULATE | (deterministic ? LT_MOE_DETERMINISTIC : 0u), nullptr,
+                           nullptr));
 }
 
 // gpu/matvec.zig:497-647: one matrix resident on the device.

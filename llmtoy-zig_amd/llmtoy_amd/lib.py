@@ -28,6 +28,7 @@ from . import ggml
 LT_OK, LT_ERR_UNSUPPORTED, LT_ERR_INVALID, LT_ERR_DEVICE, LT_ERR_OOM = range(5)
 LT_HOST_IO, LT_MOE_NORM_TOPK, LT_MOE_ACCUMULATE = 1, 2, 4
 LT_MOE_UNFUSED = 1 << 3
+LT_MOE_DETERMINISTIC = 1 << 4
 ACT_SILU, ACT_GELU_TANH = 0, 1
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -228,15 +229,18 @@ class Context:
 
     def moe_forward(self, out, x, router: Tensor, gate_up: Tensor, down: Tensor, k: int, d_expert: int,
                     act=ACT_SILU, norm_topk=False, accumulate=False, bias=None, shared=None, out_ids=None,
-                    out_w=None, unfused=False):
+                    out_w=None, unfused=False, deterministic=False):
         """One token through the MoE layer (moeForward, ops/moe.zig:18-77).
 
         shared = (Wg, Wu, Wd) adds a dense shared FFN (Gemma4 layer).
         unfused = True runs router, gate/up and down as separate launches
-        instead of the single-launch kernel."""
+        instead of the single-launch kernel.  deterministic = True adds the
+        expert outputs in slot order (bit-identical run to run); by default
+        the single-launch kernel adds them with float atomics."""
         fl = self._io(out, x, bias, out_ids, out_w)
         fl |= (LT_MOE_NORM_TOPK if norm_topk else 0) | (LT_MOE_ACCUMULATE if accumulate else 0)
         fl |= LT_MOE_UNFUSED if unfused else 0
+        fl |= LT_MOE_DETERMINISTIC if deterministic else 0
         sg, su, sd = (t.handle for t in shared) if shared else (None, None, None)
         self._check(self.lib.lt_moe_forward(self.ptr, _ptr(out)[0], _ptr(x)[0], router.handle, _ptr(bias)[0],
                                             gate_up.handle, down.handle, sg, su, sd, k, d_expert, act, fl,
