@@ -264,6 +264,16 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
     const int row = bid * 4 + wave;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
+    // atomic combine: output row bid * 256 + tid starts at base, 0, or out +
+    // base (the router blocks cover 8 * NRg * 256 >= 2048 >= D rows).  The
+    // store goes out before the router loads: stores count in vmcnt until
+    // acknowledged, and the waits for those loads would otherwise also wait
+    // for it.
+    const int orow = bid * kThreads + tid;
+    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
+        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
+        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     float4 wv[8], xv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
@@ -271,13 +281,6 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, u
             wv[i] = *reinterpret_cast<const float4 *>(wr + i * 256 + 4 * lane);
             xv[i] = *reinterpret_cast<const float4 *>(a.x + i * 256 + 4 * lane);
         }
-    // atomic combine: output row bid * 256 + tid starts at base, 0, or out +
-    // base (the router blocks cover 8 * NRg * 256 >= 2048 >= D rows)
-    const int orow = bid * kThreads + tid;
-    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
-        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
-        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
     const uint32_t c0 = epoch_peek(a.counters, bid);
 #pragma unroll
     for (int i = 0; i < 8; i++)
