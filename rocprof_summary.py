@@ -8,7 +8,7 @@
       same counters on the 256 MiB device copies bench.py --calibrate runs,
       giving the scale factors bench.py applies (counter KiB / true KiB).
   mfma <db> <out.md> "<command>"
-      MFMA busy % per kernel: SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs).
+      MFMA utilisation per kernel from rocprofv3's MfmaUtil / MfmaFlopsBF16.
 """
 import json
 import sqlite3
@@ -95,20 +95,30 @@ def traffic(fetch_db, write_db, kernel, out, fetch_cmd, write_cmd):
 
 
 def mfma(db, out, cmd):
+    """rocprofv3's derived counters MfmaUtil (= sum of SQ_VALU_MFMA_BUSY_CYCLES
+    / (max GRBM_GUI_ACTIVE x SIMDs) x 100) and MfmaFlopsBF16, per kernel."""
     con = sqlite3.connect(db)
     rows = con.execute("select dispatch_id, kernel_name, counter_name, value from counters_collection").fetchall()
     per = {}
     for did, name, cname, val in rows:
-        per.setdefault((did, short(name)), {})[cname] = val
+        d = per.setdefault((did, short(name)), {})
+        d[cname] = d.get(cname, 0.0) + val  # derived counters: one row per dispatch
     by = {}
     for (did, name), c in per.items():
-        if "SQ_VALU_MFMA_BUSY_CYCLES" in c and c.get("GRBM_GUI_ACTIVE"):
-            by.setdefault(name, []).append(100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * SIMDS))
-    lines = ["# MFMA busy: batched prefill (config 5)", "", "Command (GPU box, repo root):", "", "```", cmd, "```", "",
-             "MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) x 100, per dispatch.", "",
-             "| kernel | dispatches | mean MFMA busy % |", "|---|---:|---:|"]
+        by.setdefault(name, []).append(c)
+    lines = ["# MFMA utilisation: batched prefill (config 5)", "", "Command (GPU box, repo root):", "", "```", cmd,
+             "```", "",
+             "MfmaUtil (rocprofv3 derived counter) = sum over the GPU of SQ_VALU_MFMA_BUSY_CYCLES / (max",
+             "GRBM_GUI_ACTIVE x SIMDs) x 100; MfmaFlopsBF16 = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 (bf16 MFMA FLOPs",
+             "issued, padding rows included).", "",
+             "| kernel | dispatches | mean MfmaUtil % | mean bf16 MFMA GFLOP |", "|---|---:|---:|---:|"]
     for k, v in sorted(by.items()):
-        lines.append(f"| `{k}` | {len(v)} | {statistics.mean(v):.2f} |")
+        util = [c["MfmaUtil"] for c in v if "MfmaUtil" in c]
+        fl = [c["MfmaFlopsBF16"] for c in v if "MfmaFlopsBF16" in c]
+        if not util:
+            continue
+        lines.append(f"| `{k}` | {len(v)} | {statistics.mean(util):.2f} | "
+                     f"{statistics.mean(fl) / 1e9 if fl else float('nan'):.2f} |")
     open(out, "w").write("\n".join(lines) + "\n")
 
 
