@@ -185,7 +185,8 @@ int ensure_fused(lt_ctx *ctx) {
     const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128;
     const size_t n_hl = (size_t)lt::kFusedBlocks * 128;
     const size_t n_pl = (size_t)lt::kFusedBlocks * 4 * 128;
-    const size_t bytes = n_cnt + n_lg + n_hl + n_pl;
+    const size_t n_xcc = (size_t)lt::kFusedBlocks * 4;
+    const size_t bytes = n_cnt + n_lg + n_hl + n_pl + n_xcc;
     void *p = nullptr;
     LT_HIP(ctx, hipMalloc(&p, bytes));
     hipError_t e = hipMemset(p, 0, bytes);
@@ -196,12 +197,18 @@ int ensure_fused(lt_ctx *ctx) {
         memset(hp, 0, 64);
         e = hipHostGetDevicePointer(&dp, hp, 0);
     }
+    uint8_t *b = (uint8_t *)p;
+    // same-XCD hand-overs through L2 when the placement allows;
+    // LT_FUSED_AGENT_HANDOVER=1 forces the memory round trip (testing)
+    int local = 0;
+    if (e == hipSuccess) e = lt::probe_xcd_groups((uint32_t *)(b + n_cnt + n_lg + n_hl + n_pl), ctx->stream, &local);
+    const char *agent = getenv("LT_FUSED_AGENT_HANDOVER");
+    if (agent && agent[0] == '1') local = 0;
     if (e != hipSuccess) {
         (void)hipFree(p);
         if (hp) (void)hipHostFree(hp);
         return hip_fail(ctx, e, "fused scratch");
     }
-    uint8_t *b = (uint8_t *)p;
     ctx->fused = p;
     ctx->fused_err = (uint32_t *)hp;
     ctx->fsc.counters = (uint32_t *)b;
@@ -209,6 +216,7 @@ int ensure_fused(lt_ctx *ctx) {
     ctx->fsc.hl = (uint64_t *)(b + n_cnt + n_lg);
     ctx->fsc.pl = (uint64_t *)(b + n_cnt + n_lg + n_hl);
     ctx->fsc.err = (uint32_t *)dp;
+    ctx->fsc.xcd_local = local;
     return LT_OK;
 }
 

@@ -277,7 +277,13 @@ struct FusedScratch {
     uint64_t *hl;        // [kFusedBlocks][16] h record lines
     uint64_t *pl;        // [4 * kFusedBlocks][16] partial-output lines
     uint32_t *err;       // host-mapped error word (device address)
+    int xcd_local;       // blocks with equal index % 8 share an XCD (probe_xcd_groups)
 };
+// Launches kFusedBlocks one-wave blocks that record their XCD in dev_ids
+// [kFusedBlocks], waits, and sets *local when every block b ran on the XCD
+// of block b % 8 (the round-robin placement the fused kernel's same-XCD
+// hand-overs rely on for speed).
+hipError_t probe_xcd_groups(uint32_t *dev_ids, hipStream_t s, int *local);
 FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k);
 hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
                             const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,

@@ -26,8 +26,8 @@
 // straight into out with float atomics (agent scope): the router blocks
 // first set out to its starting value (0, the shared FFN output, or out +
 // that when accumulating) with coherent stores, and every router wavefront
-// waits for their acknowledgement before its block publishes logits, so
-// each add lands after the start value.  The order of the k adds to a row
+// waits for their acknowledgement before it publishes its logit, so each
+// add lands after the start value.  The order of the k adds to a row
 // varies, so the result's last bits may differ run to run.  With det set,
 // the down blocks publish per-slot partial rows instead and the combining
 // blocks add them in slot order (moeForward's order, ops/moe.zig:67-76):
@@ -36,8 +36,8 @@
 // Hand-over.  Results move as 64-bit words (32-bit payload, 32-bit launch
 // epoch) written and read with relaxed agent-scope atomics (global_store /
 // global_load with sc1: coherent across the XCDs' L2s without cache
-// flushes).  Every 128-byte line of hand-over words has exactly one writing
-// wavefront.  A reader waits until every word it needs carries the current
+// flushes).  Every 128-byte line of hand-over words is written by one
+// workgroup.  A reader waits until every word it needs carries the current
 // epoch.  The epoch of a launch is the launch count: block b keeps its own
 // counter counters[b] (no contended atomic), and since every launch runs the
 // same kFusedBlocks blocks, all counters stay equal.
@@ -87,12 +87,24 @@ struct FusedArgs {
     uint64_t *hl;        // h record lines [k*G][16]
     uint64_t *pl;        // partial-output lines [k*NDg*4][16]
     uint32_t *err;       // host-visible error word
-    int E, D, nsb, F, nsbd, k, norm, act, accumulate, det;
+    int E, D, nsb, F, nsbd, k, norm, act, accumulate, det, local;
     int NRg, SPG, G, NDg, NCg;
 };
 
 __device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
     __hip_atomic_store(p, (uint64_t)v | ((uint64_t)ep << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A word read only by blocks of the writer's own group.  With local set
+// (blocks with equal bid % 8 share an XCD: checked once per context by
+// probe_xcd_groups), a workgroup-scope store leaves it dirty in that XCD's
+// L2, where the readers' agent-scope loads find it: about 0.2 us instead
+// of the 0.6 us a round trip through memory takes.  Otherwise agent scope.
+__device__ __forceinline__ void hand_put_group(uint64_t *p, uint32_t v, uint32_t ep, int local) {
+    const uint64_t w = (uint64_t)v | ((uint64_t)ep << 32);
+    if (local)
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t hand_get(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -148,13 +160,16 @@ __device__ __forceinline__ void quad_header(uint32_t mine, uint32_t &h0, uint32_
 }
 
 // Dot of one Q4_K sub-block pair (64 weights: qs bytes 32p..32p+31 of a
-// super-block, w[0..7]) with the limbs of the matching 64 activations.
-__device__ __forceinline__ float q4k_pair_dot(const uint32_t (&w)[8], const PairScale &s, const Limbs &x) {
+// super-block, w[0..7]) with the limbs of the matching 64 activations; the
+// _nib form takes the nibbles already unpacked (lo[m] = w[m] & 0x0f0f0f0f,
+// hi[m] = (w[m] >> 4) & 0x0f0f0f0f).
+__device__ __forceinline__ float q4k_pair_dot_nib(const uint32_t (&lo)[8], const uint32_t (&hi)[8], const PairScale &s,
+                                                  const Limbs &x) {
     int A[4] = {0, 0, 0, 0}, B[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int m = 0; m < 4; m++) {
-        const uint32_t lo0 = w[m] & 0x0f0f0f0fu, hi0 = (w[m] >> 4) & 0x0f0f0f0fu;
-        const uint32_t lo1 = w[4 + m] & 0x0f0f0f0fu, hi1 = (w[4 + m] >> 4) & 0x0f0f0f0fu;
+        const uint32_t lo0 = lo[m], hi0 = hi[m];
+        const uint32_t lo1 = lo[4 + m], hi1 = hi[4 + m];
         A[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.a[0][m], A[0], false);
         B[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.b[0][m], B[0], false);
         A[1] = __builtin_amdgcn_sdot4((int)lo1, (int)x.a[1][m], A[1], false);
@@ -170,6 +185,16 @@ __device__ __forceinline__ float q4k_pair_dot(const uint32_t (&w)[8], const Pair
     const float t_lo = x.sp[0] * c[0] + x.sp[1] * c[1];
     const float t_hi = x.sp[2] * c[2] + x.sp[3] * c[3];
     return (s.dsc0 * t_lo - s.dmn0 * x.xs_lo) + (s.dsc1 * t_hi - s.dmn1 * x.xs_hi);
+}
+
+__device__ __forceinline__ float q4k_pair_dot(const uint32_t (&w)[8], const PairScale &s, const Limbs &x) {
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        lo[m] = w[m] & 0x0f0f0f0fu;
+        hi[m] = (w[m] >> 4) & 0x0f0f0f0fu;
+    }
+    return q4k_pair_dot_nib(lo, hi, s, x);
 }
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -255,79 +280,78 @@ __device__ __forceinline__ float half_sum4(const float (&v)[4], int lane) {
 // one rounding per product, 32 sequential chains over the 32-element
 // strides, (acc0+acc1)+(acc2+acc3) per lane l < 8, the ordered 8-lane
 // reduce, then + bias.  D % 256 == 0 and D <= 2048 (checked by the host).
-__device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int bid, int tid,
-                                            int wave, int lane) {
+// The row arrives as nsb chunks of 256 elements, one float4 per lane each,
+// all loads in flight at once.  As each chunk lands its products pass
+// through the wavefront's LDS area to the chain lanes (lane l < 32 owns
+// chain l, elements l + 32 it), which add its 8 strides: the chains run
+// while later chunks are still in flight.  The final reduce stays in
+// registers and every wavefront publishes its own logit, so the block never
+// synchronises.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, int bid, int tid, int wave,
+                                            int lane) {
 #pragma clang fp contract(off)
-    float *prod = reinterpret_cast<float *>(smem) + wave * a.D;
-    float *chain = reinterpret_cast<float *>(smem) + 4 * a.D;  // [4][32]
-    float *s_lg = chain + 4 * 32;                               // [4]
+    float *prod = reinterpret_cast<float *>(smem) + wave * 512;  // two chunk buffers
     const int row = bid * 4 + wave;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
     // atomic combine: output row bid * 256 + tid starts at base, 0, or out +
     // base (the router blocks cover 8 * NRg * 256 >= 2048 >= D rows).  The
     // store goes out before the router loads: stores count in vmcnt until
-    // acknowledged, and the waits for those loads would otherwise also wait
-    // for it.
+    // acknowledged, and it is acknowledged long before the loads return.
     const int orow = bid * kThreads + tid;
     if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
         const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
         __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // every load unconditional (chunk indices clamped), so that the waits
+    // for chunk i count only the loads issued after it
     float4 wv[8], xv[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-        if (i < a.nsb) {
-            wv[i] = *reinterpret_cast<const float4 *>(wr + i * 256 + 4 * lane);
-            xv[i] = *reinterpret_cast<const float4 *>(a.x + i * 256 + 4 * lane);
-        }
+    for (int i = 0; i < 8; i++) {
+        const int ci = i < a.nsb ? i : a.nsb - 1;
+        wv[i] = *reinterpret_cast<const float4 *>(wr + ci * 256 + 4 * lane);
+        xv[i] = *reinterpret_cast<const float4 *>(a.x + ci * 256 + 4 * lane);
+    }
+    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
     const uint32_t c0 = epoch_peek(a.counters, bid);
+    float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 8; i++) {
         if (i < a.nsb) {
             float4 pr;
             pr.x = wv[i].x * xv[i].x;
             pr.y = wv[i].y * xv[i].y;
             pr.z = wv[i].z * xv[i].z;
             pr.w = wv[i].w * xv[i].w;
-            *reinterpret_cast<float4 *>(prod + i * 256 + 4 * lane) = pr;
-        }
-    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, c0);
-    __syncthreads();
-    if (lane < 32) {
-        // chain lane: 8 reads in flight, then the 8 adds in order
-        float acc = 0.0f;
-        const int nit = a.D >> 5;  // a multiple of 8
-        for (int it0 = 0; it0 < nit; it0 += 8) {
+            float *buf = prod + (i & 1) * 256;
+            *reinterpret_cast<float4 *>(buf + 4 * lane) = pr;
+            wave_lds_sync();
             float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = prod[(it0 + u) * 32 + lane];
+            for (int u = 0; u < 8; u++) v[u] = buf[u * 32 + (lane & 31)];
 #pragma unroll
             for (int u = 0; u < 8; u++) acc = acc + v[u];
         }
-        chain[wave * 32 + lane] = acc;
     }
-    __syncthreads();
-    if (lane == 0 && valid) {
-        const float *ch = chain + wave * 32;
-        float acc8[8];
+    // lanes l < 8: (c[l] + c[l+8]) + (c[l+16] + c[l+24]); then the ordered
+    // sum over l
+    const float s2 = acc + dpp<0x128>(acc);
+    const float a8 = s2 + xor16(s2);
+    float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), 0));
 #pragma unroll
-        for (int l = 0; l < 8; l++) {
-            const float s01 = ch[l] + ch[8 + l];
-            const float s23 = ch[16 + l] + ch[24 + l];
-            acc8[l] = s01 + s23;
-        }
-        float sum = acc8[0];
-#pragma unroll
-        for (int l = 1; l < 8; l++) sum = sum + acc8[l];
-        if (a.bias) sum = sum + a.bias[row];
-        s_lg[wave] = sum;
-    }
-    // every wavefront's output-row stores are acknowledged (memory-side)
-    // before the logits that let down blocks start adding
+    for (int l = 1; l < 8; l++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), l));
+    if (a.bias) sum = sum + bias;
+    // this wavefront's output-row stores are acknowledged (memory-side)
+    // before the logit that lets down blocks start adding
     if (!a.det) __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid < 4 && bid * 4 + tid < a.E) hand_put(a.lg + bid * 16 + tid, __float_as_uint(s_lg[tid]), *s_ep);
+    if (lane == 0 && valid) hand_put(a.lg + bid * 16 + wave, __float_as_uint(sum), c0 + 1u);
+    if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
 // ---------------------------------------------------------------- gate/up
@@ -479,7 +503,7 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
         const uint32_t gb = (uint32_t)__shfl((int)pb, src, 64);
         uint32_t word = lane < 4 ? ga : (lane < 8 ? gb : (lane == 8 ? __float_as_uint(sp) : __float_as_uint(xs)));
         if (*s_fail) word = lane < 8 ? 0u : 0x7fc00000u;  // routing timed out: NaN record
-        if (lane < kRecWords) hand_put(a.hl + (size_t)g * 16 + lane, word, ep);
+        if (lane < kRecWords) hand_put_group(a.hl + (size_t)g * 16 + lane, word, ep, a.local);
     }
 }
 
@@ -578,12 +602,25 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
             hw[i] = *reinterpret_cast<const uint32_t *>(a.dn_hdr + blk * 16 + 4 * p);
         }
     }
+    // scales decoded, and the nibbles of rows 0-1 unpacked, while the h
+    // records are awaited (the dots after their arrival are VALU-bound; all
+    // four rows unpacked would exceed 128 VGPRs); the empty asm keeps the
+    // compiler from sinking the unpacking to its use
     PairScale ps[4];
+    uint32_t nlo[2][8], nhi[2][8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         uint32_t h0, h1, h2, h3;
         quad_header(hw[i], h0, h1, h2, h3);
         ps[i] = pair_scale(h0, h1, h2, h3, p);
+        if (i >= 2) continue;
+        const uint32_t w8[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            nlo[i][m] = w8[m] & 0x0f0f0f0fu;
+            nhi[i][m] = (w8[m] >> 4) & 0x0f0f0f0fu;
+            asm volatile("" : "+v"(nlo[i][m]), "+v"(nhi[i][m]));
+        }
     }
     // the slot's h records: thread 0 waits for one record line, then thread
     // q*10 + wl (q < 25) reads word wl of lines q + 25 m, all loads of a
@@ -655,8 +692,12 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         xl.xs_hi = xs4.z + xs4.w;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t w8[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
-            v[i] = q4k_pair_dot(w8, ps[i], xl);
+            if (i < 2) {
+                v[i] = q4k_pair_dot_nib(nlo[i], nhi[i], ps[i], xl);
+            } else {
+                const uint32_t w8[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
+                v[i] = q4k_pair_dot(w8, ps[i], xl);
+            }
         }
     }
     // row rg*4 + (l16 >> 2) in lanes l16 = 0, 4, 8, 12 of each group; the
@@ -732,7 +773,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     if (tid == 0) s_fail = 0;
     int u = i;
     if (u < a.NRg) {
-        role_router(a, smem, &s_ep, bid, tid, wave, lane);
+        role_router(a, smem, bid, tid, wave, lane);
         return;
     }
     u -= a.NRg;
@@ -758,7 +799,29 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     if (tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
 }
 
+// Block b records the XCD it runs on (hardware register XCC_ID).
+__global__ void k_xcc_probe(uint32_t *ids) {
+    if (threadIdx.x != 0) return;
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    ids[blockIdx.x] = v & 0xfu;
+}
+
 }  // namespace
+
+hipError_t probe_xcd_groups(uint32_t *dev_ids, hipStream_t s, int *local) {
+    *local = 0;
+    hipLaunchKernelGGL(k_xcc_probe, dim3(kFusedBlocks), dim3(64), 0, s, dev_ids);
+    hipError_t e = hipGetLastError();
+    uint32_t ids[kFusedBlocks];
+    if (e == hipSuccess) e = hipMemcpyAsync(ids, dev_ids, sizeof(ids), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return e;
+    int same = 1;
+    for (int b = 8; b < kFusedBlocks; b++) same &= ids[b] == ids[b & 7];
+    *local = same;
+    return hipSuccess;
+}
 
 FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
     FusedPlan pl{};
@@ -775,7 +838,7 @@ FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
     if (8 * (pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg) > kFusedBlocks) return pl;
     if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;                 // h record lines
     if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;       // partial lines
-    const size_t lds_router = (size_t)4 * D * 4 + 4 * 32 * 4 + 16;
+    const size_t lds_router = (size_t)4 * 512 * 4;
     const size_t lds_down = (size_t)pl.G * 40;
     const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
     pl.lds = lds_router > lds_down ? lds_router : lds_down;
@@ -823,6 +886,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     fa.act = (int)act;
     fa.accumulate = accumulate;
     fa.det = deterministic;
+    fa.local = sc.xcd_local;
     fa.NRg = pl.NRg;
     fa.SPG = pl.SPG;
     fa.G = pl.G;
