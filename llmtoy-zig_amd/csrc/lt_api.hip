@@ -182,7 +182,7 @@ int launch_rc(lt_ctx *ctx, hipError_t e, const char *what) {
 int ensure_fused(lt_ctx *ctx) {
     if (ctx->fused) return LT_OK;
     const size_t n_cnt = (size_t)lt::kFusedBlocks * 4;
-    const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128;
+    const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128 * 8;
     const size_t n_hl = (size_t)lt::kFusedBlocks * 128;
     const size_t n_pl = (size_t)lt::kFusedBlocks * 4 * 128;
     const size_t n_xcc = (size_t)lt::kFusedBlocks * 4;

@@ -259,6 +259,7 @@ hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint
 // keeps the per-block launch counters equal.
 constexpr int kFusedBlocks = 1024;
 constexpr int kFusedMaxRouterBlocks = 64;  // E <= 256, 4 logits per block
+constexpr int kLgCopy = kFusedMaxRouterBlocks * 16;  // words per copy of the logits (8 copies)
 struct FusedPlan {
     bool ok;     // the shape fits the fused kernel
     int per;     // logits per lane in the top-k wavefront (2 or 4)
@@ -273,7 +274,7 @@ struct FusedPlan {
 // when allocated and never cleared again (words carry launch epochs).
 struct FusedScratch {
     uint32_t *counters;  // [kFusedBlocks]
-    uint64_t *lg;        // [kFusedMaxRouterBlocks][16] logit lines
+    uint64_t *lg;        // [8][kLgCopy] logit words, one copy per XCD group
     uint64_t *hl;        // [kFusedBlocks][16] h record lines
     uint64_t *pl;        // [4 * kFusedBlocks][16] partial-output lines
     uint32_t *err;       // host-mapped error word (device address)

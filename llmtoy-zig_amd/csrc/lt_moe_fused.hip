@@ -34,10 +34,11 @@
 // bit-identical results at the cost of one more hand-over.
 //
 // Hand-over.  Results move as 64-bit words (32-bit payload, 32-bit launch
-// epoch) written and read with relaxed agent-scope atomics (global_store /
-// global_load with sc1: coherent across the XCDs' L2s without cache
-// flushes).  Every 128-byte line of hand-over words is written by one
-// workgroup.  A reader waits until every word it needs carries the current
+// epoch) written and read with relaxed atomics: agent-scope loads (sc1:
+// coherent across the XCDs' L2s without cache flushes) and agent-scope
+// stores, or workgroup-scope stores for the h records, which only blocks on
+// the writer's XCD read (see hand_put_group).  Each word has one writing
+// wavefront.  A reader waits until every word it needs carries the current
 // epoch.  The epoch of a launch is the launch count: block b keeps its own
 // counter counters[b] (no contended atomic), and since every launch runs the
 // same kFusedBlocks blocks, all counters stay equal.
@@ -83,7 +84,7 @@ struct FusedArgs {
     uint32_t *ids_out;
     float *w_out;
     uint32_t *counters;  // [kFusedBlocks]
-    uint64_t *lg;        // logit lines [8*NRg][16]
+    uint64_t *lg;        // logits, 8 copies of kLgCopy words (logit r = word r)
     uint64_t *hl;        // h record lines [k*G][16]
     uint64_t *pl;        // partial-output lines [k*NDg*4][16]
     uint32_t *err;       // host-visible error word
@@ -210,22 +211,25 @@ __device__ __forceinline__ bool probe_wait(const uint64_t *w, uint32_t ep, uint6
     return true;
 }
 
-// One wavefront waits for the E logits (logit r is word r & 3 of line
-// r >> 2) and returns them in v[j] = logit lane + 64j.  Lane 0 first waits
-// for one line (chosen by block index, spreading the probes over the lines),
+// One wavefront waits for the E logits and returns them in v[j] = logit
+// lane + 64j.  The router publishes 8 copies (logit r = word r of each) and
+// a block reads copy bid % 8: with one copy, the 640 reading wavefronts
+// queued on the same few lines at the memory side.  Lane 0 first waits for
+// one line (chosen by block index, spreading the probes over the lines),
 // then the wavefront reads all of them.  False on timeout.
 template <int PER>
 __device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], int lane) {
     const uint64_t t0 = wall_clock64();
     bool ok = true;
-    if (lane == 0) ok = probe_wait(a.lg + (size_t)(blockIdx.x % ((a.E + 3) >> 2)) * 16, ep, t0);
+    const uint64_t *lg = a.lg + (size_t)(blockIdx.x & 7) * kLgCopy;  // this group's copy
+    if (lane == 0) ok = probe_wait(lg + (size_t)((blockIdx.x >> 3) % ((a.E + 15) >> 4)) * 16, ep, t0);
     if (!__all(ok)) return false;
     while (true) {
         uint64_t wv[PER];
 #pragma unroll
         for (int j = 0; j < PER; j++) {
             const int r = lane + 64 * j;
-            wv[j] = r < a.E ? hand_get(a.lg + (r >> 2) * 16 + (r & 3)) : ((uint64_t)ep << 32);
+            wv[j] = r < a.E ? hand_get(lg + r) : ((uint64_t)ep << 32);
         }
         bool good = true;
 #pragma unroll
@@ -350,7 +354,7 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
     // this wavefront's output-row stores are acknowledged (memory-side)
     // before the logit that lets down blocks start adding
     if (!a.det) __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0 && valid) hand_put(a.lg + bid * 16 + wave, __float_as_uint(sum), c0 + 1u);
+    if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
