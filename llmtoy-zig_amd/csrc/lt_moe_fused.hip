@@ -89,6 +89,7 @@ struct FusedArgs {
     uint64_t *pl;        // partial-output lines [k*NDg*4][16]
     uint32_t *err;       // host-visible error word
     int E, D, nsb, F, nsbd, k, norm, act, accumulate, det, local;
+    int dn_delay;  // wall-clock ticks from seeing the logits to the down weight loads
     int NRg, SPG, G, NDg, NCg;
 };
 
@@ -578,11 +579,15 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     __syncthreads();
     const uint32_t ep = *s_ep;
-    // full softmax + top-k before the weight loads: they then start a little
-    // after the gate/up blocks' loads, which are needed first
+    // The gate/up weights are needed first: the down weight loads wait until
+    // dn_delay ticks after the logits are seen, when most of the gate/up
+    // stream has arrived, so that its tail is not shared with them (the
+    // down weights then land shortly before the h records).
+    __shared__ uint64_t s_seen;
     if (wave == 0) {
         float lv[PER];
         const bool ok = poll_logits<PER>(a, ep, lv, lane);
+        if (lane == 0) s_seen = wall_clock64();
         uint32_t key[PER];
         int my_i;
         float my_p;
@@ -592,6 +597,10 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     __syncthreads();
     uint32_t e = s_ids[s];
     if (e >= (uint32_t)a.E) e = 0;
+    {
+        const uint64_t t_go = s_seen + (uint64_t)a.dn_delay;
+        while (wall_clock64() < t_go) __builtin_amdgcn_s_sleep(4);
+    }
     uint4 q0[4], q1[4];
     uint32_t hw[4];
 #pragma unroll
@@ -891,6 +900,13 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     fa.accumulate = accumulate;
     fa.det = deterministic;
     fa.local = sc.xcd_local;
+    // Down weight loads start 0.7 us (the gate/up blocks' top-k) plus the
+    // time 80% of the gate/up weights take at 5 TB/s (the burst rate
+    // measured for this stream) after the logits are seen, in 10 ns ticks;
+    // tuned on config 3 (14.2 MB: 296 ticks; 200 or 360 are 0.2-0.4 us
+    // slower per layer).
+    const double gu_bytes = (double)k * 2.0 * F * fa.nsb * 144.0;
+    fa.dn_delay = 70 + (int)(0.8 * gu_bytes / 50000.0);
     fa.NRg = pl.NRg;
     fa.SPG = pl.SPG;
     fa.G = pl.G;
