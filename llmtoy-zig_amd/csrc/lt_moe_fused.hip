@@ -165,11 +165,28 @@ __device__ __forceinline__ void quad_header(uint32_t mine, uint32_t &h0, uint32_
 // super-block, w[0..7]) with the limbs of the matching 64 activations; the
 // _nib form takes the nibbles already unpacked (lo[m] = w[m] & 0x0f0f0f0f,
 // hi[m] = (w[m] >> 4) & 0x0f0f0f0f).
+// First product of an accumulator chain: the three-operand v_dot4_i32_i8
+// with an inline 0 (the compiler's choice, v_dot4c, needs a v_mov of 0
+// first: 8 of the pair's ~56 VALU instructions).
+__device__ __forceinline__ int sdot4_first(int a, int b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ float q4k_pair_dot_nib(const uint32_t (&lo)[8], const uint32_t (&hi)[8], const PairScale &s,
                                                   const Limbs &x) {
-    int A[4] = {0, 0, 0, 0}, B[4] = {0, 0, 0, 0};
+    int A[4], B[4];
+    A[0] = sdot4_first((int)lo[0], (int)x.a[0][0]);
+    B[0] = sdot4_first((int)lo[0], (int)x.b[0][0]);
+    A[1] = sdot4_first((int)lo[4], (int)x.a[1][0]);
+    B[1] = sdot4_first((int)lo[4], (int)x.b[1][0]);
+    A[2] = sdot4_first((int)hi[0], (int)x.a[2][0]);
+    B[2] = sdot4_first((int)hi[0], (int)x.b[2][0]);
+    A[3] = sdot4_first((int)hi[4], (int)x.a[3][0]);
+    B[3] = sdot4_first((int)hi[4], (int)x.b[3][0]);
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
+    for (int m = 1; m < 4; m++) {
         const uint32_t lo0 = lo[m], hi0 = hi[m];
         const uint32_t lo1 = lo[4 + m], hi1 = hi[4 + m];
         A[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.a[0][m], A[0], false);
