@@ -264,6 +264,7 @@ struct FusedPlan {
     bool ok;     // the shape fits the fused kernel
     int per;     // logits per lane in the top-k wavefront (2 or 4)
     int NRg;     // router blocks per XCD group
+    int rb;      // logit rows per router block (2, or 4 when the grid is full)
     int SPG;     // slots per XCD group (ceil(k / 8))
     int G;       // h groups of 16 per slot (down K / 16)
     int NDg;     // down blocks per slot

@@ -13,7 +13,8 @@
 // blocks publish h and its down blocks read that h.  Within group x the
 // in-group index i = bid / 8 picks the role:
 //
-//   i < NRg                 router: logit rows 4*bid + [0, 4), dotf32 order
+//   i < NRg                 router: logit rows 2*bid + [0, 2), dotf32 order
+//                           (4*bid + [0, 4) when the grid has no room)
 //   next SPG*G              gate/up: slot x + 8u, h group jg (16 values)
 //   next SPG*NDg            down: slot x + 8u, rows 64j + [0, 64)
 //   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
@@ -90,6 +91,7 @@ struct FusedArgs {
     uint32_t *err;       // host-visible error word
     int E, D, nsb, F, nsbd, k, norm, act, accumulate, det, local;
     int dn_delay;  // wall-clock ticks from seeing the logits to the down weight loads
+    int rb;        // logit rows per router block: 2 or 4
     int NRg, SPG, G, NDg, NCg;
 };
 
@@ -373,6 +375,87 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
     // before the logit that lets down blocks start adding
     if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
+    if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
+}
+
+// Router, two logit rows per block (rows 2 bid + (w >> 1)): wavefront w owns
+// chains 16 (w & 1) + [0, 16) of its row, so a CU moves 16 KB of router
+// rows (4 rows: 32 KB) and the rows arrive sooner, while each chain still
+// adds its strides as they land: load q, lane L take the float4 of stride
+// it = 16q + L/4, chains 16 (w & 1) + 4 (L & 3) + [0, 4); the products pass
+// through the wavefront's LDS to chain lanes c < 16.  Then (acc0+acc1) is
+// formed in each wavefront (lanes l and l + 8), (acc2+acc3) crosses to the
+// row's first wavefront through LDS, and it finishes the ordered 8-lane sum
+// and the bias: the operations of role_router in the same order.
+__device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *smem, int bid, int tid, int wave,
+                                                 int lane) {
+#pragma clang fp contract(off)
+    const int nit = a.D >> 5;                                       // strides per chain
+    float *prod = reinterpret_cast<float *>(smem) + wave * 512;    // two [16][16] chunk buffers
+    float *xch = reinterpret_cast<float *>(smem) + 4 * 512;        // [2][8]
+    const int h = wave & 1, rl = wave >> 1;
+    const int row = 2 * bid + rl;
+    const bool valid = row < a.E;
+    const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
+    // atomic combine: output rows start values, as in role_router
+    const int orow = bid * kThreads + tid;
+    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
+        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
+        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // every load unconditional (stride clamped), so that the wait for load
+    // q counts only the loads issued after it
+    float4 wv[4], xv[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int it = 16 * q + (lane >> 2);
+        it = it < nit ? it : nit - 1;
+        const int e = 32 * it + 16 * h + 4 * (lane & 3);
+        wv[q] = *reinterpret_cast<const float4 *>(wr + e);
+        xv[q] = *reinterpret_cast<const float4 *>(a.x + e);
+    }
+    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (16 * q < nit) {
+            float4 pr;
+            pr.x = wv[q].x * xv[q].x;
+            pr.y = wv[q].y * xv[q].y;
+            pr.z = wv[q].z * xv[q].z;
+            pr.w = wv[q].w * xv[q].w;
+            float *buf = prod + (q & 1) * 256;
+            *reinterpret_cast<float4 *>(buf + 4 * lane) = pr;
+            wave_lds_sync();
+            // n = 8 or 16 strides in this load; reads past n stay inside the
+            // buffer and are not added
+            const int n = nit - 16 * q < 16 ? nit - 16 * q : 16;
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = buf[u * 16 + (lane & 15)];
+#pragma unroll
+            for (int u0 = 0; u0 < 16; u0 += 8)
+                if (u0 < n)
+#pragma unroll
+                    for (int u = 0; u < 8; u++) acc = acc + v[u0 + u];
+        }
+    }
+    // lanes l < 8: chains 16h + l and 16h + l + 8
+    const float s2 = acc + dpp<0x128>(acc);
+    if (h == 1 && lane < 8) xch[rl * 8 + lane] = s2;
+    // every wavefront's output-row stores are acknowledged (memory-side)
+    // before the logits that let down blocks start adding
+    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (h == 0) {
+        const float a8 = s2 + xch[rl * 8 + (lane & 7)];
+        float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), 0));
+#pragma unroll
+        for (int l = 1; l < 8; l++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), l));
+        if (a.bias) sum = sum + bias;
+        if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
+    }
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
@@ -803,7 +886,10 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     if (tid == 0) s_fail = 0;
     int u = i;
     if (u < a.NRg) {
-        role_router(a, smem, bid, tid, wave, lane);
+        if (a.rb == 2)
+            role_router_pair(a, smem, bid, tid, wave, lane);
+        else
+            role_router(a, smem, bid, tid, wave, lane);
         return;
     }
     u -= a.NRg;
@@ -860,15 +946,21 @@ FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
     if (Kd % 256 != 0 || Kd < F || Kd > 1024) return pl;  // 16 lanes = 4 super-blocks x 4 pairs
     if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return pl;
     pl.per = E <= 128 ? 2 : 4;
-    pl.NRg = (E + 31) / 32;
+    // two logit rows per router block where the grid has room, else four
+    pl.rb = 2;
+    pl.NRg = (E + 15) / 16;
     pl.SPG = (k + 7) / 8;
     pl.G = Kd / 16;
     pl.NDg = (D + kDownRows - 1) / kDownRows;
     pl.NCg = pl.NDg;
+    if (8 * (pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg) > kFusedBlocks) {
+        pl.rb = 4;
+        pl.NRg = (E + 31) / 32;
+    }
     if (8 * (pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg) > kFusedBlocks) return pl;
     if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;                 // h record lines
     if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;       // partial lines
-    const size_t lds_router = (size_t)4 * 512 * 4;
+    const size_t lds_router = (size_t)(4 * 512 + 16) * 4;
     const size_t lds_down = (size_t)pl.G * 40;
     const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
     pl.lds = lds_router > lds_down ? lds_router : lds_down;
@@ -925,6 +1017,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     const double gu_bytes = (double)k * 2.0 * F * fa.nsb * 144.0;
     fa.dn_delay = 70 + (int)(0.8 * gu_bytes / 50000.0);
     fa.NRg = pl.NRg;
+    fa.rb = pl.rb;
     fa.SPG = pl.SPG;
     fa.G = pl.G;
     fa.NDg = pl.NDg;
