@@ -21,6 +21,9 @@ Measurement:
     FETCH_SIZE + WRITE_SIZE (profiles/moe_fused_cfg3_pmc.json), scaled by
     the counters' reading on a copy kernel of known size.  The three-launch
     path (LT_MOE_UNFUSED) is timed per kernel too, for comparison.
+  * gguf_load: the same layer written to a GGUF file and read back through
+    the GGUF reader; parse and upload times, and a bit-identity check of the
+    decode output against the in-memory weights (outside the timed steps).
   * cpu_baseline: the oracle's restatement of the reference CPU path
     (quantMatvecPar row split over a persistent pool + moeForward), timed on
     this host on a bounded sample of the same inputs.
@@ -110,6 +113,45 @@ def calibrate_copy(ctx, nbytes=256 << 20):
     log(f"calibration: 3 x {nbytes >> 20} MiB device copies")
 
 
+def gguf_load(ctx, w, x, base):
+    """The config-3 layer written to a GGUF file, read back through the GGUF
+    reader (mapped, parsed, tensors viewed in place) and uploaded: parse and
+    upload times, and whether the decode output from the file's tensors is
+    bit-identical to the output from the in-memory weights."""
+    import tempfile
+
+    import numpy as np
+
+    import llmtoy_amd as lt
+    from llmtoy_amd import gguf
+
+    with tempfile.TemporaryDirectory() as td:
+        path = gguf.write_moe_layer(os.path.join(td, "cfg3_layer.gguf"), w, k=K)
+        t = time.perf_counter()
+        r = gguf.GgufReader(path)
+        cfg = gguf.moe_config(r)
+        L = gguf.load_moe_layer(r, 0, cfg)
+        parse_ms = (time.perf_counter() - t) * 1e3
+        t = time.perf_counter()
+        tens = lt.upload_moe(ctx, L)
+        ctx.sync()
+        upload_s = time.perf_counter() - t
+        outs = []
+        for tt in (tens, base):
+            o = np.zeros(D, np.float32)
+            ctx.moe_forward(o, x, *tt, cfg.n_experts_used, cfg.d_expert, norm_topk=True, deterministic=True)
+            outs.append(o)
+        nbytes = sum(tt.nbytes for tt in tens)
+        res = {"file_bytes": os.path.getsize(path), "parse_ms": round(parse_ms, 3),
+               "upload_ms": round(upload_s * 1e3, 2), "upload_gbps": round(nbytes / upload_s / 1e9, 2),
+               "output_bit_identical": bool(np.array_equal(outs[0], outs[1])),
+               "note": "pageable host->device copies from the mapped file (PCIe), not in the timed decode"}
+        for tt in tens:
+            tt.free()
+        del L, r
+    return res
+
+
 def bench_prefill(args):
     """Config-5 batched prefill (512 tokens): extra workload for the MFMA path."""
     import numpy as np
@@ -173,6 +215,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF file load + upload check")
     ap.add_argument("--workload", choices=["decode", "prefill"], default="decode")
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
@@ -220,6 +263,10 @@ def main():
     parity = {"ids_bit_exact": bool(np.array_equal(ids_h, rids)),
               "rel_l2": float(np.linalg.norm(out_h - ref) / np.linalg.norm(ref))}
     log(f"parity: {parity}")
+    gguf_res = None
+    if not args.no_gguf:
+        gguf_res = gguf_load(ctx, w, xs[0], base)
+        log(f"GGUF file load: {gguf_res}")
 
     X = DeviceArray.from_numpy(np.stack(xs))
     out = DeviceArray((D,), np.float32)
@@ -358,6 +405,8 @@ def main():
         "roofline": roofline,
         "parity": parity,
     }
+    if gguf_res is not None:
+        result["gguf_load"] = gguf_res
 
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1, 64)

@@ -258,11 +258,9 @@ class Context:
 
 
 def upload_moe(ctx: Context, w) -> tuple:
-    """Upload a synth.MoEWeights: returns (router, gate_up, down) tensors."""
-    if w.router_type == ggml.F32:
-        router = ctx.upload(w.router, ggml.F32, w.n_experts, w.d_model)
-    else:
-        router = ctx.upload(w.router, w.router_type, w.n_experts, w.d_model)
-    gate_up = ctx.upload(w.gate_up, ggml.Q4_K, 2 * w.d_expert, w.d_model, w.n_experts)
-    down = ctx.upload(w.down, ggml.Q4_K, w.d_model, w.down_cols, w.n_experts)
+    """Upload a synth.MoEWeights or gguf.MoELayer: returns (router, gate_up,
+    down) tensors.  Expert types default to Q4_K (synth.MoEWeights)."""
+    router = ctx.upload(w.router, w.router_type, w.n_experts, w.d_model)
+    gate_up = ctx.upload(w.gate_up, getattr(w, "gate_up_type", ggml.Q4_K), 2 * w.d_expert, w.d_model, w.n_experts)
+    down = ctx.upload(w.down, getattr(w, "down_type", ggml.Q4_K), w.d_model, w.down_cols, w.n_experts)
     return router, gate_up, down
