@@ -89,9 +89,17 @@ void *lt_stream(lt_ctx *ctx);
  * cols must be a multiple of the block size (32 for Q8_0, 256 for K-quants);
  * pad shorter rows with zero blocks.  The host buffer may be freed after the
  * call returns.  The device copy is repacked into a planar layout with the
- * same byte count. */
+ * same byte count: the GGUF bytes cross PCIe in 4 MiB pieces through pinned
+ * staging buffers (up to 8 in flight) and a device kernel splits them into
+ * the planes.  The context keeps that staging (up to 64 MiB pinned host and
+ * 64 MiB device memory) until lt_destroy. */
 int lt_tensor_upload(lt_ctx *ctx, const void *host_bytes, size_t nbytes, uint32_t ggml_type, size_t rows,
                      size_t cols, size_t n_experts, lt_tensor **out_tensor);
+/* Read an uploaded tensor back as GGUF block bytes (nbytes must equal
+ * lt_tensor_bytes); the inverse of lt_tensor_upload.  No counterpart in the
+ * reference (its uploads are write-only); it lets a caller verify an upload
+ * byte for byte. */
+int lt_tensor_read(lt_ctx *ctx, const lt_tensor *t, void *host_bytes, size_t nbytes);
 /* Copy an uploaded tensor (same layout) to a new device allocation; used to
  * rotate weight copies so that timing is not served from the 256 MB cache. */
 int lt_tensor_clone(lt_ctx *ctx, const lt_tensor *src, lt_tensor **out_tensor);

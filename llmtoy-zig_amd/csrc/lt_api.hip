@@ -41,6 +41,8 @@ struct lt_ctx {
     void *fused = nullptr;
     uint32_t *fused_err = nullptr;
     lt::FusedScratch fsc{};
+    // pinned + device staging of tensor uploads and read-backs (allocated on first use)
+    lt::UploadStaging up{};
 };
 
 namespace {
@@ -104,46 +106,6 @@ size_t block_bytes(uint32_t type) {
 
 // Largest row length the LDS-staged kernels take (x is staged as fp32).
 constexpr size_t kMaxQuantCols = 16384;
-
-// Planar repack of GGUF rows (see lt_internal.h).
-void repack(const uint8_t *src, uint8_t *dst, const DevTensor &t) {
-    const size_t R = t.total_rows, nb = t.blocks_per_row;
-    const size_t nblk = R * nb;
-    switch (t.type) {
-    case LT_TYPE_F32: memcpy(dst, src, t.bytes); break;
-    case LT_TYPE_Q8_0: {
-        uint8_t *qs = dst, *d = dst + nblk * 32;
-        for (size_t b = 0; b < nblk; b++) {
-            const uint8_t *blk = src + b * 34;
-            d[2 * b] = blk[0];
-            d[2 * b + 1] = blk[1];
-            memcpy(qs + b * 32, blk + 2, 32);
-        }
-        break;
-    }
-    case LT_TYPE_Q4_K: {
-        uint8_t *hdr = dst, *qs = dst + nblk * 16;
-        for (size_t b = 0; b < nblk; b++) {
-            const uint8_t *blk = src + b * 144;
-            memcpy(hdr + b * 16, blk, 16);
-            memcpy(qs + b * 128, blk + 16, 128);
-        }
-        break;
-    }
-    case LT_TYPE_Q6_K: {
-        uint8_t *ql = dst, *qh = dst + nblk * 128, *sc = qh + nblk * 64, *d = sc + nblk * 16;
-        for (size_t b = 0; b < nblk; b++) {
-            const uint8_t *blk = src + b * 210;
-            memcpy(ql + b * 128, blk, 128);
-            memcpy(qh + b * 64, blk + 128, 64);
-            memcpy(sc + b * 16, blk + 192, 16);
-            d[2 * b] = blk[208];
-            d[2 * b + 1] = blk[209];
-        }
-        break;
-    }
-    }
-}
 
 void set_planes(DevTensor &t) {
     const size_t nblk = t.total_rows * t.blocks_per_row;
@@ -289,6 +251,7 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     if (ctx->ticket) (void)hipFree(ctx->ticket);
     if (ctx->fused) (void)hipFree(ctx->fused);
     if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
+    lt::free_staging(ctx->up);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -330,27 +293,23 @@ extern "C" int lt_tensor_upload(lt_ctx *ctx, const void *host_bytes, size_t nbyt
         delete t;
         return hip_fail(ctx, e, "hipMalloc(tensor)");
     }
-    std::vector<uint8_t> planar;
-    const uint8_t *src = (const uint8_t *)host_bytes;
-    if (type != LT_TYPE_F32) {
-        try {
-            planar.resize(nbytes);
-        } catch (...) {
-            (void)hipFree(t->t.base);
-            delete t;
-            return fail(ctx, LT_ERR_OOM, "host repack buffer");
-        }
-        repack(src, planar.data(), t->t);
-        src = planar.data();
-    }
-    e = hipMemcpy(t->t.base, src, nbytes, hipMemcpyHostToDevice);
+    set_planes(t->t);
+    e = lt::upload_planar(ctx->up, ctx->device, t->t, (const uint8_t *)host_bytes);
     if (e != hipSuccess) {
         (void)hipFree(t->t.base);
         delete t;
-        return hip_fail(ctx, e, "hipMemcpy(tensor)");
+        return hip_fail(ctx, e, "tensor upload");
     }
-    set_planes(t->t);
     *out_tensor = t;
+    return LT_OK;
+}
+
+extern "C" int lt_tensor_read(lt_ctx *ctx, const lt_tensor *t, void *host_bytes, size_t nbytes) {
+    if (!ctx || !t || !host_bytes) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (nbytes != t->t.bytes) return fail(ctx, LT_ERR_INVALID, "nbytes %zu != tensor bytes %zu", nbytes, t->t.bytes);
+    LT_HIP(ctx, hipSetDevice(ctx->device));
+    LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    LT_HIP(ctx, lt::download_planar(ctx->up, t->t, (uint8_t *)host_bytes));
     return LT_OK;
 }
 

@@ -216,10 +216,31 @@ __device__ __forceinline__ float4 ldg16f(const float *p) { return *reinterpret_c
 
 }  // namespace lt
 
+namespace lt {
+// ------------------------------------------- host <-> device tensor copies
+// (lt_upload.hip) Raw GGUF blocks cross PCIe in kUpChunk pieces staged in
+// pinned host memory, up to kUpWorkers pieces in flight on their own
+// streams; a device kernel splits each piece into the planes.
+constexpr int kUpWorkers = 8;
+constexpr int kUpSlots = 2 * kUpWorkers;  // two staging slots per worker
+constexpr size_t kUpChunk = 4u << 20;     // bytes per staging slot
+struct UploadStaging {
+    int workers = 0;  // workers whose stream and slots exist
+    hipStream_t st[kUpWorkers] = {};
+    uint8_t *pinned[kUpSlots] = {};
+    uint8_t *dev[kUpSlots] = {};
+    hipEvent_t ev[kUpSlots] = {};
+};
+// t.base must hold t.bytes; src holds the tensor's GGUF blocks.  Returns
+// after every copy has finished.
+hipError_t upload_planar(UploadStaging &S, int device, const DevTensor &t, const uint8_t *src);
+// The inverse: the tensor's GGUF blocks into dst (t.bytes bytes).
+hipError_t download_planar(UploadStaging &S, const DevTensor &t, uint8_t *dst);
+void free_staging(UploadStaging &S);
+
 // --------------------------------------------------------------- launchers
 // Each returns hipSuccess or the launch error.  All shapes are validated by
 // the caller (lt_api.cpp) before these are called.
-namespace lt {
 hipError_t launch_matvec_q4k(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
                              hipStream_t s);
 hipError_t launch_matvec_q8_0(const DevTensor &W, const float *x, float *y, hipStream_t s);

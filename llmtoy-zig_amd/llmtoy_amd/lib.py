@@ -64,7 +64,7 @@ _ERRS = {LT_ERR_UNSUPPORTED: UnsupportedError, LT_ERR_INVALID: InvalidError, LT_
          LT_ERR_OOM: OomError}
 
 EXPORTS = [
-    "lt_init", "lt_destroy", "lt_last_error", "lt_sync", "lt_stream", "lt_tensor_upload", "lt_tensor_clone",
+    "lt_init", "lt_destroy", "lt_last_error", "lt_sync", "lt_stream", "lt_tensor_upload", "lt_tensor_read", "lt_tensor_clone",
     "lt_tensor_free", "lt_tensor_bytes", "lt_matvec", "lt_ffn_dense", "lt_moe_router_topk", "lt_expert_gate_up_id",
     "lt_expert_down_id", "lt_moe_forward", "lt_moe_prefill",
 ]
@@ -88,6 +88,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "lt_sync": (i32, [vp]),
         "lt_stream": (vp, [vp]),
         "lt_tensor_upload": (i32, [vp, vp, sz, u32, sz, sz, sz, C.POINTER(vp)]),
+        "lt_tensor_read": (i32, [vp, vp, vp, sz]),
         "lt_tensor_clone": (i32, [vp, vp, C.POINTER(vp)]),
         "lt_tensor_free": (i32, [vp, vp]),
         "lt_tensor_bytes": (sz, [vp]),
@@ -138,6 +139,12 @@ class Tensor:
     @property
     def nbytes(self) -> int:
         return int(self.ctx.lib.lt_tensor_bytes(self.handle))
+
+    def read(self) -> np.ndarray:
+        """The tensor's GGUF block bytes, read back from the device."""
+        out = np.empty(self.nbytes, np.uint8)
+        self.ctx._check(self.ctx.lib.lt_tensor_read(self.ctx.ptr, self.handle, out.ctypes.data, out.nbytes))
+        return out
 
     def clone(self) -> "Tensor":
         h = C.c_void_p()

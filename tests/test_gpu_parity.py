@@ -146,6 +146,44 @@ def test_gpu_matvec_f32_bit_exact(ctx, rows, cols):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
+# ------------------------------------------------------------------ upload / read-back
+# Uploads move GGUF blocks through pinned 4 MiB pieces (several in flight)
+# and split them into planes on the device; reading back joins them again.
+# Sizes cover one block, ragged workgroup tails, one piece exactly and
+# more pieces than in-flight workers.
+@pytest.mark.parametrize("gtype,blocks", [
+    (ggml.Q8_0, 1), (ggml.Q8_0, 65), (ggml.Q8_0, 123328), (ggml.Q8_0, 8 * 123328 + 777),
+    (ggml.Q4_K, 1), (ggml.Q4_K, 63), (ggml.Q4_K, 29120), (ggml.Q4_K, 29121), (ggml.Q4_K, 20 * 29120 + 5),
+    (ggml.Q6_K, 3), (ggml.Q6_K, 19968 + 64), (ggml.Q6_K, 17 * 19968 + 1),
+    (ggml.F32, 1), (ggml.F32, 1048576 + 3), (ggml.F32, 9 * 1048576)])
+def test_gpu_upload_read_round_trip(ctx, gtype, blocks):
+    g = np.random.default_rng(blocks * 31 + gtype)
+    data = g.integers(0, 256, blocks * ggml.BLOCK_BYTES[gtype], dtype=np.uint8)
+    cols = ggml.BLOCK_ELEMS[gtype]
+    print(f"upload round trip type {gtype} blocks {blocks}", flush=True)
+    t = ctx.upload(data, gtype, blocks, cols)
+    back = t.read()
+    t.free()
+    assert np.array_equal(back, data)
+
+
+def test_gpu_upload_read_config3_experts(ctx, cfg3):
+    # the full 340 MB expert tensors of the headline layer
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    assert np.array_equal(gate_up.read(), w.gate_up.reshape(-1))
+    assert np.array_equal(down.read(), w.down.reshape(-1))
+    assert np.array_equal(router.read().view(np.float32), w.router.reshape(-1))
+
+
+def test_gpu_read_rejects_wrong_size(ctx):
+    t = ctx.upload(np.zeros(34, np.uint8), ggml.Q8_0, 1, 32)
+    buf = np.zeros(33, np.uint8)
+    with pytest.raises(InvalidError):
+        ctx._check(ctx.lib.lt_tensor_read(ctx.ptr, t.handle, buf.ctypes.data, buf.nbytes))
+    t.free()
+
+
 # ------------------------------------------------------------------ golden fixtures
 @pytest.mark.parametrize("name", ["mv_f32", "mv_q8_0", "mv_q4_k", "mv_q4_k_pad", "mv_q6_k_pad"])
 def test_gpu_golden_matvec(ctx, name):
