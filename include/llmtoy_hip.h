@@ -56,7 +56,14 @@ enum {
     LT_MOE_DETERMINISTIC = 1u << 4 /* lt_moe_forward: add the k expert outputs in slot order (bit-identical
                                       results run to run, like the reference's moeForward, ops/moe.zig:67-76);
                                       without it the single-launch kernel adds them with float atomics in
-                                      arrival order (faster; last bits may vary between runs) */
+                                      arrival order (faster; last bits may vary between runs) */,
+    LT_NORM_PRECISE = 1u << 5,     /* RMS norms: sum the squares sequentially in index order on one lane,
+                                      the reference's CPU order (math.zig:19-25), so results are bit-exact
+                                      with it; default: a fixed-shape tree sum (same bits every run, within
+                                      a few ulp of the CPU order; n dependent adds saved).  The reference's
+                                      GPU norms offer the same choice (rmsnorm.glsl flag bit 1) */
+    LT_NORM_ONE_PLUS_W = 1u << 6   /* lt_rmsnorm / lt_add_rmsnorm: multiply by (1 + w) instead of w
+                                      (rmsnorm.glsl flag bit 0) */
 };
 
 typedef struct lt_ctx lt_ctx;
@@ -171,6 +178,56 @@ int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_tensor *rou
 int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt_tensor *router,
                    const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
                    uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);
+
+/* ---- RMS norms and the Gemma4 MoE block (Gemma4's steps around the MoE layer) ----
+ * Row length n <= 16384 floats; eps in [0, 1].  Every product and sum is a
+ * separately rounded fp32 operation and rms_inv = 1 / sqrt(ss / n + eps)
+ * with correctly rounded division and square root, as in the reference.
+ * flags: LT_HOST_IO, LT_NORM_PRECISE (and where noted LT_NORM_ONE_PLUS_W). */
+
+/* math.rmsnorm (ops/math.zig:19-25): out = x * rms_inv(x) * w; w == NULL is
+ * rmsnormRaw (42-48).  Each of rows rows of n floats is normalised on its
+ * own (the reference normalises one vector: rows = 1).  out may equal x.
+ * Also takes LT_NORM_ONE_PLUS_W.  Replaces the rmsnorm pipeline
+ * (gpu/shaders/rmsnorm.glsl). */
+int lt_rmsnorm(lt_ctx *ctx, float *out, const float *x, const float *w, uint32_t rows, uint32_t n, float eps,
+               uint32_t flags);
+/* out = rmsnorm(a + b, w), the sum rounded first (gemma4/forward.zig:489-490;
+ * gpu/shaders/add_rmsnorm.glsl).  Also takes LT_NORM_ONE_PLUS_W. */
+int lt_add_rmsnorm(lt_ctx *ctx, float *out, const float *a, const float *b, const float *w, uint32_t rows,
+                   uint32_t n, float eps, uint32_t flags);
+/* math.rmsnormWeightedAndRawScaled (ops/math.zig:51-82): one RMS of x;
+ * weighted_out = x * rms_inv * w, raw_scaled_out = x * (rms_inv *
+ * raw_global_scale) * raw_scale.  Gemma4 uses it for the expert and router
+ * inputs (gemma4/forward.zig:403-414). */
+int lt_rmsnorm_weighted_raw_scaled(lt_ctx *ctx, float *weighted_out, float *raw_scaled_out, const float *x,
+                                   const float *w, const float *raw_scale, float raw_global_scale, uint32_t n,
+                                   float eps, uint32_t flags);
+/* The Gemma4 MoE tail in one launch (gemma4/forward.zig:482-497; on the
+ * reference's GPU, GpuWeights.recordMoeResidualTail, gemma4/gpu_weights.zig:
+ * 3349-3410):  m = rmsnorm(moe, post_ffw_norm_2); c = dense_ffn + m;
+ * x = x + rmsnorm(c, post_ffw_norm); then x *= layer_output_scale unless it
+ * is 1.  x is read and written. */
+int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float *dense_ffn, const float *post_ffw_norm_2,
+                const float *post_ffw_norm, float layer_output_scale, uint32_t n, float eps, uint32_t flags);
+/* The whole Gemma4 MoE block of one decode token after the dense FFN
+ * (gemma4/forward.zig:403-497; GpuWeights.runExpertBatch with MoeTailParams,
+ * gemma4/gpu_weights.zig:2748-3149):
+ *   moe_in, router_in = rmsnormWeightedAndRawScaled(x, pre_ffw_norm_2,
+ *                       router_scale, 1 / sqrt(d_model))
+ *   routerTopKSoftmax(router, router_in) -> k ids, softmax probabilities p
+ *   moe = sum_k down_exps_scale[id] * p * down_id(act(gate_id moe_in) * up_id moe_in)
+ *   x   = lt_moe_tail(x, moe, dense_ffn, ...)
+ * x [d_model] is updated in place; dense_ffn is the dense FFN output after
+ * post_ffw_norm_1.  down_exps_scale [n_experts] may be NULL (all ones).
+ * router: F32 or Q8_0; experts: Q4_K.  flags: LT_HOST_IO, LT_NORM_PRECISE,
+ * LT_MOE_NORM_TOPK.  out_ids / out_w (may be NULL) get the selection and its
+ * probabilities (router_out at the selected ids). */
+int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn, const lt_tensor *router,
+                        const lt_tensor *gate_up, const lt_tensor *down, const float *pre_ffw_norm_2,
+                        const float *router_scale, const float *down_exps_scale, const float *post_ffw_norm_2,
+                        const float *post_ffw_norm, float layer_output_scale, float eps, uint32_t k,
+                        uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);
 
 #ifdef __cplusplus
 }

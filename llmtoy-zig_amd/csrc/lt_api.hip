@@ -32,7 +32,7 @@ struct lt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // context-owned device scratch, grown on demand
-    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh, pf;
+    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh, pf, nrm;
     // arrival ticket of the router's last-block top-k; zeroed once at init,
     // every launch leaves it at zero again
     unsigned *ticket = nullptr;
@@ -245,7 +245,8 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     DevBuf *bufs[] = {&ctx->x, &ctx->out, &ctx->logits, &ctx->h, &ctx->ids, &ctx->w,
-                      &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh, &ctx->pf};
+                      &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh, &ctx->pf,
+                      &ctx->nrm};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (ctx->ticket) (void)hipFree(ctx->ticket);
@@ -748,6 +749,228 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
         if (out_w)
             LT_HIP(ctx, hipMemcpyAsync(out_w, wsp + logits_b + ids_b, (size_t)T * k * 4, hipMemcpyDeviceToHost,
                                        ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+// ------------------------------------------------------------- norms, Gemma4 block
+namespace {
+
+constexpr uint32_t kNormFlags = LT_HOST_IO | LT_NORM_PRECISE | LT_NORM_ONE_PLUS_W;
+
+// 256-byte aligned float slices of ctx->nrm, sized up front by need().
+struct Arena {
+    size_t bytes = 0;
+    uint8_t *base = nullptr;
+    static size_t round(size_t n) { return (n * 4 + 255) & ~(size_t)255; }
+    void need(size_t n) { bytes += round(n); }
+    float *take(size_t n) {
+        float *p = reinterpret_cast<float *>(base);
+        base += round(n);
+        return p;
+    }
+};
+
+int arena_open(lt_ctx *ctx, Arena &a) {
+    int rc = ensure(ctx, ctx->nrm, a.bytes);
+    if (rc) return rc;
+    a.base = (uint8_t *)ctx->nrm.p;
+    return LT_OK;
+}
+
+// Host input -> arena slice (LT_HOST_IO), or the device pointer itself.
+int io_in(lt_ctx *ctx, bool host, Arena &a, const float *src, size_t n, const float **dst) {
+    if (!src || !host) {
+        *dst = src;
+        return LT_OK;
+    }
+    float *d = a.take(n);
+    LT_HIP(ctx, hipMemcpyAsync(d, src, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    *dst = d;
+    return LT_OK;
+}
+
+int check_norm(lt_ctx *ctx, uint32_t rows, uint32_t n, float eps, uint32_t flags, uint32_t allowed) {
+    if (n == 0 || n > (uint32_t)lt::kMaxNormCols)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "row length %u (device norms: 1..%d)", n, lt::kMaxNormCols);
+    if (rows == 0 || rows > 65536) return fail(ctx, LT_ERR_INVALID, "rows=%u out of range (1..65536)", rows);
+    if (!(eps >= 0.0f) || eps > 1.0f) return fail(ctx, LT_ERR_INVALID, "eps must be in [0, 1]");
+    if (flags & ~allowed) return fail(ctx, LT_ERR_INVALID, "unknown flags 0x%x", flags & ~allowed);
+    return LT_OK;
+}
+
+int norm_run(lt_ctx *ctx, int op, const float *a, const float *b, const float *w, const float *w2, float *out,
+             float *out2, uint32_t rows, uint32_t n, float eps, float scale, uint32_t flags) {
+    return launch_rc(ctx,
+                     lt::launch_norm(op, a, b, w, w2, out, out2, (int)rows, (int)n, eps, scale,
+                                     (flags & LT_NORM_PRECISE) ? 1 : 0, (flags & LT_NORM_ONE_PLUS_W) ? 1 : 0,
+                                     ctx->stream),
+                     "rmsnorm");
+}
+
+// Shared body of lt_rmsnorm / lt_add_rmsnorm.
+int rmsnorm_entry(lt_ctx *ctx, int op, float *out, const float *a, const float *b, const float *w, uint32_t rows,
+                  uint32_t n, float eps, uint32_t flags) {
+    int rc = check_norm(ctx, rows, n, eps, flags, kNormFlags);
+    if (rc) return rc;
+    const bool host = flags & LT_HOST_IO;
+    const size_t len = (size_t)rows * n;
+    Arena ar;
+    if (host) {
+        ar.need(len), ar.need(len), ar.need(n);
+        if (b) ar.need(len);
+        if ((rc = arena_open(ctx, ar))) return rc;
+    }
+    const float *da, *db, *dw;
+    if ((rc = io_in(ctx, host, ar, a, len, &da)) || (rc = io_in(ctx, host, ar, b, len, &db)) ||
+        (rc = io_in(ctx, host, ar, w, n, &dw)))
+        return rc;
+    float *dout = host ? ar.take(len) : out;
+    if ((rc = norm_run(ctx, op, da, db, dw, nullptr, dout, nullptr, rows, n, eps, 1.0f, flags))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(out, dout, len * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+}  // namespace
+
+extern "C" int lt_rmsnorm(lt_ctx *ctx, float *out, const float *x, const float *w, uint32_t rows, uint32_t n,
+                          float eps, uint32_t flags) {
+    if (!ctx || !out || !x) return fail(ctx, LT_ERR_INVALID, "null argument");
+    return rmsnorm_entry(ctx, 0, out, x, nullptr, w, rows, n, eps, flags);
+}
+
+extern "C" int lt_add_rmsnorm(lt_ctx *ctx, float *out, const float *a, const float *b, const float *w, uint32_t rows,
+                              uint32_t n, float eps, uint32_t flags) {
+    if (!ctx || !out || !a || !b || !w) return fail(ctx, LT_ERR_INVALID, "null argument");
+    return rmsnorm_entry(ctx, 1, out, a, b, w, rows, n, eps, flags);
+}
+
+extern "C" int lt_rmsnorm_weighted_raw_scaled(lt_ctx *ctx, float *weighted_out, float *raw_scaled_out,
+                                              const float *x, const float *w, const float *raw_scale,
+                                              float raw_global_scale, uint32_t n, float eps, uint32_t flags) {
+    if (!ctx || !weighted_out || !raw_scaled_out || !x || !w || !raw_scale)
+        return fail(ctx, LT_ERR_INVALID, "null argument");
+    int rc = check_norm(ctx, 1, n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE);
+    if (rc) return rc;
+    const bool host = flags & LT_HOST_IO;
+    Arena ar;
+    if (host) {
+        for (int i = 0; i < 5; i++) ar.need(n);
+        if ((rc = arena_open(ctx, ar))) return rc;
+    }
+    const float *dx, *dw, *ds;
+    if ((rc = io_in(ctx, host, ar, x, n, &dx)) || (rc = io_in(ctx, host, ar, w, n, &dw)) ||
+        (rc = io_in(ctx, host, ar, raw_scale, n, &ds)))
+        return rc;
+    float *dwo = host ? ar.take(n) : weighted_out, *dro = host ? ar.take(n) : raw_scaled_out;
+    if ((rc = norm_run(ctx, 2, dx, nullptr, dw, ds, dwo, dro, 1, n, eps, raw_global_scale, flags))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(weighted_out, dwo, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipMemcpyAsync(raw_scaled_out, dro, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+extern "C" int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float *dense_ffn,
+                           const float *post_ffw_norm_2, const float *post_ffw_norm, float layer_output_scale,
+                           uint32_t n, float eps, uint32_t flags) {
+    if (!ctx || !x || !moe || !dense_ffn || !post_ffw_norm_2 || !post_ffw_norm)
+        return fail(ctx, LT_ERR_INVALID, "null argument");
+    int rc = check_norm(ctx, 1, n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE);
+    if (rc) return rc;
+    const bool host = flags & LT_HOST_IO;
+    Arena ar;
+    if (host) {
+        for (int i = 0; i < 5; i++) ar.need(n);
+        if ((rc = arena_open(ctx, ar))) return rc;
+    }
+    const float *dm, *dd, *dw2, *dw, *dx;
+    if ((rc = io_in(ctx, host, ar, moe, n, &dm)) || (rc = io_in(ctx, host, ar, dense_ffn, n, &dd)) ||
+        (rc = io_in(ctx, host, ar, post_ffw_norm_2, n, &dw2)) || (rc = io_in(ctx, host, ar, post_ffw_norm, n, &dw)) ||
+        (rc = io_in(ctx, host, ar, x, n, &dx)))
+        return rc;
+    float *xo = const_cast<float *>(dx);
+    if ((rc = norm_run(ctx, 3, dm, dd, dw, dw2, xo, nullptr, 1, n, eps, layer_output_scale, flags))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(x, xo, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
+    return LT_OK;
+}
+
+extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn, const lt_tensor *router,
+                                   const lt_tensor *gate_up, const lt_tensor *down, const float *pre_ffw_norm_2,
+                                   const float *router_scale, const float *down_exps_scale,
+                                   const float *post_ffw_norm_2, const float *post_ffw_norm,
+                                   float layer_output_scale, float eps, uint32_t k, uint32_t d_expert, uint32_t act,
+                                   uint32_t flags, uint32_t *out_ids, float *out_w) {
+    if (!ctx || !x || !dense_ffn || !pre_ffw_norm_2 || !router_scale || !post_ffw_norm_2 || !post_ffw_norm)
+        return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
+    if (!router || !gate_up || !down) return fail(ctx, LT_ERR_INVALID, "null tensor");
+    const size_t n = gate_up->t.cols;
+    int rc;
+    if ((rc = check_router(ctx, router, n, k))) return rc;
+    if ((rc = check_experts(ctx, gate_up, down, n, d_expert, router->t.total_rows))) return rc;
+    if ((rc = check_norm(ctx, 1, (uint32_t)n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE | LT_MOE_NORM_TOPK)))
+        return rc;
+    const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
+    const size_t E = R.total_rows, Kd = D.cols;
+    const bool host = flags & LT_HOST_IO;
+    Arena ar;
+    for (int i = 0; i < 3; i++) ar.need(n);  // moe_in, router_in, moe
+    if (host) {
+        for (int i = 0; i < 6; i++) ar.need(n);  // x, dense, four norm vectors
+        ar.need(E);
+    }
+    if ((rc = arena_open(ctx, ar))) return rc;
+    float *moe_in = ar.take(n), *router_in = ar.take(n), *moe = ar.take(n);
+    const float *dx, *dd, *dpre, *drs, *dds, *dp2, *dp;
+    if ((rc = io_in(ctx, host, ar, x, n, &dx)) || (rc = io_in(ctx, host, ar, dense_ffn, n, &dd)) ||
+        (rc = io_in(ctx, host, ar, pre_ffw_norm_2, n, &dpre)) || (rc = io_in(ctx, host, ar, router_scale, n, &drs)) ||
+        (rc = io_in(ctx, host, ar, down_exps_scale, E, &dds)) ||
+        (rc = io_in(ctx, host, ar, post_ffw_norm_2, n, &dp2)) || (rc = io_in(ctx, host, ar, post_ffw_norm, n, &dp)))
+        return rc;
+    float *xio = const_cast<float *>(dx);
+    // gemma4/forward.zig:405-414: expert input and router input from one RMS of x
+    const float inv_sqrt_d = 1.0f / sqrtf((float)n);
+    if ((rc = norm_run(ctx, 2, dx, nullptr, dpre, drs, moe_in, router_in, 1, (uint32_t)n, eps, inv_sqrt_d, flags)))
+        return rc;
+    // 417 routerTopKSoftmax, then the selected experts (463-479, GpuWeights.runExpertBatch)
+    if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
+    float *h = (float *)ctx->eh.p;
+    const uint32_t norm = (flags & LT_MOE_NORM_TOPK) ? 1u : 0u;
+    if (E <= kRoutedGateUpMaxExperts) {
+        if ((rc = router_dev(ctx, R, router_in, nullptr, 0, flags))) return rc;
+        rc = launch_rc(ctx,
+                       lt::launch_expert_gate_up_q4k_routed(GU, moe_in, (const float *)ctx->logits.p, k, norm,
+                                                            d_expert, (uint32_t)Kd, act, h, (uint32_t *)ctx->ids.p,
+                                                            (float *)ctx->w.p, ctx->stream),
+                       "expert_gate_up_routed");
+    } else {
+        if ((rc = router_dev(ctx, R, router_in, nullptr, k, flags))) return rc;
+        rc = launch_rc(ctx,
+                       lt::launch_expert_gate_up_q4k(GU, moe_in, (const uint32_t *)ctx->ids.p, k, d_expert,
+                                                     (uint32_t)Kd, act, h, ctx->stream),
+                       "expert_gate_up");
+    }
+    if (rc) return rc;
+    if ((rc = launch_rc(ctx,
+                        lt::launch_expert_down_q4k(D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k,
+                                                   nullptr, 0, moe, ctx->stream, dds),
+                        "expert_down")))
+        return rc;
+    // 482-497: post_ffw_norm_2, + dense FFN, post_ffw_norm, residual, layer_output_scale
+    if ((rc = norm_run(ctx, 3, moe, dd, dp, dp2, xio, nullptr, 1, (uint32_t)n, eps, layer_output_scale, flags)))
+        return rc;
+    if ((rc = copy_routing_out(ctx, k, out_ids, out_w, host))) return rc;
+    if (host) {
+        LT_HIP(ctx, hipMemcpyAsync(x, xio, n * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
     }
     return LT_OK;

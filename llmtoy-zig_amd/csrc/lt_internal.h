@@ -238,6 +238,16 @@ hipError_t upload_planar(UploadStaging &S, int device, const DevTensor &t, const
 hipError_t download_planar(UploadStaging &S, const DevTensor &t, uint8_t *dst);
 void free_staging(UploadStaging &S);
 
+// ------------------------------------------------------ norms (lt_norm.hip)
+constexpr int kMaxNormCols = 16384;  // row staged in LDS (64 KiB)
+// op 0: out = rmsnorm(a, w) (w null: no weight); 1: out = rmsnorm(a + b, w);
+// 2: out = weighted, out2 = raw-scaled (w2 = raw_scale, scale = global);
+// 3: MoE tail, out = x in place, a = moe, b = dense, w2 = post_ffw_norm_2,
+// w = post_ffw_norm, scale = layer_output_scale.  One workgroup per row.
+hipError_t launch_norm(int op, const float *a, const float *b, const float *w, const float *w2, float *out,
+                       float *out2, int rows, int n, float eps, float scale, int precise, int one_plus_w,
+                       hipStream_t s);
+
 // --------------------------------------------------------------- launchers
 // Each returns hipSuccess or the launch error.  All shapes are validated by
 // the caller (lt_api.cpp) before these are called.
@@ -273,7 +283,8 @@ hipError_t launch_expert_gate_up_q4k_routed(const DevTensor &GU, const float *x,
                                             uint32_t norm, uint32_t d_expert, uint32_t down_cols, uint32_t act,
                                             float *h, uint32_t *ids_out, float *w_out, hipStream_t s);
 hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
-                                  uint32_t k, const float *base, int accumulate, float *out, hipStream_t s);
+                                  uint32_t k, const float *base, int accumulate, float *out, hipStream_t s,
+                                  const float *dscale = nullptr);
 
 // The whole decode MoE layer in one launch (lt_moe_fused.hip): F32 router,
 // Q4_K gate_up and down.  The grid is always kFusedBlocks workgroups, which

@@ -343,6 +343,7 @@ hipError_t launch_expert_gate_up_q4k_routed(const DevTensor &GU, const float *x,
 // ------------------------------------------------------------------------
 // Expert-indexed down with the weighted combine fused:
 //   out[i] = base[i] + sum_{s in slot order} w[s] * (D_{ids[s]} row i) . h[s]
+// (w[s] times dscale[ids[s]] when a per-expert down scale is given)
 // (base = previous out with accumulate, the shared-FFN output, or 0).
 // Block: NW = min(nsb, 4) waves x RD output rows.  Wave w handles
 // super-blocks w, w+NW, ... of the K = down_cols dimension; lane = (slot
@@ -357,7 +358,7 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
                                                          const uint32_t *__restrict__ ids,
                                                          const float *__restrict__ wts, int k, int n_experts,
                                                          int rows_per_expert, int nsb, const float *base,
-                                                         int accumulate, float *out) {
+                                                         int accumulate, const float *dscale, float *out) {
     __shared__ float part[RD][16][16];  // [row][slot][super-block]
     const int NW = blockDim.x / kWave;
     const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -403,7 +404,11 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
                 float t = part[r][s][0];
                 for (int b = 1; b < nsb; b++) t += part[r][s][b];
                 const uint32_t e = ids[s];
-                if (e < (uint32_t)n_experts) acc += wts[s] * t;
+                if (e < (uint32_t)n_experts) {
+                    // expert_scale = down_exps_scale[e] * w (gemma4/forward.zig:477)
+                    const float ws = dscale ? dscale[e] * wts[s] : wts[s];
+                    acc += ws * t;
+                }
             }
             if (base) acc = base[row] + acc;
             out[row] = acc;
@@ -412,14 +417,15 @@ __global__ void __launch_bounds__(256) k_expert_down_q4k(const uint8_t *__restri
 }
 
 hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
-                                  uint32_t k, const float *base, int accumulate, float *out, hipStream_t s) {
+                                  uint32_t k, const float *base, int accumulate, float *out, hipStream_t s,
+                                  const float *dscale) {
     constexpr int RD = 2;  // 2 rows per block: 7.5 -> 6.5 us against 8 rows (config 3)
     const int nsb = (int)D.blocks_per_row;  // <= 16, k <= 16: checked by the API layer
     const int nw = nsb < 4 ? nsb : 4;
     const int rows = (int)D.rows;
     dim3 grid((rows + RD - 1) / RD);
     hipLaunchKernelGGL((k_expert_down_q4k<RD>), grid, dim3(64 * nw), 0, s, D.p0, D.p1, h, ids, w, (int)k,
-                       (int)D.n_experts, rows, nsb, base, accumulate, out);
+                       (int)D.n_experts, rows, nsb, base, accumulate, dscale, out);
     return hipGetLastError();
 }
 

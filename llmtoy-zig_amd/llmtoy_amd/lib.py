@@ -29,6 +29,8 @@ LT_OK, LT_ERR_UNSUPPORTED, LT_ERR_INVALID, LT_ERR_DEVICE, LT_ERR_OOM = range(5)
 LT_HOST_IO, LT_MOE_NORM_TOPK, LT_MOE_ACCUMULATE = 1, 2, 4
 LT_MOE_UNFUSED = 1 << 3
 LT_MOE_DETERMINISTIC = 1 << 4
+LT_NORM_PRECISE = 1 << 5
+LT_NORM_ONE_PLUS_W = 1 << 6
 ACT_SILU, ACT_GELU_TANH = 0, 1
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -66,7 +68,8 @@ _ERRS = {LT_ERR_UNSUPPORTED: UnsupportedError, LT_ERR_INVALID: InvalidError, LT_
 EXPORTS = [
     "lt_init", "lt_destroy", "lt_last_error", "lt_sync", "lt_stream", "lt_tensor_upload", "lt_tensor_read", "lt_tensor_clone",
     "lt_tensor_free", "lt_tensor_bytes", "lt_matvec", "lt_ffn_dense", "lt_moe_router_topk", "lt_expert_gate_up_id",
-    "lt_expert_down_id", "lt_moe_forward", "lt_moe_prefill",
+    "lt_expert_down_id", "lt_moe_forward", "lt_moe_prefill", "lt_rmsnorm", "lt_add_rmsnorm",
+    "lt_rmsnorm_weighted_raw_scaled", "lt_moe_tail", "lt_gemma4_moe_block",
 ]
 
 _lib = None
@@ -99,6 +102,12 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "lt_expert_down_id": (i32, [vp, vp, vp, vp, vp, u32, vp, u32]),
         "lt_moe_forward": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
         "lt_moe_prefill": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
+        "lt_rmsnorm": (i32, [vp, vp, vp, vp, u32, u32, C.c_float, u32]),
+        "lt_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, u32, u32, C.c_float, u32]),
+        "lt_rmsnorm_weighted_raw_scaled": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, u32, C.c_float, u32]),
+        "lt_moe_tail": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, u32, C.c_float, u32]),
+        "lt_gemma4_moe_block": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_float, C.c_float, u32, u32,
+                                      u32, u32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -262,6 +271,63 @@ class Context:
                                             gate_up.handle, down.handle, k, d_expert, act, fl, _ptr(out_ids)[0],
                                             _ptr(out_w)[0]))
         return out
+
+
+def _norm_io(ctx, *arrays):
+    return ctx._io(*arrays)
+
+
+def _rows_n(x):
+    shape = getattr(x, "shape", (len(x),))
+    return (1, shape[0]) if len(shape) == 1 else (shape[0], shape[1])
+
+
+def rmsnorm(ctx: Context, out, x, w=None, eps=1e-6, precise=False, one_plus_w=False):
+    """math.rmsnorm (w given) / rmsnormRaw (w None) on each row of x ([n] or [rows, n])."""
+    rows, n = _rows_n(x)
+    fl = _norm_io(ctx, out, x, w) | (LT_NORM_PRECISE if precise else 0) | (LT_NORM_ONE_PLUS_W if one_plus_w else 0)
+    ctx._check(ctx.lib.lt_rmsnorm(ctx.ptr, _ptr(out)[0], _ptr(x)[0], _ptr(w)[0], rows, n, eps, fl))
+    return out
+
+
+def add_rmsnorm(ctx: Context, out, a, b, w, eps=1e-6, precise=False, one_plus_w=False):
+    rows, n = _rows_n(a)
+    fl = _norm_io(ctx, out, a, b, w) | (LT_NORM_PRECISE if precise else 0) | (LT_NORM_ONE_PLUS_W if one_plus_w else 0)
+    ctx._check(ctx.lib.lt_add_rmsnorm(ctx.ptr, _ptr(out)[0], _ptr(a)[0], _ptr(b)[0], _ptr(w)[0], rows, n, eps, fl))
+    return out
+
+
+def rmsnorm_weighted_raw_scaled(ctx: Context, weighted_out, raw_scaled_out, x, w, raw_scale, raw_global_scale,
+                                eps=1e-6, precise=False):
+    fl = _norm_io(ctx, weighted_out, raw_scaled_out, x, w, raw_scale) | (LT_NORM_PRECISE if precise else 0)
+    ctx._check(ctx.lib.lt_rmsnorm_weighted_raw_scaled(ctx.ptr, _ptr(weighted_out)[0], _ptr(raw_scaled_out)[0],
+                                                      _ptr(x)[0], _ptr(w)[0], _ptr(raw_scale)[0], raw_global_scale,
+                                                      _rows_n(x)[1], eps, fl))
+
+
+def moe_tail(ctx: Context, x, moe, dense_ffn, post_ffw_norm_2, post_ffw_norm, layer_output_scale=1.0, eps=1e-6,
+             precise=False):
+    """gemma4/forward.zig:482-497 in one launch; x is updated in place."""
+    fl = _norm_io(ctx, x, moe, dense_ffn, post_ffw_norm_2, post_ffw_norm) | (LT_NORM_PRECISE if precise else 0)
+    ctx._check(ctx.lib.lt_moe_tail(ctx.ptr, _ptr(x)[0], _ptr(moe)[0], _ptr(dense_ffn)[0], _ptr(post_ffw_norm_2)[0],
+                                   _ptr(post_ffw_norm)[0], layer_output_scale, _rows_n(x)[1], eps, fl))
+    return x
+
+
+def gemma4_moe_block(ctx: Context, x, dense_ffn, router: Tensor, gate_up: Tensor, down: Tensor, k: int,
+                     d_expert: int, norms: dict, layer_output_scale=1.0, eps=1e-6, act=ACT_GELU_TANH,
+                     precise=False, norm_topk=False, out_ids=None, out_w=None):
+    """The Gemma4 MoE block of one token (gemma4/forward.zig:403-497); x is
+    updated in place.  norms: pre_ffw_norm_2, router_scale, down_exps_scale
+    (or None), post_ffw_norm_2, post_ffw_norm."""
+    ds = norms.get("down_exps_scale")
+    vecs = [norms["pre_ffw_norm_2"], norms["router_scale"], ds, norms["post_ffw_norm_2"], norms["post_ffw_norm"]]
+    fl = _norm_io(ctx, x, dense_ffn, *vecs, out_ids, out_w)
+    fl |= (LT_NORM_PRECISE if precise else 0) | (LT_MOE_NORM_TOPK if norm_topk else 0)
+    ctx._check(ctx.lib.lt_gemma4_moe_block(ctx.ptr, _ptr(x)[0], _ptr(dense_ffn)[0], router.handle, gate_up.handle,
+                                           down.handle, *(_ptr(v)[0] for v in vecs), layer_output_scale, eps, k,
+                                           d_expert, act, fl, _ptr(out_ids)[0], _ptr(out_w)[0]))
+    return x
 
 
 def upload_moe(ctx: Context, w) -> tuple:

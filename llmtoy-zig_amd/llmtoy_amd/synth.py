@@ -186,6 +186,27 @@ def config4(n_experts: int = 128, d_model: int = 2816, d_expert: int = 704, d_sh
         d_shared=d_shared)
 
 
+def gemma4_norms(config: int, d_model: int, n_experts: int, tid0: int = 40) -> dict:
+    """Norm and scale vectors of one Gemma4 MoE block (gemma4/weights.zig:
+    pre_ffw_norm_2, router_scale, down_exps_scale, post_ffw_norm_2,
+    post_ffw_norm), drawn around 1 so that no step is an identity."""
+    def around1(tid, n, sd):
+        return (1.0 + sd * stream(config, tid0 + tid).standard_normal(n)).astype(np.float32)
+    return dict(pre_ffw_norm_2=around1(0, d_model, 0.2), router_scale=around1(1, d_model, 0.1),
+                down_exps_scale=around1(2, n_experts, 0.25), post_ffw_norm_2=around1(3, d_model, 0.2),
+                post_ffw_norm=around1(4, d_model, 0.2))
+
+
+def config4_block(n_experts: int = 128, d_model: int = 2816, d_expert: int = 704) -> dict:
+    """The config-4 layer inside a Gemma4 block: x (residual stream), the
+    dense FFN output after post_ffw_norm_1, norm vectors, Q8_0 router, Q4_K
+    experts (K padded to 768), GELU, top-8, layer_output_scale 0.75."""
+    down_cols = (d_expert + 255) // 256 * 256
+    w = moe_weights(4, d_model, n_experts, d_expert, down_cols=down_cols, router_type=ggml.Q8_0)
+    return dict(x=normal(stream(4, 50), (d_model,)), dense_ffn=normal(stream(4, 51), (d_model,)), weights=w, k=8,
+                norms=gemma4_norms(4, d_model, n_experts), layer_output_scale=0.75, eps=1e-6)
+
+
 def config5(T: int = 512, weights: MoEWeights | None = None) -> dict:
     """Batched prefill of the config-3 layer with Zipf-biased router logits."""
     w = weights if weights is not None else moe_weights(3, 2048, 128, 768)

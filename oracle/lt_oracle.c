@@ -31,6 +31,19 @@
  *                         no reference code: pinned by their closed form only.
  *   lto_moe_layer_shared  gemma4/forward.zig:392-397, 417, 463-479  composition.
  *   lto_moe_prefill       T x lto_moe_forward (main.zig:1916-1922 prefills per token).
+ *   lto_rmsnorm           math.zig:19-25 (rmsnorm), 42-48 (rmsnormRaw: w == NULL) and
+ *                         the (1 + w) convention of rmsnorm.glsl.  KATs math.zig:344-354;
+ *                         a hand-derived case fixing the sequential sum of squares;
+ *                         closed forms on power-of-two vectors; float64.
+ *   lto_add_rmsnorm       add_rmsnorm.glsl semantics on the CPU order of
+ *                         gemma4/forward.zig:489-490 (a + b, then rmsnorm).  float64,
+ *                         equality with lto_rmsnorm of the rounded sum.
+ *   lto_rmsnorm_wrs       math.zig:51-82 (rmsnormWeightedAndRawScaled).  KAT math.zig:356-376
+ *                         (against separate passes); float64.
+ *   lto_gemma4_moe_block  gemma4/forward.zig:403-418, 463-497: router-input prep, router,
+ *                         expert loop with down_exps_scale, post_ffw_norm_2, combine with the
+ *                         dense FFN, post_ffw_norm, residual, layer_output_scale.  Composition
+ *                         of the pinned pieces; float64 restatement; planted-mistake checks.
  *
  * Floating point: every a*b+c below is a rounded multiply followed by a rounded
  * add (the file is compiled with -ffp-contract=off), vector reductions are the
@@ -784,4 +797,125 @@ int lto_moe_prefill(float *out, const float *X, size_t T, const float *router_w,
         if (rc) return rc;
     }
     return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMS normalisation: math.zig:19-25 (rmsnorm), 42-48 (rmsnormRaw).          */
+/* ss is the sequential fp32 sum of v*v in index order; rms_inv =           */
+/* 1 / sqrt(ss / n + eps) with correctly rounded sqrt and division; each    */
+/* output is (v * rms_inv) * w.  one_plus_w uses (1 + w) (rmsnorm.glsl      */
+/* flag bit 0); w == NULL multiplies by nothing (rmsnormRaw).               */
+static float rms_inv_of(const float *x, size_t n, float eps) {
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float sq = x[i] * x[i];
+        ss = ss + sq;
+    }
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+void lto_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps, int one_plus_w) {
+    const float r = rms_inv_of(x, n, eps);
+    const float bias = one_plus_w ? 1.0f : 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i] * r;
+        out[i] = w ? v * (bias + w[i]) : v;
+    }
+}
+
+/* out = rmsnorm(a + b, w): the sum is rounded first (gemma4/forward.zig:489-490). */
+void lto_add_rmsnorm(float *out, const float *a, const float *b, const float *w, size_t n, float eps,
+                     int one_plus_w) {
+    float *v = (float *)malloc(n * 4);
+    if (!v) return;
+    for (size_t i = 0; i < n; i++) v[i] = a[i] + b[i];
+    lto_rmsnorm(out, v, w, n, eps, one_plus_w);
+    free(v);
+}
+
+/* math.zig:51-82: one ss for both outputs; weighted = (x * rms_inv) * w,
+ * raw = (x * (rms_inv * raw_global_scale)) * raw_scale. */
+void lto_rmsnorm_wrs(float *weighted_out, float *raw_scaled_out, const float *x, const float *w,
+                     const float *raw_scale, float raw_global_scale, size_t n, float eps) {
+    const float r = rms_inv_of(x, n, eps);
+    const float raw_base = r * raw_global_scale;
+    for (size_t i = 0; i < n; i++) {
+        float a = x[i] * r;
+        float b = x[i] * raw_base;
+        weighted_out[i] = a * w[i];
+        raw_scaled_out[i] = b * raw_scale[i];
+    }
+}
+
+/* The MoE tail alone (gemma4/forward.zig:482-497): moe = rmsnorm(moe, w2);
+ * ffn = ffn + moe; ffn = rmsnorm(ffn, w); x = x + ffn; x *= los (if != 1).
+ * moe and ffn are overwritten as in the reference. */
+void lto_moe_tail(float *x, float *moe, float *ffn, const float *post_ffw_norm_2, const float *post_ffw_norm,
+                  float layer_output_scale, size_t n, float eps) {
+    lto_rmsnorm(moe, moe, post_ffw_norm_2, n, eps, 0);
+    for (size_t i = 0; i < n; i++) ffn[i] = ffn[i] + moe[i];
+    lto_rmsnorm(ffn, ffn, post_ffw_norm, n, eps, 0);
+    for (size_t i = 0; i < n; i++) x[i] = x[i] + ffn[i];
+    if (layer_output_scale != 1.0f)
+        for (size_t i = 0; i < n; i++) x[i] = x[i] * layer_output_scale;
+}
+
+/* Gemma4 MoE block after the dense FFN (gemma4/forward.zig:403-497).
+ * x [d] is the residual stream (updated in place); dense_ffn [d] the dense
+ * FFN output after post_ffw_norm_1 (not modified here: copied).
+ * down_exps_scale may be NULL (all ones). */
+int lto_gemma4_moe_block(float *x, const float *dense_ffn, size_t d_model, const uint8_t *router_w,
+                         uint32_t router_type, size_t n_experts, const uint8_t *gate_up, uint32_t gu_type,
+                         const uint8_t *down, uint32_t dn_type, size_t down_cols, size_t k, size_t d_expert,
+                         const float *pre_ffw_norm_2, const float *router_scale, const float *down_exps_scale,
+                         const float *post_ffw_norm_2, const float *post_ffw_norm, float layer_output_scale,
+                         float eps, uint32_t act, lto_pool *pool, uint32_t *out_ids, float *out_w) {
+    if (k == 0 || k > 16 || down_cols < d_expert) return -1;
+    size_t nthreads = (size_t)lto_pool_threads(pool);
+    size_t max_cols = d_model > down_cols ? d_model : down_cols;
+    float *moe_in = (float *)calloc(d_model, 4), *router_in = (float *)calloc(d_model, 4);
+    float *moe = (float *)calloc(d_model, 4), *ffn = (float *)calloc(d_model, 4);
+    float *scores = (float *)calloc(n_experts, 4), *scratch = (float *)calloc(nthreads * max_cols, 4);
+    float *eg = (float *)calloc(down_cols, 4), *eu = (float *)calloc(d_expert, 4), *ed = (float *)calloc(d_model, 4);
+    int rc = -2;
+    if (!moe_in || !router_in || !moe || !ffn || !scores || !scratch || !eg || !eu || !ed) goto done;
+    {
+        /* 403-418: shared residual RMS for the expert and router inputs */
+        const float inv_sqrt_d = 1.0f / sqrtf((float)d_model);
+        lto_rmsnorm_wrs(moe_in, router_in, x, pre_ffw_norm_2, router_scale, inv_sqrt_d, d_model, eps);
+        size_t top[16];
+        rc = lto_router_topk_softmax(scores, top, k, router_w, router_type, n_experts, d_model, router_in, scratch,
+                                     pool);
+        if (rc) goto done;
+        /* 463-479: expert loop */
+        size_t gu_rb = lto_row_bytes(gu_type, d_model), gu_per = 2 * d_expert * gu_rb;
+        size_t dn_rb = lto_row_bytes(dn_type, down_cols), dn_per = d_model * dn_rb;
+        for (size_t i = 0; i < k; i++) {
+            size_t e = top[i];
+            float w_score = scores[e];
+            const uint8_t *gd = gate_up + e * gu_per;
+            lto_quant_matvec_par(eg, gd, gu_type, moe_in, d_expert, d_model, scratch, pool);
+            lto_quant_matvec_par(eu, gd + d_expert * gu_rb, gu_type, moe_in, d_expert, d_model, scratch, pool);
+            for (size_t j = 0; j < d_expert; j++) {
+                float a = act_apply(act, eg[j]);
+                eg[j] = a * eu[j];
+            }
+            for (size_t j = d_expert; j < down_cols; j++) eg[j] = 0.0f;
+            lto_quant_matvec_par(ed, down + e * dn_per, dn_type, eg, d_model, down_cols, scratch, pool);
+            float expert_scale = (down_exps_scale ? down_exps_scale[e] : 1.0f) * w_score;
+            for (size_t j = 0; j < d_model; j++) {
+                float t = expert_scale * ed[j];
+                moe[j] = moe[j] + t;
+            }
+            if (out_ids) out_ids[i] = (uint32_t)e;
+            if (out_w) out_w[i] = w_score;
+        }
+        /* 482-497: the tail */
+        memcpy(ffn, dense_ffn, d_model * 4);
+        lto_moe_tail(x, moe, ffn, post_ffw_norm_2, post_ffw_norm, layer_output_scale, d_model, eps);
+        rc = 0;
+    }
+done:
+    free(moe_in); free(router_in); free(moe); free(ffn); free(scores); free(scratch); free(eg); free(eu); free(ed);
+    return rc;
 }

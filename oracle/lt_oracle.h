@@ -133,6 +133,27 @@ int lto_moe_prefill(float *out, const float *X, size_t T, const float *router_w,
                     size_t d_model, size_t k, size_t d_expert, uint32_t act, uint32_t flags,
                     lto_pool *pool, uint32_t *out_ids, float *out_w);
 
+/* ---- RMS norms and the Gemma4 MoE block: src/ops/math.zig, gemma4/forward.zig ---- */
+/* math.zig:19-25 / 42-48 (w == NULL); one_plus_w: out = x*r*(1+w)          */
+void lto_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps, int one_plus_w);
+/* rmsnorm(a + b, w) with the sum rounded first                              */
+void lto_add_rmsnorm(float *out, const float *a, const float *b, const float *w, size_t n, float eps,
+                     int one_plus_w);
+/* math.zig:51-82 rmsnormWeightedAndRawScaled                                */
+void lto_rmsnorm_wrs(float *weighted_out, float *raw_scaled_out, const float *x, const float *w,
+                     const float *raw_scale, float raw_global_scale, size_t n, float eps);
+/* gemma4/forward.zig:482-497; moe and ffn are overwritten                   */
+void lto_moe_tail(float *x, float *moe, float *ffn, const float *post_ffw_norm_2, const float *post_ffw_norm,
+                  float layer_output_scale, size_t n, float eps);
+/* gemma4/forward.zig:403-497: x (in/out) through the MoE block; dense_ffn is
+ * the dense FFN output after post_ffw_norm_1. down_exps_scale may be NULL.  */
+int lto_gemma4_moe_block(float *x, const float *dense_ffn, size_t d_model, const uint8_t *router_w,
+                         uint32_t router_type, size_t n_experts, const uint8_t *gate_up, uint32_t gu_type,
+                         const uint8_t *down, uint32_t dn_type, size_t down_cols, size_t k, size_t d_expert,
+                         const float *pre_ffw_norm_2, const float *router_scale, const float *down_exps_scale,
+                         const float *post_ffw_norm_2, const float *post_ffw_norm, float layer_output_scale,
+                         float eps, uint32_t act, lto_pool *pool, uint32_t *out_ids, float *out_w);
+
 #ifdef __cplusplus
 }
 #endif

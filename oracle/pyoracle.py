@@ -64,6 +64,12 @@ def lib() -> C.CDLL:
             "lto_ffn_dense": (C.c_int, [vp, vp, vp, vp, u32, vp, sz, sz, u32, vp]),
             "lto_moe_prefill": (C.c_int, [vp, vp, sz, vp, sz, vp, vp, u32, vp, u32, sz, sz, sz, sz, u32, u32, vp,
                                           vp, vp]),
+            "lto_rmsnorm": (None, [vp, vp, vp, sz, f, C.c_int]),
+            "lto_add_rmsnorm": (None, [vp, vp, vp, vp, sz, f, C.c_int]),
+            "lto_rmsnorm_wrs": (None, [vp, vp, vp, vp, vp, f, sz, f]),
+            "lto_moe_tail": (None, [vp, vp, vp, vp, vp, f, sz, f]),
+            "lto_gemma4_moe_block": (C.c_int, [vp, vp, sz, vp, u32, sz, vp, u32, vp, u32, sz, sz, sz, vp, vp, vp,
+                                               vp, vp, f, f, u32, vp, vp, vp]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -275,3 +281,54 @@ def moe_prefill(w, X, k, act=ACT_SILU, norm_topk=False, bias=None, pool: Pool | 
     if rc:
         raise ValueError(f"moe_prefill failed ({rc})")
     return out, ids, wt
+
+
+# ---------------------------------------------------------------- norms, Gemma4 block
+def rmsnorm(x, w=None, eps=1e-6, one_plus_w=False) -> np.ndarray:
+    """math.rmsnorm (w given) / rmsnormRaw (w None)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().lto_rmsnorm(_p(out), _p(x), None if w is None else _p(_f32(w)), x.size, eps, int(one_plus_w))
+    return out
+
+
+def add_rmsnorm(a, b, w, eps=1e-6, one_plus_w=False) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    lib().lto_add_rmsnorm(_p(out), _p(a), _p(b), _p(_f32(w)), a.size, eps, int(one_plus_w))
+    return out
+
+
+def rmsnorm_wrs(x, w, raw_scale, raw_global_scale, eps=1e-6):
+    """math.rmsnormWeightedAndRawScaled: returns (weighted, raw_scaled)."""
+    x = _f32(x)
+    wo, ro = np.empty_like(x), np.empty_like(x)
+    lib().lto_rmsnorm_wrs(_p(wo), _p(ro), _p(x), _p(_f32(w)), _p(_f32(raw_scale)), raw_global_scale, x.size, eps)
+    return wo, ro
+
+
+def moe_tail(x, moe, ffn, post_ffw_norm_2, post_ffw_norm, layer_output_scale=1.0, eps=1e-6) -> np.ndarray:
+    """gemma4/forward.zig:482-497 on copies; returns the new x."""
+    x, moe, ffn = _f32(x).copy(), _f32(moe).copy(), _f32(ffn).copy()
+    lib().lto_moe_tail(_p(x), _p(moe), _p(ffn), _p(_f32(post_ffw_norm_2)), _p(_f32(post_ffw_norm)),
+                       layer_output_scale, x.size, eps)
+    return x
+
+
+def gemma4_moe_block(w, x, dense_ffn, k, norms, layer_output_scale=1.0, eps=1e-6, act=ACT_GELU_TANH,
+                     pool: Pool | None = None):
+    """gemma4/forward.zig:403-497 on a synth.MoEWeights; norms: dict with
+    pre_ffw_norm_2, router_scale, down_exps_scale (or None), post_ffw_norm_2,
+    post_ffw_norm.  Returns (new x, ids, router probabilities)."""
+    x = _f32(x).copy()
+    ids = np.zeros(k, dtype=np.uint32)
+    wt = np.zeros(k, dtype=np.float32)
+    ds = norms.get("down_exps_scale")
+    rc = lib().lto_gemma4_moe_block(
+        _p(x), _p(_f32(dense_ffn)), w.d_model, _p(_u8(w.router)), w.router_type, w.n_experts, _p(_u8(w.gate_up)),
+        Q4_K, _p(_u8(w.down)), Q4_K, w.down_cols, k, w.d_expert, _p(_f32(norms["pre_ffw_norm_2"])),
+        _p(_f32(norms["router_scale"])), None if ds is None else _p(_f32(ds)), _p(_f32(norms["post_ffw_norm_2"])),
+        _p(_f32(norms["post_ffw_norm"])), layer_output_scale, eps, act, _pp(pool), _p(ids), _p(wt))
+    if rc:
+        raise ValueError(f"gemma4_moe_block failed ({rc})")
+    return x, ids, wt
