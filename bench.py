@@ -213,6 +213,111 @@ def bench_prefill(args):
     print(json.dumps(result), flush=True)
 
 
+# config-4 Gemma4 block (d_model 2816, 128 experts, d_expert 704 padded to 768, top-8, Q8_0 router)
+G4_D, G4_E, G4_F, G4_KD = 2816, 128, 704, 768
+G4_EXPERT_BYTES = 2 * G4_F * (G4_D // 256) * 144 + G4_D * (G4_KD // 256) * 144  # 3,446,784 B
+G4_ROUTER_BYTES = G4_E * (G4_D // 32) * 34                                        # 382,976 B
+# selected experts + router + x read/written + dense + 5 norm vectors (4 x d, 1 x E)
+G4_BLOCK_BYTES = K * G4_EXPERT_BYTES + G4_ROUTER_BYTES + 3 * G4_D * 4 + 4 * G4_D * 4 + G4_E * 4
+
+
+def bench_gemma4(args):
+    """Config-4 layer inside the Gemma4 block (router-input prep, Q8_0 router,
+    Q4_K experts with down_exps_scale, GELU, MoE tail): one decode token per step."""
+    import numpy as np
+
+    import llmtoy_amd as lt
+    import pyoracle as orc
+    from llmtoy_amd import lib as ltlib, synth
+    from llmtoy_amd.hip import DeviceArray, Event, Graph, sync_stream
+
+    c = synth.config4_block()
+    w, nm = c["weights"], c["norms"]
+    ctx = lt.Context(0)
+    base = lt.upload_moe(ctx, w)
+    copies = [base] + [tuple(t.clone() for t in base) for _ in range(args.copies - 1)]
+    xs = np.stack([c["x"]] + [synth.normal(synth.stream(4, 70 + i), (G4_D,)) for i in range(1, args.xpool)])
+    # parity of the benchmarked configuration (reference-order norms, then the default tree sums)
+    parity = {}
+    with orc.Pool(min(16, os.cpu_count() or 1)) as pool:
+        ref, rids, _ = orc.gemma4_moe_block(w, xs[0], c["dense_ffn"], K, nm, c["layer_output_scale"], c["eps"],
+                                            pool=pool)
+    for precise in (True, False):
+        ids = np.zeros(K, np.uint32)
+        got = ltlib.gemma4_moe_block(ctx, xs[0].copy(), c["dense_ffn"], *base, K, G4_F, nm, c["layer_output_scale"],
+                                     c["eps"], precise=precise, out_ids=ids)
+        parity["precise" if precise else "tree"] = {
+            "ids_bit_exact": bool(np.array_equal(ids, rids)),
+            "rel_l2": float(np.linalg.norm(got - ref) / np.linalg.norm(ref))}
+    log(f"gemma4 block parity: {parity}")
+    X = DeviceArray.from_numpy(xs)
+    dense = DeviceArray.from_numpy(c["dense_ffn"])
+    dn = {k: (DeviceArray.from_numpy(v) if v is not None else None) for k, v in nm.items()}
+    stream = ctx.stream
+
+    def step(i):
+        r, g, d = copies[i % args.copies]
+        ltlib.gemma4_moe_block(ctx, X.row(i % args.xpool), dense, r, g, d, K, G4_F, dn, c["layer_output_scale"],
+                               c["eps"])
+
+    for i in range(args.warmup):
+        step(i)
+    sync_stream(stream)
+    G = 64
+    graph = Graph(stream, lambda: [step(i) for i in range(G)])
+    graph.launch()
+    sync_stream(stream)
+    n_graphs = max(1, args.steps // G)
+    e0, e1 = Event(), Event()
+    t = time.perf_counter()
+    e0.record(stream)
+    for _ in range(n_graphs):
+        graph.launch()
+    e1.record(stream)
+    sync_stream(stream)
+    wall = time.perf_counter() - t
+    steps = n_graphs * G
+    us = wall / steps * 1e6
+    dev_us = e0.elapsed_ms(e1) * 1e3 / steps
+    gbps = G4_BLOCK_BYTES / (dev_us * 1e-6) / 1e9
+    log(f"gemma4 block: {us:.2f} us/token wall, {dev_us:.2f} us/token device, {gbps:.0f} GB/s")
+    result = {"metric": "Gemma4 MoE block decode us/token (config-4 layer + router-input prep + MoE tail)",
+              "value": round(us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+              "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "dtype": "fp32", "data": "synthetic",
+              "config": {"workload": "gemma4_moe_block_cfg4", "d_model": G4_D, "n_experts": G4_E,
+                         "d_expert": G4_F, "down_cols": G4_KD, "top_k": K, "router": "Q8_0", "experts": "Q4_K",
+                         "act": "gelu_tanh", "norm_sum": "tree", "weight_copies": args.copies,
+                         "x_pool": args.xpool, "graph_steps": G},
+              "device_us_per_token": round(dev_us, 3),
+              "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                           "frac": round(gbps / PEAK_GBPS, 4), "traffic": None,
+                           "kernel": "whole block (5 launches per token)", "algorithmic_bytes": G4_BLOCK_BYTES},
+              "parity": parity}
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        with orc.Pool(threads) as pool:
+            orc.gemma4_moe_block(w, xs[0], c["dense_ffn"], K, nm, c["layer_output_scale"], c["eps"], pool=pool)
+            ts, t_end, i = [], time.perf_counter() + args.cpu_seconds / 2, 0
+            while (time.perf_counter() < t_end or len(ts) < 20) and len(ts) < 2000:
+                t0 = time.perf_counter()
+                orc.gemma4_moe_block(w, xs[i % len(xs)], c["dense_ffn"], K, nm, c["layer_output_scale"], c["eps"],
+                                     pool=pool)
+                ts.append(time.perf_counter() - t0)
+                i += 1
+        result["cpu_baseline"] = {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/token",
+                                  "cores": threads, "kind": "port",
+                                  "sample": f"{len(ts)} config-4 block tokens, median; oracle lto_gemma4_moe_block "
+                                            f"(quantMatvecPar rows over a {threads}-thread pool)"}
+    print(json.dumps(result), flush=True)
+    graph.destroy()
+    for a in [X, dense] + [v for v in dn.values() if v is not None]:
+        a.free()
+    for cp in copies:
+        for tns in cp:
+            tns.free()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,7 +330,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF file load + upload check")
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "prefill", "gemma4"], default="decode")
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -238,6 +343,11 @@ def main():
         args.steps = args.steps or 50
         args.warmup = args.warmup if args.warmup is not None else 5
         bench_prefill(args)
+        return
+    if args.workload == "gemma4":
+        args.steps = args.steps or 2048
+        args.warmup = args.warmup if args.warmup is not None else 64
+        bench_gemma4(args)
         return
     args.steps = args.steps or 4096
     args.warmup = args.warmup if args.warmup is not None else 256
