@@ -17,6 +17,13 @@
 //                                  experts are not on the device, which the
 //                                  caller answers with its CPU loop,
 //                                  gemma4/forward.zig:434-480)
+//   rmsnorm, rmsnormWeightedAndRawScaled
+//                                  ops/math.zig:19-25, 42-48, 51-82
+//   MoeTailParams                  gemma4/gpu_weights.zig:100-109
+//   GpuWeights::runMoeBlock        runExpertBatch with the GPU router and
+//                                  the MoE residual tail (gpu_weights.zig:
+//                                  2748-3149, 3349-3410; the CPU order of
+//                                  gemma4/forward.zig:403-497)
 //
 // Zig error unions become llmtoy::Exception carrying an Error kind; the
 // reference's std.debug.panic on an unsupported type (math.zig:206, 223)
@@ -172,6 +179,36 @@ inline void moeForward(GpuContext &g, float *out, const RawMatrix &router_w, con
                            nullptr));
 }
 
+// ops/math.zig:19-25 (rmsnorm) and 42-48 (rmsnormRaw: weight == nullptr) on
+// host vectors of n floats.  precise: the reference's index-order sum of
+// squares (bit-exact with the CPU code); otherwise a fixed tree order.
+inline void rmsnorm(GpuContext &g, float *out, const float *x, const float *weight, size_t n, float eps,
+                    bool precise = false) {
+    g.check(lt_rmsnorm(g.raw(), out, x, weight, 1, (uint32_t)n, eps, LT_HOST_IO | (precise ? LT_NORM_PRECISE : 0u)));
+}
+
+// ops/math.zig:51-82
+inline void rmsnormWeightedAndRawScaled(GpuContext &g, float *weighted_out, float *raw_scaled_out, const float *x,
+                                        const float *weight, const float *raw_scale, float raw_global_scale,
+                                        size_t n, float eps, bool precise = false) {
+    g.check(lt_rmsnorm_weighted_raw_scaled(g.raw(), weighted_out, raw_scaled_out, x, weight, raw_scale,
+                                           raw_global_scale, (uint32_t)n, eps,
+                                           LT_HOST_IO | (precise ? LT_NORM_PRECISE : 0u)));
+}
+
+// gemma4/gpu_weights.zig:100-109: what the MoE residual tail needs.
+struct MoeTailParams {
+    float eps;
+    float *x;                 // residual stream, updated in place
+    const float *dense_ffn;   // dense FFN output after post_ffw_norm_1
+    float layer_output_scale;
+};
+
+// The per-layer vectors of the Gemma4 MoE block (gemma4/weights.zig).
+struct Gemma4MoeNorms {
+    const float *pre_ffw_norm_2, *router_scale, *down_exps_scale, *post_ffw_norm_2, *post_ffw_norm;
+};
+
 // gpu/matvec.zig:497-647: one matrix resident on the device.
 class MatvecSession {
    public:
@@ -231,6 +268,27 @@ class GpuWeights {
                                        (uint32_t)down_cols_, act, h.data(), LT_HOST_IO));
         g_->check(lt_expert_down_id(g_->raw(), down_, h.data(), ids.data(), w.data(), (uint32_t)n, moe_buf,
                                     LT_HOST_IO | LT_MOE_ACCUMULATE));
+    }
+
+    // The whole MoE block of one token on the device: router-input prep,
+    // routerTopKSoftmax on router_w, the selected experts scaled by
+    // down_exps_scale, and the tail (post_ffw_norm_2, + dense FFN,
+    // post_ffw_norm, residual, layer_output_scale) -- runExpertBatch with the
+    // GPU router and MoeTailParams.  tail.x is updated in place; top_idx and
+    // router_out_sel (may be null) receive the selection and its softmax
+    // probabilities.
+    void runMoeBlock(const RawMatrix &router_w, const Gemma4MoeNorms &nm, size_t n_experts_used,
+                     const MoeTailParams &tail, size_t *top_idx = nullptr, float *router_out_sel = nullptr,
+                     uint32_t act = LT_ACT_GELU_TANH, bool precise = false) {
+        if (!on_gpu_) throw Exception(Error::ExpertNotOnGpu, LT_ERR_UNSUPPORTED, "experts are not on the GPU");
+        std::vector<uint32_t> ids(n_experts_used);
+        g_->check(lt_gemma4_moe_block(g_->raw(), tail.x, tail.dense_ffn, g_->tensor(router_w), gate_up_, down_,
+                                      nm.pre_ffw_norm_2, nm.router_scale, nm.down_exps_scale, nm.post_ffw_norm_2,
+                                      nm.post_ffw_norm, tail.layer_output_scale, tail.eps, (uint32_t)n_experts_used,
+                                      (uint32_t)d_expert_, act, LT_HOST_IO | (precise ? LT_NORM_PRECISE : 0u),
+                                      ids.data(), router_out_sel));
+        if (top_idx)
+            for (size_t i = 0; i < n_experts_used; i++) top_idx[i] = ids[i];
     }
 
    private:

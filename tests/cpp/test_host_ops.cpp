@@ -211,6 +211,45 @@ static void test_expert_not_on_gpu(GpuContext &g) {  // gemma4/forward.zig:434-4
     EXPECT(thrown);
 }
 
+static void test_rmsnorm_kat(GpuContext &g) {  // ops/math.zig:344-354
+    const float x[4] = {1, 2, 3, 4}, w[4] = {1, 1, 1, 1};
+    float out[4];
+    rmsnorm(g, out, x, w, 4, 1e-8f);
+    const float rms = std::sqrt((1.0f + 4.0f + 9.0f + 16.0f) / 4.0f);
+    EXPECT(std::fabs(out[0] - x[0] / rms) <= 1e-5f && std::fabs(out[3] - x[3] / rms) <= 1e-5f);
+    float wo[4], ro[4], ref_w[4], ref_r[4];
+    const float xs[4] = {3, -4, 1, 2}, ww[4] = {0.5f, 1.25f, -0.75f, 2.0f}, sc[4] = {2.0f, 0.25f, -1.0f, 0.5f};
+    rmsnormWeightedAndRawScaled(g, wo, ro, xs, ww, sc, 0.125f, 4, 1e-6f, true);  // math.zig:356-376
+    lto_rmsnorm_wrs(ref_w, ref_r, xs, ww, sc, 0.125f, 4, 1e-6f);
+    EXPECT(std::memcmp(wo, ref_w, sizeof wo) == 0 && std::memcmp(ro, ref_r, sizeof ro) == 0);
+}
+
+static void test_run_moe_block(GpuContext &g) {  // gemma4/forward.zig:403-497
+    Layer L(404);
+    Scoped sc{g, L};
+    Rng r{405};
+    auto vec = [&](size_t n, float c, float a) {
+        std::vector<float> v(n);
+        for (auto &t : v) t = c + (r.uniform() - 0.5f) * a;
+        return v;
+    };
+    const std::vector<float> pre = vec(L.D, 1, 0.4f), rs = vec(L.D, 1, 0.2f), ds = vec(L.E, 1, 0.5f),
+                             p2 = vec(L.D, 1, 0.4f), p = vec(L.D, 1, 0.4f), dense = vec(L.D, 0, 2);
+    const Gemma4MoeNorms nm{pre.data(), rs.data(), ds.data(), p2.data(), p.data()};
+    std::vector<float> x = L.x, ref = L.x;
+    GpuWeights gw(g, L.GU(), L.DN(), L.E, L.F);
+    size_t top[4];
+    gw.runMoeBlock(L.R(), nm, L.k, MoeTailParams{1e-6f, x.data(), dense.data(), 0.75f}, top, nullptr,
+                   LT_ACT_GELU_TANH, true);
+    uint32_t rids[4];
+    EXPECT(lto_gemma4_moe_block(ref.data(), dense.data(), L.D, (const uint8_t *)L.router.data(), LTO_F32, L.E,
+                                L.gate_up.data(), LTO_Q4_K, L.down.data(), LTO_Q4_K, L.F, L.k, L.F, pre.data(),
+                                rs.data(), ds.data(), p2.data(), p.data(), 0.75f, 1e-6f, LTO_ACT_GELU_TANH, nullptr,
+                                rids, nullptr) == 0);
+    for (size_t i = 0; i < L.k; i++) EXPECT(top[i] == rids[i]);
+    EXPECT(rel_l2(x, ref) < 1e-3);
+}
+
 int main(int argc, char **argv) {
     const std::vector<std::pair<std::string, std::function<void(GpuContext &)>>> tests = {
         {"gpu matvec Q8_0 correctness", test_q8_0_correctness},
@@ -223,6 +262,8 @@ int main(int argc, char **argv) {
         {"moeForward: accumulates the weighted experts into out", test_moe_forward_accumulates},
         {"runExpertBatch: matches the CPU expert loop", test_run_expert_batch},
         {"runExpertBatch: non-device experts raise ExpertNotOnGpu", test_expert_not_on_gpu},
+        {"rmsnorm: all-ones weight is pure normalisation", test_rmsnorm_kat},
+        {"runMoeBlock: matches the Gemma4 CPU block", test_run_moe_block},
     };
     if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
         for (auto &t : tests) std::printf("%s\n", t.first.c_str());

@@ -59,7 +59,7 @@ def test_cpp_host_layer_builds_and_lists_tests():
     out = subprocess.run([CPP_TEST, "--list"], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0
     names = out.stdout.splitlines()
-    assert "gpu matvec Q4_K scale" in names and len(names) == 10
+    assert "gpu matvec Q4_K scale" in names and len(names) == 12
 
 
 @pytest.mark.gpu
