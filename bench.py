@@ -318,6 +318,66 @@ def bench_gemma4(args):
     ctx.close()
 
 
+def bench_formats(args):
+    """Dense matvec over the Gemma4 APEX expert formats (Q5_0, Q5_1, IQ4_NL,
+    Q3_K) and Q4_K for comparison: one [131072 x 4096] matrix per format, two
+    copies alternated so reads come from HBM; mean launch duration from a HIP
+    event pair on the library stream around back-to-back launches."""
+    import numpy as np
+
+    import llmtoy_amd as lt
+    import pyoracle as orc
+    from llmtoy_amd import ggml, synth
+    from llmtoy_amd.hip import DeviceArray, Event, sync_stream
+
+    rows, cols = 131072, 4096
+    ctx = lt.Context(0)
+    stream = ctx.stream
+    g = np.random.default_rng(7)
+    x = synth.normal(g, (cols,))
+    X = DeviceArray.from_numpy(x)
+    Y = DeviceArray((rows,), np.float32)
+    per = {}
+    for gtype in (ggml.Q5_0, ggml.Q5_1, ggml.IQ4_NL, ggml.Q3_K, ggml.Q4_K):
+        name = ggml.NAMES[gtype]
+        # parity on a 512-row slice, then the full-size copies (generated in slices)
+        m = np.concatenate([synth.quant_matrix(np.random.default_rng(100 + i), gtype, 8192, cols)
+                            for i in range(rows // 8192)])
+        t0 = ctx.upload(m, gtype, rows, cols)
+        t1 = t0.clone()
+        y = np.zeros(rows, np.float32)
+        ctx.quant_matvec(y, t0, x)
+        ref = orc.quant_matvec(m[:512], gtype, x, 512, cols)
+        err = float(np.max(np.abs(y[:512] - ref)) / np.max(np.abs(ref)))
+        nbytes = m.nbytes
+        del m
+        for i in range(8):
+            ctx.quant_matvec(Y, (t0, t1)[i & 1], X)
+        sync_stream(stream)
+        n = 64
+        a, b = Event(), Event()
+        a.record(stream)
+        for i in range(n):
+            ctx.quant_matvec(Y, (t0, t1)[i & 1], X)
+        b.record(stream)
+        sync_stream(stream)
+        us = a.elapsed_ms(b) * 1e3 / n
+        gbps = (nbytes + cols * 4 + rows * 4) / (us * 1e-6) / 1e9
+        per[name] = {"us": round(us, 2), "gbps": round(gbps, 1), "frac": round(gbps / PEAK_GBPS, 4),
+                     "weight_bytes": nbytes, "max_rel_err": err}
+        log(f"matvec {name} {rows}x{cols}: {us:.1f} us, {gbps:.0f} GB/s, parity max rel {err:.2e}")
+        t0.free()
+        t1.free()
+    result = {"metric": "dense matvec GB/s per GGUF format (131072 x 4096, batch 1)", "unit": "GB/s",
+              "value": per["Q3_K"]["gbps"], "higher_is_better": True, "n_gpus": 1, "dtype": "fp32",
+              "data": "synthetic", "config": {"workload": "matvec_formats", "rows": rows, "cols": cols},
+              "per_format": per}
+    print(json.dumps(result), flush=True)
+    X.free()
+    Y.free()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -330,7 +390,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF file load + upload check")
-    ap.add_argument("--workload", choices=["decode", "prefill", "gemma4"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "prefill", "gemma4", "formats"], default="decode")
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -343,6 +403,9 @@ def main():
         args.steps = args.steps or 50
         args.warmup = args.warmup if args.warmup is not None else 5
         bench_prefill(args)
+        return
+    if args.workload == "formats":
+        bench_formats(args)
         return
     if args.workload == "gemma4":
         args.steps = args.steps or 2048

@@ -41,7 +41,12 @@ enum {
     LT_TYPE_F16 = 1,
     LT_TYPE_Q8_0 = 8,
     LT_TYPE_Q4_K = 12,
-    LT_TYPE_Q6_K = 14
+    LT_TYPE_Q6_K = 14,
+    /* the Gemma4 APEX expert formats (quant/dequant.zig:189-217, 366-486, 607-659) */
+    LT_TYPE_Q5_0 = 6,
+    LT_TYPE_Q5_1 = 7,
+    LT_TYPE_Q3_K = 11,
+    LT_TYPE_IQ4_NL = 20
 };
 
 /* Gated-FFN activation: SiLU (ops/math.zig:37-40) or GELU-tanh (math.zig:84-88). */

@@ -89,7 +89,11 @@ size_t block_elems(uint32_t type) {
     case LT_TYPE_F32: return 1;
     case LT_TYPE_Q8_0: return 32;
     case LT_TYPE_Q4_K:
-    case LT_TYPE_Q6_K: return 256;
+    case LT_TYPE_Q6_K:
+    case LT_TYPE_Q3_K: return 256;
+    case LT_TYPE_Q5_0:
+    case LT_TYPE_Q5_1:
+    case LT_TYPE_IQ4_NL: return 32;
     default: return 0;
     }
 }
@@ -100,6 +104,10 @@ size_t block_bytes(uint32_t type) {
     case LT_TYPE_Q8_0: return 34;
     case LT_TYPE_Q4_K: return 144;
     case LT_TYPE_Q6_K: return 210;
+    case LT_TYPE_Q5_0: return 22;
+    case LT_TYPE_Q5_1: return 24;
+    case LT_TYPE_IQ4_NL: return 18;
+    case LT_TYPE_Q3_K: return 110;
     default: return 0;
     }
 }
@@ -119,6 +127,22 @@ void set_planes(DevTensor &t) {
         t.p1 = b + nblk * 128;
         t.p2 = t.p1 + nblk * 64;
         t.p3 = t.p2 + nblk * 16;
+        break;
+    case LT_TYPE_Q5_0:  // qs [16], qh [4], d [2]
+        t.p1 = b + nblk * 16;
+        t.p2 = t.p1 + nblk * 4;
+        break;
+    case LT_TYPE_Q5_1:  // qs [16], qh [4], d and m [4]
+        t.p1 = b + nblk * 16;
+        t.p2 = t.p1 + nblk * 4;
+        break;
+    case LT_TYPE_IQ4_NL:  // qs [16], d [2]
+        t.p1 = b + nblk * 16;
+        break;
+    case LT_TYPE_Q3_K:  // qs [64], hmask [32], scales [12], d [2]
+        t.p1 = b + nblk * 64;
+        t.p2 = t.p1 + nblk * 32;
+        t.p3 = t.p2 + nblk * 12;
         break;
     default: break;
     }
@@ -198,6 +222,10 @@ int matvec_dev(lt_ctx *ctx, const DevTensor &W, const float *x, float *y) {
     case LT_TYPE_Q8_0: e = lt::launch_matvec_q8_0(W, x, y, ctx->stream); break;
     case LT_TYPE_Q6_K: e = lt::launch_matvec_q6k(W, x, y, ctx->stream); break;
     case LT_TYPE_F32: e = lt::launch_matvec_f32(W, x, y, ctx->stream); break;
+    case LT_TYPE_Q5_0:
+    case LT_TYPE_Q5_1:
+    case LT_TYPE_IQ4_NL:
+    case LT_TYPE_Q3_K: e = lt::launch_matvec_fmt(W, x, y, ctx->stream); break;
     default: return fail(ctx, LT_ERR_UNSUPPORTED, "matvec: unsupported type %u", W.type);
     }
     return launch_rc(ctx, e, "matvec");

@@ -1,0 +1,197 @@
+// lt_formats.hip -- matvec over the Gemma4 APEX expert formats: Q5_0, Q5_1,
+// IQ4_NL (32-element blocks) and Q3_K (256-element super-blocks), on the
+// planar layout lt_tensor_upload makes:
+//
+//   Q5_0    qs [R][nb][16], qh [R][nb][4] (u32 LE), d [R][nb] (f16)
+//           value = d * ((nibble | high bit << 4) - 16)       dequant.zig:189-217
+//   Q5_1    qs [R][nb][16], qh [R][nb][4], dm [R][nb][2] (f16 d, f16 m)
+//           value = d * (nibble | high bit << 4) + m          dequant.zig:456-486
+//   IQ4_NL  qs [R][nb][16], d [R][nb]
+//           value = d * table[nibble]                         dequant.zig:607-640
+//   Q3_K    qs [R][nsb][64], hmask [R][nsb][32], scales [R][nsb][12], d [R][nsb]
+//           element 128h + 32j + 16g + l: value = d * (sc[8h + 2j + g] - 32)
+//           * (((qs[32h + 16g + l] >> 2j) & 3) - 4 * !(hmask[16g + l] >> (j + 4h) & 1))
+//                                                             dequant.zig:366-454
+//
+// Work unit: one 32-element block (Q5_0/Q5_1/IQ4_NL) or one 128-element
+// half super-block (Q3_K).  One wavefront per row, lanes striding over the
+// row's units; x staged once per workgroup in LDS.  fp32 accumulation in an
+// order of our own: parity with the reference's quantMatvec is to tolerance
+// (its GPU matvec fuzz bound, 1e-4 of max |y|), not bit-exact.
+#include "llmtoy_hip.h"
+#include "lt_internal.h"
+
+namespace lt {
+
+namespace {
+
+constexpr int kFmtWaves = 4;  // rows per workgroup
+
+__constant__ float kIq4nlTable[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+__device__ __forceinline__ float f16_at(const uint8_t *p) {
+    return f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(p));
+}
+
+// Sum of q[e] * x[e] for the 32 elements of a Q5 block: nibble e of qs
+// (e < 16 low, else high nibble of byte e - 16), high bit e of qh; bias
+// subtracts 16 (Q5_0) or nothing (Q5_1).  Also returns the sum of x (Q5_1's m).
+__device__ __forceinline__ float q5_block_dot(uint4 qv, uint32_t qh, const float *x, float bias, float &xsum) {
+    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+    float acc = 0.f, sx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
+        const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
+        const float xl[4] = {lo.x, lo.y, lo.z, lo.w}, xh[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int e = 4 * i + b;
+            const uint32_t byte = (w[i] >> (8 * b)) & 0xffu;
+            const float ql = (float)((byte & 15u) | (((qh >> e) & 1u) << 4)) - bias;
+            const float qhv = (float)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - bias;
+            acc += ql * xl[b] + qhv * xh[b];
+            sx += xl[b] + xh[b];
+        }
+    }
+    xsum = sx;
+    return acc;
+}
+
+__device__ __forceinline__ float iq4_block_dot(uint4 qv, const float *x, const float *tab) {
+    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
+        const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
+        const float xl[4] = {lo.x, lo.y, lo.z, lo.w}, xh[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t byte = (w[i] >> (8 * b)) & 0xffu;
+            acc += tab[byte & 15u] * xl[b] + tab[byte >> 4] * xh[b];
+        }
+    }
+    return acc;
+}
+
+// Q3_K scale i (0..15) from the 12 packed bytes s[0..2] (little-endian
+// dwords): low 4 bits from byte i (i < 8) or the high nibble of byte i - 8,
+// high 2 bits from bits 2 (i / 4) of byte 8 + i % 4.
+__device__ __forceinline__ int q3k_scale(const uint32_t s[3], int i) {
+    const uint32_t lo = i < 8 ? (s[i >> 2] >> (8 * (i & 3))) & 15u : (s[(i - 8) >> 2] >> (8 * ((i - 8) & 3) + 4)) & 15u;
+    const uint32_t hi = (s[2] >> (8 * (i & 3) + 2 * (i >> 2))) & 3u;
+    return (int)(lo | (hi << 4));
+}
+
+// Half h of a Q3_K super-block (128 elements) against x[128 h ...].
+__device__ __forceinline__ float q3k_half_dot(const uint8_t *qs64, const uint8_t *hm32, const uint32_t sc[3],
+                                              float d, int h, const float *x) {
+    const uint4 q0 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h);
+    const uint4 q1 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h + 16);
+    const uint4 m0 = *reinterpret_cast<const uint4 *>(hm32);
+    const uint4 m1 = *reinterpret_cast<const uint4 *>(hm32 + 16);
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    float total = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const float *xs = x + 128 * h + 32 * j + 16 * g;
+            float acc = 0.f;
+#pragma unroll
+            for (int w4 = 0; w4 < 4; w4++) {
+                const float4 xv = *reinterpret_cast<const float4 *>(xs + 4 * w4);
+                const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+                const uint32_t qword = qw[4 * g + w4], mword = mw[4 * g + w4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int q2 = (int)((qword >> (8 * b + 2 * j)) & 3u);
+                    const int hb = (int)((mword >> (8 * b + j + 4 * h)) & 1u);
+                    acc += (float)(q2 - 4 + 4 * hb) * xa[b];
+                }
+            }
+            total += (d * (float)(q3k_scale(sc, 8 * h + 2 * j + g) - 32)) * acc;
+        }
+    }
+    return total;
+}
+
+template <int T>
+__global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, const float *__restrict__ x,
+                                                               float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats
+    __shared__ float tab[16];
+    const int cols = (int)W.cols;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) xs[i] = x[i];
+    if (T == LT_TYPE_IQ4_NL && threadIdx.x < 16) tab[threadIdx.x] = kIq4nlTable[threadIdx.x];
+    __syncthreads();
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const size_t row = (size_t)blockIdx.x * kFmtWaves + wave;
+    if (row >= W.total_rows) return;
+    const int nb = (int)W.blocks_per_row;
+    float acc = 0.f;
+    if (T == LT_TYPE_Q3_K) {
+        for (int u = lane; u < 2 * nb; u += kWave) {
+            const size_t sb = row * nb + (u >> 1);
+            const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
+            const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
+            acc += q3k_half_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 1,
+                                xs + 256 * (u >> 1));
+        }
+    } else {
+        for (int u = lane; u < nb; u += kWave) {
+            const size_t b = row * nb + u;
+            const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
+            const float *xb = xs + 32 * u;
+            if (T == LT_TYPE_IQ4_NL) {
+                acc += f16_at(W.p1 + b * 2) * iq4_block_dot(qv, xb, tab);
+            } else {
+                const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
+                float sx;
+                if (T == LT_TYPE_Q5_0) {
+                    acc += f16_at(W.p2 + b * 2) * q5_block_dot(qv, qh, xb, 16.f, sx);
+                } else {  // Q5_1: d * sum(q x) + m * sum(x)
+                    const float dot = q5_block_dot(qv, qh, xb, 0.f, sx);
+                    acc += f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * sx;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (lane == 0) y[row] = acc;
+}
+
+template <int T>
+hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    const size_t lds = W.cols * sizeof(float);
+    static bool lds_set[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!lds_set[dev]) {  // rows up to 16 K floats stage 64 KiB of x
+        e = hipFuncSetAttribute((const void *)k_matvec_fmt<T>, hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+        if (e != hipSuccess) return e;
+        lds_set[dev] = true;
+    }
+    const dim3 grid((unsigned)((W.total_rows + kFmtWaves - 1) / kFmtWaves));
+    hipLaunchKernelGGL(k_matvec_fmt<T>, grid, dim3(64 * kFmtWaves), lds, s, W, x, y);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_matvec_fmt(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    switch (W.type) {
+    case LT_TYPE_Q5_0: return launch_t<LT_TYPE_Q5_0>(W, x, y, s);
+    case LT_TYPE_Q5_1: return launch_t<LT_TYPE_Q5_1>(W, x, y, s);
+    case LT_TYPE_IQ4_NL: return launch_t<LT_TYPE_IQ4_NL>(W, x, y, s);
+    case LT_TYPE_Q3_K: return launch_t<LT_TYPE_Q3_K>(W, x, y, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace lt

@@ -13,6 +13,11 @@
 //   Q6_K  (210 B / 256 elements, dequant.zig:219-235)
 //         ql plane [R][nsb][128], qh plane [R][nsb][64],
 //         sc plane [R][nsb][16] (int8), d plane [R][nsb] (f16)
+//   Q5_0  qs [R][nb][16], qh [R][nb][4], d [R][nb]        (22 B / 32)
+//   Q5_1  qs [R][nb][16], qh [R][nb][4], d|m [R][nb][2]   (24 B / 32)
+//   IQ4_NL qs [R][nb][16], d [R][nb]                      (18 B / 32)
+//   Q3_K  qs [R][nsb][64], hmask [R][nsb][32], scales [R][nsb][12],
+//         d [R][nsb]                                      (110 B / 256)
 //   F32   [R][cols]
 //
 // R = n_experts * rows (expert e owns rows [e*rows, (e+1)*rows)).
@@ -256,6 +261,8 @@ hipError_t launch_matvec_q4k(const DevTensor &W, size_t row0, size_t nrows, cons
 hipError_t launch_matvec_q8_0(const DevTensor &W, const float *x, float *y, hipStream_t s);
 hipError_t launch_matvec_q6k(const DevTensor &W, const float *x, float *y, hipStream_t s);
 hipError_t launch_matvec_f32(const DevTensor &W, const float *x, float *y, hipStream_t s);
+// Q5_0, Q5_1, IQ4_NL, Q3_K (lt_formats.hip)
+hipError_t launch_matvec_fmt(const DevTensor &W, const float *x, float *y, hipStream_t s);
 hipError_t launch_gate_up_q8_0(const DevTensor &Wg, const DevTensor &Wu, const float *x, uint32_t act,
                                float *h, hipStream_t s);
 // Router logits (F32 or Q8_0 router, exact reference order) plus softmax /

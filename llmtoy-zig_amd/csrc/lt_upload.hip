@@ -22,35 +22,46 @@ constexpr int kBlkPerWG = 64;        // blocks per workgroup; chunk starts are m
 constexpr uint32_t kMaxBlockBytes = 210;
 constexpr size_t kPad = 16;          // device chunk buffers hold this many bytes past the data
 
-// Plane s of a block type: bytes [off, off + 2^lg) of every block, stored
+// Plane s of a block type: bytes [off, off + len) of every block, stored
 // contiguously per block in plane s (set_planes order: p0, p1, p2, p3).
+// Every len is a multiple of 2 and every plane starts 4-byte aligned.
 struct PlaneArgs {
     uint8_t *plane[4];
-    uint32_t off[4], lg[4];
+    uint32_t off[4], len[4];
     int nseg;
     uint32_t bb;  // block bytes
 };
 
 bool plane_args(const DevTensor &t, PlaneArgs &a) {
     const size_t nblk = t.total_rows * t.blocks_per_row;
-    uint32_t len[4];
     switch (t.type) {
     case LT_TYPE_Q8_0:  // qs (bytes 2..33), d (bytes 0..1)
-        a = {{}, {2, 0}, {5, 1}, 2, 34};
+        a = {{}, {2, 0}, {32, 2}, 2, 34};
         break;
     case LT_TYPE_Q4_K:  // d, dmin, scales (0..15), quants (16..143)
-        a = {{}, {0, 16}, {4, 7}, 2, 144};
+        a = {{}, {0, 16}, {16, 128}, 2, 144};
         break;
     case LT_TYPE_Q6_K:  // ql, qh, scales, d
-        a = {{}, {0, 128, 192, 208}, {7, 6, 4, 1}, 4, 210};
+        a = {{}, {0, 128, 192, 208}, {128, 64, 16, 2}, 4, 210};
+        break;
+    case LT_TYPE_Q5_0:  // qs (6..21), qh (2..5), d (0..1)
+        a = {{}, {6, 2, 0}, {16, 4, 2}, 3, 22};
+        break;
+    case LT_TYPE_Q5_1:  // qs (8..23), qh (4..7), d and m (0..3)
+        a = {{}, {8, 4, 0}, {16, 4, 4}, 3, 24};
+        break;
+    case LT_TYPE_IQ4_NL:  // qs (2..17), d (0..1)
+        a = {{}, {2, 0}, {16, 2}, 2, 18};
+        break;
+    case LT_TYPE_Q3_K:  // qs (32..95), hmask (0..31), scales (96..107), d (108..109)
+        a = {{}, {32, 0, 96, 108}, {64, 32, 12, 2}, 4, 110};
         break;
     default: return false;
     }
     size_t at = 0;
     for (int s = 0; s < a.nseg; s++) {
-        len[s] = 1u << a.lg[s];
         a.plane[s] = t.base + at;
-        at += nblk * len[s];
+        at += nblk * a.len[s];
     }
     return at == t.bytes;
 }
@@ -70,19 +81,19 @@ __global__ __launch_bounds__(256) void k_blocks_to_planes(const uint8_t *__restr
     __syncthreads();
     const uint8_t *lb = reinterpret_cast<const uint8_t *>(lds);
     for (int s = 0; s < a.nseg; s++) {
-        const uint32_t lg = a.lg[s], m = (1u << lg) - 1, off = a.off[s], rb = n << lg;
-        uint8_t *dst = a.plane[s] + ((blk0 + b0) << lg);
+        const uint32_t len = a.len[s], off = a.off[s], rb = n * len;
+        uint8_t *dst = a.plane[s] + (blk0 + b0) * len;
         for (uint32_t j0 = 4 * threadIdx.x; j0 < rb; j0 += 4 * blockDim.x) {
             if (j0 + 4 <= rb) {
                 uint32_t v = 0;
 #pragma unroll
                 for (uint32_t q = 0; q < 4; q++) {
                     const uint32_t j = j0 + q;
-                    v |= (uint32_t)lb[(j >> lg) * a.bb + off + (j & m)] << (8 * q);
+                    v |= (uint32_t)lb[(j / len) * a.bb + off + j % len] << (8 * q);
                 }
                 *reinterpret_cast<uint32_t *>(dst + j0) = v;
             } else {
-                for (uint32_t j = j0; j < rb; j++) dst[j] = lb[(j >> lg) * a.bb + off + (j & m)];
+                for (uint32_t j = j0; j < rb; j++) dst[j] = lb[(j / len) * a.bb + off + j % len];
             }
         }
     }
@@ -98,18 +109,18 @@ __global__ __launch_bounds__(256) void k_planes_to_blocks(uint8_t *__restrict__ 
     const uint32_t nw = (n * a.bb + 3) / 4;
     uint8_t *lb = reinterpret_cast<uint8_t *>(lds);
     for (int s = 0; s < a.nseg; s++) {
-        const uint32_t lg = a.lg[s], m = (1u << lg) - 1, off = a.off[s], rb = n << lg;
-        const uint8_t *src = a.plane[s] + ((blk0 + b0) << lg);
+        const uint32_t len = a.len[s], off = a.off[s], rb = n * len;
+        const uint8_t *src = a.plane[s] + (blk0 + b0) * len;
         for (uint32_t j0 = 4 * threadIdx.x; j0 < rb; j0 += 4 * blockDim.x) {
             if (j0 + 4 <= rb) {
                 const uint32_t v = *reinterpret_cast<const uint32_t *>(src + j0);
 #pragma unroll
                 for (uint32_t q = 0; q < 4; q++) {
                     const uint32_t j = j0 + q;
-                    lb[(j >> lg) * a.bb + off + (j & m)] = (uint8_t)(v >> (8 * q));
+                    lb[(j / len) * a.bb + off + j % len] = (uint8_t)(v >> (8 * q));
                 }
             } else {
-                for (uint32_t j = j0; j < rb; j++) lb[(j >> lg) * a.bb + off + (j & m)] = src[j];
+                for (uint32_t j = j0; j < rb; j++) lb[(j / len) * a.bb + off + j % len] = src[j];
             }
         }
     }

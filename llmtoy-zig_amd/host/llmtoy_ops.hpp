@@ -44,7 +44,9 @@
 namespace llmtoy {
 
 // GgmlType ids (gguf/types.zig:23-53) of the formats on this path.
-enum class GgmlType : uint32_t { f32 = 0, f16 = 1, q8_0 = 8, q4_k = 12, q6_k = 14 };
+enum class GgmlType : uint32_t {
+    f32 = 0, f16 = 1, q5_0 = 6, q5_1 = 7, q8_0 = 8, q3_k = 11, q4_k = 12, q6_k = 14, iq4_nl = 20
+};
 
 enum class Error { Unsupported, Invalid, NotOnGpu, ExpertNotOnGpu, Device, OutOfMemory };
 
@@ -83,6 +85,10 @@ inline size_t rowBytes(GgmlType t, size_t cols) {
     case GgmlType::q8_0: return (cols / 32) * 34;
     case GgmlType::q4_k: return (cols / 256) * 144;
     case GgmlType::q6_k: return (cols / 256) * 210;
+    case GgmlType::q5_0: return (cols / 32) * 22;
+    case GgmlType::q5_1: return (cols / 32) * 24;
+    case GgmlType::iq4_nl: return (cols / 32) * 18;
+    case GgmlType::q3_k: return (cols / 256) * 110;
     }
     throw Exception(Error::Unsupported, LT_ERR_UNSUPPORTED, "unsupported quant type in rowBytes");
 }
@@ -215,9 +221,11 @@ class MatvecSession {
     // nullopt when the device path does not cover the type (the reference
     // returns null and the caller stays on the CPU, matvec.zig:564-577).
     static std::optional<MatvecSession> initFromRaw(GpuContext &g, const RawMatrix &m) {
-        if (m.type != GgmlType::f32 && m.type != GgmlType::q8_0 && m.type != GgmlType::q4_k &&
-            m.type != GgmlType::q6_k)
-            return std::nullopt;
+        switch (m.type) {
+        case GgmlType::f32: case GgmlType::q8_0: case GgmlType::q4_k: case GgmlType::q6_k:
+        case GgmlType::q5_0: case GgmlType::q5_1: case GgmlType::iq4_nl: case GgmlType::q3_k: break;
+        default: return std::nullopt;
+        }
         try {
             return MatvecSession(g, g.tensor(m), m.rows);
         } catch (const Exception &e) {

@@ -9,10 +9,12 @@ from __future__ import annotations
 import numpy as np
 
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+Q5_0, Q5_1, Q3_K, IQ4_NL = 6, 7, 11, 20  # the Gemma4 APEX expert formats (dequant.zig:189-659)
 
-BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210}
-NAMES = {F32: "F32", F16: "F16", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q5_0: 32, Q5_1: 32, Q3_K: 256, IQ4_NL: 32}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q5_0: 22, Q5_1: 24, Q3_K: 110, IQ4_NL: 18}
+NAMES = {F32: "F32", F16: "F16", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q5_0: "Q5_0", Q5_1: "Q5_1",
+         Q3_K: "Q3_K", IQ4_NL: "IQ4_NL"}
 
 
 def row_bytes(ggml_type: int, cols: int) -> int:

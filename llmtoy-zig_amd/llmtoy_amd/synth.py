@@ -94,6 +94,42 @@ def q6k_matrix(g: np.random.Generator, rows: int, cols: int, valid_cols: int | N
     return blk.reshape(rows, nsb * 210)
 
 
+def small_block_matrix(g: np.random.Generator, gtype: int, rows: int, cols: int) -> np.ndarray:
+    """uint8 [rows, row_bytes] of Q5_0 / Q5_1 / IQ4_NL blocks: uniform quant
+    bits, d = |N| * 0.01 (Q5_1 also m = N * 0.01)."""
+    assert cols % 32 == 0
+    nb = cols // 32
+    bb = ggml.BLOCK_BYTES[gtype]
+    blk = g.integers(0, 256, size=(rows, nb, bb), dtype=np.uint8)
+    blk[..., 0:2] = ggml.f16_bits(_absn(g, (rows, nb), 0.01)).view(np.uint8).reshape(rows, nb, 2)
+    if gtype == ggml.Q5_1:
+        blk[..., 2:4] = ggml.f16_bits(normal(g, (rows, nb), 0.01)).view(np.uint8).reshape(rows, nb, 2)
+    return blk.reshape(rows, nb * bb)
+
+
+def q3k_matrix(g: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """uint8 [rows, row_bytes] of Q3_K super-blocks: uniform hmask/quant/scale
+    bytes, d = |N| * 0.002."""
+    assert cols % 256 == 0
+    nsb = cols // 256
+    blk = g.integers(0, 256, size=(rows, nsb, 110), dtype=np.uint8)
+    blk[..., 108:110] = ggml.f16_bits(_absn(g, (rows, nsb), 0.002)).view(np.uint8).reshape(rows, nsb, 2)
+    return blk.reshape(rows, nsb * 110)
+
+
+def quant_matrix(g: np.random.Generator, gtype: int, rows: int, cols: int) -> np.ndarray:
+    """Random rows of any device-path type."""
+    if gtype == ggml.Q8_0:
+        return q8_0_matrix(g, rows, cols)
+    if gtype == ggml.Q4_K:
+        return q4k_matrix(g, rows, cols)
+    if gtype == ggml.Q6_K:
+        return q6k_matrix(g, rows, cols)
+    if gtype == ggml.Q3_K:
+        return q3k_matrix(g, rows, cols)
+    return small_block_matrix(g, gtype, rows, cols)
+
+
 def normal(g, shape, scale=1.0) -> np.ndarray:
     return (g.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(np.float32)
 

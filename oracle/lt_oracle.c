@@ -61,6 +61,10 @@
 #define Q8_0_BYTES 34
 #define Q4_K_BYTES 144
 #define Q6_K_BYTES 210
+#define Q5_0_BYTES 22
+#define Q5_1_BYTES 24
+#define IQ4_NL_BYTES 18
+#define Q3_K_BYTES 110
 
 /* ------------------------------------------------------------------------ */
 /* f16 -> f32, exact (subnormals, signed zero, inf, NaN kept).              */
@@ -256,6 +260,141 @@ void lto_matvec_f32(float *out, const float *mat, const float *vec, size_t rows,
 }
 
 /* math.zig:194-208 (integer division: a partial trailing block is dropped) */
+/* ------------------------------------------------------------------------ */
+/* Q5_0 (dequant.zig:189-217): 22 B / 32: d, qh (u32 LE), 16 nibble bytes;   */
+/* val = d * ((nib | hb << 4) - 16); element j: low nibble of qs[j], bit j   */
+/* of qh; element j + 16: high nibble of qs[j], bit j + 16.                   */
+static inline int q5_0_val(const uint8_t *blk, int e) {
+    uint32_t qh;
+    memcpy(&qh, blk + 2, 4);
+    const uint8_t q = blk[6 + (e & 15)];
+    const int nib = e < 16 ? (q & 15) : (q >> 4);
+    return (nib | (int)(((qh >> e) & 1u) << 4)) - 16;
+}
+
+void lto_dequant_q5_0(const uint8_t *data, float *out, size_t n) {
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = data + b * Q5_0_BYTES;
+        const float d = f16_at(blk);
+        for (int e = 0; e < 32; e++) out[b * 32 + e] = d * (float)q5_0_val(blk, e);
+    }
+}
+
+/* dequant.zig:92-133 dotQ5_0: per block 8 lane accumulators over groups g =
+ * 0..3 (elements 8g + l), acc[l] += q5 * v; total += reduce_ordered(acc) * d. */
+float lto_dot_q5_0(const uint8_t *data, const float *vec, size_t n) {
+    float total = 0.0f;
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = data + b * Q5_0_BYTES;
+        const float d = f16_at(blk);
+        const float *v = vec + b * 32;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int g = 0; g < 4; g++)
+            for (int l = 0; l < 8; l++) {
+                float p = (float)q5_0_val(blk, 8 * g + l) * v[8 * g + l];
+                acc[l] = acc[l] + p;
+            }
+        float r = acc[0];
+        for (int l = 1; l < 8; l++) r = r + acc[l];
+        float t = r * d;
+        total = total + t;
+    }
+    return total;
+}
+
+/* Q5_1 (dequant.zig:456-486): 24 B / 32: d, m, qh[4], qs[16];
+ * val = d * (nib | hb << 4) + m (rounded multiply, then add). */
+void lto_dequant_q5_1(const uint8_t *data, float *out, size_t n) {
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = data + b * Q5_1_BYTES;
+        const float d = f16_at(blk), m = f16_at(blk + 2);
+        const uint8_t *qh = blk + 4, *qs = blk + 8;
+        for (int j = 0; j < 16; j++) {
+            int hi0 = ((qh[j / 8] >> (j % 8)) & 1) << 4;
+            int hi1 = ((qh[(j + 16) / 8] >> ((j + 16) % 8)) & 1) << 4;
+            float q0 = (float)((qs[j] & 15) | hi0), q1 = (float)((qs[j] >> 4) | hi1);
+            float t0 = d * q0, t1 = d * q1;
+            out[b * 32 + j] = t0 + m;
+            out[b * 32 + j + 16] = t1 + m;
+        }
+    }
+}
+
+/* IQ4_NL (dequant.zig:607-659): 18 B / 32: d, 16 nibble bytes indexing a
+ * fixed non-linear table. */
+static const float kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+void lto_dequant_iq4_nl(const uint8_t *data, float *out, size_t n) {
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = data + b * IQ4_NL_BYTES;
+        const float d = f16_at(blk);
+        for (int j = 0; j < 16; j++) {
+            out[b * 32 + j] = d * kIq4nl[blk[2 + j] & 15];
+            out[b * 32 + j + 16] = d * kIq4nl[blk[2 + j] >> 4];
+        }
+    }
+}
+
+/* dequant.zig:642-658 dotIQ4NL: one scalar accumulator per block, adding
+ * element j then element j + 16 for j = 0..15; total += d * acc. */
+float lto_dot_iq4_nl(const uint8_t *data, const float *vec, size_t n) {
+    float total = 0.0f;
+    for (size_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = data + b * IQ4_NL_BYTES;
+        const float d = f16_at(blk);
+        const float *v = vec + b * 32;
+        float acc = 0.0f;
+        for (int j = 0; j < 16; j++) {
+            const uint8_t q = blk[2 + j];
+            float p0 = kIq4nl[q & 15] * v[j];
+            acc = acc + p0;
+            float p1 = kIq4nl[q >> 4] * v[j + 16];
+            acc = acc + p1;
+        }
+        float t = d * acc;
+        total = total + t;
+    }
+    return total;
+}
+
+/* Q3_K (dequant.zig:366-454): 110 B / 256: hmask[32], qs[64], 12 packed
+ * scale bytes (16 six-bit values, ggml kmask unpacking), f16 d.
+ * Element n = 128 h + 32 j + 16 g + l: q2 = (qs[32 h + 16 g + l] >> 2j) & 3,
+ * high bit = hmask[16 g + l] & (1 << (j + 4 h)); value = dl * (q2 - 4 * !hi)
+ * with dl = d * (sc[8 h + 2 j + g] - 32). */
+void lto_q3k_scales(const uint8_t *s, uint8_t *sc) {
+    uint32_t a0, a1, tmp, aux[4];
+    memcpy(&a0, s, 4);
+    memcpy(&a1, s + 4, 4);
+    memcpy(&tmp, s + 8, 4);
+    const uint32_t k1 = 0x03030303u, k2 = 0x0f0f0f0fu;
+    aux[2] = ((a0 >> 4) & k2) | (((tmp >> 4) & k1) << 4);
+    aux[3] = ((a1 >> 4) & k2) | (((tmp >> 6) & k1) << 4);
+    aux[0] = (a0 & k2) | (((tmp >> 0) & k1) << 4);
+    aux[1] = (a1 & k2) | (((tmp >> 2) & k1) << 4);
+    memcpy(sc, aux, 16);
+}
+
+void lto_dequant_q3_k(const uint8_t *data, float *out, size_t n) {
+    for (size_t b = 0; b < n / QK_K; b++) {
+        const uint8_t *blk = data + b * Q3_K_BYTES;
+        const uint8_t *hmask = blk, *qs = blk + 32;
+        const float d = f16_at(blk + 108);
+        uint8_t sc[16];
+        lto_q3k_scales(blk + 96, sc);
+        for (int h = 0; h < 2; h++)
+            for (int j = 0; j < 4; j++)
+                for (int g = 0; g < 2; g++) {
+                    const float dl = d * ((float)sc[8 * h + 2 * j + g] - 32.0f);
+                    for (int l = 0; l < 16; l++) {
+                        const int q2 = (qs[32 * h + 16 * g + l] >> (2 * j)) & 3;
+                        const int hi = (hmask[16 * g + l] >> (j + 4 * h)) & 1;
+                        out[b * QK_K + 128 * h + 32 * j + 16 * g + l] = (float)(q2 - (hi ? 0 : 4)) * dl;
+                    }
+                }
+    }
+}
+
 size_t lto_row_bytes(uint32_t type, size_t cols) {
     switch (type) {
     case LTO_F32: return cols * 4;
@@ -263,6 +402,10 @@ size_t lto_row_bytes(uint32_t type, size_t cols) {
     case LTO_Q8_0: return (cols / Q8_0_ELEMS) * Q8_0_BYTES;
     case LTO_Q4_K: return (cols / QK_K) * Q4_K_BYTES;
     case LTO_Q6_K: return (cols / QK_K) * Q6_K_BYTES;
+    case LTO_Q5_0: return (cols / 32) * Q5_0_BYTES;
+    case LTO_Q5_1: return (cols / 32) * Q5_1_BYTES;
+    case LTO_IQ4_NL: return (cols / 32) * IQ4_NL_BYTES;
+    case LTO_Q3_K: return (cols / QK_K) * Q3_K_BYTES;
     default: return 0;
     }
 }
@@ -275,19 +418,26 @@ int lto_dequant_row(const uint8_t *data, float *out, uint32_t type, size_t cols)
     case LTO_Q8_0: lto_dequant_q8_0(data, out, cols); return 0;
     case LTO_Q4_K: lto_dequant_q4_k(data, out, cols); return 0;
     case LTO_Q6_K: lto_dequant_q6_k(data, out, cols); return 0;
+    case LTO_Q5_0: lto_dequant_q5_0(data, out, cols); return 0;
+    case LTO_Q5_1: lto_dequant_q5_1(data, out, cols); return 0;
+    case LTO_IQ4_NL: lto_dequant_iq4_nl(data, out, cols); return 0;
+    case LTO_Q3_K: lto_dequant_q3_k(data, out, cols); return 0;
     default: return -1;
     }
 }
 
 static inline float row_dot(const uint8_t *row, uint32_t type, const float *vec, size_t cols, float *row_buf) {
     if (type == LTO_Q8_0) return lto_dot_q8_0(row, vec, cols);
+    if (type == LTO_Q5_0) return lto_dot_q5_0(row, vec, cols);   /* math.zig:152-155 */
+    if (type == LTO_IQ4_NL) return lto_dot_iq4_nl(row, vec, cols); /* math.zig:156-159 */
     if (type == LTO_F32 && ((uintptr_t)row % 4) == 0) return lto_dotf32((const float *)row, vec, cols);
     lto_dequant_row(row, row_buf, type, cols);
     return lto_dotf32(row_buf, vec, cols);
 }
 
 static int type_ok(uint32_t t) {
-    return t == LTO_F32 || t == LTO_F16 || t == LTO_Q8_0 || t == LTO_Q4_K || t == LTO_Q6_K;
+    return t == LTO_F32 || t == LTO_F16 || t == LTO_Q8_0 || t == LTO_Q4_K || t == LTO_Q6_K || t == LTO_Q5_0 ||
+           t == LTO_Q5_1 || t == LTO_IQ4_NL || t == LTO_Q3_K;
 }
 
 /* math.zig:133-171 */

@@ -26,7 +26,8 @@ extern "C" {
 #endif
 
 /* GgmlType ids, src/gguf/types.zig:23-53 */
-enum { LTO_F32 = 0, LTO_F16 = 1, LTO_Q8_0 = 8, LTO_Q4_K = 12, LTO_Q6_K = 14 };
+enum { LTO_F32 = 0, LTO_F16 = 1, LTO_Q5_0 = 6, LTO_Q5_1 = 7, LTO_Q8_0 = 8, LTO_Q3_K = 11, LTO_Q4_K = 12,
+       LTO_Q6_K = 14, LTO_IQ4_NL = 20 };
 
 /* activations for the gated FFN (src/ops/math.zig:37-40, 84-88) */
 enum { LTO_ACT_SILU = 0, LTO_ACT_GELU_TANH = 1 };
@@ -54,6 +55,15 @@ void lto_dequant_q6_k(const uint8_t *data, float *out, size_t n);     /* 237-277
 void lto_q4k_scale_min(int j, const uint8_t *scales, uint8_t *sc, uint8_t *mn); /* 291-300 */
 
 /* ---- ops: src/ops/math.zig ---------------------------------------------- */
+/* the Gemma4 APEX expert formats: dequant.zig:189-217 (Q5_0, dotQ5_0 92-133),
+ * 366-454 (Q3_K), 456-486 (Q5_1), 607-659 (IQ4_NL, dotIQ4NL 642-658)      */
+void lto_dequant_q5_0(const uint8_t *data, float *out, size_t n);
+float lto_dot_q5_0(const uint8_t *data, const float *vec, size_t n);
+void lto_dequant_q5_1(const uint8_t *data, float *out, size_t n);
+void lto_dequant_iq4_nl(const uint8_t *data, float *out, size_t n);
+float lto_dot_iq4_nl(const uint8_t *data, const float *vec, size_t n);
+void lto_q3k_scales(const uint8_t *scales12, uint8_t *sc16);
+void lto_dequant_q3_k(const uint8_t *data, float *out, size_t n);
 float lto_dotf32(const float *a, const float *b, size_t n);           /* 96-116 */
 size_t lto_row_bytes(uint32_t type, size_t cols);                     /* 194-208 (0 = unsupported) */
 int lto_dequant_row(const uint8_t *data, float *out, uint32_t type, size_t cols); /* 211-225 */

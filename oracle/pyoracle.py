@@ -15,6 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "build", "liblt_oracle.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+Q5_0, Q5_1, Q3_K, IQ4_NL = 6, 7, 11, 20
 ACT_SILU, ACT_GELU_TANH = 0, 1
 NORM_TOPK = 1
 
@@ -64,6 +65,9 @@ def lib() -> C.CDLL:
             "lto_ffn_dense": (C.c_int, [vp, vp, vp, vp, u32, vp, sz, sz, u32, vp]),
             "lto_moe_prefill": (C.c_int, [vp, vp, sz, vp, sz, vp, vp, u32, vp, u32, sz, sz, sz, sz, u32, u32, vp,
                                           vp, vp]),
+            "lto_dot_q5_0": (f, [vp, vp, sz]),
+            "lto_dot_iq4_nl": (f, [vp, vp, sz]),
+            "lto_q3k_scales": (None, [vp, vp]),
             "lto_rmsnorm": (None, [vp, vp, vp, sz, f, C.c_int]),
             "lto_add_rmsnorm": (None, [vp, vp, vp, vp, sz, f, C.c_int]),
             "lto_rmsnorm_wrs": (None, [vp, vp, vp, vp, vp, f, sz, f]),
@@ -131,6 +135,22 @@ def dot_q8_0(data, vec) -> np.float32:
     vec = _f32(vec)
     d = _u8(data)
     return np.float32(lib().lto_dot_q8_0(_p(d), _p(vec), vec.size))
+
+
+def dot_q5_0(data, vec) -> np.float32:
+    vec = _f32(vec)
+    return np.float32(lib().lto_dot_q5_0(_p(_u8(data)), _p(vec), vec.size))
+
+
+def dot_iq4_nl(data, vec) -> np.float32:
+    vec = _f32(vec)
+    return np.float32(lib().lto_dot_iq4_nl(_p(_u8(data)), _p(vec), vec.size))
+
+
+def q3k_scales(scales12) -> np.ndarray:
+    out = np.zeros(16, np.uint8)
+    lib().lto_q3k_scales(_p(_u8(np.ascontiguousarray(scales12, np.uint8))), _p(out))
+    return out
 
 
 def dotf32(a, b) -> np.float32:

@@ -266,6 +266,8 @@ def write_test_file(path, w, k=8, split=False, scale=None):
     wr.add_tensor("test.q8_0", (1024, 96), ggml.Q8_0, synth.q8_0_matrix(g, 96, 1024))
     wr.add_tensor("test.q6_k", (1024, 80), ggml.Q6_K, synth.q6k_matrix(g, 80, 1024))
     wr.add_tensor("test.q4_k", (1024, 64), ggml.Q4_K, synth.q4k_matrix(g, 64, 1024))
+    for t, name in ((ggml.Q5_0, "q5_0"), (ggml.Q5_1, "q5_1"), (ggml.IQ4_NL, "iq4_nl"), (ggml.Q3_K, "q3_k")):
+        wr.add_tensor(f"test.{name}", (1024, 48), t, synth.quant_matrix(g, t, 48, 1024))
     wr.add_tensor("test.v1024", (1024,), ggml.F32, synth.normal(g, (1024,)))
     wr.write(path)
     return x
@@ -307,7 +309,7 @@ def test_gpu_matvec_weights_from_gguf(ctx, tmp_path):
     write_test_file(p, w)
     r = gguf.GgufReader(p)
     v = r.tensor_bytes(r.tensor("test.v1024")).view(np.float32)
-    for name in ("test.q8_0", "test.q6_k", "test.q4_k"):
+    for name in ("test.q8_0", "test.q6_k", "test.q4_k", "test.q5_0", "test.q5_1", "test.iq4_nl", "test.q3_k"):
         info = r.tensor(name)
         m = r.raw_matrix(name, info.dims[1], info.dims[0])
         print(f"gguf matvec {name} {m.rows}x{m.cols}", flush=True)
