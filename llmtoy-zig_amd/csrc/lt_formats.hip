@@ -13,9 +13,10 @@
 //           * (((qs[32h + 16g + l] >> 2j) & 3) - 4 * !(hmask[16g + l] >> (j + 4h) & 1))
 //                                                             dequant.zig:366-454
 //
-// Work unit: one 32-element block (Q5_0/Q5_1/IQ4_NL) or one 128-element
-// half super-block (Q3_K).  One wavefront per row, lanes striding over the
-// row's units; x staged once per workgroup in LDS.  fp32 accumulation in an
+// Work unit: one 32-element block (Q5_0/Q5_1/IQ4_NL) or one 32-element
+// group of a Q3_K super-block (one scale pair).  A wavefront takes 1-8 rows
+// at a time (lanes striding over each row's units) and the workgroups walk
+// all rows, so x is staged in LDS once per workgroup.  fp32 accumulation in an
 // order of our own: parity with the reference's quantMatvec is to tolerance
 // (its GPU matvec fuzz bound, 1e-4 of max |y|), not bit-exact.
 #include "llmtoy_hip.h"
@@ -84,88 +85,99 @@ __device__ __forceinline__ int q3k_scale(const uint32_t s[3], int i) {
     return (int)(lo | (hi << 4));
 }
 
-// Half h of a Q3_K super-block (128 elements) against x[128 h ...].
-__device__ __forceinline__ float q3k_half_dot(const uint8_t *qs64, const uint8_t *hm32, const uint32_t sc[3],
-                                              float d, int h, const float *x) {
+// Group u = 4 h + j of a Q3_K super-block: elements 128 h + 32 j + [0, 32)
+// (16 from qs[32 h ..] and hmask[0 ..], 16 from qs[32 h + 16 ..] and
+// hmask[16 ..]) against x.
+__device__ __forceinline__ float q3k_group_dot(const uint8_t *qs64, const uint8_t *hm32, const uint32_t sc[3],
+                                               float d, int u, const float *x) {
+    const int h = u >> 2, j = u & 3;
     const uint4 q0 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h);
     const uint4 q1 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h + 16);
     const uint4 m0 = *reinterpret_cast<const uint4 *>(hm32);
     const uint4 m1 = *reinterpret_cast<const uint4 *>(hm32 + 16);
     const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    const int qsh = 2 * j, msh = j + 4 * h;
     float total = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int g = 0; g < 2; g++) {
+        float acc = 0.f;
 #pragma unroll
-        for (int g = 0; g < 2; g++) {
-            const float *xs = x + 128 * h + 32 * j + 16 * g;
-            float acc = 0.f;
+        for (int w4 = 0; w4 < 4; w4++) {
+            const float4 xv = *reinterpret_cast<const float4 *>(x + 16 * g + 4 * w4);
+            const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+            const uint32_t qword = qw[4 * g + w4] >> qsh, mword = mw[4 * g + w4] >> msh;
 #pragma unroll
-            for (int w4 = 0; w4 < 4; w4++) {
-                const float4 xv = *reinterpret_cast<const float4 *>(xs + 4 * w4);
-                const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
-                const uint32_t qword = qw[4 * g + w4], mword = mw[4 * g + w4];
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const int q2 = (int)((qword >> (8 * b + 2 * j)) & 3u);
-                    const int hb = (int)((mword >> (8 * b + j + 4 * h)) & 1u);
-                    acc += (float)(q2 - 4 + 4 * hb) * xa[b];
-                }
+            for (int b = 0; b < 4; b++) {
+                const int q2 = (int)((qword >> (8 * b)) & 3u);
+                const int hb = (int)((mword >> (8 * b)) & 1u);
+                acc += (float)(q2 - 4 + 4 * hb) * xa[b];
             }
-            total += (d * (float)(q3k_scale(sc, 8 * h + 2 * j + g) - 32)) * acc;
         }
+        total += (d * (float)(q3k_scale(sc, 8 * h + 2 * j + g) - 32)) * acc;
     }
     return total;
 }
 
-template <int T>
+// Workgroup = kFmtWaves waves; a wave takes RPW rows at a time (64 / RPW
+// lanes per row, striding over the row's units) and walks the rows with a
+// grid-wide stride, so x is staged in LDS once per workgroup.
+template <int T, int RPW>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, const float *__restrict__ x,
                                                                float *__restrict__ y) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats
     __shared__ float tab[16];
+    constexpr int LPR = kWave / RPW;
     const int cols = (int)W.cols;
     for (int i = threadIdx.x; i < cols; i += blockDim.x) xs[i] = x[i];
     if (T == LT_TYPE_IQ4_NL && threadIdx.x < 16) tab[threadIdx.x] = kIq4nlTable[threadIdx.x];
     __syncthreads();
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const size_t row = (size_t)blockIdx.x * kFmtWaves + wave;
-    if (row >= W.total_rows) return;
+    const int r = lane / LPR, sub = lane % LPR;
     const int nb = (int)W.blocks_per_row;
-    float acc = 0.f;
-    if (T == LT_TYPE_Q3_K) {
-        for (int u = lane; u < 2 * nb; u += kWave) {
-            const size_t sb = row * nb + (u >> 1);
-            const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
-            const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
-            acc += q3k_half_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 1,
-                                xs + 256 * (u >> 1));
-        }
-    } else {
-        for (int u = lane; u < nb; u += kWave) {
-            const size_t b = row * nb + u;
-            const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
-            const float *xb = xs + 32 * u;
-            if (T == LT_TYPE_IQ4_NL) {
-                acc += f16_at(W.p1 + b * 2) * iq4_block_dot(qv, xb, tab);
+    const int U = T == LT_TYPE_Q3_K ? 8 * nb : nb;  // units per row
+    const size_t stride = (size_t)gridDim.x * kFmtWaves * RPW;
+    for (size_t row0 = ((size_t)blockIdx.x * kFmtWaves + wave) * RPW; row0 < W.total_rows; row0 += stride) {
+        const size_t row = row0 + r;
+        const bool live = row < W.total_rows;
+        float acc = 0.f;
+        if (live) {
+            if (T == LT_TYPE_Q3_K) {
+                for (int u = sub; u < U; u += LPR) {
+                    const size_t sb = row * nb + (u >> 3);
+                    const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
+                    const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
+                    acc += q3k_group_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 7,
+                                         xs + 256 * (u >> 3) + 32 * (u & 7));
+                }
             } else {
-                const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
-                float sx;
-                if (T == LT_TYPE_Q5_0) {
-                    acc += f16_at(W.p2 + b * 2) * q5_block_dot(qv, qh, xb, 16.f, sx);
-                } else {  // Q5_1: d * sum(q x) + m * sum(x)
-                    const float dot = q5_block_dot(qv, qh, xb, 0.f, sx);
-                    acc += f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * sx;
+                for (int u = sub; u < U; u += LPR) {
+                    const size_t b = row * nb + u;
+                    const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
+                    const float *xb = xs + 32 * u;
+                    if (T == LT_TYPE_IQ4_NL) {
+                        acc += f16_at(W.p1 + b * 2) * iq4_block_dot(qv, xb, tab);
+                    } else {
+                        const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
+                        float sx;
+                        if (T == LT_TYPE_Q5_0) {
+                            acc += f16_at(W.p2 + b * 2) * q5_block_dot(qv, qh, xb, 16.f, sx);
+                        } else {  // Q5_1: d * sum(q x) + m * sum(x)
+                            const float dot = q5_block_dot(qv, qh, xb, 0.f, sx);
+                            acc += f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * sx;
+                        }
+                    }
                 }
             }
         }
-    }
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-    if (lane == 0) y[row] = acc;
+        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+        if (live && sub == 0) y[row] = acc;
+    }
 }
 
-template <int T>
-hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+template <int T, int RPW>
+hipError_t launch_tr(const DevTensor &W, const float *x, float *y, hipStream_t s) {
     const size_t lds = W.cols * sizeof(float);
     static bool lds_set[64] = {};
     int dev = 0;
@@ -173,13 +185,27 @@ hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s)
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     if (!lds_set[dev]) {  // rows up to 16 K floats stage 64 KiB of x
-        e = hipFuncSetAttribute((const void *)k_matvec_fmt<T>, hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+        e = hipFuncSetAttribute((const void *)k_matvec_fmt<T, RPW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                65536);
         if (e != hipSuccess) return e;
         lds_set[dev] = true;
     }
-    const dim3 grid((unsigned)((W.total_rows + kFmtWaves - 1) / kFmtWaves));
-    hipLaunchKernelGGL(k_matvec_fmt<T>, grid, dim3(64 * kFmtWaves), lds, s, W, x, y);
+    // up to 8 workgroups per CU, each walking many rows
+    const size_t need = (W.total_rows + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    const dim3 grid((unsigned)(need < 2048 ? need : 2048));
+    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), lds, s, W, x, y);
     return hipGetLastError();
+}
+
+// Rows per wave: enough lanes per row for the row's units (32-element
+// blocks, or 32-element Q3_K groups), the rest of the wave on more rows.
+template <int T>
+hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    const size_t U = T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row;
+    if (U >= 48) return launch_tr<T, 1>(W, x, y, s);
+    if (U >= 24) return launch_tr<T, 2>(W, x, y, s);
+    if (U >= 12) return launch_tr<T, 4>(W, x, y, s);
+    return launch_tr<T, 8>(W, x, y, s);
 }
 
 }  // namespace
