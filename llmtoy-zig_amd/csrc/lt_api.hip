@@ -507,13 +507,20 @@ int copy_routing_out(lt_ctx *ctx, uint32_t k, uint32_t *ids, float *w, bool host
     return LT_OK;
 }
 
+// Expert formats: Q4_K (tuned kernels, single-launch layer) and the Gemma4
+// APEX formats Q3_K, Q5_0, Q5_1, IQ4_NL (lt_formats.hip).
+bool is_fmt(uint32_t t) {
+    return t == LT_TYPE_Q5_0 || t == LT_TYPE_Q5_1 || t == LT_TYPE_IQ4_NL || t == LT_TYPE_Q3_K;
+}
+bool expert_type_ok(uint32_t t) { return t == LT_TYPE_Q4_K || is_fmt(t); }
+
 int check_experts(lt_ctx *ctx, const lt_tensor *gate_up, const lt_tensor *down, size_t d_model, uint32_t d_expert,
-                  size_t n_experts) {
+                  size_t n_experts, uint32_t k = 0) {
     if (!gate_up || !down) return fail(ctx, LT_ERR_INVALID, "null expert tensor");
     const DevTensor &GU = gate_up->t, &D = down->t;
-    if (GU.type != LT_TYPE_Q4_K || D.type != LT_TYPE_Q4_K)
-        return fail(ctx, LT_ERR_UNSUPPORTED, "expert types %u/%u: the device expert path takes Q4_K", GU.type,
-                    D.type);
+    if (!expert_type_ok(GU.type) || !expert_type_ok(D.type))
+        return fail(ctx, LT_ERR_UNSUPPORTED, "expert types %u/%u (device expert path: Q4_K, Q3_K, Q5_0, Q5_1, IQ4_NL)",
+                    GU.type, D.type);
     if (GU.cols != d_model || GU.rows != 2 * (size_t)d_expert)
         return fail(ctx, LT_ERR_INVALID, "gate_up per-expert shape %zux%zu != %ux%zu", GU.rows, GU.cols,
                     2 * d_expert, d_model);
@@ -523,9 +530,33 @@ int check_experts(lt_ctx *ctx, const lt_tensor *gate_up, const lt_tensor *down, 
     if (GU.n_experts != D.n_experts || (n_experts && GU.n_experts != n_experts))
         return fail(ctx, LT_ERR_INVALID, "expert counts differ (gate_up %zu, down %zu, router %zu)", GU.n_experts,
                     D.n_experts, n_experts);
-    if (GU.cols > 8192) return fail(ctx, LT_ERR_UNSUPPORTED, "d_model %zu > 8192", GU.cols);
-    if (D.blocks_per_row > 16) return fail(ctx, LT_ERR_UNSUPPORTED, "down row length %zu > 4096", D.cols);
+    if (GU.cols > (GU.type == LT_TYPE_Q4_K ? 8192u : 16384u))
+        return fail(ctx, LT_ERR_UNSUPPORTED, "d_model %zu too long for the gate/up kernel", GU.cols);
+    if (D.type == LT_TYPE_Q4_K && D.blocks_per_row > 16)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "down row length %zu > 4096", D.cols);
+    if (is_fmt(D.type) && (size_t)(k ? k : 1) * D.cols > 16384)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "k * down row length %zu > 16384 (LDS staging of h)",
+                    (size_t)(k ? k : 1) * D.cols);
     return LT_OK;
+}
+
+// gate/up of the k selected experts into h [k][Kd] (ids on the device)
+int gate_up_dev(lt_ctx *ctx, const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k, uint32_t d_expert,
+                uint32_t Kd, uint32_t act, float *h) {
+    if (GU.type == LT_TYPE_Q4_K)
+        return launch_rc(ctx, lt::launch_expert_gate_up_q4k(GU, x, ids, k, d_expert, Kd, act, h, ctx->stream),
+                         "expert_gate_up");
+    return launch_rc(ctx, lt::launch_expert_gate_up_fmt(GU, x, ids, k, d_expert, Kd, act, h, ctx->stream),
+                     "expert_gate_up_fmt");
+}
+
+int down_dev(lt_ctx *ctx, const DevTensor &D, const float *h, const uint32_t *ids, const float *w, uint32_t k,
+             const float *base, int accumulate, const float *dscale, float *out) {
+    if (D.type == LT_TYPE_Q4_K)
+        return launch_rc(ctx, lt::launch_expert_down_q4k(D, h, ids, w, k, base, accumulate, out, ctx->stream, dscale),
+                         "expert_down");
+    return launch_rc(ctx, lt::launch_expert_down_fmt(D, h, ids, w, k, base, accumulate, dscale, out, ctx->stream),
+                     "expert_down_fmt");
 }
 
 }  // namespace
@@ -564,10 +595,12 @@ extern "C" int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const
     if (k == 0 || k > kMaxK) return fail(ctx, LT_ERR_INVALID, "k=%u out of range", k);
     if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
     const DevTensor &GU = gate_up->t;
-    if (GU.type != LT_TYPE_Q4_K) return fail(ctx, LT_ERR_UNSUPPORTED, "gate_up type %u: device path takes Q4_K", GU.type);
+    if (!expert_type_ok(GU.type)) return fail(ctx, LT_ERR_UNSUPPORTED, "gate_up type %u not on the device path", GU.type);
     if (GU.rows != 2 * (size_t)d_expert) return fail(ctx, LT_ERR_INVALID, "gate_up rows %zu != 2*d_expert", GU.rows);
-    if (down_cols < d_expert || down_cols % 256) return fail(ctx, LT_ERR_INVALID, "down_cols %u", down_cols);
-    if (GU.cols > 8192) return fail(ctx, LT_ERR_UNSUPPORTED, "d_model %zu > 8192", GU.cols);
+    if (down_cols < d_expert || down_cols % (GU.type == LT_TYPE_Q4_K ? 256 : 32))
+        return fail(ctx, LT_ERR_INVALID, "down_cols %u", down_cols);
+    if (GU.cols > (GU.type == LT_TYPE_Q4_K ? 8192u : 16384u))
+        return fail(ctx, LT_ERR_UNSUPPORTED, "d_model %zu too long for the gate/up kernel", GU.cols);
     const bool host = flags & LT_HOST_IO;
     const float *dx = x;
     const uint32_t *dids = ids;
@@ -581,9 +614,7 @@ extern "C" int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const
         if ((rc = ensure(ctx, ctx->out, (size_t)k * down_cols * 4))) return rc;
         dh = (float *)ctx->out.p;
     }
-    rc = launch_rc(ctx, lt::launch_expert_gate_up_q4k(GU, dx, dids, k, d_expert, down_cols, act, dh, ctx->stream),
-                   "expert_gate_up");
-    if (rc) return rc;
+    if ((rc = gate_up_dev(ctx, GU, dx, dids, k, d_expert, down_cols, act, dh))) return rc;
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(h, dh, (size_t)k * down_cols * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -596,8 +627,11 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
     if (!ctx || !down || !h || !ids || !weights || !out) return fail(ctx, LT_ERR_INVALID, "null argument");
     if (k == 0 || k > kMaxK) return fail(ctx, LT_ERR_INVALID, "k=%u out of range", k);
     const DevTensor &D = down->t;
-    if (D.type != LT_TYPE_Q4_K) return fail(ctx, LT_ERR_UNSUPPORTED, "down type %u: device path takes Q4_K", D.type);
-    if (D.blocks_per_row > 16) return fail(ctx, LT_ERR_UNSUPPORTED, "down row length %zu > 4096", D.cols);
+    if (!expert_type_ok(D.type)) return fail(ctx, LT_ERR_UNSUPPORTED, "down type %u not on the device path", D.type);
+    if (D.type == LT_TYPE_Q4_K && D.blocks_per_row > 16)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "down row length %zu > 4096", D.cols);
+    if (is_fmt(D.type) && (size_t)k * D.cols > 16384)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "k * down row length > 16384 (LDS staging of h)");
     const bool host = flags & LT_HOST_IO;
     const float *dh = h, *dw = weights;
     const uint32_t *dids = ids;
@@ -616,11 +650,8 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
         }
         dout = (float *)ctx->out.p;
     }
-    rc = launch_rc(ctx,
-                   lt::launch_expert_down_q4k(D, dh, dids, dw, k, nullptr, (flags & LT_MOE_ACCUMULATE) ? 1 : 0, dout,
-                                              ctx->stream),
-                   "expert_down");
-    if (rc) return rc;
+    if ((rc = down_dev(ctx, D, dh, dids, dw, k, nullptr, (flags & LT_MOE_ACCUMULATE) ? 1 : 0, nullptr, dout)))
+        return rc;
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dout, D.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -642,7 +673,7 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
         base = (const float *)ctx->shared.p;
     }
     const size_t Kd = D.cols;
-    if (!(flags & LT_MOE_UNFUSED) && R.type == LT_TYPE_F32) {
+    if (!(flags & LT_MOE_UNFUSED) && R.type == LT_TYPE_F32 && GU.type == LT_TYPE_Q4_K && D.type == LT_TYPE_Q4_K) {
         const lt::FusedPlan pl = lt::plan_moe_fused((int)R.total_rows, (int)GU.cols, (int)d_expert, (int)Kd, (int)k);
         if (pl.ok) {
             if ((rc = ensure_fused(ctx)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
@@ -659,7 +690,7 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
     }
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
-    if (R.total_rows <= kRoutedGateUpMaxExperts) {
+    if (GU.type == LT_TYPE_Q4_K && R.total_rows <= kRoutedGateUpMaxExperts) {
         // logits only; each gate/up block selects its expert from them
         if ((rc = router_dev(ctx, R, x, bias, 0, flags))) return rc;
         rc = launch_rc(ctx,
@@ -670,16 +701,11 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
                        "expert_gate_up_routed");
     } else {
         if ((rc = router_dev(ctx, R, x, bias, k, flags))) return rc;
-        rc = launch_rc(ctx,
-                       lt::launch_expert_gate_up_q4k(GU, x, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd,
-                                                     act, h, ctx->stream),
-                       "expert_gate_up");
+        rc = gate_up_dev(ctx, GU, x, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act, h);
     }
     if (rc) return rc;
-    return launch_rc(ctx,
-                     lt::launch_expert_down_q4k(D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k, base,
-                                                (flags & LT_MOE_ACCUMULATE) ? 1 : 0, out, ctx->stream),
-                     "expert_down");
+    return down_dev(ctx, D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k, base,
+                    (flags & LT_MOE_ACCUMULATE) ? 1 : 0, nullptr, out);
 }
 
 }  // namespace
@@ -694,7 +720,7 @@ extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_
     const size_t d_model = gate_up->t.cols;
     int rc;
     if ((rc = check_router(ctx, router, d_model, k))) return rc;
-    if ((rc = check_experts(ctx, gate_up, down, d_model, d_expert, router->t.total_rows))) return rc;
+    if ((rc = check_experts(ctx, gate_up, down, d_model, d_expert, router->t.total_rows, k))) return rc;
     const bool shared = sh_gate || sh_up || sh_down;
     if (shared) {
         if (!sh_gate || !sh_up || !sh_down) return fail(ctx, LT_ERR_INVALID, "shared FFN needs gate, up and down");
@@ -739,6 +765,8 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
     int rc;
     if ((rc = check_router(ctx, router, D, k))) return rc;
     if ((rc = check_experts(ctx, gate_up, down, D, d_expert, router->t.total_rows))) return rc;
+    if (gate_up->t.type != LT_TYPE_Q4_K || down->t.type != LT_TYPE_Q4_K)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "batched prefill takes Q4_K experts");
     if (d_expert % 64 || D % 128)
         return fail(ctx, LT_ERR_UNSUPPORTED, "prefill tiles need d_expert %% 64 == 0 and d_model %% 128 == 0");
     if ((size_t)T * k > (1u << 20)) return fail(ctx, LT_ERR_UNSUPPORTED, "T*k > 2^20");
@@ -944,7 +972,7 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     const size_t n = gate_up->t.cols;
     int rc;
     if ((rc = check_router(ctx, router, n, k))) return rc;
-    if ((rc = check_experts(ctx, gate_up, down, n, d_expert, router->t.total_rows))) return rc;
+    if ((rc = check_experts(ctx, gate_up, down, n, d_expert, router->t.total_rows, k))) return rc;
     if ((rc = check_norm(ctx, 1, (uint32_t)n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE | LT_MOE_NORM_TOPK)))
         return rc;
     const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
@@ -973,7 +1001,7 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
     const uint32_t norm = (flags & LT_MOE_NORM_TOPK) ? 1u : 0u;
-    if (E <= kRoutedGateUpMaxExperts) {
+    if (GU.type == LT_TYPE_Q4_K && E <= kRoutedGateUpMaxExperts) {
         if ((rc = router_dev(ctx, R, router_in, nullptr, 0, flags))) return rc;
         rc = launch_rc(ctx,
                        lt::launch_expert_gate_up_q4k_routed(GU, moe_in, (const float *)ctx->logits.p, k, norm,
@@ -982,16 +1010,10 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
                        "expert_gate_up_routed");
     } else {
         if ((rc = router_dev(ctx, R, router_in, nullptr, k, flags))) return rc;
-        rc = launch_rc(ctx,
-                       lt::launch_expert_gate_up_q4k(GU, moe_in, (const uint32_t *)ctx->ids.p, k, d_expert,
-                                                     (uint32_t)Kd, act, h, ctx->stream),
-                       "expert_gate_up");
+        rc = gate_up_dev(ctx, GU, moe_in, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act, h);
     }
     if (rc) return rc;
-    if ((rc = launch_rc(ctx,
-                        lt::launch_expert_down_q4k(D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k,
-                                                   nullptr, 0, moe, ctx->stream, dds),
-                        "expert_down")))
+    if ((rc = down_dev(ctx, D, h, (const uint32_t *)ctx->ids.p, (const float *)ctx->w.p, k, nullptr, 0, dds, moe)))
         return rc;
     // 482-497: post_ffw_norm_2, + dense FFN, post_ffw_norm, residual, layer_output_scale
     if ((rc = norm_run(ctx, 3, moe, dd, dp, dp2, xio, nullptr, 1, (uint32_t)n, eps, layer_output_scale, flags)))

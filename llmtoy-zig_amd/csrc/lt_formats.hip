@@ -119,6 +119,48 @@ __device__ __forceinline__ float q3k_group_dot(const uint8_t *qs64, const uint8_
     return total;
 }
 
+// Contribution of unit u of a row (block u, or Q3_K group u) against the
+// row's x (xs = element 0 of the row's columns, in LDS).
+template <int T>
+__device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u, const float *xs, const float *tab) {
+    const int nb = (int)W.blocks_per_row;
+    if (T == LT_TYPE_Q3_K) {
+        const size_t sb = row * nb + (u >> 3);
+        const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
+        const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
+        return q3k_group_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 7,
+                             xs + 256 * (u >> 3) + 32 * (u & 7));
+    }
+    const size_t b = row * nb + u;
+    const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
+    const float *xb = xs + 32 * u;
+    if (T == LT_TYPE_IQ4_NL) return f16_at(W.p1 + b * 2) * iq4_block_dot(qv, xb, tab);
+    const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
+    float sx;
+    if (T == LT_TYPE_Q5_0) return f16_at(W.p2 + b * 2) * q5_block_dot(qv, qh, xb, 16.f, sx);
+    const float dot = q5_block_dot(qv, qh, xb, 0.f, sx);  // Q5_1: d * sum(q x) + m * sum(x)
+    return f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * sx;
+}
+
+template <int T>
+__device__ __forceinline__ int units_per_row(const DevTensor &W) {
+    return T == LT_TYPE_Q3_K ? 8 * (int)W.blocks_per_row : (int)W.blocks_per_row;
+}
+
+template <int LPR>
+__device__ __forceinline__ float seg_sum(float v) {
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+template <int T>
+__device__ __forceinline__ void stage(float *dst, const float *src, int n, float *tab) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+    if (T == LT_TYPE_IQ4_NL && threadIdx.x < 16) tab[threadIdx.x] = kIq4nlTable[threadIdx.x];
+    __syncthreads();
+}
+
 // Workgroup = kFmtWaves waves; a wave takes RPW rows at a time (64 / RPW
 // lanes per row, striding over the row's units) and walks the rows with a
 // grid-wide stride, so x is staged in LDS once per workgroup.
@@ -128,84 +170,187 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, cons
     extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats
     __shared__ float tab[16];
     constexpr int LPR = kWave / RPW;
-    const int cols = (int)W.cols;
-    for (int i = threadIdx.x; i < cols; i += blockDim.x) xs[i] = x[i];
-    if (T == LT_TYPE_IQ4_NL && threadIdx.x < 16) tab[threadIdx.x] = kIq4nlTable[threadIdx.x];
-    __syncthreads();
+    stage<T>(xs, x, (int)W.cols, tab);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int r = lane / LPR, sub = lane % LPR;
-    const int nb = (int)W.blocks_per_row;
-    const int U = T == LT_TYPE_Q3_K ? 8 * nb : nb;  // units per row
+    const int U = units_per_row<T>(W);
     const size_t stride = (size_t)gridDim.x * kFmtWaves * RPW;
     for (size_t row0 = ((size_t)blockIdx.x * kFmtWaves + wave) * RPW; row0 < W.total_rows; row0 += stride) {
         const size_t row = row0 + r;
         const bool live = row < W.total_rows;
         float acc = 0.f;
-        if (live) {
-            if (T == LT_TYPE_Q3_K) {
-                for (int u = sub; u < U; u += LPR) {
-                    const size_t sb = row * nb + (u >> 3);
-                    const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
-                    const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
-                    acc += q3k_group_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 7,
-                                         xs + 256 * (u >> 3) + 32 * (u & 7));
-                }
-            } else {
-                for (int u = sub; u < U; u += LPR) {
-                    const size_t b = row * nb + u;
-                    const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
-                    const float *xb = xs + 32 * u;
-                    if (T == LT_TYPE_IQ4_NL) {
-                        acc += f16_at(W.p1 + b * 2) * iq4_block_dot(qv, xb, tab);
-                    } else {
-                        const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
-                        float sx;
-                        if (T == LT_TYPE_Q5_0) {
-                            acc += f16_at(W.p2 + b * 2) * q5_block_dot(qv, qh, xb, 16.f, sx);
-                        } else {  // Q5_1: d * sum(q x) + m * sum(x)
-                            const float dot = q5_block_dot(qv, qh, xb, 0.f, sx);
-                            acc += f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * sx;
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+        if (live)
+            for (int u = sub; u < U; u += LPR) acc += unit_dot<T>(W, row, u, xs, tab);
+        acc = seg_sum<LPR>(acc);
         if (live && sub == 0) y[row] = acc;
     }
 }
 
+// Expert-indexed gate/up (ops/moe.zig:55-73): slot s = blockIdx.y, expert
+// e = ids[s]; row pair j = (gate row e 2F + j, up row e 2F + F + j);
+// h[s][j] = act(gate . x) * (up . x), h[s][F, down_cols) = 0.  Waves walk
+// the row pairs of their slot with a stride of gridDim.x * kFmtWaves * RPW.
 template <int T, int RPW>
-hipError_t launch_tr(const DevTensor &W, const float *x, float *y, hipStream_t s) {
-    const size_t lds = W.cols * sizeof(float);
-    static bool lds_set[64] = {};
+__global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, const float *__restrict__ x,
+                                                                  const uint32_t *__restrict__ ids, int F,
+                                                                  int down_cols, uint32_t act, float *__restrict__ h) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];
+    __shared__ float tab[16];
+    constexpr int LPR = kWave / RPW;
+    stage<T>(xs, x, (int)W.cols, tab);
+    const int s = blockIdx.y;
+    const uint32_t e = __builtin_amdgcn_readfirstlane(ids[s]);
+    float *hs = h + (size_t)s * down_cols;
+    if (blockIdx.x == 0)
+        for (int j = F + threadIdx.x; j < down_cols; j += blockDim.x) hs[j] = 0.f;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int r = lane / LPR, sub = lane % LPR;
+    const int U = units_per_row<T>(W);
+    const bool valid = e < (uint32_t)W.n_experts;
+    const int stride = gridDim.x * kFmtWaves * RPW;
+    for (int j0 = (blockIdx.x * kFmtWaves + wave) * RPW; j0 < F; j0 += stride) {
+        const int j = j0 + r;
+        const bool live = j < F;
+        float ag = 0.f, au = 0.f;
+        if (live && valid) {
+            const size_t g = (size_t)e * 2 * F + j, up = g + F;
+            for (int u = sub; u < U; u += LPR) {
+                ag += unit_dot<T>(W, g, u, xs, tab);
+                au += unit_dot<T>(W, up, u, xs, tab);
+            }
+        }
+        ag = seg_sum<LPR>(ag);
+        au = seg_sum<LPR>(au);
+        if (live && sub == 0) hs[j] = valid ? act_apply(act, ag) * au : 0.f;  // invalid id: the slot adds zeros
+    }
+}
+
+// Expert-indexed down with the weighted combine (ops/moe.zig:67-76):
+//   out[i] = base[i] + (accumulate ? out[i] : 0) + sum_s w'[s] (D_{ids[s]} row i) . h[s]
+// with w'[s] = dscale[ids[s]] * w[s] when a per-expert down scale is given
+// (gemma4/forward.zig:477).  h [k][down_cols] is staged in LDS once per
+// workgroup; waves walk the output rows.
+template <int T, int RPW>
+__global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W, const float *__restrict__ h,
+                                                                    const uint32_t *__restrict__ ids,
+                                                                    const float *__restrict__ wts, int k,
+                                                                    const float *base, int accumulate,
+                                                                    const float *dscale, float *out) {
+    extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats
+    __shared__ float tab[16];
+    constexpr int LPR = kWave / RPW;
+    const int Kd = (int)W.cols;
+    stage<T>(hsm, h, k * Kd, tab);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int r = lane / LPR, sub = lane % LPR;
+    const int U = units_per_row<T>(W);
+    const int D = (int)W.rows;
+    const int stride = gridDim.x * kFmtWaves * RPW;
+    for (int i0 = (blockIdx.x * kFmtWaves + wave) * RPW; i0 < D; i0 += stride) {
+        const int i = i0 + r;
+        const bool live = i < D;
+        float acc = 0.f;
+        if (live) {
+            for (int s = 0; s < k; s++) {
+                const uint32_t e = ids[s];
+                if (e >= (uint32_t)W.n_experts) continue;
+                const float ws = dscale ? dscale[e] * wts[s] : wts[s];
+                float t = 0.f;
+                for (int u = sub; u < U; u += LPR) t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, tab);
+                acc += ws * t;
+            }
+        }
+        acc = seg_sum<LPR>(acc);
+        if (live && sub == 0) {
+            float v = accumulate ? out[i] + acc : acc;
+            out[i] = base ? base[i] + v : v;
+        }
+    }
+}
+
+int pick_rpw(size_t units) { return units >= 48 ? 1 : units >= 24 ? 2 : units >= 12 ? 4 : 8; }
+
+// Allow up to 64 KiB of dynamic LDS, once per kernel and device.
+hipError_t allow_lds(const void *fn, bool *set) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (!lds_set[dev]) {  // rows up to 16 K floats stage 64 KiB of x
-        e = hipFuncSetAttribute((const void *)k_matvec_fmt<T, RPW>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                65536);
-        if (e != hipSuccess) return e;
-        lds_set[dev] = true;
-    }
+    if (set[dev]) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+    if (e == hipSuccess) set[dev] = true;
+    return e;
+}
+
+template <int T, int RPW>
+hipError_t launch_mv(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    static bool set[64] = {};
+    hipError_t e = allow_lds((const void *)k_matvec_fmt<T, RPW>, set);
+    if (e != hipSuccess) return e;
     // up to 8 workgroups per CU, each walking many rows
     const size_t need = (W.total_rows + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 2048 ? need : 2048));
-    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), lds, s, W, x, y);
+    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), W.cols * sizeof(float), s, W, x, y);
     return hipGetLastError();
 }
 
-// Rows per wave: enough lanes per row for the row's units (32-element
-// blocks, or 32-element Q3_K groups), the rest of the wave on more rows.
+template <int T, int RPW>
+hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, int k, int F, int down_cols,
+                     uint32_t act, float *h, hipStream_t s) {
+    static bool set[64] = {};
+    hipError_t e = allow_lds((const void *)k_expert_gu_fmt<T, RPW>, set);
+    if (e != hipSuccess) return e;
+    const int need = (F + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    const dim3 grid((unsigned)(need < 32 ? need : 32), (unsigned)k);  // 32 x k workgroups walk the rows
+    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), W.cols * sizeof(float), s, W, x, ids,
+                       F, down_cols, act, h);
+    return hipGetLastError();
+}
+
+template <int T, int RPW>
+hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, const float *w, int k,
+                     const float *base, int accumulate, const float *dscale, float *out, hipStream_t s) {
+    static bool set[64] = {};
+    hipError_t e = allow_lds((const void *)k_expert_down_fmt<T, RPW>, set);
+    if (e != hipSuccess) return e;
+    const int D = (int)W.rows;
+    const int need = (D + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    const dim3 grid((unsigned)(need < 256 ? need : 256));
+    hipLaunchKernelGGL((k_expert_down_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (size_t)k * W.cols * sizeof(float),
+                       s, W, h, ids, w, k, base, accumulate, dscale, out);
+    return hipGetLastError();
+}
+
 template <int T>
 hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s) {
-    const size_t U = T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row;
-    if (U >= 48) return launch_tr<T, 1>(W, x, y, s);
-    if (U >= 24) return launch_tr<T, 2>(W, x, y, s);
-    if (U >= 12) return launch_tr<T, 4>(W, x, y, s);
-    return launch_tr<T, 8>(W, x, y, s);
+    switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
+    case 1: return launch_mv<T, 1>(W, x, y, s);
+    case 2: return launch_mv<T, 2>(W, x, y, s);
+    case 4: return launch_mv<T, 4>(W, x, y, s);
+    default: return launch_mv<T, 8>(W, x, y, s);
+    }
+}
+
+template <int T>
+hipError_t launch_gu_t(const DevTensor &W, const float *x, const uint32_t *ids, int k, int F, int down_cols,
+                       uint32_t act, float *h, hipStream_t s) {
+    switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
+    case 1: return launch_gu<T, 1>(W, x, ids, k, F, down_cols, act, h, s);
+    case 2: return launch_gu<T, 2>(W, x, ids, k, F, down_cols, act, h, s);
+    case 4: return launch_gu<T, 4>(W, x, ids, k, F, down_cols, act, h, s);
+    default: return launch_gu<T, 8>(W, x, ids, k, F, down_cols, act, h, s);
+    }
+}
+
+template <int T>
+hipError_t launch_dn_t(const DevTensor &W, const float *h, const uint32_t *ids, const float *w, int k,
+                       const float *base, int accumulate, const float *dscale, float *out, hipStream_t s) {
+    switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
+    case 1: return launch_dn<T, 1>(W, h, ids, w, k, base, accumulate, dscale, out, s);
+    case 2: return launch_dn<T, 2>(W, h, ids, w, k, base, accumulate, dscale, out, s);
+    case 4: return launch_dn<T, 4>(W, h, ids, w, k, base, accumulate, dscale, out, s);
+    default: return launch_dn<T, 8>(W, h, ids, w, k, base, accumulate, dscale, out, s);
+    }
 }
 
 }  // namespace
@@ -216,6 +361,31 @@ hipError_t launch_matvec_fmt(const DevTensor &W, const float *x, float *y, hipSt
     case LT_TYPE_Q5_1: return launch_t<LT_TYPE_Q5_1>(W, x, y, s);
     case LT_TYPE_IQ4_NL: return launch_t<LT_TYPE_IQ4_NL>(W, x, y, s);
     case LT_TYPE_Q3_K: return launch_t<LT_TYPE_Q3_K>(W, x, y, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_expert_gate_up_fmt(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
+                                     uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, hipStream_t s) {
+    const int K = (int)k, F = (int)d_expert, Kd = (int)down_cols;
+    switch (GU.type) {
+    case LT_TYPE_Q5_0: return launch_gu_t<LT_TYPE_Q5_0>(GU, x, ids, K, F, Kd, act, h, s);
+    case LT_TYPE_Q5_1: return launch_gu_t<LT_TYPE_Q5_1>(GU, x, ids, K, F, Kd, act, h, s);
+    case LT_TYPE_IQ4_NL: return launch_gu_t<LT_TYPE_IQ4_NL>(GU, x, ids, K, F, Kd, act, h, s);
+    case LT_TYPE_Q3_K: return launch_gu_t<LT_TYPE_Q3_K>(GU, x, ids, K, F, Kd, act, h, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_expert_down_fmt(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
+                                  uint32_t k, const float *base, int accumulate, const float *dscale, float *out,
+                                  hipStream_t s) {
+    const int K = (int)k;
+    switch (D.type) {
+    case LT_TYPE_Q5_0: return launch_dn_t<LT_TYPE_Q5_0>(D, h, ids, w, K, base, accumulate, dscale, out, s);
+    case LT_TYPE_Q5_1: return launch_dn_t<LT_TYPE_Q5_1>(D, h, ids, w, K, base, accumulate, dscale, out, s);
+    case LT_TYPE_IQ4_NL: return launch_dn_t<LT_TYPE_IQ4_NL>(D, h, ids, w, K, base, accumulate, dscale, out, s);
+    case LT_TYPE_Q3_K: return launch_dn_t<LT_TYPE_Q3_K>(D, h, ids, w, K, base, accumulate, dscale, out, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -263,6 +263,13 @@ hipError_t launch_matvec_q6k(const DevTensor &W, const float *x, float *y, hipSt
 hipError_t launch_matvec_f32(const DevTensor &W, const float *x, float *y, hipStream_t s);
 // Q5_0, Q5_1, IQ4_NL, Q3_K (lt_formats.hip)
 hipError_t launch_matvec_fmt(const DevTensor &W, const float *x, float *y, hipStream_t s);
+// Expert-indexed gate/up and down over those formats (lt_formats.hip); the
+// down staging needs k * down_cols * 4 <= 64 KiB, x rows <= 16384 floats.
+hipError_t launch_expert_gate_up_fmt(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
+                                     uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, hipStream_t s);
+hipError_t launch_expert_down_fmt(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
+                                  uint32_t k, const float *base, int accumulate, const float *dscale, float *out,
+                                  hipStream_t s);
 hipError_t launch_gate_up_q8_0(const DevTensor &Wg, const DevTensor &Wu, const float *x, uint32_t act,
                                float *h, hipStream_t s);
 // Router logits (F32 or Q8_0 router, exact reference order) plus softmax /

@@ -252,7 +252,11 @@ class GpuWeights {
         try {
             gate_up_ = g.tensor(gate_up_exps, n_experts);
             down_ = g.tensor(down_exps, n_experts);
-            on_gpu_ = gate_up_exps.type == GgmlType::q4_k && down_exps.type == GgmlType::q4_k;
+            auto ok = [](GgmlType t) {
+                return t == GgmlType::q4_k || t == GgmlType::q3_k || t == GgmlType::q5_0 || t == GgmlType::q5_1 ||
+                       t == GgmlType::iq4_nl;
+            };
+            on_gpu_ = ok(gate_up_exps.type) && ok(down_exps.type);
         } catch (const Exception &e) {
             if (e.kind != Error::Unsupported) throw;
             on_gpu_ = false;  // stays on the CPU path

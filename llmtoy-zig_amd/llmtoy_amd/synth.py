@@ -148,31 +148,45 @@ class MoEWeights:
     down_cols: int
     router: np.ndarray          # fp32 [E, D] or Q8_0 bytes [E, row_bytes]
     router_type: int
-    gate_up: np.ndarray         # Q4_K bytes [E * 2F, row_bytes(D)]
-    down: np.ndarray            # Q4_K bytes [E * D, row_bytes(down_cols)]
+    gate_up: np.ndarray         # expert bytes [E * 2F, row_bytes(D)]
+    down: np.ndarray            # expert bytes [E * D, row_bytes(down_cols)]
     extra: dict = field(default_factory=dict)
+    gate_up_type: int = ggml.Q4_K
+    down_type: int = ggml.Q4_K
 
 
 def moe_weights(config: int, d_model: int, n_experts: int, d_expert: int, down_cols: int | None = None,
-                router_type: int = ggml.F32, tid0: int = 0) -> MoEWeights:
+                router_type: int = ggml.F32, tid0: int = 0, gate_up_type: int = ggml.Q4_K,
+                down_type: int = ggml.Q4_K) -> MoEWeights:
     """Router + flattened expert tensors (gate rows then up rows per expert,
     ops/moe.zig:55-73).  Experts are generated one at a time so a subset of
-    experts can be regenerated identically."""
+    experts can be regenerated identically.  Down columns past d_expert are
+    zero (K padding)."""
     down_cols = down_cols or d_expert
     if router_type == ggml.F32:
         router = normal(stream(config, tid0 + 1), (n_experts, d_model), 0.02)
     else:
         router = q8_0_matrix(stream(config, tid0 + 1), n_experts, d_model)
-    gu_rb = ggml.row_bytes(ggml.Q4_K, d_model)
-    dn_rb = ggml.row_bytes(ggml.Q4_K, down_cols)
+    gu_rb = ggml.row_bytes(gate_up_type, d_model)
+    dn_rb = ggml.row_bytes(down_type, down_cols)
     gate_up = np.empty((n_experts * 2 * d_expert, gu_rb), dtype=np.uint8)
     down = np.empty((n_experts * d_model, dn_rb), dtype=np.uint8)
     for e in range(n_experts):
-        gate_up[e * 2 * d_expert:(e + 1) * 2 * d_expert] = q4k_matrix(
-            stream(config, tid0 + 1000 + e), 2 * d_expert, d_model)
-        down[e * d_model:(e + 1) * d_model] = q4k_matrix(
-            stream(config, tid0 + 5000 + e), d_model, down_cols, valid_cols=d_expert)
-    return MoEWeights(d_model, n_experts, d_expert, down_cols, router, router_type, gate_up, down)
+        g1, g2 = stream(config, tid0 + 1000 + e), stream(config, tid0 + 5000 + e)
+        if gate_up_type == ggml.Q4_K:
+            gate_up[e * 2 * d_expert:(e + 1) * 2 * d_expert] = q4k_matrix(g1, 2 * d_expert, d_model)
+        else:
+            gate_up[e * 2 * d_expert:(e + 1) * 2 * d_expert] = quant_matrix(g1, gate_up_type, 2 * d_expert, d_model)
+        if down_type == ggml.Q4_K:
+            down[e * d_model:(e + 1) * d_model] = q4k_matrix(g2, d_model, down_cols, valid_cols=d_expert)
+        else:
+            dm = quant_matrix(g2, down_type, d_model, down_cols)
+            be, bb = ggml.BLOCK_ELEMS[down_type], ggml.BLOCK_BYTES[down_type]
+            assert d_expert % be == 0
+            dm[:, (d_expert // be) * bb:] = 0  # zero blocks: every element 0
+            down[e * d_model:(e + 1) * d_model] = dm
+    return MoEWeights(d_model, n_experts, d_expert, down_cols, router, router_type, gate_up, down,
+                      gate_up_type=gate_up_type, down_type=down_type)
 
 
 # ---------------------------------------------------------------- configs

@@ -118,6 +118,14 @@ def _pp(pool):
     return pool.ptr if pool is not None else None
 
 
+def _gut(w):
+    return getattr(w, "gate_up_type", Q4_K)
+
+
+def _dnt(w):
+    return getattr(w, "down_type", Q4_K)
+
+
 def f16_to_f32(raw: int) -> float:
     return float(np.float32(lib().lto_f16_to_f32(int(raw))))
 
@@ -255,8 +263,8 @@ def moe_forward(w, x, k, act=ACT_SILU, norm_topk=False, bias=None, pool: Pool | 
     wt = np.zeros(k, dtype=np.float32)
     agree = C.c_int(0)
     b = None if bias is None else _f32(bias)
-    rc = lib().lto_moe_forward(_p(o), _p(_f32(w.router)), w.n_experts, _p(b), _p(_u8(w.gate_up)), Q4_K,
-                               _p(_u8(w.down)), Q4_K, w.down_cols, _p(x), w.d_model, k, w.d_expert, act,
+    rc = lib().lto_moe_forward(_p(o), _p(_f32(w.router)), w.n_experts, _p(b), _p(_u8(w.gate_up)), _gut(w),
+                               _p(_u8(w.down)), _dnt(w), w.down_cols, _p(x), w.d_model, k, w.d_expert, act,
                                NORM_TOPK if norm_topk else 0, _pp(pool), _p(ids), _p(wt), C.byref(agree))
     if rc:
         raise ValueError(f"moe_forward failed ({rc})")
@@ -270,7 +278,8 @@ def moe_layer_shared(w, x, k, sh_gate, sh_up, sh_down, d_shared, act=ACT_GELU_TA
     ids = np.zeros(k, dtype=np.uint32)
     wt = np.zeros(k, dtype=np.float32)
     rc = lib().lto_moe_layer_shared(_p(out), _p(x), w.d_model, _p(_u8(w.router)), w.router_type, w.n_experts,
-                                    _p(_u8(w.gate_up)), Q4_K, _p(_u8(w.down)), Q4_K, w.down_cols, k, w.d_expert,
+                                    _p(_u8(w.gate_up)), _gut(w), _p(_u8(w.down)), _dnt(w), w.down_cols, k,
+                                    w.d_expert,
                                     _p(_u8(sh_gate)), _p(_u8(sh_up)), _p(_u8(sh_down)), Q8_0, d_shared, act,
                                     _pp(pool), _p(ids), _p(wt))
     if rc:
@@ -346,7 +355,7 @@ def gemma4_moe_block(w, x, dense_ffn, k, norms, layer_output_scale=1.0, eps=1e-6
     ds = norms.get("down_exps_scale")
     rc = lib().lto_gemma4_moe_block(
         _p(x), _p(_f32(dense_ffn)), w.d_model, _p(_u8(w.router)), w.router_type, w.n_experts, _p(_u8(w.gate_up)),
-        Q4_K, _p(_u8(w.down)), Q4_K, w.down_cols, k, w.d_expert, _p(_f32(norms["pre_ffw_norm_2"])),
+        _gut(w), _p(_u8(w.down)), _dnt(w), w.down_cols, k, w.d_expert, _p(_f32(norms["pre_ffw_norm_2"])),
         _p(_f32(norms["router_scale"])), None if ds is None else _p(_f32(ds)), _p(_f32(norms["post_ffw_norm_2"])),
         _p(_f32(norms["post_ffw_norm"])), layer_output_scale, eps, act, _pp(pool), _p(ids), _p(wt))
     if rc:

@@ -48,3 +48,73 @@ def test_gpu_formats_expert_layout_and_large_upload(ctx, gtype):
     t.free()
     ref = orc.quant_matvec(m, gtype, x, E * rows, cols)
     assert max_rel(y, ref) < 1e-4
+
+
+# ------------------------------------------------------------------ experts in these formats
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("gu,dn,F", [(ggml.Q3_K, ggml.Q5_0, 704), (ggml.Q3_K, ggml.Q5_1, 704),
+                                     (ggml.Q3_K, ggml.IQ4_NL, 704), (ggml.Q5_0, ggml.Q3_K, 768),
+                                     (ggml.IQ4_NL, ggml.Q4_K, 768), (ggml.Q4_K, ggml.IQ4_NL, 768)])
+def test_gpu_moe_forward_apex_formats(ctx, pool, gu, dn, F):
+    import llmtoy_amd as lt
+    w = synth.moe_weights(43, 2816, 32, F, gate_up_type=gu, down_type=dn)
+    R, GU, DN = lt.upload_moe(ctx, w)
+    x = synth.normal(synth.stream(43, 1), (2816,))
+    print(f"moe_forward gate_up {ggml.NAMES[gu]} down {ggml.NAMES[dn]}", flush=True)
+    out = np.zeros(2816, np.float32)
+    ids = np.zeros(8, np.uint32)
+    ctx.moe_forward(out, x, R, GU, DN, 8, F, act=lt.ACT_GELU_TANH, out_ids=ids)
+    ref, rids, _, agree = orc.moe_forward(w, x, 8, act=orc.ACT_GELU_TANH, pool=pool)
+    for t in (R, GU, DN):
+        t.free()
+    assert agree and np.array_equal(np.sort(ids), np.sort(rids))
+    assert rel_l2(out, ref) < 1e-3
+
+
+def test_gpu_gemma4_block_apex_formats(ctx, pool):
+    # Gemma4 APEX: Q8_0 router, Q3_K gate/up, IQ4_NL down, with every norm step
+    import llmtoy_amd as lt
+    from llmtoy_amd import lib as ltlib
+    w = synth.moe_weights(44, 2816, 32, 704, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K,
+                          down_type=ggml.IQ4_NL)
+    tens = lt.upload_moe(ctx, w)
+    x, dense = synth.normal(synth.stream(44, 1), (2816,)), synth.normal(synth.stream(44, 2), (2816,))
+    nm = synth.gemma4_norms(44, 2816, 32)
+    ids = np.zeros(8, np.uint32)
+    got = ltlib.gemma4_moe_block(ctx, x.copy(), dense, *tens, 8, 704, nm, 0.75, 1e-6, precise=True, out_ids=ids)
+    ref, rids, _ = orc.gemma4_moe_block(w, x, dense, 8, nm, 0.75, 1e-6, pool=pool)
+    for t in tens:
+        t.free()
+    assert ids.tolist() == rids.tolist() and rel_l2(got, ref) < 1e-3
+
+
+@pytest.mark.parametrize("gtype", FMTS)
+def test_gpu_expert_id_entry_points(ctx, gtype):
+    # lt_expert_gate_up_id / lt_expert_down_id (GpuWeights.runExpertBatch's two stages)
+    import llmtoy_amd as lt
+    E, D, F = 12, 1024, 512
+    w = synth.moe_weights(45, D, E, F, gate_up_type=gtype, down_type=gtype)
+    _, GU, DN = lt.upload_moe(ctx, w)
+    x = synth.normal(synth.stream(45, 1), (D,))
+    ids = np.array([3, 11, 0, 7, 3], np.uint32)
+    wts = np.array([0.4, 0.3, 0.15, 0.1, 0.05], np.float32)
+    h = np.zeros((5, F), np.float32)
+    ctx.expert_gate_up_id(GU, x, ids, 5, F, F, h, act=lt.ACT_SILU)
+    out = np.full(D, 0.5, np.float32)
+    ctx.expert_down_id(DN, h, ids, wts, 5, out, accumulate=True)
+    GU.free()
+    DN.free()
+    gu = w.gate_up.reshape(E, 2 * F, -1)
+    dn = w.down.reshape(E, D, -1)
+    want_out = np.full(D, 0.5, np.float64)
+    for s, e in enumerate(ids):
+        g = orc.quant_matvec(gu[e, :F], gtype, x, F, D).astype(np.float64)
+        u = orc.quant_matvec(gu[e, F:], gtype, x, F, D).astype(np.float64)
+        want_h = g / (1 + np.exp(-g)) * u
+        assert rel_l2(h[s], want_h) < 1e-4
+        want_out += float(wts[s]) * orc.quant_matvec(dn[e], gtype, h[s], D, F).astype(np.float64)
+    assert rel_l2(out, want_out) < 1e-4
