@@ -228,10 +228,13 @@ def bench_gemma4(args):
 
     import llmtoy_amd as lt
     import pyoracle as orc
-    from llmtoy_amd import lib as ltlib, synth
+    from llmtoy_amd import ggml, lib as ltlib, synth
     from llmtoy_amd.hip import DeviceArray, Event, Graph, sync_stream
 
     c = synth.config4_block()
+    if args.apex:  # the Gemma4 APEX expert formats: Q3_K gate/up, IQ4_NL down (K = d_expert, no padding)
+        c["weights"] = synth.moe_weights(4, G4_D, G4_E, G4_F, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K,
+                                         down_type=ggml.IQ4_NL)
     w, nm = c["weights"], c["norms"]
     ctx = lt.Context(0)
     base = lt.upload_moe(ctx, w)
@@ -279,19 +282,22 @@ def bench_gemma4(args):
     steps = n_graphs * G
     us = wall / steps * 1e6
     dev_us = e0.elapsed_ms(e1) * 1e3 / steps
-    gbps = G4_BLOCK_BYTES / (dev_us * 1e-6) / 1e9
+    expert_bytes = (w.gate_up.nbytes + w.down.nbytes) // G4_E
+    block_bytes = G4_BLOCK_BYTES - K * G4_EXPERT_BYTES + K * expert_bytes
+    gbps = block_bytes / (dev_us * 1e-6) / 1e9
     log(f"gemma4 block: {us:.2f} us/token wall, {dev_us:.2f} us/token device, {gbps:.0f} GB/s")
     result = {"metric": "Gemma4 MoE block decode us/token (config-4 layer + router-input prep + MoE tail)",
               "value": round(us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
               "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "dtype": "fp32", "data": "synthetic",
               "config": {"workload": "gemma4_moe_block_cfg4", "d_model": G4_D, "n_experts": G4_E,
-                         "d_expert": G4_F, "down_cols": G4_KD, "top_k": K, "router": "Q8_0", "experts": "Q4_K",
+                         "d_expert": G4_F, "down_cols": w.down_cols, "top_k": K, "router": "Q8_0",
+                         "experts": f"{ggml.NAMES[w.gate_up_type]} gate/up, {ggml.NAMES[w.down_type]} down",
                          "act": "gelu_tanh", "norm_sum": "tree", "weight_copies": args.copies,
                          "x_pool": args.xpool, "graph_steps": G},
               "device_us_per_token": round(dev_us, 3),
               "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                            "frac": round(gbps / PEAK_GBPS, 4), "traffic": None,
-                           "kernel": "whole block (5 launches per token)", "algorithmic_bytes": G4_BLOCK_BYTES},
+                           "kernel": "whole block (5 launches per token)", "algorithmic_bytes": block_bytes},
               "parity": parity}
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -390,6 +396,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF file load + upload check")
+    ap.add_argument("--apex", action="store_true",
+                    help="--workload gemma4 with the APEX expert formats (Q3_K gate/up, IQ4_NL down)")
     ap.add_argument("--workload", choices=["decode", "prefill", "gemma4", "formats"], default="decode")
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")

@@ -301,7 +301,7 @@ hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, in
     hipError_t e = allow_lds((const void *)k_expert_gu_fmt<T, RPW>, set);
     if (e != hipSuccess) return e;
     const int need = (F + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
-    const dim3 grid((unsigned)(need < 32 ? need : 32), (unsigned)k);  // 32 x k workgroups walk the rows
+    const dim3 grid((unsigned)(need < 128 ? need : 128), (unsigned)k);  // up to 128 x k workgroups walk the rows
     hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), W.cols * sizeof(float), s, W, x, ids,
                        F, down_cols, act, h);
     return hipGetLastError();
@@ -315,7 +315,7 @@ hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, co
     if (e != hipSuccess) return e;
     const int D = (int)W.rows;
     const int need = (D + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
-    const dim3 grid((unsigned)(need < 256 ? need : 256));
+    const dim3 grid((unsigned)(need < 1024 ? need : 1024));
     hipLaunchKernelGGL((k_expert_down_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (size_t)k * W.cols * sizeof(float),
                        s, W, h, ids, w, k, base, accumulate, dscale, out);
     return hipGetLastError();
