@@ -225,7 +225,9 @@ int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float *dense_ffn,
  *   x   = lt_moe_tail(x, moe, dense_ffn, ...)
  * x [d_model] is updated in place; dense_ffn is the dense FFN output after
  * post_ffw_norm_1.  down_exps_scale [n_experts] may be NULL (all ones).
- * router: F32 or Q8_0; experts: Q4_K.  flags: LT_HOST_IO, LT_NORM_PRECISE,
+ * router: F32 or Q8_0; experts: Q4_K, Q3_K, Q5_0, Q5_1 or IQ4_NL (device x:
+ * 16-byte aligned).  With a Q8_0 router and the default tree sums, the
+ * router-input prep runs inside the router kernel.  flags: LT_HOST_IO, LT_NORM_PRECISE,
  * LT_MOE_NORM_TOPK.  out_ids / out_w (may be NULL) get the selection and its
  * probabilities (router_out at the selected ids). */
 int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn, const lt_tensor *router,

@@ -483,14 +483,14 @@ int check_router(lt_ctx *ctx, const lt_tensor *router, size_t d_model, uint32_t 
 // logits -> ids/w in context buffers (and scores, if non-NULL); x, bias,
 // scores device pointers.
 int router_dev(lt_ctx *ctx, const DevTensor &R, const float *x, const float *bias, uint32_t k, uint32_t flags,
-               float *scores = nullptr) {
+               float *scores = nullptr, const lt::RouterPrep *prep = nullptr) {
     int rc;
     if ((rc = ensure(ctx, ctx->logits, R.total_rows * 4)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
         (rc = ensure(ctx, ctx->w, kMaxK * 4)))
         return rc;
     float *logits = (float *)ctx->logits.p;
     hipError_t e = lt::launch_router(R, x, bias, logits, ctx->ticket, k, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u,
-                                     (uint32_t *)ctx->ids.p, (float *)ctx->w.p, scores, ctx->stream);
+                                     (uint32_t *)ctx->ids.p, (float *)ctx->w.p, scores, ctx->stream, prep);
     return launch_rc(ctx, e, "router_topk");
 }
 
@@ -978,6 +978,7 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
     const size_t E = R.total_rows, Kd = D.cols;
     const bool host = flags & LT_HOST_IO;
+    if (!host && !aligned16(x)) return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
     Arena ar;
     for (int i = 0; i < 3; i++) ar.need(n);  // moe_in, router_in, moe
     if (host) {
@@ -993,23 +994,28 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
         (rc = io_in(ctx, host, ar, post_ffw_norm_2, n, &dp2)) || (rc = io_in(ctx, host, ar, post_ffw_norm, n, &dp)))
         return rc;
     float *xio = const_cast<float *>(dx);
-    // gemma4/forward.zig:405-414: expert input and router input from one RMS of x
+    // gemma4/forward.zig:405-414: expert input and router input from one RMS
+    // of x -- inside the Q8_0 router with the tree sum, else a kernel of its own
     const float inv_sqrt_d = 1.0f / sqrtf((float)n);
-    if ((rc = norm_run(ctx, 2, dx, nullptr, dpre, drs, moe_in, router_in, 1, (uint32_t)n, eps, inv_sqrt_d, flags)))
+    const bool fuse_prep = !(flags & LT_NORM_PRECISE) && R.type == LT_TYPE_Q8_0;
+    const lt::RouterPrep prep{drs, dpre, moe_in, inv_sqrt_d, eps};
+    const float *rin = fuse_prep ? dx : router_in;
+    if (!fuse_prep &&
+        (rc = norm_run(ctx, 2, dx, nullptr, dpre, drs, moe_in, router_in, 1, (uint32_t)n, eps, inv_sqrt_d, flags)))
         return rc;
     // 417 routerTopKSoftmax, then the selected experts (463-479, GpuWeights.runExpertBatch)
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
     const uint32_t norm = (flags & LT_MOE_NORM_TOPK) ? 1u : 0u;
     if (GU.type == LT_TYPE_Q4_K && E <= kRoutedGateUpMaxExperts) {
-        if ((rc = router_dev(ctx, R, router_in, nullptr, 0, flags))) return rc;
+        if ((rc = router_dev(ctx, R, rin, nullptr, 0, flags, nullptr, fuse_prep ? &prep : nullptr))) return rc;
         rc = launch_rc(ctx,
                        lt::launch_expert_gate_up_q4k_routed(GU, moe_in, (const float *)ctx->logits.p, k, norm,
                                                             d_expert, (uint32_t)Kd, act, h, (uint32_t *)ctx->ids.p,
                                                             (float *)ctx->w.p, ctx->stream),
                        "expert_gate_up_routed");
     } else {
-        if ((rc = router_dev(ctx, R, router_in, nullptr, k, flags))) return rc;
+        if ((rc = router_dev(ctx, R, rin, nullptr, k, flags, nullptr, fuse_prep ? &prep : nullptr))) return rc;
         rc = gate_up_dev(ctx, GU, moe_in, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act, h);
     }
     if (rc) return rc;

@@ -275,8 +275,17 @@ hipError_t launch_gate_up_q8_0(const DevTensor &Wg, const DevTensor &Wu, const f
 // Router logits (F32 or Q8_0 router, exact reference order) plus softmax /
 // top-k in the same launch.  ticket: a zero-initialised counter owned by the
 // caller, left at zero after every launch.  k = 0 computes logits only.
+// Gemma4 router-input prep fused into the Q8_0 router (null raw_scale: off).
+struct RouterPrep {
+    const float *raw_scale;   // router_scale [cols]
+    const float *weight;      // pre_ffw_norm_2 [cols]
+    float *moe_in;            // [cols], written: (x * rms_inv) * weight
+    float raw_global_scale;   // 1 / sqrt(cols)
+    float eps;
+};
 hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, float *logits, unsigned *ticket,
-                         uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s);
+                         uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s,
+                         const RouterPrep *prep = nullptr);
 // Router logits for T tokens (X [T][cols] -> logits [T][rows]) and per-token
 // softmax + top-k (ids, w: [T][k]).
 hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, const float *bias, float *logits,

@@ -120,14 +120,45 @@ __global__ void __launch_bounds__(64) k_router_f32(const float *__restrict__ W, 
 
 // One block (2 waves) per row: thread b computes block b's term
 // reduce(acc)*d exactly, then thread 0 adds the terms in block order.
+// With pa.raw_scale set (decode, one token), the router input is the
+// Gemma4 prep of x (math.zig:51-82): every block takes the RMS of x in one
+// fixed tree order (same bits in every block), uses
+// (x * (rms_inv * raw_global_scale)) * raw_scale as its input, and writes its
+// share of moe_in = (x * rms_inv) * weight for the expert kernels.
 __global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ dp,
                                                      const float *__restrict__ x, const float *__restrict__ bias,
-                                                     float *__restrict__ logits, int nb, int rows, TopkArgs ta) {
+                                                     float *__restrict__ logits, int nb, int rows, TopkArgs ta,
+                                                     RouterPrep pa) {
 #pragma clang fp contract(off)
     extern __shared__ float term[];
     x += (size_t)blockIdx.y * nb * 32;  // token blockIdx.y of a batch (decode: 0)
     logits += (size_t)blockIdx.y * rows;
     const int row = blockIdx.x;
+    const int n = nb * 32;
+    float raw_base = 0.0f;
+    if (pa.raw_scale) {
+        __shared__ float red[3];
+        // float4 loads, 8 in flight per thread (n is a multiple of 32)
+        float ss = 0.0f;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll 8
+        for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
+            const float4 v4 = x4[i];
+            ss = ss + v4.x * v4.x;
+            ss = ss + v4.y * v4.y;
+            ss = ss + v4.z * v4.z;
+            ss = ss + v4.w * v4.w;
+        }
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off, kWave);
+        if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+        __syncthreads();
+        const float r = 1.0f / sqrtf((red[0] + red[1]) / (float)n + pa.eps);
+        raw_base = r * pa.raw_global_scale;
+        const int per = (n + gridDim.x - 1) / gridDim.x;
+        for (int i = row * per + threadIdx.x; i < n && i < (row + 1) * per; i += blockDim.x)
+            pa.moe_in[i] = (x[i] * r) * pa.weight[i];
+    }
     for (int b = threadIdx.x; b < nb; b += blockDim.x) {
         const int8_t *q = qs + ((size_t)row * nb + b) * 32;
         const float *v = x + b * 32;
@@ -135,13 +166,25 @@ __global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ 
         float acc[8];
 #pragma unroll
         for (int l = 0; l < 8; l++) acc[l] = 0.0f;
+        if (pa.raw_scale) {
+            const float *rs = pa.raw_scale + b * 32;
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int l = 0; l < 8; l++) {
-                float p = (float)q[8 * j + l] * v[8 * j + l];
-                acc[l] = acc[l] + p;
-            }
+                for (int l = 0; l < 8; l++) {
+                    const float vin = (v[8 * j + l] * raw_base) * rs[8 * j + l];
+                    float p = (float)q[8 * j + l] * vin;
+                    acc[l] = acc[l] + p;
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int l = 0; l < 8; l++) {
+                    float p = (float)q[8 * j + l] * v[8 * j + l];
+                    acc[l] = acc[l] + p;
+                }
+        }
         float r = acc[0];
 #pragma unroll
         for (int l = 1; l < 8; l++) r = r + acc[l];
@@ -158,7 +201,10 @@ __global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ 
 }
 
 hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, float *logits, unsigned *ticket,
-                         uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s) {
+                         uint32_t k, uint32_t norm, uint32_t *ids, float *w, float *scores, hipStream_t s,
+                         const RouterPrep *prep) {
+    const RouterPrep pa = prep ? *prep : RouterPrep{};
+    if (pa.raw_scale && R.type == 0) return hipErrorInvalidValue;  // the prep is fused into the Q8_0 router only
     const TopkArgs ta{ticket, (int)k, (int)norm, ids, w, scores};
     const int rows = (int)R.total_rows;
     if (R.type == 0) {  // F32
@@ -168,7 +214,7 @@ hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, 
     } else {  // Q8_0
         const int nb = (int)R.blocks_per_row;
         hipLaunchKernelGGL(k_router_q8_0, dim3(rows), dim3(128), nb * sizeof(float), s, (const int8_t *)R.p0,
-                           (const uint16_t *)R.p1, x, bias, logits, nb, rows, ta);
+                           (const uint16_t *)R.p1, x, bias, logits, nb, rows, ta, pa);
     }
     return hipGetLastError();
 }
@@ -299,7 +345,7 @@ hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, cons
     else
         hipLaunchKernelGGL(k_router_q8_0, dim3(rows, T), dim3(128), R.blocks_per_row * sizeof(float), s,
                            (const int8_t *)R.p0, (const uint16_t *)R.p1, X, bias, logits, (int)R.blocks_per_row,
-                           rows, none);
+                           rows, none, RouterPrep{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (rows <= 64)
