@@ -31,6 +31,11 @@
  *                         no reference code: pinned by their closed form only.
  *   lto_moe_layer_shared  gemma4/forward.zig:392-397, 417, 463-479  composition.
  *   lto_moe_prefill       T x lto_moe_forward (main.zig:1916-1922 prefills per token).
+ *   lto_dequant_q5_0, lto_dot_q5_0, lto_dequant_q5_1, lto_dequant_iq4_nl, lto_dot_iq4_nl,
+ *   lto_q3k_scales, lto_dequant_q3_k
+ *                         dequant.zig:80-217, 366-486, 607-659.  Decoders written from the
+ *                         block layouts (tests/test_oracle_formats.py), the reference's dot
+ *                         KATs (716-758), hand-derived accumulation-order cases, float64.
  *   lto_rmsnorm           math.zig:19-25 (rmsnorm), 42-48 (rmsnormRaw: w == NULL) and
  *                         the (1 + w) convention of rmsnorm.glsl.  KATs math.zig:344-354;
  *                         a hand-derived case fixing the sequential sum of squares;
