@@ -118,9 +118,14 @@ struct TensorInfo {
     uint32_t type = 0;
     uint64_t offset = 0;
 
+    // Product of the dims; a product past 2^63 (a corrupt header) saturates
+    // there, so byteSize is then larger than any file and tensorBytes fails.
     uint64_t n_elements() const {
         uint64_t n = 1;
-        for (uint64_t d : dims) n *= d;
+        for (uint64_t d : dims) {
+            if (d && n > (1ull << 63) / d) return 1ull << 63;
+            n *= d;
+        }
         return n;
     }
     // Exact byte size of the stored weights: (n / block elements) * block
@@ -336,7 +341,8 @@ class GgufReader {
         const uint8_t *p = tensorBytes(t, nb);
         RawMatrix m{p, nb, (GgmlType)t.type, rows, cols};
         const BlockSize b = block_size(t.type);
-        if (!b.elems || cols % b.elems || rows * (cols / b.elems) * b.bytes > nb)
+        const uint64_t rb = b.elems ? (cols / b.elems) * b.bytes : 0;  // one row; cols < 2^40 in any real file
+        if (!b.elems || cols % b.elems || rb == 0 || cols > (1ull << 40) || rows > nb / rb)
             throw Exception(Error::Truncated, "gguf: tensor " + name + " does not hold " + std::to_string(rows) +
                                                   " rows of " + std::to_string(cols));
         return m;

@@ -186,6 +186,10 @@ static void test_bad_value_type_and_huge_counts() {
     Buf t;
     t.put<uint32_t>(0x46554747u).put<uint32_t>(3).put<uint64_t>(1ull << 50).put<uint64_t>(0);
     EXPECT(parse_error(t.b) == gguf::Error::Truncated);
+    gguf::TensorInfo big;  // dims whose product overflows 64 bits saturate
+    big.type = 12;
+    big.dims = {1ull << 40, 1ull << 40};
+    EXPECT(big.n_elements() == (1ull << 63) && big.byteSize() > (1ull << 50));
 }
 
 // byteSize against each block layout's byte count (d/dmin halves, scale
