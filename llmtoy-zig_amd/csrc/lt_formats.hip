@@ -238,8 +238,15 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
                                                                     const float *dscale, float *out) {
     extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats
     __shared__ float tab[16];
+    __shared__ uint32_t s_e[16];
+    __shared__ float s_w[16];
     constexpr int LPR = kWave / RPW;
     const int Kd = (int)W.cols;
+    if ((int)threadIdx.x < k) {  // the slots' experts and combine weights, once per workgroup
+        const uint32_t e = ids[threadIdx.x];
+        s_e[threadIdx.x] = e;
+        s_w[threadIdx.x] = e < (uint32_t)W.n_experts ? (dscale ? dscale[e] * wts[threadIdx.x] : wts[threadIdx.x]) : 0.f;
+    }
     stage<T>(hsm, h, k * Kd, tab);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int r = lane / LPR, sub = lane % LPR;
@@ -252,12 +259,11 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
         float acc = 0.f;
         if (live) {
             for (int s = 0; s < k; s++) {
-                const uint32_t e = ids[s];
+                const uint32_t e = s_e[s];
                 if (e >= (uint32_t)W.n_experts) continue;
-                const float ws = dscale ? dscale[e] * wts[s] : wts[s];
                 float t = 0.f;
                 for (int u = sub; u < U; u += LPR) t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, tab);
-                acc += ws * t;
+                acc += s_w[s] * t;
             }
         }
         acc = seg_sum<LPR>(acc);
