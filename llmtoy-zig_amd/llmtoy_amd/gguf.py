@@ -345,6 +345,36 @@ def load_moe_layer(r: GgufReader, layer: int, cfg: MoEConfig | None = None) -> M
     return MoELayer(d, E, F, down_cols, router_data, router.type, gate_up, dn.data, gu_type, dn.type, extra)
 
 
+def _load_vec(r: GgufReader, name: str, n: int) -> np.ndarray:
+    """gemma4/loader.zig:182-199 loadNorm: an F32 or F16 vector of n values."""
+    t = r.tensor(name)
+    if t.n_elements() != n:
+        raise GgufError("BadValueType", f"{name} has {t.n_elements()} values, expected {n}")
+    raw = r.tensor_bytes(t)
+    if t.type == ggml.F32:
+        return raw.view(np.float32).copy()
+    if t.type == ggml.F16:
+        return raw.view(np.float16).astype(np.float32)
+    raise GgufError("BadValueType", f"{name}: type {t.type} (norms are F32 or F16)")
+
+
+def load_gemma4_norms(r: GgufReader, layer: int, cfg: MoEConfig | None = None) -> tuple:
+    """The vectors of a Gemma4 MoE block (gemma4/loader.zig:121-163):
+    (norms dict for lt gemma4_moe_block, layer_output_scale).  A missing
+    layer_output_scale is 1, as loadScalar returns (201-214)."""
+    cfg = cfg or moe_config(r)
+    d, E = cfg.d_model, cfg.n_experts
+    p = f"blk.{layer}."
+    norms = {"pre_ffw_norm_2": _load_vec(r, p + "pre_ffw_norm_2.weight", d),
+             "router_scale": _load_vec(r, p + "ffn_gate_inp.scale", d),
+             "down_exps_scale": _load_vec(r, p + "ffn_down_exps.scale", E),
+             "post_ffw_norm_2": _load_vec(r, p + "post_ffw_norm_2.weight", d),
+             "post_ffw_norm": _load_vec(r, p + "post_ffw_norm.weight", d)}
+    t = r.data.find(p + "layer_output_scale.weight")
+    los = 1.0 if t is None or t.type not in (ggml.F32, ggml.F16) else float(_load_vec(r, t.name, 1)[0])
+    return norms, los
+
+
 # ---------------------------------------------------------------- writer
 class GgufWriter:
     """Builds GGUF files: header, metadata, tensor infos, then each tensor's
@@ -423,13 +453,14 @@ def moe_layer_writer(w, layer: int = 0, arch: str = "qwen3moe", k: int = 8, spli
     wr.add(f"{arch}.expert_feed_forward_length", UINT32, F)
     p = f"blk.{layer}."
     wr.add_tensor(p + "ffn_gate_inp.weight", (d, E), w.router_type, w.router)
+    gut, dnt = getattr(w, "gate_up_type", ggml.Q4_K), getattr(w, "down_type", ggml.Q4_K)
     if split:
         gu = w.gate_up.reshape(E, 2, F, -1)
-        wr.add_tensor(p + "ffn_gate_exps.weight", (d, F, E), ggml.Q4_K, gu[:, 0])
-        wr.add_tensor(p + "ffn_up_exps.weight", (d, F, E), ggml.Q4_K, gu[:, 1])
+        wr.add_tensor(p + "ffn_gate_exps.weight", (d, F, E), gut, gu[:, 0])
+        wr.add_tensor(p + "ffn_up_exps.weight", (d, F, E), gut, gu[:, 1])
     else:
-        wr.add_tensor(p + "ffn_gate_up_exps.weight", (d, 2 * F, E), ggml.Q4_K, w.gate_up)
-    wr.add_tensor(p + "ffn_down_exps.weight", (dc, d, E), ggml.Q4_K, w.down)
+        wr.add_tensor(p + "ffn_gate_up_exps.weight", (d, 2 * F, E), gut, w.gate_up)
+    wr.add_tensor(p + "ffn_down_exps.weight", (dc, d, E), dnt, w.down)
     for key, arr in (extra or {}).items():
         arr = np.asarray(arr, dtype=np.float32)
         wr.add_tensor(p + key, (arr.size,), ggml.F32, arr)

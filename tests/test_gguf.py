@@ -331,3 +331,49 @@ def test_gpu_cpp_reader_runs_gguf_layer(split, tmp_path):
     out = subprocess.run([CPP, "--gpu", p], capture_output=True, text=True, timeout=120)
     print(out.stdout[-3000:])
     assert out.returncode == 0 and "ALL PASSED" in out.stdout, out.stdout + out.stderr
+
+
+def write_gemma4_layer(path, w, nm, los, version=3):
+    """A Gemma4 MoE block's tensors under the loader's names (gemma4/loader.zig:121-163)."""
+    wr = gguf.moe_layer_writer(w, arch="gemma4", version=version,
+                               extra={"ffn_down_exps.scale": nm["down_exps_scale"],
+                                      "ffn_gate_inp.scale": nm["router_scale"]})
+    for key in ("pre_ffw_norm_2", "post_ffw_norm_2", "post_ffw_norm"):
+        wr.add_tensor(f"blk.0.{key}.weight", (w.d_model,), ggml.F32, nm[key])
+    wr.add_tensor("blk.0.layer_output_scale.weight", (1,), ggml.F32, np.array([los], np.float32))
+    return wr.write(path)
+
+
+def test_gemma4_norms_from_gguf(tmp_path):
+    w = synth.moe_weights(46, 512, 8, 256, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K, down_type=ggml.IQ4_NL)
+    nm = synth.gemma4_norms(46, 512, 8)
+    r = gguf.GgufReader(write_gemma4_layer(str(tmp_path / "g4.gguf"), w, nm, 0.625))
+    got, los = gguf.load_gemma4_norms(r, 0)
+    assert los == 0.625 and all(np.array_equal(got[k], nm[k]) for k in nm)
+    L = gguf.load_moe_layer(r, 0)
+    assert (L.gate_up_type, L.down_type, L.router_type) == (ggml.Q3_K, ggml.IQ4_NL, ggml.Q8_0)
+    assert np.array_equal(L.gate_up, w.gate_up) and np.array_equal(L.down, w.down)
+
+
+@pytest.mark.gpu
+def test_gpu_gemma4_block_from_gguf_apex(ctx, tmp_path):
+    # the whole Gemma4 MoE block from a file: Q8_0 router, Q3_K gate/up and
+    # IQ4_NL down experts, every norm vector and the output scale read back
+    import pyoracle as orc
+    from llmtoy_amd import lib as ltlib
+    w = synth.moe_weights(47, 2816, 16, 704, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K,
+                          down_type=ggml.IQ4_NL)
+    nm = synth.gemma4_norms(47, 2816, 16)
+    r = gguf.GgufReader(write_gemma4_layer(str(tmp_path / "g4.gguf"), w, nm, 0.75))
+    L = gguf.load_moe_layer(r, 0)
+    norms, los = gguf.load_gemma4_norms(r, 0)
+    x, dense = synth.normal(synth.stream(47, 1), (2816,)), synth.normal(synth.stream(47, 2), (2816,))
+    tens = lt.upload_moe(ctx, L)
+    ids = np.zeros(8, np.uint32)
+    got = ltlib.gemma4_moe_block(ctx, x.copy(), dense, *tens, 8, L.d_expert, norms, los, 1e-6, precise=True,
+                                 out_ids=ids)
+    for t in tens:
+        t.free()
+    ref, rids, _ = orc.gemma4_moe_block(w, x, dense, 8, nm, 0.75, 1e-6)
+    assert ids.tolist() == rids.tolist()
+    assert float(np.linalg.norm(got - ref) / np.linalg.norm(ref)) < 1e-3

@@ -204,3 +204,35 @@ def test_gpu_gemma4_block_f32_router(ctx, pool):
     for t in tens:
         t.free()
     assert ids.tolist() == rids.tolist() and rel_l2(got, ref) < 1e-3
+
+
+@pytest.mark.parametrize("apex", [False, True])
+def test_gpu_gemma4_block_graph_replay_matches_eager(ctx, apex):
+    # the block captured into a hipGraph (no allocation, no memset inside)
+    # replays to the eager result bit for bit, with eager work between
+    # replays; x is updated in place, so each replay starts from a fresh copy
+    from llmtoy_amd.hip import D2D, DeviceArray, Graph, check, hip
+    if apex:
+        w = synth.moe_weights(48, 2816, 16, 704, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K,
+                              down_type=ggml.IQ4_NL)
+    else:
+        w = synth.moe_weights(48, 2816, 16, 704, down_cols=768, router_type=ggml.Q8_0)
+    tens = lt.upload_moe(ctx, w)
+    nm = synth.gemma4_norms(48, 2816, 16)
+    dn = {k: DeviceArray.from_numpy(v) for k, v in nm.items()}
+    x0 = synth.normal(synth.stream(48, 1), (2816,))
+    dense = synth.normal(synth.stream(48, 2), (2816,))
+    eager = ltlib.gemma4_moe_block(ctx, x0.copy(), dense, *tens, 8, 704, nm, 0.75, 1e-6)
+    X0, X, D = DeviceArray.from_numpy(x0), DeviceArray((2816,), np.float32), DeviceArray.from_numpy(dense)
+    g = Graph(ctx.stream, lambda: ltlib.gemma4_moe_block(ctx, X, D, *tens, 8, 704, dn, 0.75, 1e-6))
+    for rep in range(3):
+        check(hip().hipMemcpy(X.ptr, X0.ptr, 2816 * 4, D2D), "hipMemcpy D2D")
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(X.numpy().view(np.uint32), eager.view(np.uint32)), rep
+        ltlib.gemma4_moe_block(ctx, x0.copy(), dense, *tens, 8, 704, nm, 1.0, 1e-6)  # eager work between
+    g.destroy()
+    for a in [X0, X, D] + list(dn.values()):
+        a.free()
+    for t in tens:
+        t.free()
