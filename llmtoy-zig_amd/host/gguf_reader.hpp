@@ -10,6 +10,7 @@
 //   rawMatrix (a 2-D weight as a RawMatrix)         model/loader.zig:190-204
 //   rawMatrix3D (expert tensors as one RawMatrix)   gemma4/loader.zig:275-292
 //   moeConfig / moeLayer (MoE keys and tensors)     gemma4/loader.zig:27-83, 152-163
+//   loadNorm / gemma4Norms (block vectors)          gemma4/loader.zig:121-163, 182-214
 //
 // Same layout rules as the reference: little-endian fields; v1 counts are
 // u32, v2/v3 counts u64; tensor data starts at the header end rounded up to
@@ -440,6 +441,56 @@ inline MoeLayer moeLayer(const GgufReader &r, const MoeConfig &c, size_t layer) 
     L.down_exps_scale = f32(p + "ffn_down_exps.scale", E);
     L.router_scale = f32(p + "ffn_gate_inp.scale", d);
     return L;
+}
+
+// gemma4/loader.zig:182-199 loadNorm: an F32 or F16 vector of n values
+// (F16 converted exactly).
+inline std::vector<float> loadNorm(const GgufReader &r, const std::string &name, size_t n) {
+    const TensorInfo &t = r.tensor(name);
+    if (t.n_elements() != n) throw Exception(Error::BadValueType, "gguf: " + name + " has the wrong length");
+    size_t nb;
+    const uint8_t *p = r.tensorBytes(t, nb);
+    std::vector<float> v(n);
+    if (t.type == 0) {
+        std::memcpy(v.data(), p, n * 4);
+    } else if (t.type == 1) {
+        for (size_t i = 0; i < n; i++) {
+            const uint32_t h = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 8);
+            const uint32_t sign = (h >> 15) << 31, e = (h >> 10) & 31, m = h & 1023;
+            float f;
+            if (e == 0) {
+                f = (float)m * 5.9604644775390625e-08f;  // m * 2^-24, exact
+                if (sign) f = -f;
+            } else {
+                const uint32_t bits = sign | (e == 31 ? 0x7f800000u | (m << 13) : ((e + 112u) << 23) | (m << 13));
+                std::memcpy(&f, &bits, 4);
+            }
+            v[i] = f;
+        }
+    } else {
+        throw Exception(Error::BadValueType, "gguf: " + name + " is neither F32 nor F16");
+    }
+    return v;
+}
+
+// The vectors of a Gemma4 MoE block (gemma4/loader.zig:121-163); a missing
+// layer_output_scale is 1, as loadScalar returns (201-214).
+struct Gemma4Norms {
+    std::vector<float> pre_ffw_norm_2, router_scale, down_exps_scale, post_ffw_norm_2, post_ffw_norm;
+    float layer_output_scale = 1.0f;
+};
+
+inline Gemma4Norms gemma4Norms(const GgufReader &r, const MoeConfig &c, size_t layer) {
+    const std::string p = "blk." + std::to_string(layer) + ".";
+    Gemma4Norms g;
+    g.pre_ffw_norm_2 = loadNorm(r, p + "pre_ffw_norm_2.weight", c.d_model);
+    g.router_scale = loadNorm(r, p + "ffn_gate_inp.scale", c.d_model);
+    g.down_exps_scale = loadNorm(r, p + "ffn_down_exps.scale", c.n_experts);
+    g.post_ffw_norm_2 = loadNorm(r, p + "post_ffw_norm_2.weight", c.d_model);
+    g.post_ffw_norm = loadNorm(r, p + "post_ffw_norm.weight", c.d_model);
+    const TensorInfo *t = r.data.find(p + "layer_output_scale.weight");
+    if (t && (t->type == 0 || t->type == 1) && t->n_elements() == 1) g.layer_output_scale = loadNorm(r, t->name, 1)[0];
+    return g;
 }
 
 }  // namespace gguf

@@ -399,7 +399,7 @@ static int run_gpu(const char *path) {
                 c.d_model, c.n_experts, c.n_experts_used, c.d_expert, L.down_cols);
     GpuContext g(0);
     int bad = 0;
-    {
+    if (L.router.type == GgmlType::f32) {  // moeForward takes the fp32 router (ops/moe.zig:18-28)
         std::vector<float> out(c.d_model, 0.0f), ref(c.d_model, 0.0f);
         moeForward(g, out.data(), L.router, L.gate_up, L.down, x, c.n_experts_used, c.d_expert, true);
         std::vector<uint32_t> ids(c.n_experts_used);
@@ -435,6 +435,29 @@ static int run_gpu(const char *path) {
             std::printf("runExpertBatch with ffn_down_exps.scale: rel-L2 %.3g\n", e3);
             bad += !(e3 < 1e-3);
         }
+    }
+    if (r.data.find("blk.0.pre_ffw_norm_2.weight")) {  // a Gemma4 block: runMoeBlock against the CPU block
+        const gguf::Gemma4Norms nm = gguf::gemma4Norms(r, c, 0);
+        const float *dense = f32_tensor(r, "test.dense", c.d_model);
+        std::vector<float> xg(x, x + c.d_model), xr(x, x + c.d_model);
+        GpuWeights gw(g, L.gate_up, L.down, c.n_experts, c.d_expert);
+        std::vector<size_t> top(c.n_experts_used);
+        gw.runMoeBlock(L.router, {nm.pre_ffw_norm_2.data(), nm.router_scale.data(), nm.down_exps_scale.data(),
+                                  nm.post_ffw_norm_2.data(), nm.post_ffw_norm.data()},
+                       c.n_experts_used, MoeTailParams{1e-6f, xg.data(), dense, nm.layer_output_scale}, top.data(),
+                       nullptr, LT_ACT_GELU_TANH, true);
+        std::vector<uint32_t> rids(c.n_experts_used);
+        const int rc = lto_gemma4_moe_block(
+            xr.data(), dense, c.d_model, L.router.data, (uint32_t)L.router.type, c.n_experts, L.gate_up.data,
+            (uint32_t)L.gate_up.type, L.down.data, (uint32_t)L.down.type, L.down_cols, c.n_experts_used, c.d_expert,
+            nm.pre_ffw_norm_2.data(), nm.router_scale.data(), nm.down_exps_scale.data(), nm.post_ffw_norm_2.data(),
+            nm.post_ffw_norm.data(), nm.layer_output_scale, 1e-6f, LTO_ACT_GELU_TANH, nullptr, rids.data(), nullptr);
+        bool same = rc == 0;
+        for (size_t i = 0; i < top.size(); i++) same = same && top[i] == rids[i];
+        const double e = rel_l2(xg, xr);
+        std::printf("runMoeBlock (Gemma4 block, output scale %g): ids %s, rel-L2 %.3g\n", nm.layer_output_scale,
+                    same ? "match" : "DIFFER", e);
+        bad += !(same && e < 1e-3);
     }
     for (const gguf::TensorInfo &t : r.data.tensors) {
         if (t.name.rfind("test.", 0) != 0 || t.dims.size() != 2) continue;

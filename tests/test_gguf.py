@@ -356,6 +356,27 @@ def test_gemma4_norms_from_gguf(tmp_path):
 
 
 @pytest.mark.gpu
+def test_gpu_cpp_reader_runs_gemma4_block(tmp_path):
+    # the C++ reader and host layer: gemma4Norms + GpuWeights::runMoeBlock from a file
+    w = synth.moe_weights(49, 2816, 16, 704, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K,
+                          down_type=ggml.IQ4_NL)
+    nm = synth.gemma4_norms(49, 2816, 16)
+    wr = gguf.moe_layer_writer(w, arch="gemma4", extra={"ffn_down_exps.scale": nm["down_exps_scale"],
+                                                         "ffn_gate_inp.scale": nm["router_scale"]})
+    for key in ("pre_ffw_norm_2", "post_ffw_norm_2", "post_ffw_norm"):
+        wr.add_tensor(f"blk.0.{key}.weight", (2816,), ggml.F16 if key == "post_ffw_norm" else ggml.F32,
+                      nm[key].astype(np.float16) if key == "post_ffw_norm" else nm[key])
+    wr.add_tensor("blk.0.layer_output_scale.weight", (1,), ggml.F32, np.array([0.75], np.float32))
+    wr.add_tensor("test.x", (2816,), ggml.F32, synth.normal(synth.stream(49, 1), (2816,)))
+    wr.add_tensor("test.dense", (2816,), ggml.F32, synth.normal(synth.stream(49, 2), (2816,)))
+    p = wr.write(str(tmp_path / "g4cpp.gguf"))
+    print("running tests/cpp/build/test_gguf --gpu on a Gemma4 block file", flush=True)
+    out = subprocess.run([CPP, "--gpu", p], capture_output=True, text=True, timeout=120)
+    print(out.stdout[-3000:])
+    assert out.returncode == 0 and "runMoeBlock" in out.stdout and "ALL PASSED" in out.stdout, out.stdout + out.stderr
+
+
+@pytest.mark.gpu
 def test_gpu_gemma4_block_from_gguf_apex(ctx, tmp_path):
     # the whole Gemma4 MoE block from a file: Q8_0 router, Q3_K gate/up and
     # IQ4_NL down experts, every norm vector and the output scale read back
