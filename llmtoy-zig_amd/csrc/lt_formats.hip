@@ -28,50 +28,75 @@ namespace {
 
 constexpr int kFmtWaves = 4;  // rows per workgroup
 
-__constant__ float kIq4nlTable[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-
 __device__ __forceinline__ float f16_at(const uint8_t *p) {
     return f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(p));
 }
 
-// Sum of q[e] * x[e] for the 32 elements of a Q5 block: nibble e of qs
-// (e < 16 low, else high nibble of byte e - 16), high bit e of qh; bias
-// subtracts 16 (Q5_0) or nothing (Q5_1).  Also returns the sum of x (Q5_1's m).
-__device__ __forceinline__ float q5_block_dot(uint4 qv, uint32_t qh, const float *x, float bias, float &xsum) {
-    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
-    float acc = 0.f, sx = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
-        const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
-        const float xl[4] = {lo.x, lo.y, lo.z, lo.w}, xh[4] = {hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int e = 4 * i + b;
-            const uint32_t byte = (w[i] >> (8 * b)) & 0xffu;
-            const float ql = (float)((byte & 15u) | (((qh >> e) & 1u) << 4)) - bias;
-            const float qhv = (float)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - bias;
-            acc += ql * xl[b] + qhv * xh[b];
-            sx += xl[b] + xh[b];
-        }
-    }
-    xsum = sx;
-    return acc;
-}
+// Unsigned 5-bit codes of a Q5 block as bytes: word i of the result holds
+// elements 4i..4i+3 (low nibbles of qs word i + high bit 4i..4i+3 of qh) and
+// word 4 + i elements 16+4i..16+4i+3 (high nibbles + bits 16+4i..).  The
+// four high bits of an element group spread into bits 4, 12, 20, 28 with one
+// 24-bit multiply: (v * 0x204081) & 0x01010101 puts bit j of v at bit 8j,
+// and no two partial products meet.
+__device__ __forceinline__ uint32_t spread4(uint32_t v4) { return (__umul24(v4, 0x204081u) & 0x01010101u) << 4; }
 
-__device__ __forceinline__ float iq4_block_dot(uint4 qv, const float *x, const float *tab) {
+// Byte i of v as a float (one v_cvt_f32_ubyte<i>).
+__device__ __forceinline__ float ubyte_f(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xffu); }
+
+// sum over the block of (code) * x: codes 0..31 as unsigned bytes,
+// converted with v_cvt_f32_ubyte0..3.
+__device__ __forceinline__ float q5u_block_dot(uint4 qv, uint32_t qh, const float *x) {
     const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
         const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
-        const float xl[4] = {lo.x, lo.y, lo.z, lo.w}, xh[4] = {hi.x, hi.y, hi.z, hi.w};
+        const uint32_t cl = (w[i] & 0x0f0f0f0fu) | spread4((qh >> (4 * i)) & 15u);
+        const uint32_t ch = ((w[i] >> 4) & 0x0f0f0f0fu) | spread4((qh >> (16 + 4 * i)) & 15u);
+        acc += ubyte_f(cl, 0) * lo.x;
+        acc += ubyte_f(cl, 1) * lo.y;
+        acc += ubyte_f(cl, 2) * lo.z;
+        acc += ubyte_f(cl, 3) * lo.w;
+        acc += ubyte_f(ch, 0) * hi.x;
+        acc += ubyte_f(ch, 1) * hi.y;
+        acc += ubyte_f(ch, 2) * hi.z;
+        acc += ubyte_f(ch, 3) * hi.w;
+    }
+    return acc;
+}
+
+// IQ4_NL table + 128 as unsigned bytes (1..241): entries 0-3, 4-7, 8-11, 12-15.
+constexpr uint32_t kIq4T0 = 0x3f2d1801u, kIq4T1 = 0x766a5d4fu, kIq4T2 = 0xa6998d81u, kIq4T3 = 0xf1d9c5b5u;
+
+// table[n] + 128 for the four nibbles in the bytes of n4 (each 0..15):
+// v_perm_b32 picks bytes by 3-bit index from the low and high half tables,
+// bit 3 chooses between them (v_bfi_b32 on a byte mask).
+__device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n4) {
+    const uint32_t sel = n4 & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4T1, kIq4T0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4T3, kIq4T2, sel);
+    const uint32_t b3 = (n4 >> 3) & 0x01010101u;
+    const uint32_t m = (b3 << 8) - b3;  // 0x00 or 0xff per byte
+    return (hi & m) | (lo & ~m);
+}
+
+__device__ __forceinline__ float iq4u_block_dot(uint4 qv, const float *x) {
+    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+    float acc = 0.f;
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const uint32_t byte = (w[i] >> (8 * b)) & 0xffu;
-            acc += tab[byte & 15u] * xl[b] + tab[byte >> 4] * xh[b];
-        }
+    for (int i = 0; i < 4; i++) {
+        const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
+        const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
+        const uint32_t tl = iq4_lookup4(w[i] & 0x0f0f0f0fu), th = iq4_lookup4((w[i] >> 4) & 0x0f0f0f0fu);
+        acc += ubyte_f(tl, 0) * lo.x;
+        acc += ubyte_f(tl, 1) * lo.y;
+        acc += ubyte_f(tl, 2) * lo.z;
+        acc += ubyte_f(tl, 3) * lo.w;
+        acc += ubyte_f(th, 0) * hi.x;
+        acc += ubyte_f(th, 1) * hi.y;
+        acc += ubyte_f(th, 2) * hi.z;
+        acc += ubyte_f(th, 3) * hi.w;
     }
     return acc;
 }
@@ -120,9 +145,10 @@ __device__ __forceinline__ float q3k_group_dot(const uint8_t *qs64, const uint8_
 }
 
 // Contribution of unit u of a row (block u, or Q3_K group u) against the
-// row's x (xs = element 0 of the row's columns, in LDS).
+// row's x (xs = element 0 of the row's columns, in LDS; xsum = per-block sums
+// of x, for the offsets the unsigned codes leave out).
 template <int T>
-__device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u, const float *xs, const float *tab) {
+__device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u, const float *xs, const float *xsum) {
     const int nb = (int)W.blocks_per_row;
     if (T == LT_TYPE_Q3_K) {
         const size_t sb = row * nb + (u >> 3);
@@ -134,12 +160,12 @@ __device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u,
     const size_t b = row * nb + u;
     const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
     const float *xb = xs + 32 * u;
-    if (T == LT_TYPE_IQ4_NL) return f16_at(W.p1 + b * 2) * iq4_block_dot(qv, xb, tab);
+    if (T == LT_TYPE_IQ4_NL)  // d * (sum (table + 128) x - 128 sum x)
+        return f16_at(W.p1 + b * 2) * (iq4u_block_dot(qv, xb) - 128.f * xsum[u]);
     const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
-    float sx;
-    if (T == LT_TYPE_Q5_0) return f16_at(W.p2 + b * 2) * q5_block_dot(qv, qh, xb, 16.f, sx);
-    const float dot = q5_block_dot(qv, qh, xb, 0.f, sx);  // Q5_1: d * sum(q x) + m * sum(x)
-    return f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * sx;
+    const float dot = q5u_block_dot(qv, qh, xb);
+    if (T == LT_TYPE_Q5_0) return f16_at(W.p2 + b * 2) * (dot - 16.f * xsum[u]);  // codes - 16
+    return f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * xsum[u];        // Q5_1: d q + m
 }
 
 template <int T>
@@ -154,11 +180,21 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
+// Stage n floats into LDS and, for the 32-element block formats, their
+// per-block sums (sums[j] = sum of dst[32 j .. 32 j + 32)) right after them.
 template <int T>
-__device__ __forceinline__ void stage(float *dst, const float *src, int n, float *tab) {
+__device__ __forceinline__ void stage(float *dst, const float *src, int n) {
     for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
-    if (T == LT_TYPE_IQ4_NL && threadIdx.x < 16) tab[threadIdx.x] = kIq4nlTable[threadIdx.x];
     __syncthreads();
+    if (T != LT_TYPE_Q3_K) {
+        for (int j = threadIdx.x; j < n / 32; j += blockDim.x) {
+            float t = 0.f;
+#pragma unroll 8
+            for (int e = 0; e < 32; e++) t += dst[32 * j + e];
+            dst[n + j] = t;
+        }
+        __syncthreads();
+    }
 }
 
 // Workgroup = kFmtWaves waves; a wave takes RPW rows at a time (64 / RPW
@@ -167,10 +203,10 @@ __device__ __forceinline__ void stage(float *dst, const float *src, int n, float
 template <int T, int RPW>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, const float *__restrict__ x,
                                                                float *__restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats
-    __shared__ float tab[16];
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + cols / 32 block sums
     constexpr int LPR = kWave / RPW;
-    stage<T>(xs, x, (int)W.cols, tab);
+    stage<T>(xs, x, (int)W.cols);
+    const float *xsum = xs + W.cols;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int r = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
@@ -180,7 +216,7 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, cons
         const bool live = row < W.total_rows;
         float acc = 0.f;
         if (live)
-            for (int u = sub; u < U; u += LPR) acc += unit_dot<T>(W, row, u, xs, tab);
+            for (int u = sub; u < U; u += LPR) acc += unit_dot<T>(W, row, u, xs, xsum);
         acc = seg_sum<LPR>(acc);
         if (live && sub == 0) y[row] = acc;
     }
@@ -194,10 +230,10 @@ template <int T, int RPW>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, const float *__restrict__ x,
                                                                   const uint32_t *__restrict__ ids, int F,
                                                                   int down_cols, uint32_t act, float *__restrict__ h) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];
-    __shared__ float tab[16];
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + cols / 32 block sums
     constexpr int LPR = kWave / RPW;
-    stage<T>(xs, x, (int)W.cols, tab);
+    stage<T>(xs, x, (int)W.cols);
+    const float *xsum = xs + W.cols;
     const int s = blockIdx.y;
     const uint32_t e = __builtin_amdgcn_readfirstlane(ids[s]);
     float *hs = h + (size_t)s * down_cols;
@@ -215,8 +251,8 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, c
         if (live && valid) {
             const size_t g = (size_t)e * 2 * F + j, up = g + F;
             for (int u = sub; u < U; u += LPR) {
-                ag += unit_dot<T>(W, g, u, xs, tab);
-                au += unit_dot<T>(W, up, u, xs, tab);
+                ag += unit_dot<T>(W, g, u, xs, xsum);
+                au += unit_dot<T>(W, up, u, xs, xsum);
             }
         }
         ag = seg_sum<LPR>(ag);
@@ -236,8 +272,7 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
                                                                     const float *__restrict__ wts, int k,
                                                                     const float *base, int accumulate,
                                                                     const float *dscale, float *out) {
-    extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats
-    __shared__ float tab[16];
+    extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats + their block sums
     __shared__ uint32_t s_e[16];
     __shared__ float s_w[16];
     constexpr int LPR = kWave / RPW;
@@ -247,7 +282,8 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
         s_e[threadIdx.x] = e;
         s_w[threadIdx.x] = e < (uint32_t)W.n_experts ? (dscale ? dscale[e] * wts[threadIdx.x] : wts[threadIdx.x]) : 0.f;
     }
-    stage<T>(hsm, h, k * Kd, tab);
+    stage<T>(hsm, h, k * Kd);
+    const float *hsum = hsm + k * Kd;  // block sums: slot s's at hsum + s * (Kd / 32)
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int r = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
@@ -262,7 +298,8 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
                 const uint32_t e = s_e[s];
                 if (e >= (uint32_t)W.n_experts) continue;
                 float t = 0.f;
-                for (int u = sub; u < U; u += LPR) t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, tab);
+                for (int u = sub; u < U; u += LPR)
+                    t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, hsum + s * (Kd / 32));
                 acc += s_w[s] * t;
             }
         }
@@ -283,7 +320,7 @@ hipError_t allow_lds(const void *fn, bool *set) {
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     if (set[dev]) return hipSuccess;
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 65536 + 2048);
     if (e == hipSuccess) set[dev] = true;
     return e;
 }
@@ -296,7 +333,8 @@ hipError_t launch_mv(const DevTensor &W, const float *x, float *y, hipStream_t s
     // up to 8 workgroups per CU, each walking many rows
     const size_t need = (W.total_rows + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 2048 ? need : 2048));
-    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), W.cols * sizeof(float), s, W, x, y);
+    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (W.cols + W.cols / 32) * sizeof(float), s,
+                       W, x, y);
     return hipGetLastError();
 }
 
@@ -308,7 +346,8 @@ hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, in
     if (e != hipSuccess) return e;
     const int need = (F + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 128 ? need : 128), (unsigned)k);  // up to 128 x k workgroups walk the rows
-    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), W.cols * sizeof(float), s, W, x, ids,
+    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (W.cols + W.cols / 32) * sizeof(float),
+                       s, W, x, ids,
                        F, down_cols, act, h);
     return hipGetLastError();
 }
@@ -322,8 +361,9 @@ hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, co
     const int D = (int)W.rows;
     const int need = (D + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 1024 ? need : 1024));
-    hipLaunchKernelGGL((k_expert_down_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (size_t)k * W.cols * sizeof(float),
-                       s, W, h, ids, w, k, base, accumulate, dscale, out);
+    hipLaunchKernelGGL((k_expert_down_fmt<T, RPW>), grid, dim3(64 * kFmtWaves),
+                       ((size_t)k * W.cols + (size_t)k * W.cols / 32) * sizeof(float), s, W, h, ids, w, k, base,
+                       accumulate, dscale, out);
     return hipGetLastError();
 }
 
