@@ -28,6 +28,14 @@ namespace {
 
 constexpr int kFmtWaves = 4;  // rows per workgroup
 
+// Length of the x runs whose sums are staged beside x: one Q3_K scale's 16
+// elements, or one 32-element block.
+template <int T>
+constexpr int kSumLen = T == LT_TYPE_Q3_K ? 16 : 32;
+
+template <int T>
+size_t lds_floats(size_t n) { return n + n / kSumLen<T>; }
+
 __device__ __forceinline__ float f16_at(const uint8_t *p) {
     return f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(p));
 }
@@ -112,9 +120,12 @@ __device__ __forceinline__ int q3k_scale(const uint32_t s[3], int i) {
 
 // Group u = 4 h + j of a Q3_K super-block: elements 128 h + 32 j + [0, 32)
 // (16 from qs[32 h ..] and hmask[0 ..], 16 from qs[32 h + 16 ..] and
-// hmask[16 ..]) against x.
+// hmask[16 ..]) against x.  Each element's 3-bit unsigned code
+// c = q2 | hbit << 2 (value c - 4) is built four to a dword and converted
+// with v_cvt_f32_ubyte<i>; the -4 folds into x16 = the sums of the group's
+// two 16-element halves of x.
 __device__ __forceinline__ float q3k_group_dot(const uint8_t *qs64, const uint8_t *hm32, const uint32_t sc[3],
-                                               float d, int u, const float *x) {
+                                               float d, int u, const float *x, const float *x16) {
     const int h = u >> 2, j = u & 3;
     const uint4 q0 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h);
     const uint4 q1 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h + 16);
@@ -130,23 +141,20 @@ __device__ __forceinline__ float q3k_group_dot(const uint8_t *qs64, const uint8_
 #pragma unroll
         for (int w4 = 0; w4 < 4; w4++) {
             const float4 xv = *reinterpret_cast<const float4 *>(x + 16 * g + 4 * w4);
-            const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
-            const uint32_t qword = qw[4 * g + w4] >> qsh, mword = mw[4 * g + w4] >> msh;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int q2 = (int)((qword >> (8 * b)) & 3u);
-                const int hb = (int)((mword >> (8 * b)) & 1u);
-                acc += (float)(q2 - 4 + 4 * hb) * xa[b];
-            }
+            const uint32_t c = ((qw[4 * g + w4] >> qsh) & 0x03030303u) | (((mw[4 * g + w4] >> msh) & 0x01010101u) << 2);
+            acc += ubyte_f(c, 0) * xv.x;
+            acc += ubyte_f(c, 1) * xv.y;
+            acc += ubyte_f(c, 2) * xv.z;
+            acc += ubyte_f(c, 3) * xv.w;
         }
-        total += (d * (float)(q3k_scale(sc, 8 * h + 2 * j + g) - 32)) * acc;
+        total += (d * (float)(q3k_scale(sc, 8 * h + 2 * j + g) - 32)) * (acc - 4.f * x16[g]);
     }
     return total;
 }
 
 // Contribution of unit u of a row (block u, or Q3_K group u) against the
-// row's x (xs = element 0 of the row's columns, in LDS; xsum = per-block sums
-// of x, for the offsets the unsigned codes leave out).
+// row's x (xs = element 0 of the row's columns, in LDS; xsum = sums of x over
+// kSumLen<T> elements, for the offsets the unsigned codes leave out).
 template <int T>
 __device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u, const float *xs, const float *xsum) {
     const int nb = (int)W.blocks_per_row;
@@ -155,7 +163,7 @@ __device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u,
         const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
         const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
         return q3k_group_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 7,
-                             xs + 256 * (u >> 3) + 32 * (u & 7));
+                             xs + 256 * (u >> 3) + 32 * (u & 7), xsum + 2 * u);
     }
     const size_t b = row * nb + u;
     const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
@@ -180,21 +188,20 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
-// Stage n floats into LDS and, for the 32-element block formats, their
-// per-block sums (sums[j] = sum of dst[32 j .. 32 j + 32)) right after them.
+// Stage n floats into LDS and their sums over kSumLen<T> elements
+// (sums[j] = sum of dst[L j .. L j + L)) right after them.
 template <int T>
 __device__ __forceinline__ void stage(float *dst, const float *src, int n) {
+    constexpr int L = kSumLen<T>;
     for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
     __syncthreads();
-    if (T != LT_TYPE_Q3_K) {
-        for (int j = threadIdx.x; j < n / 32; j += blockDim.x) {
-            float t = 0.f;
+    for (int j = threadIdx.x; j < n / L; j += blockDim.x) {
+        float t = 0.f;
 #pragma unroll 8
-            for (int e = 0; e < 32; e++) t += dst[32 * j + e];
-            dst[n + j] = t;
-        }
-        __syncthreads();
+        for (int e = 0; e < L; e++) t += dst[L * j + e];
+        dst[n + j] = t;
     }
+    __syncthreads();
 }
 
 // Workgroup = kFmtWaves waves; a wave takes RPW rows at a time (64 / RPW
@@ -203,7 +210,7 @@ __device__ __forceinline__ void stage(float *dst, const float *src, int n) {
 template <int T, int RPW>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, const float *__restrict__ x,
                                                                float *__restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + cols / 32 block sums
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + their run sums
     constexpr int LPR = kWave / RPW;
     stage<T>(xs, x, (int)W.cols);
     const float *xsum = xs + W.cols;
@@ -230,7 +237,7 @@ template <int T, int RPW>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, const float *__restrict__ x,
                                                                   const uint32_t *__restrict__ ids, int F,
                                                                   int down_cols, uint32_t act, float *__restrict__ h) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + cols / 32 block sums
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + their run sums
     constexpr int LPR = kWave / RPW;
     stage<T>(xs, x, (int)W.cols);
     const float *xsum = xs + W.cols;
@@ -283,7 +290,7 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
         s_w[threadIdx.x] = e < (uint32_t)W.n_experts ? (dscale ? dscale[e] * wts[threadIdx.x] : wts[threadIdx.x]) : 0.f;
     }
     stage<T>(hsm, h, k * Kd);
-    const float *hsum = hsm + k * Kd;  // block sums: slot s's at hsum + s * (Kd / 32)
+    const float *hsum = hsm + k * Kd;  // run sums: slot s's at hsum + s * (Kd / kSumLen<T>)
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int r = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
@@ -299,7 +306,7 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
                 if (e >= (uint32_t)W.n_experts) continue;
                 float t = 0.f;
                 for (int u = sub; u < U; u += LPR)
-                    t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, hsum + s * (Kd / 32));
+                    t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, hsum + s * (Kd / kSumLen<T>));
                 acc += s_w[s] * t;
             }
         }
@@ -313,14 +320,15 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
 
 int pick_rpw(size_t units) { return units >= 48 ? 1 : units >= 24 ? 2 : units >= 12 ? 4 : 8; }
 
-// Allow up to 64 KiB of dynamic LDS, once per kernel and device.
+// Allow the largest staging (16384 floats and their 16-element run sums:
+// 68 KiB of dynamic LDS), once per kernel and device.
 hipError_t allow_lds(const void *fn, bool *set) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     if (set[dev]) return hipSuccess;
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 65536 + 2048);
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (16384 + 16384 / 16) * 4);
     if (e == hipSuccess) set[dev] = true;
     return e;
 }
@@ -333,7 +341,7 @@ hipError_t launch_mv(const DevTensor &W, const float *x, float *y, hipStream_t s
     // up to 8 workgroups per CU, each walking many rows
     const size_t need = (W.total_rows + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 2048 ? need : 2048));
-    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (W.cols + W.cols / 32) * sizeof(float), s,
+    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), lds_floats<T>(W.cols) * sizeof(float), s,
                        W, x, y);
     return hipGetLastError();
 }
@@ -346,7 +354,7 @@ hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, in
     if (e != hipSuccess) return e;
     const int need = (F + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 128 ? need : 128), (unsigned)k);  // up to 128 x k workgroups walk the rows
-    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), (W.cols + W.cols / 32) * sizeof(float),
+    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), lds_floats<T>(W.cols) * sizeof(float),
                        s, W, x, ids,
                        F, down_cols, act, h);
     return hipGetLastError();
@@ -362,7 +370,7 @@ hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, co
     const int need = (D + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 1024 ? need : 1024));
     hipLaunchKernelGGL((k_expert_down_fmt<T, RPW>), grid, dim3(64 * kFmtWaves),
-                       ((size_t)k * W.cols + (size_t)k * W.cols / 32) * sizeof(float), s, W, h, ids, w, k, base,
+                       lds_floats<T>((size_t)k * W.cols) * sizeof(float), s, W, h, ids, w, k, base,
                        accumulate, dscale, out);
     return hipGetLastError();
 }
