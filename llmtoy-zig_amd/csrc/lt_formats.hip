@@ -36,10 +36,6 @@ constexpr int kSumLen = T == LT_TYPE_Q3_K ? 16 : 32;
 template <int T>
 size_t lds_floats(size_t n) { return n + n / kSumLen<T>; }
 
-__device__ __forceinline__ float f16_at(const uint8_t *p) {
-    return f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(p));
-}
-
 // Unsigned 5-bit codes of a Q5 block as bytes: word i of the result holds
 // elements 4i..4i+3 (low nibbles of qs word i + high bit 4i..4i+3 of qh) and
 // word 4 + i elements 16+4i..16+4i+3 (high nibbles + bits 16+4i..).  The
@@ -52,14 +48,13 @@ __device__ __forceinline__ uint32_t spread4(uint32_t v4) { return (__umul24(v4, 
 __device__ __forceinline__ float ubyte_f(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xffu); }
 
 // sum over the block of (code) * x: codes 0..31 as unsigned bytes,
-// converted with v_cvt_f32_ubyte0..3.
-__device__ __forceinline__ float q5u_block_dot(uint4 qv, uint32_t qh, const float *x) {
+// converted with v_cvt_f32_ubyte0..3.  x4[i] holds elements 4i..4i+3.
+__device__ __forceinline__ float q5u_block_dot(uint4 qv, uint32_t qh, const float4 *x4) {
     const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
-        const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
+        const float4 lo = x4[i], hi = x4[4 + i];
         const uint32_t cl = (w[i] & 0x0f0f0f0fu) | spread4((qh >> (4 * i)) & 15u);
         const uint32_t ch = ((w[i] >> 4) & 0x0f0f0f0fu) | spread4((qh >> (16 + 4 * i)) & 15u);
         acc += ubyte_f(cl, 0) * lo.x;
@@ -89,13 +84,12 @@ __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n4) {
     return (hi & m) | (lo & ~m);
 }
 
-__device__ __forceinline__ float iq4u_block_dot(uint4 qv, const float *x) {
+__device__ __forceinline__ float iq4u_block_dot(uint4 qv, const float4 *x4) {
     const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 lo = *reinterpret_cast<const float4 *>(x + 4 * i);
-        const float4 hi = *reinterpret_cast<const float4 *>(x + 16 + 4 * i);
+        const float4 lo = x4[i], hi = x4[4 + i];
         const uint32_t tl = iq4_lookup4(w[i] & 0x0f0f0f0fu), th = iq4_lookup4((w[i] >> 4) & 0x0f0f0f0fu);
         acc += ubyte_f(tl, 0) * lo.x;
         acc += ubyte_f(tl, 1) * lo.y;
@@ -109,71 +103,127 @@ __device__ __forceinline__ float iq4u_block_dot(uint4 qv, const float *x) {
     return acc;
 }
 
-// Q3_K scale i (0..15) from the 12 packed bytes s[0..2] (little-endian
+// Q3_K scale i (0..15) from the 12 packed bytes s0, s1, s2 (little-endian
 // dwords): low 4 bits from byte i (i < 8) or the high nibble of byte i - 8,
-// high 2 bits from bits 2 (i / 4) of byte 8 + i % 4.
-__device__ __forceinline__ int q3k_scale(const uint32_t s[3], int i) {
-    const uint32_t lo = i < 8 ? (s[i >> 2] >> (8 * (i & 3))) & 15u : (s[(i - 8) >> 2] >> (8 * ((i - 8) & 3) + 4)) & 15u;
-    const uint32_t hi = (s[2] >> (8 * (i & 3) + 2 * (i >> 2))) & 3u;
+// high 2 bits from bits 2 (i / 4) of byte 8 + i % 4.  The dword is picked by
+// a select, not an array index, so the words stay in registers.
+__device__ __forceinline__ int q3k_scale(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const int b = i & 7;
+    const uint32_t lo = (((b & 4) ? s1 : s0) >> (8 * (b & 3) + 4 * (i >> 3))) & 15u;
+    const uint32_t hi = (s2 >> (8 * (i & 3) + 2 * (i >> 2))) & 3u;
     return (int)(lo | (hi << 4));
 }
 
-// Group u = 4 h + j of a Q3_K super-block: elements 128 h + 32 j + [0, 32)
+// Raw weight words of one unit of one row, loaded before any arithmetic so
+// that a lane's loads for several rows are in flight together.
+template <int T>
+struct UnitW {
+    uint4 q;      // qs
+    uint32_t qh;  // Q5_0 / Q5_1 high bits
+    uint32_t dm;  // f16 d in the low half; Q5_1: f16 m in the high half
+};
+template <>
+struct UnitW<LT_TYPE_Q3_K> {
+    uint4 q0, q1;    // qs[32 h ..], qs[32 h + 16 ..] of the unit's half h
+    uint4 m0, m1;    // hmask[0 ..], hmask[16 ..]
+    uint32_t sc[3];  // the 12 packed scale bytes
+    uint32_t d;      // f16 d in the low half
+};
+
+// Unit u of `row`: block u, or group u (super-block u / 8, group u % 8).
+template <int T>
+__device__ __forceinline__ UnitW<T> load_unit(const DevTensor &W, size_t row, int u) {
+    const size_t nb = W.blocks_per_row;
+    UnitW<T> w;
+    if constexpr (T == LT_TYPE_Q3_K) {
+        const size_t sb = row * nb + (u >> 3);
+        const uint8_t *qs = W.p0 + sb * 64 + 32 * ((u >> 2) & 1);
+        w.q0 = *reinterpret_cast<const uint4 *>(qs);
+        w.q1 = *reinterpret_cast<const uint4 *>(qs + 16);
+        w.m0 = *reinterpret_cast<const uint4 *>(W.p1 + sb * 32);
+        w.m1 = *reinterpret_cast<const uint4 *>(W.p1 + sb * 32 + 16);
+        const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
+        w.sc[0] = s3[0];
+        w.sc[1] = s3[1];
+        w.sc[2] = s3[2];
+        w.d = *reinterpret_cast<const uint16_t *>(W.p3 + sb * 2);
+    } else {
+        const size_t b = row * nb + u;
+        w.q = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
+        if constexpr (T == LT_TYPE_IQ4_NL) {
+            w.qh = 0;
+            w.dm = *reinterpret_cast<const uint16_t *>(W.p1 + b * 2);
+        } else {
+            w.qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
+            w.dm = T == LT_TYPE_Q5_1 ? *reinterpret_cast<const uint32_t *>(W.p2 + b * 4)
+                                     : (uint32_t)*reinterpret_cast<const uint16_t *>(W.p2 + b * 2);
+        }
+    }
+    return w;
+}
+
+// x of unit u (elements 32 u .. 32 u + 32 of the row's columns, in LDS) into
+// registers, with the sums of its runs (xsum = the run sums staged beside x):
+// s0 = the block's sum, or for Q3_K s0/s1 = the two 16-element halves.
+template <int T>
+__device__ __forceinline__ void load_x(const float *xs, const float *xsum, int u, float4 (&x4)[8], float &s0,
+                                       float &s1) {
+    const float4 *p = reinterpret_cast<const float4 *>(xs + 32 * u);
+#pragma unroll
+    for (int i = 0; i < 8; i++) x4[i] = p[i];
+    if constexpr (T == LT_TYPE_Q3_K) {
+        s0 = xsum[2 * u];
+        s1 = xsum[2 * u + 1];
+    } else {
+        s0 = xsum[u];
+        s1 = 0.f;
+    }
+}
+
+// Group u % 8 = 4 h + j of a Q3_K super-block: elements 128 h + 32 j + [0, 32)
 // (16 from qs[32 h ..] and hmask[0 ..], 16 from qs[32 h + 16 ..] and
 // hmask[16 ..]) against x.  Each element's 3-bit unsigned code
 // c = q2 | hbit << 2 (value c - 4) is built four to a dword and converted
-// with v_cvt_f32_ubyte<i>; the -4 folds into x16 = the sums of the group's
-// two 16-element halves of x.
-__device__ __forceinline__ float q3k_group_dot(const uint8_t *qs64, const uint8_t *hm32, const uint32_t sc[3],
-                                               float d, int u, const float *x, const float *x16) {
-    const int h = u >> 2, j = u & 3;
-    const uint4 q0 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h);
-    const uint4 q1 = *reinterpret_cast<const uint4 *>(qs64 + 32 * h + 16);
-    const uint4 m0 = *reinterpret_cast<const uint4 *>(hm32);
-    const uint4 m1 = *reinterpret_cast<const uint4 *>(hm32 + 16);
-    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+// with v_cvt_f32_ubyte<i>; the -4 folds into the sums of the group's two
+// 16-element halves of x.
+__device__ __forceinline__ float q3k_group_dot(const UnitW<LT_TYPE_Q3_K> &w, int u, const float4 *x4, float s0,
+                                               float s1) {
+    const int h = (u >> 2) & 1, j = u & 3;
+    const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    const uint32_t mw[8] = {w.m0.x, w.m0.y, w.m0.z, w.m0.w, w.m1.x, w.m1.y, w.m1.z, w.m1.w};
     const int qsh = 2 * j, msh = j + 4 * h;
+    const float d = f16_bits_to_f32((uint16_t)w.d);
     float total = 0.f;
 #pragma unroll
     for (int g = 0; g < 2; g++) {
         float acc = 0.f;
 #pragma unroll
         for (int w4 = 0; w4 < 4; w4++) {
-            const float4 xv = *reinterpret_cast<const float4 *>(x + 16 * g + 4 * w4);
+            const float4 xv = x4[4 * g + w4];
             const uint32_t c = ((qw[4 * g + w4] >> qsh) & 0x03030303u) | (((mw[4 * g + w4] >> msh) & 0x01010101u) << 2);
             acc += ubyte_f(c, 0) * xv.x;
             acc += ubyte_f(c, 1) * xv.y;
             acc += ubyte_f(c, 2) * xv.z;
             acc += ubyte_f(c, 3) * xv.w;
         }
-        total += (d * (float)(q3k_scale(sc, 8 * h + 2 * j + g) - 32)) * (acc - 4.f * x16[g]);
+        total += (d * (float)(q3k_scale(w.sc[0], w.sc[1], w.sc[2], 8 * h + 2 * j + g) - 32)) * (acc - 4.f * (g ? s1 : s0));
     }
     return total;
 }
 
-// Contribution of unit u of a row (block u, or Q3_K group u) against the
-// row's x (xs = element 0 of the row's columns, in LDS; xsum = sums of x over
-// kSumLen<T> elements, for the offsets the unsigned codes leave out).
+// Contribution of unit u of a row from its weight words and its x (the
+// offsets the unsigned codes leave out come back through the run sums).
 template <int T>
-__device__ __forceinline__ float unit_dot(const DevTensor &W, size_t row, int u, const float *xs, const float *xsum) {
-    const int nb = (int)W.blocks_per_row;
-    if (T == LT_TYPE_Q3_K) {
-        const size_t sb = row * nb + (u >> 3);
-        const uint32_t *s3 = reinterpret_cast<const uint32_t *>(W.p2 + sb * 12);
-        const uint32_t sc[3] = {s3[0], s3[1], s3[2]};
-        return q3k_group_dot(W.p0 + sb * 64, W.p1 + sb * 32, sc, f16_at(W.p3 + sb * 2), u & 7,
-                             xs + 256 * (u >> 3) + 32 * (u & 7), xsum + 2 * u);
+__device__ __forceinline__ float dot_unit(const UnitW<T> &w, int u, const float4 *x4, float s0, float s1) {
+    if constexpr (T == LT_TYPE_Q3_K) {
+        return q3k_group_dot(w, u, x4, s0, s1);
+    } else {
+        const float d = f16_bits_to_f32((uint16_t)w.dm);
+        if constexpr (T == LT_TYPE_IQ4_NL) return d * (iq4u_block_dot(w.q, x4) - 128.f * s0);  // table + 128
+        const float dot = q5u_block_dot(w.q, w.qh, x4);
+        if constexpr (T == LT_TYPE_Q5_0) return d * (dot - 16.f * s0);                   // codes - 16
+        return d * dot + f16_bits_to_f32((uint16_t)(w.dm >> 16)) * s0;                    // Q5_1: d q + m
     }
-    const size_t b = row * nb + u;
-    const uint4 qv = *reinterpret_cast<const uint4 *>(W.p0 + b * 16);
-    const float *xb = xs + 32 * u;
-    if (T == LT_TYPE_IQ4_NL)  // d * (sum (table + 128) x - 128 sum x)
-        return f16_at(W.p1 + b * 2) * (iq4u_block_dot(qv, xb) - 128.f * xsum[u]);
-    const uint32_t qh = *reinterpret_cast<const uint32_t *>(W.p1 + b * 4);
-    const float dot = q5u_block_dot(qv, qh, xb);
-    if (T == LT_TYPE_Q5_0) return f16_at(W.p2 + b * 2) * (dot - 16.f * xsum[u]);  // codes - 16
-    return f16_at(W.p2 + b * 4) * dot + f16_at(W.p2 + b * 4 + 2) * xsum[u];        // Q5_1: d q + m
 }
 
 template <int T>
@@ -204,10 +254,11 @@ __device__ __forceinline__ void stage(float *dst, const float *src, int n) {
     __syncthreads();
 }
 
-// Workgroup = kFmtWaves waves; a wave takes RPW rows at a time (64 / RPW
-// lanes per row, striding over the row's units) and walks the rows with a
+// Workgroup = kFmtWaves waves; a wave takes RPW groups of R rows at a time
+// (64 / RPW lanes per group, striding over the rows' units; each lane loads
+// a unit's x once and applies it to the R rows) and walks the rows with a
 // grid-wide stride, so x is staged in LDS once per workgroup.
-template <int T, int RPW>
+template <int T, int RPW, int R>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, const float *__restrict__ x,
                                                                float *__restrict__ y) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + their run sums
@@ -215,25 +266,41 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, cons
     stage<T>(xs, x, (int)W.cols);
     const float *xsum = xs + W.cols;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int r = lane / LPR, sub = lane % LPR;
+    const int grp = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
-    const size_t stride = (size_t)gridDim.x * kFmtWaves * RPW;
-    for (size_t row0 = ((size_t)blockIdx.x * kFmtWaves + wave) * RPW; row0 < W.total_rows; row0 += stride) {
-        const size_t row = row0 + r;
-        const bool live = row < W.total_rows;
-        float acc = 0.f;
-        if (live)
-            for (int u = sub; u < U; u += LPR) acc += unit_dot<T>(W, row, u, xs, xsum);
-        acc = seg_sum<LPR>(acc);
-        if (live && sub == 0) y[row] = acc;
+    const size_t n = W.total_rows;
+    const size_t stride = (size_t)gridDim.x * kFmtWaves * RPW * R;
+    for (size_t base = ((size_t)blockIdx.x * kFmtWaves + wave) * RPW * R; base < n; base += stride) {
+        const size_t row0 = base + (size_t)grp * R;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.f;
+        if (row0 < n) {
+            for (int u = sub; u < U; u += LPR) {
+                UnitW<T> w[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) w[r] = load_unit<T>(W, row0 + r < n ? row0 + r : n - 1, u);
+                float4 x4[8];
+                float s0, s1;
+                load_x<T>(xs, xsum, u, x4, s0, s1);
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[r] += dot_unit<T>(w[r], u, x4, s0, s1);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float v = seg_sum<LPR>(acc[r]);
+            if (sub == 0 && row0 + r < n) y[row0 + r] = v;
+        }
     }
 }
 
 // Expert-indexed gate/up (ops/moe.zig:55-73): slot s = blockIdx.y, expert
 // e = ids[s]; row pair j = (gate row e 2F + j, up row e 2F + F + j);
-// h[s][j] = act(gate . x) * (up . x), h[s][F, down_cols) = 0.  Waves walk
-// the row pairs of their slot with a stride of gridDim.x * kFmtWaves * RPW.
-template <int T, int RPW>
+// h[s][j] = act(gate . x) * (up . x), h[s][F, down_cols) = 0.  A lane group
+// takes R row pairs at a time (one x load per unit for 2 R rows); waves walk
+// the row pairs of their slot with a stride of gridDim.x * kFmtWaves * RPW * R.
+template <int T, int RPW, int R>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, const float *__restrict__ x,
                                                                   const uint32_t *__restrict__ ids, int F,
                                                                   int down_cols, uint32_t act, float *__restrict__ h) {
@@ -247,24 +314,40 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, c
     if (blockIdx.x == 0)
         for (int j = F + threadIdx.x; j < down_cols; j += blockDim.x) hs[j] = 0.f;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int r = lane / LPR, sub = lane % LPR;
+    const int grp = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
     const bool valid = e < (uint32_t)W.n_experts;
-    const int stride = gridDim.x * kFmtWaves * RPW;
-    for (int j0 = (blockIdx.x * kFmtWaves + wave) * RPW; j0 < F; j0 += stride) {
-        const int j = j0 + r;
-        const bool live = j < F;
-        float ag = 0.f, au = 0.f;
-        if (live && valid) {
-            const size_t g = (size_t)e * 2 * F + j, up = g + F;
+    const int stride = gridDim.x * kFmtWaves * RPW * R;
+    for (int base = (blockIdx.x * kFmtWaves + wave) * RPW * R; base < F; base += stride) {
+        const int j0 = base + grp * R;
+        float ag[R], au[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) ag[r] = au[r] = 0.f;
+        if (j0 < F && valid) {
+            const size_t g0 = (size_t)e * 2 * F;
             for (int u = sub; u < U; u += LPR) {
-                ag += unit_dot<T>(W, g, u, xs, xsum);
-                au += unit_dot<T>(W, up, u, xs, xsum);
+                UnitW<T> wg[R], wu[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const size_t j = (size_t)(j0 + r < F ? j0 + r : F - 1);
+                    wg[r] = load_unit<T>(W, g0 + j, u);
+                    wu[r] = load_unit<T>(W, g0 + F + j, u);
+                }
+                float4 x4[8];
+                float s0, s1;
+                load_x<T>(xs, xsum, u, x4, s0, s1);
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    ag[r] += dot_unit<T>(wg[r], u, x4, s0, s1);
+                    au[r] += dot_unit<T>(wu[r], u, x4, s0, s1);
+                }
             }
         }
-        ag = seg_sum<LPR>(ag);
-        au = seg_sum<LPR>(au);
-        if (live && sub == 0) hs[j] = valid ? act_apply(act, ag) * au : 0.f;  // invalid id: the slot adds zeros
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float g = seg_sum<LPR>(ag[r]), up = seg_sum<LPR>(au[r]);
+            if (sub == 0 && j0 + r < F) hs[j0 + r] = valid ? act_apply(act, g) * up : 0.f;  // invalid id: zeros
+        }
     }
 }
 
@@ -272,14 +355,15 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, c
 //   out[i] = base[i] + (accumulate ? out[i] : 0) + sum_s w'[s] (D_{ids[s]} row i) . h[s]
 // with w'[s] = dscale[ids[s]] * w[s] when a per-expert down scale is given
 // (gemma4/forward.zig:477).  h [k][down_cols] is staged in LDS once per
-// workgroup; waves walk the output rows.
+// workgroup; waves walk the output rows, and a row's lanes stride over its
+// k * units (slot, unit) pairs, so the slots' loads are in flight together.
 template <int T, int RPW>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W, const float *__restrict__ h,
                                                                     const uint32_t *__restrict__ ids,
                                                                     const float *__restrict__ wts, int k,
                                                                     const float *base, int accumulate,
                                                                     const float *dscale, float *out) {
-    extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats + their block sums
+    extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats + their run sums
     __shared__ uint32_t s_e[16];
     __shared__ float s_w[16];
     constexpr int LPR = kWave / RPW;
@@ -298,20 +382,27 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
     const int stride = gridDim.x * kFmtWaves * RPW;
     for (int i0 = (blockIdx.x * kFmtWaves + wave) * RPW; i0 < D; i0 += stride) {
         const int i = i0 + r;
-        const bool live = i < D;
         float acc = 0.f;
-        if (live) {
-            for (int s = 0; s < k; s++) {
+        if (i < D) {
+            int s = sub / U, u = sub % U;
+            while (s < k) {
                 const uint32_t e = s_e[s];
-                if (e >= (uint32_t)W.n_experts) continue;
-                float t = 0.f;
-                for (int u = sub; u < U; u += LPR)
-                    t += unit_dot<T>(W, (size_t)e * D + i, u, hsm + s * Kd, hsum + s * (Kd / kSumLen<T>));
-                acc += s_w[s] * t;
+                if (e < (uint32_t)W.n_experts) {
+                    const UnitW<T> w = load_unit<T>(W, (size_t)e * D + i, u);
+                    float4 x4[8];
+                    float s0, s1;
+                    load_x<T>(hsm + s * Kd, hsum + s * (Kd / kSumLen<T>), u, x4, s0, s1);
+                    acc += s_w[s] * dot_unit<T>(w, u, x4, s0, s1);
+                }
+                u += LPR;
+                while (u >= U) {
+                    u -= U;
+                    s++;
+                }
             }
         }
         acc = seg_sum<LPR>(acc);
-        if (live && sub == 0) {
+        if (i < D && sub == 0) {
             float v = accumulate ? out[i] + acc : acc;
             out[i] = base ? base[i] + v : v;
         }
@@ -333,30 +424,40 @@ hipError_t allow_lds(const void *fn, bool *set) {
     return e;
 }
 
+// Rows per lane group: x reuse against the weight registers a lane holds
+// (a Q3_K unit is 20 dwords, a block unit 6).
+template <int T>
+constexpr int kMvRows = T == LT_TYPE_Q3_K ? 2 : 4;
+template <int T>
+constexpr int kGuPairs = T == LT_TYPE_Q3_K ? 1 : 2;
+
 template <int T, int RPW>
 hipError_t launch_mv(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    constexpr int R = kMvRows<T>;
     static bool set[64] = {};
-    hipError_t e = allow_lds((const void *)k_matvec_fmt<T, RPW>, set);
+    hipError_t e = allow_lds((const void *)k_matvec_fmt<T, RPW, R>, set);
     if (e != hipSuccess) return e;
     // up to 8 workgroups per CU, each walking many rows
-    const size_t need = (W.total_rows + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    const size_t per = (size_t)kFmtWaves * RPW * R;
+    const size_t need = (W.total_rows + per - 1) / per;
     const dim3 grid((unsigned)(need < 2048 ? need : 2048));
-    hipLaunchKernelGGL((k_matvec_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), lds_floats<T>(W.cols) * sizeof(float), s,
-                       W, x, y);
+    hipLaunchKernelGGL((k_matvec_fmt<T, RPW, R>), grid, dim3(64 * kFmtWaves), lds_floats<T>(W.cols) * sizeof(float),
+                       s, W, x, y);
     return hipGetLastError();
 }
 
 template <int T, int RPW>
 hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, int k, int F, int down_cols,
                      uint32_t act, float *h, hipStream_t s) {
+    constexpr int R = kGuPairs<T>;
     static bool set[64] = {};
-    hipError_t e = allow_lds((const void *)k_expert_gu_fmt<T, RPW>, set);
+    hipError_t e = allow_lds((const void *)k_expert_gu_fmt<T, RPW, R>, set);
     if (e != hipSuccess) return e;
-    const int need = (F + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    const int per = kFmtWaves * RPW * R;
+    const int need = (F + per - 1) / per;
     const dim3 grid((unsigned)(need < 128 ? need : 128), (unsigned)k);  // up to 128 x k workgroups walk the rows
-    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW>), grid, dim3(64 * kFmtWaves), lds_floats<T>(W.cols) * sizeof(float),
-                       s, W, x, ids,
-                       F, down_cols, act, h);
+    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW, R>), grid, dim3(64 * kFmtWaves),
+                       lds_floats<T>(W.cols) * sizeof(float), s, W, x, ids, F, down_cols, act, h);
     return hipGetLastError();
 }
 
@@ -399,7 +500,8 @@ hipError_t launch_gu_t(const DevTensor &W, const float *x, const uint32_t *ids, 
 template <int T>
 hipError_t launch_dn_t(const DevTensor &W, const float *h, const uint32_t *ids, const float *w, int k,
                        const float *base, int accumulate, const float *dscale, float *out, hipStream_t s) {
-    switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
+    // a row's lanes share its k * units (slot, unit) pairs
+    switch (pick_rpw((size_t)k * (T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row))) {
     case 1: return launch_dn<T, 1>(W, h, ids, w, k, base, accumulate, dscale, out, s);
     case 2: return launch_dn<T, 2>(W, h, ids, w, k, base, accumulate, dscale, out, s);
     case 4: return launch_dn<T, 4>(W, h, ids, w, k, base, accumulate, dscale, out, s);
