@@ -136,6 +136,31 @@ __global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ 
     const int row = blockIdx.x;
     const int n = nb * 32;
     float raw_base = 0.0f;
+    // Decode with the prep and one block per thread: the block's operands
+    // (32 quants, d, x, raw_scale) are loaded before the RMS below, so their
+    // latency overlaps it; the products and sums are the same as in the loop.
+    const bool pre = pa.raw_scale && nb <= (int)blockDim.x;
+    const int b0 = threadIdx.x;
+    uint4 q4[2];
+    float xv[32], sv[32];
+    uint16_t d0 = 0;
+    if (pre && b0 < nb) {
+        const uint4 *qp = reinterpret_cast<const uint4 *>(qs + ((size_t)row * nb + b0) * 32);
+        q4[0] = qp[0];
+        q4[1] = qp[1];
+        d0 = dp[(size_t)row * nb + b0];
+        const float4 *xp = reinterpret_cast<const float4 *>(x + b0 * 32);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 v4 = xp[t];
+            xv[4 * t] = v4.x;
+            xv[4 * t + 1] = v4.y;
+            xv[4 * t + 2] = v4.z;
+            xv[4 * t + 3] = v4.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 32; e++) sv[e] = pa.raw_scale[b0 * 32 + e];
+    }
     if (pa.raw_scale) {
         __shared__ float red[3];
         // float4 loads, 8 in flight per thread (n is a multiple of 32)
@@ -159,7 +184,27 @@ __global__ void __launch_bounds__(128) k_router_q8_0(const int8_t *__restrict__ 
         for (int i = row * per + threadIdx.x; i < n && i < (row + 1) * per; i += blockDim.x)
             pa.moe_in[i] = (x[i] * r) * pa.weight[i];
     }
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+    if (pre && b0 < nb) {
+        const uint32_t qw[8] = {q4[0].x, q4[0].y, q4[0].z, q4[0].w, q4[1].x, q4[1].y, q4[1].z, q4[1].w};
+        float acc[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) acc[l] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                const int e = 8 * j + l;
+                const int qe = (int)(int8_t)(qw[e >> 2] >> (8 * (e & 3)));
+                const float vin = (xv[e] * raw_base) * sv[e];
+                float p = (float)qe * vin;
+                acc[l] = acc[l] + p;
+            }
+        float r = acc[0];
+#pragma unroll
+        for (int l = 1; l < 8; l++) r = r + acc[l];
+        term[b0] = r * f16_bits_to_f32(d0);
+    }
+    for (int b = pre ? nb : threadIdx.x; b < nb; b += blockDim.x) {
         const int8_t *q = qs + ((size_t)row * nb + b) * 32;
         const float *v = x + b * 32;
         const float d = f16_bits_to_f32(dp[(size_t)row * nb + b]);
