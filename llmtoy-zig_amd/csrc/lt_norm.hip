@@ -84,6 +84,24 @@ __global__ __launch_bounds__(kNormThreads) void k_norm(NormArgs p) {
     const size_t row = (size_t)blockIdx.x * n;
     const float *a = p.a + row;
     const float *b = p.b ? p.b + row : nullptr;
+    // kTail over rows of up to kPre * blockDim.x floats: the operands of the
+    // two later passes (dense, the two norm weights, x) are loaded now, so
+    // their latency overlaps the staging and the first reduction.
+    constexpr int kPre = 4;
+    const bool pre = OP == kTail && n <= kPre * (int)blockDim.x;
+    float tb[kPre], tw2[kPre], tx[kPre], tw[kPre];
+    if (pre) {
+#pragma unroll
+        for (int k = 0; k < kPre; k++) {
+            const int i = tid + k * (int)blockDim.x;
+            if (i < n) {
+                tb[k] = b[i];
+                tw2[k] = p.w2[i];
+                tx[k] = p.out[row + i];
+                tw[k] = p.w[i];
+            }
+        }
+    }
     for (int i = tid; i < n; i += blockDim.x) v[i] = OP == kAddRms ? a[i] + b[i] : a[i];
     __syncthreads();
     float r = rms_inv_of(row_sum_sq(v, n, p.precise, red), n, p.eps);
@@ -101,15 +119,34 @@ __global__ __launch_bounds__(kNormThreads) void k_norm(NormArgs p) {
             p.out2[row + i] = (v[i] * raw_base) * p.w2[i];
         }
     } else {  // kTail: v = moe
-        for (int i = tid; i < n; i += blockDim.x)
-            v[i] = b[i] + (v[i] * r) * p.w2[i];  // dense + rmsnorm(moe, w2)
+        if (pre) {
+#pragma unroll
+            for (int k = 0; k < kPre; k++) {
+                const int i = tid + k * (int)blockDim.x;
+                if (i < n) v[i] = tb[k] + (v[i] * r) * tw2[k];  // dense + rmsnorm(moe, w2)
+            }
+        } else {
+            for (int i = tid; i < n; i += blockDim.x) v[i] = b[i] + (v[i] * r) * p.w2[i];
+        }
         __syncthreads();
         r = rms_inv_of(row_sum_sq(v, n, p.precise, red), n, p.eps);
         float *x = p.out + row;
-        for (int i = tid; i < n; i += blockDim.x) {
-            float y = x[i] + (v[i] * r) * p.w[i];
-            if (p.scale != 1.0f) y = y * p.scale;
-            x[i] = y;
+        if (pre) {
+#pragma unroll
+            for (int k = 0; k < kPre; k++) {
+                const int i = tid + k * (int)blockDim.x;
+                if (i < n) {
+                    float y = tx[k] + (v[i] * r) * tw[k];
+                    if (p.scale != 1.0f) y = y * p.scale;
+                    x[i] = y;
+                }
+            }
+        } else {
+            for (int i = tid; i < n; i += blockDim.x) {
+                float y = x[i] + (v[i] * r) * p.w[i];
+                if (p.scale != 1.0f) y = y * p.scale;
+                x[i] = y;
+            }
         }
     }
 }
