@@ -409,7 +409,16 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
     }
 }
 
-int pick_rpw(size_t units) { return units >= 48 ? 1 : units >= 24 ? 2 : units >= 12 ? 4 : 8; }
+// Row groups per wave for rows of `units` work units.  A full-wave group
+// whose last pass leaves most lanes idle (88 units: 128 lane slots, 69%
+// busy) takes two 32-lane groups instead (96 slots, 92%).
+int pick_rpw(size_t units) {
+    if (units >= 48) {
+        const size_t slots64 = (units + 63) / 64 * 64, slots32 = (units + 31) / 32 * 32;
+        return units * 100 < slots64 * 85 && units * 100 >= slots32 * 85 ? 2 : 1;
+    }
+    return units >= 24 ? 2 : units >= 12 ? 4 : 8;
+}
 
 // Allow the largest staging (16384 floats and their 16-element run sums:
 // 68 KiB of dynamic LDS), once per kernel and device.
