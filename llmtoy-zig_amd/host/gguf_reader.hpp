@@ -61,6 +61,15 @@ class Exception : public std::runtime_error {
     Error kind;
 };
 
+// a * b for sizes taken from a file's metadata or tensor dims; a product
+// that does not fit in 64 bits (a corrupt or hostile header) is
+// Error::Truncated, since no file can hold that many bytes.
+inline size_t checkedMul(size_t a, size_t b, const std::string &what) {
+    size_t r;
+    if (__builtin_mul_overflow(a, b, &r)) throw Exception(Error::Truncated, "gguf: " + what + " overflows");
+    return r;
+}
+
 // A metadata value: the member named by type holds it (integers in i / u,
 // floats in f, arrays in arr with their element type in elem).
 struct MetaValue {
@@ -353,7 +362,7 @@ class GgufReader {
     // rows_per_expert, n_experts] as one RawMatrix of n_experts *
     // rows_per_expert rows.
     RawMatrix rawMatrix3D(const std::string &name, size_t n_experts, size_t rows_per_expert, size_t cols) const {
-        return rawMatrix(name, n_experts * rows_per_expert, cols);
+        return rawMatrix(name, checkedMul(n_experts, rows_per_expert, "expert rows of " + name), cols);
     }
 
     GgufData data;
@@ -415,18 +424,20 @@ inline MoeLayer moeLayer(const GgufReader &r, const MoeConfig &c, size_t layer) 
     L.d_expert = F;
     L.router = r.rawMatrix(p + "ffn_gate_inp.weight", E, d);
     if (r.data.find(p + "ffn_gate_up_exps.weight")) {
-        L.gate_up = r.rawMatrix3D(p + "ffn_gate_up_exps.weight", E, 2 * F, d);
+        L.gate_up = r.rawMatrix3D(p + "ffn_gate_up_exps.weight", E, checkedMul(2, F, "2 * d_expert"), d);
     } else {
         const RawMatrix g = r.rawMatrix3D(p + "ffn_gate_exps.weight", E, F, d);
         const RawMatrix u = r.rawMatrix3D(p + "ffn_up_exps.weight", E, F, d);
         if (g.type != u.type) throw Exception(Error::BadValueType, "gguf: gate and up experts differ in type");
-        const size_t eb = F * rowBytes(g.type, d);  // one expert's gate (or up) bytes
-        L.gate_up_copy.resize(2 * E * eb);
+        // one expert's gate (or up) bytes; both rawMatrix3D calls above have
+        // shown E * F rows fit in the file, the checks only guard the products
+        const size_t eb = checkedMul(F, rowBytes(g.type, d), "expert bytes");
+        L.gate_up_copy.resize(checkedMul(2, checkedMul(E, eb, "gate/up bytes"), "gate/up bytes"));
         for (size_t e = 0; e < E; e++) {
             std::memcpy(L.gate_up_copy.data() + 2 * e * eb, g.data + e * eb, eb);
             std::memcpy(L.gate_up_copy.data() + (2 * e + 1) * eb, u.data + e * eb, eb);
         }
-        L.gate_up = RawMatrix{L.gate_up_copy.data(), L.gate_up_copy.size(), g.type, E * 2 * F, d};
+        L.gate_up = RawMatrix{L.gate_up_copy.data(), L.gate_up_copy.size(), g.type, 2 * E * F, d};
     }
     const TensorInfo &dn = r.tensor(p + "ffn_down_exps.weight");
     L.down_cols = dn.dims.empty() ? F : (size_t)dn.dims[0];

@@ -29,7 +29,12 @@
  *                         pinned pieces (float64 restatement on small shapes).
  *                         NORM_TOPK and the router bias are BASELINE extensions with
  *                         no reference code: pinned by their closed form only.
- *   lto_moe_layer_shared  gemma4/forward.zig:392-397, 417, 463-479  composition.
+ *   lto_ffn_dense         model/forward.zig:301-308, gemma4/forward.zig:392-397  float64
+ *                         restatement on an independent Q8_0 decoder (SiLU and GELU-tanh,
+ *                         config-1 shape); planted mistakes (gate/up swapped, activation on
+ *                         up, the other activation) shown to fail it.
+ *   lto_moe_layer_shared  gemma4/forward.zig:392-397, 417, 463-479  composition; float64
+ *                         restatement of every term (shared FFN, Q8_0 router, experts).
  *   lto_moe_prefill       T x lto_moe_forward (main.zig:1916-1922 prefills per token).
  *   lto_dequant_q5_0, lto_dot_q5_0, lto_dequant_q5_1, lto_dequant_iq4_nl, lto_dot_iq4_nl,
  *   lto_q3k_scales, lto_dequant_q3_k

@@ -12,7 +12,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "build", "liblt_oracle.so")
+# LT_ORACLE_LIB selects another build of the same library (the sanitizer
+# build, oracle/build/asan/liblt_oracle.so)
+LIB_PATH = os.environ.get("LT_ORACLE_LIB") or os.path.join(HERE, "build", "liblt_oracle.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
 Q5_0, Q5_1, Q3_K, IQ4_NL = 6, 7, 11, 20

@@ -302,6 +302,68 @@ static void test_reader_file() {
     std::remove(empty.c_str());
 }
 
+// A hostile header: sizes whose products wrap around 64 bits must be
+// Error::Truncated, not a small allocation followed by a huge copy.
+// E = 1024 experts of d_expert = 2^54 rows (E * F = 2^64 wraps to 0), with
+// 1-element F32 gate and up tensors; then a fused gate_up tensor with
+// d_expert = 2^63 (2 * F wraps to 0).
+static std::string write_temp(const Buf &w) {
+    char tp[] = "/tmp/test_gguf_ovf_XXXXXX";
+    const int fd = mkstemp(tp);
+    if (fd < 0) return "";
+    close(fd);
+    FILE *fp = std::fopen(tp, "wb");
+    if (!fp) return "";
+    std::fwrite(w.b.data(), 1, w.b.size(), fp);
+    std::fclose(fp);
+    return tp;
+}
+
+static Buf overflow_file(uint64_t d_expert, bool fused) {
+    const uint64_t E = 1024;
+    Buf w;
+    w.put<uint32_t>(0x46554747u).put<uint32_t>(3).put<uint64_t>(fused ? 3 : 4).put<uint64_t>(4);
+    w.str("general.architecture").put<uint32_t>(8).str("qwen3moe");
+    w.str("qwen3moe.embedding_length").put<uint32_t>(10).put<uint64_t>(1);
+    w.str("qwen3moe.expert_count").put<uint32_t>(10).put<uint64_t>(E);
+    w.str("qwen3moe.expert_feed_forward_length").put<uint32_t>(10).put<uint64_t>(d_expert);
+    uint64_t off = 0;
+    auto tensor = [&](const char *name, std::vector<uint64_t> dims, uint64_t nbytes) {
+        w.str(name).put<uint32_t>((uint32_t)dims.size());
+        for (uint64_t d : dims) w.put<uint64_t>(d);
+        w.put<uint32_t>(0).put<uint64_t>(off);  // F32
+        off += (nbytes + 31) / 32 * 32;
+    };
+    tensor("blk.0.ffn_gate_inp.weight", {1, E}, 4 * E);
+    if (fused) {
+        tensor("blk.0.ffn_gate_up_exps.weight", {1}, 4);
+    } else {
+        tensor("blk.0.ffn_gate_exps.weight", {1}, 4);
+        tensor("blk.0.ffn_up_exps.weight", {1}, 4);
+    }
+    tensor("blk.0.ffn_down_exps.weight", {1}, 4);
+    w.pad_to(32);
+    w.b.insert(w.b.end(), off, 0);
+    return w;
+}
+
+static void test_moe_layer_size_overflow() {
+    for (int fused = 0; fused < 2; fused++) {
+        const std::string path = write_temp(overflow_file(fused ? (1ull << 63) : (1ull << 54), fused));
+        EXPECT(!path.empty());
+        bool threw = false;
+        try {
+            gguf::GgufReader r(path);
+            const gguf::MoeConfig c = gguf::moeConfig(r.data);
+            (void)gguf::moeLayer(r, c, 0);
+        } catch (const gguf::Exception &e) {
+            threw = e.kind == gguf::Error::Truncated;
+        }
+        std::remove(path.c_str());
+        EXPECT(threw);
+    }
+}
+
 // ------------------------------------------------------------------- dump
 static void dump_value(const gguf::MetaValue &v, std::string &o) {
     char tmp[64];
@@ -486,6 +548,7 @@ int main(int argc, char **argv) {
         {"parseBytes: bad value type and oversized counts", test_bad_value_type_and_huge_counts},
         {"TensorInfo.byteSize: block layouts", test_byte_size_table},
         {"GgufReader: tensorBytes, rawMatrix3D, EmptyFile", test_reader_file},
+        {"moeLayer: wrapping size products are Truncated", test_moe_layer_size_overflow},
     };
     const std::string mode = argc > 1 ? argv[1] : "";
     try {

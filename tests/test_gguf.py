@@ -15,7 +15,8 @@ import llmtoy_amd as lt
 from llmtoy_amd import ggml, gguf, synth
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-CPP = os.path.join(ROOT, "tests", "cpp", "build", "test_gguf")
+# LT_TEST_GGUF_BIN: another build of the same test (the sanitizer build)
+CPP = os.environ.get("LT_TEST_GGUF_BIN") or os.path.join(ROOT, "tests", "cpp", "build", "test_gguf")
 
 
 def s(x: str) -> bytes:
@@ -191,7 +192,7 @@ def test_cpp_reader_tests_pass():
     out = subprocess.run([CPP, "--cpu"], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0 and "ALL PASSED" in out.stdout, out.stdout + out.stderr
     names = subprocess.run([CPP, "--list"], capture_output=True, text=True, timeout=60).stdout.splitlines()
-    assert "parseBytes: synthetic GGUF v3" in names and len(names) == 8
+    assert "parseBytes: synthetic GGUF v3" in names and len(names) == 9
 
 
 @pytest.mark.parametrize("version", [1, 3])

@@ -475,30 +475,96 @@ def test_moe_forward_thread_invariant():
             assert np.array_equal(orc.moe_forward(w, x, 4, pool=p)[0], ref)
 
 
+def q8_0_decode_np(mat: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Independent Q8_0 decoder (ggml block layout: f16 d, then 32 int8 q;
+    value = d * q), float64, [rows, cols]."""
+    blk = mat.reshape(rows, cols // 32, 34)
+    d = blk[..., 0:2].copy().view(np.float16).astype(np.float64)
+    return (blk[..., 2:].view(np.int8).astype(np.float64) * d).reshape(rows, cols)
+
+
+def _act_f64(act, g):
+    if act == orc.ACT_SILU:
+        return g / (1 + np.exp(-g))
+    return 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3)))
+
+
+def _ffn_dense_f64(wg, wu, wd, x, d_model, d_ffn, act, act_on_up=False):
+    """float64 restatement of the dense gated FFN: h = act(Wg x) * (Wu x),
+    out = Wd h (model/forward.zig:304-307 with SiLU; gemma4/forward.zig:
+    392-397 with GELU-tanh).  act_on_up plants a mistake for the teeth test."""
+    g = q8_0_decode_np(wg, d_ffn, d_model) @ x.astype(np.float64)
+    u = q8_0_decode_np(wu, d_ffn, d_model) @ x.astype(np.float64)
+    h = g * _act_f64(act, u) if act_on_up else _act_f64(act, g) * u
+    return q8_0_decode_np(wd, d_model, d_ffn) @ h
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("act", [orc.ACT_SILU, orc.ACT_GELU_TANH])
+@pytest.mark.parametrize("shape", [(896, 4864), (512, 320)])
+def test_ffn_dense_vs_float64(act, shape, pool):
+    # lto_ffn_dense against the float64 restatement on the independent Q8_0
+    # decoder; (896, 4864) is config 1's Qwen2.5-0.5B shape.
+    d_model, d_ffn = shape
+    g = synth.stream(95, d_ffn)
+    wg, wu = synth.q8_0_matrix(g, d_ffn, d_model), synth.q8_0_matrix(g, d_ffn, d_model)
+    wd = synth.q8_0_matrix(g, d_model, d_ffn)
+    x = synth.normal(g, (d_model,))
+    got = orc.ffn_dense(wg, wu, wd, orc.Q8_0, x, d_model, d_ffn, act=act, pool=pool)
+    assert _rel(got, _ffn_dense_f64(wg, wu, wd, x, d_model, d_ffn, act)) < 1e-5
+
+
+def test_ffn_dense_f64_check_has_teeth(pool):
+    # Each plausible misreading of model/forward.zig:304-307 must fail the
+    # 1e-5 check above by a wide margin (> 1e-3): gate and up swapped, the
+    # activation applied to up, and GELU-tanh where SiLU is asked for (or the
+    # reverse; the two differ least, ~5e-3 on these inputs).
+    d_model, d_ffn = 512, 320
+    g = synth.stream(96, 1)
+    wg, wu = synth.q8_0_matrix(g, d_ffn, d_model), synth.q8_0_matrix(g, d_ffn, d_model)
+    wd = synth.q8_0_matrix(g, d_model, d_ffn)
+    x = synth.normal(g, (d_model,))
+    for act, other in ((orc.ACT_SILU, orc.ACT_GELU_TANH), (orc.ACT_GELU_TANH, orc.ACT_SILU)):
+        want = _ffn_dense_f64(wg, wu, wd, x, d_model, d_ffn, act)
+        swapped = orc.ffn_dense(wu, wg, wd, orc.Q8_0, x, d_model, d_ffn, act=act, pool=pool)
+        assert _rel(swapped, want) > 1e-3
+        right = orc.ffn_dense(wg, wu, wd, orc.Q8_0, x, d_model, d_ffn, act=act, pool=pool)
+        act_on_up = _ffn_dense_f64(wg, wu, wd, x, d_model, d_ffn, act, act_on_up=True)
+        assert _rel(right, act_on_up) > 1e-3
+        wrong_act = orc.ffn_dense(wg, wu, wd, orc.Q8_0, x, d_model, d_ffn, act=other, pool=pool)
+        assert _rel(wrong_act, want) > 1e-3
+
+
 def test_moe_layer_shared_composition(pool):
     # Config-4 layer = shared dense FFN + routerTopKSoftmax(Q8_0) + expert loop
+    # (gemma4/forward.zig:392-398, 417, 463-479), every term from float64
+    # restatements on the independent decoders.
     w = synth.moe_weights(93, 512, 8, 192, down_cols=256, router_type=ggml.Q8_0)
     x = synth.normal(synth.stream(93, 7), (512,))
     shg = synth.q8_0_matrix(synth.stream(93, 20), 320, 512)
     shu = synth.q8_0_matrix(synth.stream(93, 21), 320, 512)
     shd = synth.q8_0_matrix(synth.stream(93, 22), 512, 320)
     out, ids, wt = orc.moe_layer_shared(w, x, 2, shg, shu, shd, 320, pool=pool)
-    shared = orc.ffn_dense(shg, shu, shd, orc.Q8_0, x, 512, 320, act=orc.ACT_GELU_TANH, pool=pool)
-    logits = orc.quant_matvec(w.router, orc.Q8_0, x, 8, 512)
-    ref_ids, probs = orc.softmax_topk(logits, 2)
-    assert ids.tolist() == ref_ids.tolist()
-    assert np.allclose(wt, probs[ref_ids], rtol=1e-6)
+    shared = _ffn_dense_f64(shg, shu, shd, x, 512, 320, orc.ACT_GELU_TANH)
+    logits = q8_0_decode_np(w.router, 8, 512) @ x.astype(np.float64)
+    p = np.exp(logits - logits.max())
+    p /= p.sum()
+    order = sorted(range(8), key=lambda e: (-p[e], e))[:2]
+    assert ids.tolist() == order
+    assert np.allclose(wt, p[order], rtol=1e-5)
     gu = q4k_decode_np(w.gate_up).reshape(8, 384, 512).astype(np.float64)
     dn = q4k_decode_np(w.down).reshape(8, 512, 256).astype(np.float64)
     moe = np.zeros(512)
-    for e, we in zip(ids, wt):
+    for e, we in zip(order, p[order]):
         g, u = gu[e, :192] @ x, gu[e, 192:] @ x
-        a = 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3)))
         h = np.zeros(256)
-        h[:192] = a * u
-        moe += float(we) * (dn[e] @ h)
-    want = shared.astype(np.float64) + moe
-    assert np.linalg.norm(out - want) / np.linalg.norm(want) < 1e-5
+        h[:192] = _act_f64(orc.ACT_GELU_TANH, g) * u
+        moe += we * (dn[e] @ h)
+    want = shared + moe
+    assert _rel(out, want) < 1e-5
 
 
 def test_moe_prefill_is_per_token(pool):
