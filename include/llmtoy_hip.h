@@ -12,6 +12,22 @@
  * Without LT_HOST_IO a call returns once the work is enqueued on the
  * context's stream (lt_sync waits for it).
  *
+ * Graph capture.  Calls with device pointers (no LT_HOST_IO) may be captured
+ * into a HIP graph on the context's stream (lt_stream).  Make one call with
+ * the same shapes before capturing: the first call sizes the context's
+ * scratch, and the first single-launch MoE call runs a one-time device probe
+ * that cannot be captured (such a call returns LT_ERR_INVALID).  Scratch is
+ * never freed before lt_destroy -- a later call with larger shapes gets new
+ * buffers and retires the old ones -- so a captured graph stays valid for the
+ * life of the context.  Replays of a graph and direct calls share scratch, so
+ * they must not run concurrently (use the context's stream).
+ *
+ * Errors found on the device.  The single-launch MoE kernel bounds each of
+ * its waits (200 ms); a wait that runs out makes that call's outputs NaN and
+ * sets an error word.  A device-pointer call returns before that is known:
+ * the next lt_sync (or LT_HOST_IO call) returns LT_ERR_DEVICE and clears it.
+ * Callers that use device pointers should check lt_sync.
+ *
  * Reference citations are paths in the llmtoy-zig tree.
  */
 #ifndef LLMTOY_HIP_H

@@ -33,6 +33,9 @@ struct lt_ctx {
     std::string err;
     // context-owned device scratch, grown on demand
     DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh, pf, nrm;
+    // buffers replaced by larger ones; a HIP graph captured earlier may still
+    // reference them, so they are released only by lt_destroy
+    std::vector<void *> retired;
     // arrival ticket of the router's last-block top-k; zeroed once at init,
     // every launch leaves it at zero again
     unsigned *ticket = nullptr;
@@ -69,19 +72,35 @@ int hip_fail(lt_ctx *ctx, hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
     } while (0)
 
+// Context scratch of at least `bytes`.  A buffer is never freed before
+// lt_destroy: a call captured into a HIP graph keeps the scratch addresses
+// it was captured with, so a larger call later gets a new buffer and the old
+// one is retired (kept allocated).  Capacities at least double, which bounds
+// the retired bytes by the final capacity.
 int ensure(lt_ctx *ctx, DevBuf &b, size_t bytes) {
     if (bytes == 0) bytes = 256;
     if (b.cap >= bytes) return LT_OK;
-    if (b.p) {
-        LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        LT_HIP(ctx, hipFree(b.p));
-        b.p = nullptr;
-        b.cap = 0;
-    }
     size_t cap = (bytes + 4095) & ~(size_t)4095;
-    LT_HIP(ctx, hipMalloc(&b.p, cap));
+    if (cap < 2 * b.cap) cap = 2 * b.cap;
+    if (b.p) {
+        try {
+            ctx->retired.reserve(ctx->retired.size() + 1);  // so that push_back below cannot throw
+        } catch (...) {
+            return fail(ctx, LT_ERR_OOM, "host allocation failed");
+        }
+    }
+    void *p = nullptr;
+    LT_HIP(ctx, hipMalloc(&p, cap));
+    if (b.p) ctx->retired.push_back(b.p);
+    b.p = p;
     b.cap = cap;
     return LT_OK;
+}
+
+// True while the context's stream is being captured into a graph.
+bool capturing(lt_ctx *ctx) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(ctx->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
 size_t block_elems(uint32_t type) {
@@ -167,6 +186,11 @@ int launch_rc(lt_ctx *ctx, hipError_t e, const char *what) {
 // Allocates and zeroes the fused kernel's hand-over memory (once).
 int ensure_fused(lt_ctx *ctx) {
     if (ctx->fused) return LT_OK;
+    // the one-time set-up synchronises the stream (XCD placement probe)
+    if (capturing(ctx))
+        return fail(ctx, LT_ERR_INVALID,
+                    "the first single-launch MoE call on a context cannot be captured into a graph: make one call "
+                    "before capturing");
     const size_t n_cnt = (size_t)lt::kFusedBlocks * 4;
     const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128 * 8;
     const size_t n_hl = (size_t)lt::kFusedBlocks * 128;
@@ -211,8 +235,12 @@ int ensure_fused(lt_ctx *ctx) {
 int check_fused_err(lt_ctx *ctx) {
     if (!ctx->fused_err) return LT_OK;
     const uint32_t v = __atomic_exchange_n(ctx->fused_err, 0u, __ATOMIC_SEQ_CST);
-    if (v) return fail(ctx, LT_ERR_DEVICE, "fused MoE kernel: a hand-over wait timed out (code %u)", v);
-    return LT_OK;
+    if (!v) return LT_OK;
+    // Later launches publish h through memory (agent scope) instead of an
+    // XCD's L2, in case the placement the one-time probe saw has changed.
+    ctx->fsc.xcd_local = 0;
+    return fail(ctx, LT_ERR_DEVICE, "fused MoE kernel: a hand-over wait timed out (code %u); outputs of that call are NaN",
+                v);
 }
 
 int matvec_dev(lt_ctx *ctx, const DevTensor &W, const float *x, float *y) {
@@ -277,6 +305,7 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
                       &ctx->nrm};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
+    for (void *p : ctx->retired) (void)hipFree(p);
     if (ctx->ticket) (void)hipFree(ctx->ticket);
     if (ctx->fused) (void)hipFree(ctx->fused);
     if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);

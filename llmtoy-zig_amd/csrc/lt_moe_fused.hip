@@ -20,8 +20,12 @@
 //   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
 //
 // (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = NCg = ceil(D /
-// 64)).  The placement only affects speed: every hand-over below is coherent
-// across XCDs.
+// 64)).  Every hand-over is coherent across XCDs except the h records when
+// local is set: those are workgroup-scope stores that only the writer's L2
+// holds, correct only while the round-robin placement holds (probed once per
+// context by probe_xcd_groups).  Were it to change, the down blocks' bounded
+// waits would time out (NaN outputs, the error word set); the host then
+// reports LT_ERR_DEVICE at the next synchronising call and clears local.
 //
 // Combine.  By default the down blocks add their slot's weighted rows
 // straight into out with float atomics (agent scope): the router blocks

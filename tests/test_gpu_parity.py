@@ -441,6 +441,55 @@ def test_gpu_graph_replay_matches_eager(ctx, cfg3):
         a.free()
 
 
+def test_gpu_graph_survives_scratch_growth():
+    # A graph captured with small shapes stays valid after a larger call grows
+    # the context's scratch: the old buffers are retired, never freed before
+    # lt_destroy (the three-launch path uses the h, logits, ids and weight
+    # scratch).  Fresh context, so its scratch starts at the small shapes.
+    from llmtoy_amd.hip import DeviceArray, Graph
+    small = synth.moe_weights(31, 512, 16, 256)
+    big = synth.moe_weights(32, 2048, 32, 768)
+    xs = synth.normal(synth.stream(31, 7), (512,))
+    xb = synth.normal(synth.stream(32, 7), (2048,))
+    with lt.Context(0) as c2:
+        ts, tb = lt.upload_moe(c2, small), lt.upload_moe(c2, big)
+        eager = np.zeros(512, np.float32)
+        c2.moe_forward(eager, xs, *ts, 2, 256, unfused=True)  # sizes the scratch for the small shape
+        xd, od = DeviceArray.from_numpy(xs), DeviceArray((512,), np.float32)
+        g = Graph(c2.stream, lambda: c2.moe_forward(od, xd, *ts, 2, 256, unfused=True))
+        ob = np.zeros(2048, np.float32)
+        c2.moe_forward(ob, xb, *tb, 8, 768, unfused=True)  # grows h (2 x 256 -> 8 x 768 floats) and more
+        for _ in range(2):
+            g.launch()
+            c2.sync()
+            assert np.array_equal(od.numpy().view(np.uint32), eager.view(np.uint32))
+        g.destroy()
+        for a in (xd, od):
+            a.free()
+        for t in ts + tb:
+            t.free()
+
+
+def test_gpu_first_fused_call_not_capturable(cfg3):
+    # the single-launch kernel's one-time set-up synchronises the stream, so
+    # a context's first such call under capture is refused, not broken
+    from llmtoy_amd.hip import DeviceArray, Graph
+    c, _ = cfg3
+    w = c["weights"]
+    with lt.Context(0) as c2:
+        tens = lt.upload_moe(c2, w)
+        xd, od = DeviceArray.from_numpy(c["x"]), DeviceArray((w.d_model,), np.float32)
+        with pytest.raises(InvalidError, match="cannot be captured"):
+            Graph(c2.stream, lambda: c2.moe_forward(od, xd, *tens, 8, w.d_expert, norm_topk=True))
+        o = np.zeros(w.d_model, np.float32)
+        c2.moe_forward(o, c["x"], *tens, 8, w.d_expert, norm_topk=True)  # the context still works
+        assert np.isfinite(o).all()
+        for a in (xd, od):
+            a.free()
+        for t in tens:
+            t.free()
+
+
 def test_gpu_errors(ctx):
     with pytest.raises(UnsupportedError):
         ctx.upload(np.zeros(64, np.uint8), ggml.F16, 1, 32)
