@@ -190,6 +190,23 @@ int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_tensor *rou
                    const lt_tensor *sh_up, const lt_tensor *sh_down, uint32_t k, uint32_t d_expert, uint32_t act,
                    uint32_t flags, uint32_t *out_ids, float *out_w);
 
+/* lt_moe_forward without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, serving loops that forbid hipMalloc.  Same
+ * arguments and results as lt_moe_forward, on the single-launch kernel only:
+ * F32 router, Q4_K gate_up and down, d_model 256..2048 (a multiple of 256),
+ * down K <= 1024, <= 256 experts, k <= 16, no shared FFN (sh_* must be NULL),
+ * device pointers only (flags: LT_MOE_NORM_TOPK, LT_MOE_ACCUMULATE,
+ * LT_MOE_DETERMINISTIC); any other shape, type or flag returns
+ * LT_ERR_UNSUPPORTED or LT_ERR_INVALID.  Its scratch is the library's static
+ * device array of 729,600 bytes per GPU (held until the process ends, set up
+ * by lt_init): all calls on one GPU share it, so calls that overlap on one
+ * GPU (several streams or contexts at once) race. */
+int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, const lt_tensor *router,
+                           const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down,
+                           const lt_tensor *sh_gate, const lt_tensor *sh_up, const lt_tensor *sh_down, uint32_t k,
+                           uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);
+
 /* Batched prefill of one MoE layer over T tokens (X, out: [T, d_model]):
  * per-token routing as lt_moe_router_topk, tokens sorted per expert, grouped
  * expert GEMM with bf16 MFMA (fp32 accumulation) over Q4_K weights

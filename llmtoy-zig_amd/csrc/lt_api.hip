@@ -39,11 +39,19 @@ struct lt_ctx {
     // arrival ticket of the router's last-block top-k; zeroed once at init,
     // every launch leaves it at zero again
     unsigned *ticket = nullptr;
-    // hand-over memory of the fused MoE kernel (allocated on first use) and
-    // its host-mapped error word
+    // hand-over memory of the fused MoE kernel (allocated on first use); the
+    // host-mapped error word it reports timed-out waits in (set up by
+    // lt_init, with err_dev its device address); whether blocks with equal
+    // index % 8 share an XCD (probed by lt_init)
     void *fused = nullptr;
     uint32_t *fused_err = nullptr;
+    uint32_t *err_dev = nullptr;
+    int xcd_local = 0;
     lt::FusedScratch fsc{};
+    // the library's static scratch on this device (lt_noalloc.hip), used by
+    // lt_moe_forward_noalloc
+    uint8_t *na_base = nullptr;
+    lt::FusedScratch na_fsc{};
     // pinned + device staging of tensor uploads and read-backs (allocated on first use)
     lt::UploadStaging up{};
 };
@@ -186,48 +194,44 @@ int launch_rc(lt_ctx *ctx, hipError_t e, const char *what) {
 // Allocates and zeroes the fused kernel's hand-over memory (once).
 int ensure_fused(lt_ctx *ctx) {
     if (ctx->fused) return LT_OK;
-    // the one-time set-up synchronises the stream (XCD placement probe)
+    // the one-time set-up clears the memory with a synchronous memset
     if (capturing(ctx))
         return fail(ctx, LT_ERR_INVALID,
                     "the first single-launch MoE call on a context cannot be captured into a graph: make one call "
                     "before capturing");
-    const size_t n_cnt = (size_t)lt::kFusedBlocks * 4;
-    const size_t n_lg = (size_t)lt::kFusedMaxRouterBlocks * 128 * 8;
-    const size_t n_hl = (size_t)lt::kFusedBlocks * 128;
-    const size_t n_pl = (size_t)lt::kFusedBlocks * 4 * 128;
-    const size_t n_xcc = (size_t)lt::kFusedBlocks * 4;
-    const size_t bytes = n_cnt + n_lg + n_hl + n_pl + n_xcc;
     void *p = nullptr;
-    LT_HIP(ctx, hipMalloc(&p, bytes));
-    hipError_t e = hipMemset(p, 0, bytes);
-    void *hp = nullptr;
-    if (e == hipSuccess) e = hipHostMalloc(&hp, 64, hipHostMallocMapped);
-    void *dp = nullptr;
-    if (e == hipSuccess) {
-        memset(hp, 0, 64);
-        e = hipHostGetDevicePointer(&dp, hp, 0);
-    }
-    uint8_t *b = (uint8_t *)p;
-    // same-XCD hand-overs through L2 when the placement allows;
-    // LT_FUSED_AGENT_HANDOVER=1 forces the memory round trip (testing)
-    int local = 0;
-    if (e == hipSuccess) e = lt::probe_xcd_groups((uint32_t *)(b + n_cnt + n_lg + n_hl + n_pl), ctx->stream, &local);
-    const char *agent = getenv("LT_FUSED_AGENT_HANDOVER");
-    if (agent && agent[0] == '1') local = 0;
+    LT_HIP(ctx, hipMalloc(&p, lt::kFusedScratchBytes));
+    const hipError_t e = hipMemset(p, 0, lt::kFusedScratchBytes);
     if (e != hipSuccess) {
         (void)hipFree(p);
-        if (hp) (void)hipHostFree(hp);
         return hip_fail(ctx, e, "fused scratch");
     }
     ctx->fused = p;
-    ctx->fused_err = (uint32_t *)hp;
-    ctx->fsc.counters = (uint32_t *)b;
-    ctx->fsc.lg = (uint64_t *)(b + n_cnt);
-    ctx->fsc.hl = (uint64_t *)(b + n_cnt + n_lg);
-    ctx->fsc.pl = (uint64_t *)(b + n_cnt + n_lg + n_hl);
-    ctx->fsc.err = (uint32_t *)dp;
-    ctx->fsc.xcd_local = local;
+    ctx->fsc = lt::fused_scratch_at((uint8_t *)p, ctx->err_dev, ctx->xcd_local);
     return LT_OK;
+}
+
+// lt_init's device set-up: the host-mapped error word, the address of this
+// device's static scratch, and the XCD placement probe (run once, into the
+// static scratch's probe area).  LT_FUSED_AGENT_HANDOVER=1 turns the same-XCD
+// hand-over off (testing).
+hipError_t init_device_state(lt_ctx *ctx) {
+    void *hp = nullptr, *dp = nullptr;
+    hipError_t e = hipHostMalloc(&hp, 64, hipHostMallocMapped);
+    if (e != hipSuccess) return e;
+    memset(hp, 0, 64);
+    ctx->fused_err = (uint32_t *)hp;
+    if ((e = hipHostGetDevicePointer(&dp, hp, 0)) != hipSuccess) return e;
+    ctx->err_dev = (uint32_t *)dp;
+    if ((e = lt::noalloc_scratch(ctx->device, &ctx->na_base)) != hipSuccess) return e;
+    int local = 0;
+    if ((e = lt::probe_xcd_groups((uint32_t *)(ctx->na_base + lt::kFusedXccOff), ctx->stream, &local)) != hipSuccess)
+        return e;
+    const char *agent = getenv("LT_FUSED_AGENT_HANDOVER");
+    if (agent && agent[0] == '1') local = 0;
+    ctx->xcd_local = local;
+    ctx->na_fsc = lt::fused_scratch_at(ctx->na_base, ctx->err_dev, local);
+    return hipSuccess;
 }
 
 // A fused-kernel wait that ran into its time limit (the outputs of that
@@ -238,7 +242,7 @@ int check_fused_err(lt_ctx *ctx) {
     if (!v) return LT_OK;
     // Later launches publish h through memory (agent scope) instead of an
     // XCD's L2, in case the placement the one-time probe saw has changed.
-    ctx->fsc.xcd_local = 0;
+    ctx->xcd_local = ctx->fsc.xcd_local = ctx->na_fsc.xcd_local = 0;
     return fail(ctx, LT_ERR_DEVICE, "fused MoE kernel: a hand-over wait timed out (code %u); outputs of that call are NaN",
                 v);
 }
@@ -286,8 +290,10 @@ extern "C" int lt_init(int device, lt_ctx **out_ctx) {
     }
     hipError_t e = hipMalloc((void **)&ctx->ticket, 256);
     if (e == hipSuccess) e = hipMemset(ctx->ticket, 0, 256);
+    if (e == hipSuccess) e = init_device_state(ctx);
     if (e != hipSuccess) {
         if (ctx->ticket) (void)hipFree(ctx->ticket);
+        if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return e == hipErrorOutOfMemory ? LT_ERR_OOM : LT_ERR_DEVICE;
@@ -779,6 +785,51 @@ extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
         return check_fused_err(ctx);
     }
+    return LT_OK;
+}
+
+extern "C" int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, const lt_tensor *router,
+                                      const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down,
+                                      const lt_tensor *sh_gate, const lt_tensor *sh_up, const lt_tensor *sh_down,
+                                      uint32_t k, uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids,
+                                      float *out_w) {
+    if (!ctx || !out || !x) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (act > LT_ACT_GELU_TANH) return fail(ctx, LT_ERR_INVALID, "unknown activation %u", act);
+    if (!router || !gate_up || !down) return fail(ctx, LT_ERR_INVALID, "null tensor");
+    if (flags & ~(uint32_t)(LT_MOE_NORM_TOPK | LT_MOE_ACCUMULATE | LT_MOE_DETERMINISTIC))
+        return fail(ctx, LT_ERR_INVALID,
+                    "allocation-free MoE: flags 0x%x not allowed (device pointers only: no LT_HOST_IO; no "
+                    "LT_MOE_UNFUSED)",
+                    flags & ~(uint32_t)(LT_MOE_NORM_TOPK | LT_MOE_ACCUMULATE | LT_MOE_DETERMINISTIC));
+    if (sh_gate || sh_up || sh_down)
+        return fail(ctx, LT_ERR_UNSUPPORTED, "allocation-free MoE: no shared FFN (it needs context scratch)");
+    const size_t d_model = gate_up->t.cols;
+    int rc;
+    if ((rc = check_router(ctx, router, d_model, k))) return rc;
+    if ((rc = check_experts(ctx, gate_up, down, d_model, d_expert, router->t.total_rows, k))) return rc;
+    if (!aligned16(x)) return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
+    const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
+    if (R.type != LT_TYPE_F32 || GU.type != LT_TYPE_Q4_K || D.type != LT_TYPE_Q4_K)
+        return fail(ctx, LT_ERR_UNSUPPORTED,
+                    "allocation-free MoE: single-launch kernel only (F32 router, Q4_K gate_up and down)");
+    const lt::FusedPlan pl = lt::plan_moe_fused((int)R.total_rows, (int)GU.cols, (int)d_expert, (int)D.cols, (int)k);
+    if (!pl.ok)
+        return fail(ctx, LT_ERR_UNSUPPORTED,
+                    "allocation-free MoE: shape beyond the static scratch's kernel (d_model %zu, %zu experts, "
+                    "d_expert %u, down K %zu, k %u; limits: d_model 256..2048 in steps of 256, down K <= 1024, "
+                    "<= 256 experts, k <= 16)",
+                    GU.cols, R.total_rows, d_expert, D.cols, k);
+    uint32_t *ids_dev = (uint32_t *)(ctx->na_base + lt::kFusedIdsOff);
+    float *w_dev = (float *)(ctx->na_base + lt::kFusedWOff);
+    rc = launch_rc(ctx,
+                   lt::launch_moe_fused(pl, R, router_bias, GU, D, x, (int)k, (int)d_expert, act,
+                                        (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, nullptr,
+                                        (flags & LT_MOE_ACCUMULATE) ? 1 : 0, (flags & LT_MOE_DETERMINISTIC) ? 1 : 0,
+                                        out, ids_dev, w_dev, ctx->na_fsc, ctx->stream),
+                   "moe_fused (allocation-free)");
+    if (rc) return rc;
+    if (out_ids) LT_HIP(ctx, hipMemcpyAsync(out_ids, ids_dev, k * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    if (out_w) LT_HIP(ctx, hipMemcpyAsync(out_w, w_dev, k * 4, hipMemcpyDeviceToDevice, ctx->stream));
     return LT_OK;
 }
 

@@ -336,6 +336,33 @@ struct FusedScratch {
     uint32_t *err;       // host-mapped error word (device address)
     int xcd_local;       // blocks with equal index % 8 share an XCD (probe_xcd_groups)
 };
+// Byte layout of that hand-over memory (a context's own allocation, or the
+// library's static scratch in lt_noalloc.hip): launch counters, 8 logit
+// copies, h record lines, partial-output lines, the XCD probe's ids, and
+// the routing outputs (ids, weights) of the allocation-free entry point.
+constexpr size_t kFusedCntOff = 0;
+constexpr size_t kFusedLgOff = kFusedCntOff + (size_t)kFusedBlocks * 4;
+constexpr size_t kFusedHlOff = kFusedLgOff + (size_t)8 * kLgCopy * 8;
+constexpr size_t kFusedPlOff = kFusedHlOff + (size_t)kFusedBlocks * 16 * 8;
+constexpr size_t kFusedXccOff = kFusedPlOff + (size_t)kFusedBlocks * 4 * 16 * 8;
+constexpr size_t kFusedIdsOff = kFusedXccOff + (size_t)kFusedBlocks * 4;
+constexpr size_t kFusedWOff = kFusedIdsOff + 256;
+constexpr size_t kFusedScratchBytes = kFusedWOff + 256;  // 729,600 B
+// counters, lg, hl, pl at base; err and xcd_local are the caller's
+inline FusedScratch fused_scratch_at(uint8_t *base, uint32_t *err, int xcd_local) {
+    FusedScratch s;
+    s.counters = reinterpret_cast<uint32_t *>(base + kFusedCntOff);
+    s.lg = reinterpret_cast<uint64_t *>(base + kFusedLgOff);
+    s.hl = reinterpret_cast<uint64_t *>(base + kFusedHlOff);
+    s.pl = reinterpret_cast<uint64_t *>(base + kFusedPlOff);
+    s.err = err;
+    s.xcd_local = xcd_local;
+    return s;
+}
+// Device address of this GPU's copy of the static scratch of lt_noalloc.hip
+// (kFusedScratchBytes, zero when the library loads); `device` must be the
+// current device.  The address is looked up once per device and kept.
+hipError_t noalloc_scratch(int device, uint8_t **base);
 // Launches kFusedBlocks one-wave blocks that record their XCD in dev_ids
 // [kFusedBlocks], waits, and sets *local when every block b ran on the XCD
 // of block b % 8 (the round-robin placement the fused kernel's same-XCD

@@ -68,7 +68,7 @@ _ERRS = {LT_ERR_UNSUPPORTED: UnsupportedError, LT_ERR_INVALID: InvalidError, LT_
 EXPORTS = [
     "lt_init", "lt_destroy", "lt_last_error", "lt_sync", "lt_stream", "lt_tensor_upload", "lt_tensor_read", "lt_tensor_clone",
     "lt_tensor_free", "lt_tensor_bytes", "lt_matvec", "lt_ffn_dense", "lt_moe_router_topk", "lt_expert_gate_up_id",
-    "lt_expert_down_id", "lt_moe_forward", "lt_moe_prefill", "lt_rmsnorm", "lt_add_rmsnorm",
+    "lt_expert_down_id", "lt_moe_forward", "lt_moe_forward_noalloc", "lt_moe_prefill", "lt_rmsnorm", "lt_add_rmsnorm",
     "lt_rmsnorm_weighted_raw_scaled", "lt_moe_tail", "lt_gemma4_moe_block",
 ]
 
@@ -101,6 +101,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "lt_expert_gate_up_id": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp, u32]),
         "lt_expert_down_id": (i32, [vp, vp, vp, vp, vp, u32, vp, u32]),
         "lt_moe_forward": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
+        "lt_moe_forward_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
         "lt_moe_prefill": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
         "lt_rmsnorm": (i32, [vp, vp, vp, vp, u32, u32, C.c_float, u32]),
         "lt_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, u32, u32, C.c_float, u32]),
@@ -261,6 +262,20 @@ class Context:
         self._check(self.lib.lt_moe_forward(self.ptr, _ptr(out)[0], _ptr(x)[0], router.handle, _ptr(bias)[0],
                                             gate_up.handle, down.handle, sg, su, sd, k, d_expert, act, fl,
                                             _ptr(out_ids)[0], _ptr(out_w)[0]))
+        return out
+
+    def moe_forward_noalloc(self, out, x, router: Tensor, gate_up: Tensor, down: Tensor, k: int, d_expert: int,
+                            act=ACT_SILU, norm_topk=False, accumulate=False, bias=None, out_ids=None, out_w=None,
+                            deterministic=False):
+        """lt_moe_forward_noalloc: moe_forward on the library's static scratch
+        (no device allocation); device arrays only."""
+        fl = (LT_MOE_NORM_TOPK if norm_topk else 0) | (LT_MOE_ACCUMULATE if accumulate else 0)
+        fl |= LT_MOE_DETERMINISTIC if deterministic else 0
+        if self._io(out, x, bias, out_ids, out_w):
+            raise InvalidError("moe_forward_noalloc takes device arrays only")
+        self._check(self.lib.lt_moe_forward_noalloc(self.ptr, _ptr(out)[0], _ptr(x)[0], router.handle, _ptr(bias)[0],
+                                                    gate_up.handle, down.handle, None, None, None, k, d_expert, act,
+                                                    fl, _ptr(out_ids)[0], _ptr(out_w)[0]))
         return out
 
     def moe_prefill(self, out, X, router: Tensor, gate_up: Tensor, down: Tensor, k: int, d_expert: int,

@@ -642,7 +642,12 @@ def test_gpu_fused_agent_handover_matches_local(ctx, cfg3):
     # same values: the slot-order combine gives the same bits
     c, _ = cfg3
     w = c["weights"]
-    ctx2 = lt.Context(0)
+    # the knob is read when a context is created
+    os.environ["LT_FUSED_AGENT_HANDOVER"] = "1"
+    try:
+        ctx2 = lt.Context(0)
+    finally:
+        del os.environ["LT_FUSED_AGENT_HANDOVER"]
     try:
         t1 = lt.upload_moe(ctx, w)
         t2 = lt.upload_moe(ctx2, w)
@@ -650,14 +655,8 @@ def test_gpu_fused_agent_handover_matches_local(ctx, cfg3):
             x = synth.config3_x(500 + i)
             o1 = np.zeros(w.d_model, np.float32)
             o2 = np.zeros(w.d_model, np.float32)
-            # the knob is read at a context's first fused call: ctx's has
-            # happened before it is set, ctx2's happens while it is set
             ctx.moe_forward(o1, x, *t1, 8, w.d_expert, norm_topk=True, deterministic=True)
-            os.environ["LT_FUSED_AGENT_HANDOVER"] = "1"
-            try:
-                ctx2.moe_forward(o2, x, *t2, 8, w.d_expert, norm_topk=True, deterministic=True)
-            finally:
-                del os.environ["LT_FUSED_AGENT_HANDOVER"]
+            ctx2.moe_forward(o2, x, *t2, 8, w.d_expert, norm_topk=True, deterministic=True)
             assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32)), i
         for t in t1 + t2:
             t.free()

@@ -1,0 +1,79 @@
+"""lt_moe_forward_noalloc: the single-launch MoE layer on the library's
+static scratch (no device allocation), through the C ABI, against
+lt_moe_forward on the same inputs and against the CPU oracle.  Two calls in
+a row, the second on a smaller layer, so the shared scratch is reused."""
+import numpy as np
+import pytest
+
+import llmtoy_amd as lt
+import pyoracle as orc
+from llmtoy_amd import synth
+from llmtoy_amd.hip import DeviceArray
+from llmtoy_amd.lib import InvalidError, UnsupportedError
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+def _run(ctx, fn, tens, x, k, F, det, norm):
+    D = x.shape[0]
+    xd, od = DeviceArray.from_numpy(x), DeviceArray((D,), np.float32)
+    idd, wd = DeviceArray((k,), np.uint32), DeviceArray((k,), np.float32)
+    fn(od, xd, *tens, k, F, norm_topk=norm, out_ids=idd, out_w=wd, deterministic=det)
+    ctx.sync()
+    res = od.numpy(), idd.numpy(), wd.numpy()
+    for a in (xd, od, idd, wd):
+        a.free()
+    return res
+
+
+@pytest.mark.parametrize("det", [True, False])
+def test_noalloc_matches_moe_forward_two_calls(det):
+    cases = [  # (seed, D, E, F, k, norm): the config-3 layer, then a smaller one
+        (3, 2048, 128, 768, 8, True),
+        (41, 1024, 64, 512, 4, False),
+    ]
+    with lt.Context(0) as ctx, orc.Pool(8) as pool:
+        for seed, D, E, F, k, norm in cases:
+            w = synth.config3()["weights"] if seed == 3 else synth.moe_weights(seed, D, E, F)
+            x = synth.normal(synth.stream(seed, 77), (D,))
+            tens = lt.upload_moe(ctx, w)
+            got = _run(ctx, ctx.moe_forward_noalloc, tens, x, k, F, det, norm)
+            want = _run(ctx, ctx.moe_forward, tens, x, k, F, det, norm)
+            ref, rids, rw, agree = orc.moe_forward(w, x, k, norm_topk=norm, pool=pool)
+            assert agree
+            assert np.array_equal(got[1], want[1]) and np.array_equal(got[1], rids), (seed, got[1], rids)
+            assert np.array_equal(got[2].view(np.uint32), want[2].view(np.uint32))
+            if det:  # slot-order combine: the same bits as lt_moe_forward
+                assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32)), seed
+            else:    # float-atomic combine: the order of the k adds varies
+                assert _rel(got[0], want[0]) <= 1e-6, seed
+            assert _rel(got[0], ref) <= 1e-3, seed
+            for t in tens:
+                t.free()
+
+
+def test_noalloc_rejects_what_it_cannot_run():
+    w = synth.moe_weights(42, 512, 16, 256)
+    x = synth.normal(synth.stream(42, 7), (512,))
+    with lt.Context(0) as ctx:
+        tens = lt.upload_moe(ctx, w)
+        xd, od = DeviceArray.from_numpy(x), DeviceArray((512,), np.float32)
+        with pytest.raises(InvalidError, match="device arrays only"):
+            ctx.moe_forward_noalloc(np.zeros(512, np.float32), x, *tens, 2, 256)
+        big = synth.moe_weights(43, 4096, 8, 256)
+        tb = lt.upload_moe(ctx, big)
+        xb, ob = DeviceArray((4096,), np.float32), DeviceArray((4096,), np.float32)
+        with pytest.raises(UnsupportedError, match="beyond the static scratch"):
+            ctx.moe_forward_noalloc(ob, xb, *tb, 2, 256)
+        ctx.moe_forward_noalloc(od, xd, *tens, 2, 256)  # still usable
+        ctx.sync()
+        ref, *_ = orc.moe_forward(w, x, 2)
+        assert _rel(od.numpy(), ref) <= 1e-3
+        for a in (xd, od, xb, ob):
+            a.free()
+        for t in tens + tb:
+            t.free()
