@@ -112,6 +112,25 @@ __device__ __forceinline__ float xor32(float v, bool first) {
     return __uint_as_float(first ? pr[0] : pr[1]);
 }
 
+// Workgroups of 256 threads that the persistent streaming kernels launch at
+// most: 256 CUs x 4 workgroups (their occupancy at ~120 VGPRs).
+constexpr int kStreamBlocks = 1024;
+
+// Sum over each aligned group of G consecutive lanes (G = 4, 8, 16, 32 or
+// 64), total in every lane of the group, with DPP row operations (and
+// ds_swizzle / v_permlane32_swap across rows): no LDS round trips.
+template <int G>
+__device__ __forceinline__ float group_sum_dpp(float t, bool first) {
+    static_assert(G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "G");
+    if (G >= 64) t += xor32(t, first);
+    if (G >= 32) t += xor16(t);
+    if (G >= 16) t += dpp<0x128>(t);  // row_ror:8 (lane i ^ 8 within a row)
+    if (G >= 8) t += dpp<0x141>(t);   // row_half_mirror
+    t += dpp<0x4E>(t);                // quad_perm [2,3,0,1]
+    t += dpp<0xB1>(t);                // quad_perm [1,0,3,2]
+    return t;
+}
+
 // Sums V values (V = 1, 2, 4 or 8) over the 64 lanes of a wavefront with
 // log2(V) exchange steps (each halves the values a lane carries) followed by
 // a plain reduction over the remaining lane bits.  Returns, in every lane,

@@ -155,6 +155,91 @@ __global__ void __launch_bounds__(256) k_matvec_q4k(const uint8_t *__restrict__ 
     }
 }
 
+// ------------------------------------------------------------------------
+// Streaming matvec for rows of NSB = 1, 2, 4, 8 or 16 super-blocks (config 2
+// is NSB = 16).  Persistent waves as in k_matvec_q6k_stream: lane L takes
+// chunks c = L % LPR + LPR j (j < UPL) of rows RPS apart (LPR = min(64, 8
+// NSB) lanes per row, UPL = 8 NSB / LPR chunks per lane), so its x values
+// are loop-invariant registers; slab i + 1 is loaded while slab i is
+// computed, from two static buffers; DPP row sums.
+template <int UPL>
+struct Q4Regs {
+    uint4 h[UPL], q[UPL];
+};
+
+template <int NSB>
+__global__ void __launch_bounds__(256) k_matvec_q4k_stream(const uint8_t *__restrict__ hdr,
+                                                           const uint8_t *__restrict__ qs,
+                                                           const float *__restrict__ x, float *__restrict__ y,
+                                                           int row0, int nrows) {
+    constexpr int LPR = 8 * NSB < 64 ? 8 * NSB : 64, UPL = 8 * NSB / LPR, RPS = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int l = lane % LPR, rs = lane / LPR;
+    const int stride = gridDim.x * 4 * RPS;
+    int base = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPS;
+    const bool first = p32_first(lane);
+    auto ld = [&](Q4Regs<UPL> &w, int rb) {
+        int row = rb + rs;
+        row = row < nrows ? row : nrows - 1;  // every load unconditional
+        const size_t b0 = (size_t)(row0 + row) * NSB;
+#pragma unroll
+        for (int j = 0; j < UPL; j++) {
+            const int c = l + LPR * j;
+            w.h[j] = ldg16(hdr + (b0 + (c >> 3)) * 16);
+            w.q[j] = ldg16(qs + (b0 + (c >> 3)) * 128 + (c & 7) * 16);
+        }
+    };
+    Q4Regs<UPL> a, b;
+    ld(a, base);
+    XChunk xc[UPL];
+#pragma unroll
+    for (int j = 0; j < UPL; j++) {
+        const int c = l + LPR * j;
+        const float *p = x + (c >> 3) * 256 + 64 * ((c & 7) >> 1) + 16 * (c & 1);
+#pragma unroll
+        for (int t = 0; t < 16; t += 4) {
+            const float4 lo = *reinterpret_cast<const float4 *>(p + t);
+            const float4 hi = *reinterpret_cast<const float4 *>(p + 32 + t);
+            xc[j].lo[t] = lo.x; xc[j].lo[t + 1] = lo.y; xc[j].lo[t + 2] = lo.z; xc[j].lo[t + 3] = lo.w;
+            xc[j].hi[t] = hi.x; xc[j].hi[t + 1] = hi.y; xc[j].hi[t + 2] = hi.z; xc[j].hi[t + 3] = hi.w;
+        }
+        sum_xchunk(xc[j]);
+    }
+    auto step = [&](const Q4Regs<UPL> &w, int rb) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < UPL; j++) acc += q4k_chunk_dot(w.h[j], w.q[j], (l + LPR * j) & 7, xc[j]);
+        const float v = group_sum_dpp<LPR>(acc, first);
+        const int row = rb + rs;
+        if (l == 0 && row < nrows) y[row] = v;
+    };
+    // loads stay unconditional (clamped rows); the math of a slab past the
+    // last row is skipped (wave-uniform branch)
+    for (; base < nrows; base += 2 * stride) {
+        ld(b, base + stride);
+        step(a, base);
+        ld(a, base + 2 * stride);
+        if (base + stride < nrows) step(b, base + stride);
+    }
+}
+
+template <int NSB>
+static hipError_t launch_q4k_stream(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
+                                    hipStream_t s) {
+    constexpr int LPR = 8 * NSB < 64 ? 8 * NSB : 64, RPS = 64 / LPR;
+    // 8 workgroups per CU fit below 64 VGPRs (NSB <= 8), 4 at NSB = 16
+    constexpr size_t cap = NSB <= 8 ? 2 * kStreamBlocks : kStreamBlocks;
+    // at least two row slabs per wave: the second slab's loads overlap the
+    // first one's math and x is loaded once for both (one slab per wave
+    // made config 2, 4096 rows, 7.3 us instead of 5.6)
+    const size_t slabs = (nrows + RPS - 1) / RPS;
+    size_t nblk = (slabs + 7) / 8;
+    if (nblk > cap) nblk = cap;
+    hipLaunchKernelGGL((k_matvec_q4k_stream<NSB>), dim3((unsigned)nblk), dim3(256), 0, s, W.p0, W.p1, x, y,
+                       (int)row0, (int)nrows);
+    return hipGetLastError();
+}
+
 template <int G, int CPL>
 static hipError_t launch_mv_q4k_t(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
                                   hipStream_t s) {
@@ -169,6 +254,16 @@ static hipError_t launch_mv_q4k_t(const DevTensor &W, size_t row0, size_t nrows,
 
 hipError_t launch_matvec_q4k(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
                              hipStream_t s) {
+    if ((row0 + nrows) * W.blocks_per_row < (size_t)1 << 31) {  // int row indices in the streaming kernel
+        switch (W.blocks_per_row) {
+        case 1: return launch_q4k_stream<1>(W, row0, nrows, x, y, s);
+        case 2: return launch_q4k_stream<2>(W, row0, nrows, x, y, s);
+        case 4: return launch_q4k_stream<4>(W, row0, nrows, x, y, s);
+        case 8: return launch_q4k_stream<8>(W, row0, nrows, x, y, s);
+        case 16: return launch_q4k_stream<16>(W, row0, nrows, x, y, s);
+        default: break;
+        }
+    }
     const int nch = (int)W.blocks_per_row * 8;
     if (nch <= 8) return launch_mv_q4k_t<8, 1>(W, row0, nrows, x, y, s);
     if (nch <= 16) return launch_mv_q4k_t<16, 1>(W, row0, nrows, x, y, s);
