@@ -437,6 +437,42 @@ def bench_decode(args):
         for tns in cp:
             tns.free()
     ctx.close()
+    if args.timeline:
+        timeline_report(args, w, xs)
+
+
+def timeline_report(args, w, xs, n=200):
+    """n decode steps in a context created with LT_PROFILE=timeline (rotated
+    weight copies, x pool), each followed by lt_sync so that every launch's
+    phase stamps are collected; writes lt_profile_report's text to the path."""
+    import llmtoy_amd as lt
+    from llmtoy_amd.hip import DeviceArray
+    os.environ["LT_PROFILE"] = "timeline"
+    try:
+        ctx = lt.Context(0)
+    finally:
+        del os.environ["LT_PROFILE"]
+    base = lt.upload_moe(ctx, w)
+    copies = [base] + [tuple(t.clone() for t in base) for _ in range(args.copies - 1)]
+    import numpy as np
+    X = DeviceArray.from_numpy(np.stack(xs))
+    out = DeviceArray((D,), np.float32)
+    for i in range(n):
+        ctx.moe_forward(out, X.row(i % len(xs)), *copies[i % args.copies], K, F, norm_topk=True)
+        ctx.sync()
+    rep = ctx.profile_report()
+    head = (f"Command (GPU box, repo root): python bench.py --no-cpu --no-gguf --timeline {args.timeline}\n"
+            f"Workload: config-3 decode layer, {n} eager launches, {args.copies} weight copies rotated, "
+            f"x pool of {len(xs)}; LT_PROFILE=timeline adds one store per workgroup at its end.\n\n")
+    with open(args.timeline, "w") as f:
+        f.write(head + rep)
+    log("timeline report:\n" + rep)
+    X.free()
+    out.free()
+    for cp in copies:
+        for t in cp:
+            t.free()
+    ctx.close()
 
 
 # ------------------------------------------------------------------ configs 1, 2, 2b
@@ -876,6 +912,9 @@ def main():
                     default="decode")
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
+    ap.add_argument("--timeline", metavar="PATH", default=None,
+                    help="decode: afterwards run LT_PROFILE=timeline steps in a fresh context and write the "
+                         "library's per-phase report to PATH")
     args = ap.parse_args()
 
     if args.gpus != 1:

@@ -217,6 +217,22 @@ int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt
                    const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
                    uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);
 
+/* Profiling (the counterpart of the reference's GpuProfiler, gpu/context.zig:
+ * 34-268, enabled there by LLMTOY_GPU_PROFILE).  With LT_PROFILE set when
+ * lt_init runs, every call records a HIP event pair around the device work it
+ * enqueues (not while the stream is being captured); LT_PROFILE=timeline also
+ * makes the single-launch MoE kernel record, per workgroup, the wall-clock
+ * time at which each phase of its role ended (router: first row data, logit
+ * published; gate/up: logits seen, expert known, dot products done, h
+ * published; down: logits seen, weight loads issued, h read, adds issued).
+ * Events and stamps are collected at synchronising calls (lt_sync, LT_HOST_IO
+ * calls): the stamps of the last single-launch MoE kernel before each.
+ * lt_profile_report writes a text table (per-call counts and times, per-phase
+ * medians) into buf (NUL-terminated, truncated to len) and returns the full
+ * length; 0 when LT_PROFILE is off.  No counterpart of the allocation-free
+ * entry point's spans: lt_moe_forward_noalloc records phase stamps only. */
+size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len);
+
 /* ---- RMS norms and the Gemma4 MoE block (Gemma4's steps around the MoE layer) ----
  * Row length n <= 16384 floats; eps in [0, 1].  Every product and sum is a
  * separately rounded fp32 operation and rms_inv = 1 / sqrt(ss / n + eps)

@@ -8,6 +8,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <map>
 #include <new>
 #include <string>
 #include <vector>
@@ -23,6 +25,31 @@ namespace {
 struct DevBuf {
     void *p = nullptr;
     size_t cap = 0;
+};
+
+// LT_PROFILE state: event spans around each call's device work (the
+// counterpart of the reference's GpuProfiler, gpu/context.zig:34-268) and,
+// with LT_PROFILE=timeline, the single-launch MoE kernel's phase stamps.
+struct PendingSpan {
+    hipEvent_t a, b;
+    const char *label;
+};
+struct SpanStat {
+    size_t n = 0;
+    double total_ms = 0, min_ms = 1e30, max_ms = 0;
+};
+constexpr int kRoles = 5, kPhases = lt::kStamps - 1;
+struct Profile {
+    int mode = 0;  // 0 off, 1 spans, 2 spans + timeline
+    std::vector<PendingSpan> pending;
+    std::vector<hipEvent_t> free_events;
+    std::map<std::string, SpanStat> spans;
+    uint64_t *stamps = nullptr;  // device [kFusedBlocks][kStamps]
+    bool stamps_pending = false;
+    size_t launches = 0;
+    // per launch: median and largest time of each (role, phase) over blocks, us
+    std::vector<float> med[kRoles][kPhases], last[kRoles][kPhases];
+    std::vector<float> slot_last[2][16];  // per slot: gate/up h published, down adds issued
 };
 
 }  // namespace
@@ -52,6 +79,7 @@ struct lt_ctx {
     // lt_moe_forward_noalloc
     uint8_t *na_base = nullptr;
     lt::FusedScratch na_fsc{};
+    Profile prof;
     // pinned + device staging of tensor uploads and read-backs (allocated on first use)
     lt::UploadStaging up{};
 };
@@ -109,6 +137,106 @@ int ensure(lt_ctx *ctx, DevBuf &b, size_t bytes) {
 bool capturing(lt_ctx *ctx) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     return hipStreamIsCapturing(ctx->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// An event pair around the device work one call enqueues (LT_PROFILE set;
+// not while the stream is being captured).  Resolved by prof_harvest.
+struct Span {
+    lt_ctx *ctx = nullptr;
+    hipEvent_t a = nullptr;
+    const char *label;
+    Span(lt_ctx *c, const char *l) : label(l) {
+        if (!c->prof.mode || capturing(c)) return;
+        Profile &P = c->prof;
+        hipEvent_t e = nullptr;
+        if (!P.free_events.empty()) {
+            e = P.free_events.back();
+            P.free_events.pop_back();
+        } else if (hipEventCreate(&e) != hipSuccess) {
+            return;
+        }
+        if (hipEventRecord(e, c->stream) != hipSuccess) {
+            P.free_events.push_back(e);
+            return;
+        }
+        ctx = c;
+        a = e;
+    }
+    ~Span() {
+        if (!ctx) return;
+        Profile &P = ctx->prof;
+        hipEvent_t b = nullptr;
+        if (!P.free_events.empty()) {
+            b = P.free_events.back();
+            P.free_events.pop_back();
+        } else if (hipEventCreate(&b) != hipSuccess) {
+            P.free_events.push_back(a);
+            return;
+        }
+        if (hipEventRecord(b, ctx->stream) != hipSuccess) {
+            P.free_events.push_back(a);
+            P.free_events.push_back(b);
+            return;
+        }
+        P.pending.push_back({a, b, label});
+    }
+};
+
+float median_of(std::vector<float> v) {
+    if (v.empty()) return 0.0f;
+    std::nth_element(v.begin(), v.begin() + v.size() / 2, v.end());
+    return v[v.size() / 2];
+}
+
+// After the stream is idle: resolves pending spans and, with a fused launch
+// since the last harvest, reads its phase stamps and adds that launch's
+// per-phase medians and maxima (us from the first block's start).
+void prof_harvest(lt_ctx *ctx) {
+    Profile &P = ctx->prof;
+    if (!P.mode) return;
+    for (const PendingSpan &sp : P.pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, sp.a, sp.b) == hipSuccess) {
+            SpanStat &st = P.spans[sp.label];
+            st.n++;
+            st.total_ms += ms;
+            st.min_ms = std::min(st.min_ms, (double)ms);
+            st.max_ms = std::max(st.max_ms, (double)ms);
+        }
+        P.free_events.push_back(sp.a);
+        P.free_events.push_back(sp.b);
+    }
+    P.pending.clear();
+    if (!P.stamps || !P.stamps_pending) return;
+    P.stamps_pending = false;
+    std::vector<uint64_t> st((size_t)lt::kFusedBlocks * lt::kStamps);
+    if (hipMemcpy(st.data(), P.stamps, st.size() * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
+    uint64_t t0 = ~0ull;
+    for (int b = 0; b < lt::kFusedBlocks; b++) {
+        const uint64_t *t = &st[(size_t)b * lt::kStamps];
+        if ((t[lt::kStamps - 1] & 0xff) && t[0]) t0 = std::min(t0, t[0]);
+    }
+    if (t0 == ~0ull) return;
+    std::vector<float> v[kRoles][kPhases];
+    std::vector<float> sl[2][16];
+    for (int b = 0; b < lt::kFusedBlocks; b++) {
+        const uint64_t *t = &st[(size_t)b * lt::kStamps];
+        const int role = (int)(t[lt::kStamps - 1] & 0xff), slot = (int)((t[lt::kStamps - 1] >> 8) & 15);
+        if (role <= 0 || role >= kRoles) continue;
+        for (int ph = 0; ph < kPhases; ph++)
+            if (t[ph] >= t0) v[role][ph].push_back((float)(t[ph] - t0) * 0.01f);  // 100 MHz ticks -> us
+        if ((role == 2 || role == 3) && t[4] >= t0) sl[role - 2][slot].push_back((float)(t[4] - t0) * 0.01f);
+    }
+    for (int r = 0; r < kRoles; r++)
+        for (int ph = 0; ph < kPhases; ph++) {
+            if (v[r][ph].empty()) continue;
+            P.med[r][ph].push_back(median_of(v[r][ph]));
+            P.last[r][ph].push_back(*std::max_element(v[r][ph].begin(), v[r][ph].end()));
+        }
+    for (int r = 0; r < 2; r++)
+        for (int q = 0; q < 16; q++)
+            if (!sl[r][q].empty()) P.slot_last[r][q].push_back(*std::max_element(sl[r][q].begin(), sl[r][q].end()));
+    P.launches++;
 }
 
 size_t block_elems(uint32_t type) {
@@ -208,6 +336,7 @@ int ensure_fused(lt_ctx *ctx) {
     }
     ctx->fused = p;
     ctx->fsc = lt::fused_scratch_at((uint8_t *)p, ctx->err_dev, ctx->xcd_local);
+    ctx->fsc.stamps = ctx->prof.stamps;
     return LT_OK;
 }
 
@@ -231,6 +360,18 @@ hipError_t init_device_state(lt_ctx *ctx) {
     if (agent && agent[0] == '1') local = 0;
     ctx->xcd_local = local;
     ctx->na_fsc = lt::fused_scratch_at(ctx->na_base, ctx->err_dev, local);
+    // LT_PROFILE: "timeline" = spans + phase stamps of the fused kernel;
+    // any other non-empty value except "0" = spans
+    const char *prof = getenv("LT_PROFILE");
+    if (prof && prof[0] && strcmp(prof, "0") != 0) {
+        ctx->prof.mode = strcmp(prof, "timeline") == 0 ? 2 : 1;
+        if (ctx->prof.mode == 2) {
+            const size_t nb = (size_t)lt::kFusedBlocks * lt::kStamps * 8;
+            if ((e = hipMalloc((void **)&ctx->prof.stamps, nb)) != hipSuccess) return e;
+            if ((e = hipMemset(ctx->prof.stamps, 0, nb)) != hipSuccess) return e;
+            ctx->na_fsc.stamps = ctx->prof.stamps;
+        }
+    }
     return hipSuccess;
 }
 
@@ -294,6 +435,7 @@ extern "C" int lt_init(int device, lt_ctx **out_ctx) {
     if (e != hipSuccess) {
         if (ctx->ticket) (void)hipFree(ctx->ticket);
         if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
+        if (ctx->prof.stamps) (void)hipFree(ctx->prof.stamps);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return e == hipErrorOutOfMemory ? LT_ERR_OOM : LT_ERR_DEVICE;
@@ -312,6 +454,12 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     for (void *p : ctx->retired) (void)hipFree(p);
+    for (const PendingSpan &sp : ctx->prof.pending) {
+        (void)hipEventDestroy(sp.a);
+        (void)hipEventDestroy(sp.b);
+    }
+    for (hipEvent_t e : ctx->prof.free_events) (void)hipEventDestroy(e);
+    if (ctx->prof.stamps) (void)hipFree(ctx->prof.stamps);
     if (ctx->ticket) (void)hipFree(ctx->ticket);
     if (ctx->fused) (void)hipFree(ctx->fused);
     if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
@@ -325,6 +473,7 @@ extern "C" const char *lt_last_error(const lt_ctx *ctx) { return ctx ? ctx->err.
 extern "C" int lt_sync(lt_ctx *ctx) {
     if (!ctx) return LT_ERR_INVALID;
     LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    prof_harvest(ctx);
     return check_fused_err(ctx);
 }
 
@@ -410,6 +559,7 @@ extern "C" int lt_matvec(lt_ctx *ctx, float *out, const lt_tensor *W, const floa
     if (rc) return rc;
     const DevTensor &T = W->t;
     const bool host = flags & LT_HOST_IO;
+    Span span_(ctx, "lt_matvec");
     const float *dx = x;
     float *dy = out;
     if (host) {
@@ -423,6 +573,7 @@ extern "C" int lt_matvec(lt_ctx *ctx, float *out, const lt_tensor *W, const floa
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dy, T.total_rows * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -479,6 +630,7 @@ extern "C" int lt_ffn_dense(lt_ctx *ctx, float *out, const lt_tensor *Wg, const 
     const size_t D = Wg->t.cols;
     int rc = check_ffn(ctx, Wg, Wu, Wd, D);
     if (rc) return rc;
+    Span span_(ctx, "lt_ffn_dense");
     const bool host = flags & LT_HOST_IO;
     const float *dx = x;
     float *dy = out;
@@ -493,6 +645,7 @@ extern "C" int lt_ffn_dense(lt_ctx *ctx, float *out, const lt_tensor *Wg, const 
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dy, D * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -604,6 +757,7 @@ extern "C" int lt_moe_router_topk(lt_ctx *ctx, const lt_tensor *router, const fl
     const DevTensor &R = router->t;
     const bool host = flags & LT_HOST_IO;
     const float *dx = x, *dbias = bias;
+    Span span_(ctx, "lt_moe_router_topk");
     float *dscores = scores;
     if (host) {
         if ((rc = stage_in(ctx, ctx->x, x, R.cols * 4, (const void **)&dx))) return rc;
@@ -619,6 +773,7 @@ extern "C" int lt_moe_router_topk(lt_ctx *ctx, const lt_tensor *router, const fl
         if (scores)
             LT_HIP(ctx, hipMemcpyAsync(scores, dscores, R.total_rows * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -640,6 +795,7 @@ extern "C" int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const
     const float *dx = x;
     const uint32_t *dids = ids;
     float *dh = h;
+    Span span_(ctx, "lt_expert_gate_up_id");
     int rc;
     if (host) {
         for (uint32_t s = 0; s < k; s++)
@@ -653,6 +809,7 @@ extern "C" int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(h, dh, (size_t)k * down_cols * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -669,6 +826,7 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
         return fail(ctx, LT_ERR_UNSUPPORTED, "k * down row length > 16384 (LDS staging of h)");
     const bool host = flags & LT_HOST_IO;
     const float *dh = h, *dw = weights;
+    Span span_(ctx, "lt_expert_down_id");
     const uint32_t *dids = ids;
     float *dout = out;
     int rc;
@@ -690,6 +848,7 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dout, D.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -714,6 +873,7 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
             if ((rc = ensure_fused(ctx)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
                 (rc = ensure(ctx, ctx->w, kMaxK * 4)))
                 return rc;
+            ctx->prof.stamps_pending = ctx->prof.stamps != nullptr;
             return launch_rc(ctx,
                              lt::launch_moe_fused(pl, R, bias, GU, D, x, (int)k, (int)d_expert, act,
                                                   (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, base,
@@ -761,6 +921,7 @@ extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_
         if (!sh_gate || !sh_up || !sh_down) return fail(ctx, LT_ERR_INVALID, "shared FFN needs gate, up and down");
         if ((rc = check_ffn(ctx, sh_gate, sh_up, sh_down, d_model))) return rc;
     }
+    Span span_(ctx, "lt_moe_forward");
     const bool host = flags & LT_HOST_IO;
     const float *dx = x, *dbias = router_bias;
     float *dout = out;
@@ -783,6 +944,7 @@ extern "C" int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dout, d_model * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
         return check_fused_err(ctx);
     }
     return LT_OK;
@@ -819,6 +981,7 @@ extern "C" int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, c
                     "d_expert %u, down K %zu, k %u; limits: d_model 256..2048 in steps of 256, down K <= 1024, "
                     "<= 256 experts, k <= 16)",
                     GU.cols, R.total_rows, d_expert, D.cols, k);
+    ctx->prof.stamps_pending = ctx->prof.stamps != nullptr;
     uint32_t *ids_dev = (uint32_t *)(ctx->na_base + lt::kFusedIdsOff);
     float *w_dev = (float *)(ctx->na_base + lt::kFusedWOff);
     rc = launch_rc(ctx,
@@ -851,6 +1014,7 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
         return fail(ctx, LT_ERR_UNSUPPORTED, "prefill tiles need d_expert %% 64 == 0 and d_model %% 128 == 0");
     if ((size_t)T * k > (1u << 20)) return fail(ctx, LT_ERR_UNSUPPORTED, "T*k > 2^20");
     const int E = (int)router->t.total_rows, Kd = (int)down->t.cols;
+    Span span_(ctx, "lt_moe_prefill");
     const bool host = flags & LT_HOST_IO;
     const float *dX = X, *dbias = router_bias;
     float *dout = out;
@@ -886,6 +1050,7 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
             LT_HIP(ctx, hipMemcpyAsync(out_w, wsp + logits_b + ids_b, (size_t)T * k * 4, hipMemcpyDeviceToHost,
                                        ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -950,6 +1115,7 @@ int rmsnorm_entry(lt_ctx *ctx, int op, float *out, const float *a, const float *
                   uint32_t n, float eps, uint32_t flags) {
     int rc = check_norm(ctx, rows, n, eps, flags, kNormFlags);
     if (rc) return rc;
+    Span span_(ctx, op ? "lt_add_rmsnorm" : "lt_rmsnorm");
     const bool host = flags & LT_HOST_IO;
     const size_t len = (size_t)rows * n;
     Arena ar;
@@ -967,6 +1133,7 @@ int rmsnorm_entry(lt_ctx *ctx, int op, float *out, const float *a, const float *
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dout, len * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -992,6 +1159,7 @@ extern "C" int lt_rmsnorm_weighted_raw_scaled(lt_ctx *ctx, float *weighted_out, 
         return fail(ctx, LT_ERR_INVALID, "null argument");
     int rc = check_norm(ctx, 1, n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE);
     if (rc) return rc;
+    Span span_(ctx, "lt_rmsnorm_weighted_raw_scaled");
     const bool host = flags & LT_HOST_IO;
     Arena ar;
     if (host) {
@@ -1008,6 +1176,7 @@ extern "C" int lt_rmsnorm_weighted_raw_scaled(lt_ctx *ctx, float *weighted_out, 
         LT_HIP(ctx, hipMemcpyAsync(weighted_out, dwo, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipMemcpyAsync(raw_scaled_out, dro, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -1019,6 +1188,7 @@ extern "C" int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float 
         return fail(ctx, LT_ERR_INVALID, "null argument");
     int rc = check_norm(ctx, 1, n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE);
     if (rc) return rc;
+    Span span_(ctx, "lt_moe_tail");
     const bool host = flags & LT_HOST_IO;
     Arena ar;
     if (host) {
@@ -1035,6 +1205,7 @@ extern "C" int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float 
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(x, xo, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
 }
@@ -1057,6 +1228,7 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
         return rc;
     const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
     const size_t E = R.total_rows, Kd = D.cols;
+    Span span_(ctx, "lt_gemma4_moe_block");
     const bool host = flags & LT_HOST_IO;
     if (!host && !aligned16(x)) return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
     Arena ar;
@@ -1108,6 +1280,66 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(x, xio, n * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        prof_harvest(ctx);
     }
     return LT_OK;
+}
+
+// ------------------------------------------------------------------ profiling
+extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
+    if (!ctx || !ctx->prof.mode) {
+        if (buf && len) buf[0] = 0;
+        return 0;
+    }
+    Profile &P = ctx->prof;
+    std::string o;
+    char line[256];
+    o += "LT_PROFILE spans: device time between HIP events around each call's work\n";
+    snprintf(line, sizeof line, "%-34s %8s %12s %10s %10s %10s\n", "call", "count", "total ms", "mean us", "min us",
+             "max us");
+    o += line;
+    for (const auto &kv : P.spans) {
+        const SpanStat &st = kv.second;
+        snprintf(line, sizeof line, "%-34s %8zu %12.3f %10.3f %10.3f %10.3f\n", kv.first.c_str(), st.n, st.total_ms,
+                 st.n ? st.total_ms * 1e3 / st.n : 0.0, st.min_ms * 1e3, st.max_ms * 1e3);
+        o += line;
+    }
+    if (P.mode == 2) {
+        snprintf(line, sizeof line,
+                 "\nLT_PROFILE timeline: single-launch MoE kernel, %zu launches (one per synchronising call);\n"
+                 "us from the first block's start; median over launches of the block median / the last block\n",
+                 P.launches);
+        o += line;
+        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine"};
+        static const char *phases[kRoles][kPhases] = {
+            {},
+            {"block start", "first row chunk in", "logit published"},
+            {"block start", "logits seen", "expert known", "dot products done", "h record published"},
+            {"block start", "logits seen", "weight loads issued", "h records read", "adds issued"},
+            {"block start", "rows written"}};
+        snprintf(line, sizeof line, "%-9s %-22s %10s %10s\n", "role", "phase", "median", "last");
+        o += line;
+        for (int r = 1; r < kRoles; r++)
+            for (int ph = 0; ph < kPhases; ph++) {
+                if (!phases[r][ph] || P.med[r][ph].empty()) continue;
+                snprintf(line, sizeof line, "%-9s %-22s %10.2f %10.2f\n", roles[r], phases[r][ph], median_of(P.med[r][ph]),
+                         median_of(P.last[r][ph]));
+                o += line;
+            }
+        for (int r = 0; r < 2; r++) {
+            o += r == 0 ? "gate/up h published, last block per slot:" : "down adds issued, last block per slot:   ";
+            for (int q = 0; q < 16; q++)
+                if (!P.slot_last[r][q].empty()) {
+                    snprintf(line, sizeof line, " %d:%.2f", q, median_of(P.slot_last[r][q]));
+                    o += line;
+                }
+            o += "\n";
+        }
+    }
+    if (buf && len) {
+        const size_t n = o.size() < len - 1 ? o.size() : len - 1;
+        memcpy(buf, o.data(), n);
+        buf[n] = 0;
+    }
+    return o.size();
 }

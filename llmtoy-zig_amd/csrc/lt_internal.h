@@ -354,7 +354,18 @@ struct FusedScratch {
     uint64_t *pl;        // [4 * kFusedBlocks][16] partial-output lines
     uint32_t *err;       // host-mapped error word (device address)
     int xcd_local;       // blocks with equal index % 8 share an XCD (probe_xcd_groups)
+    uint64_t *stamps = nullptr;  // LT_PROFILE=timeline: [kFusedBlocks][kStamps] phase stamps, else null
 };
+// Phase stamps of one launch (LT_PROFILE=timeline): thread 0 of block b
+// writes stamps[b * kStamps + i], wall-clock ticks (100 MHz) at the end of
+// phase i of its role, and stamps[b * kStamps + kStamps - 1] = role | slot
+// << 8 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine).
+constexpr int kStamps = 8;
+enum : int { kStampStart = 0 };
+// router: 1 first row chunk in, 2 logit published; gate/up: 1 logits seen,
+// 2 expert known, 3 dot products done, 4 h record published; down: 1 logits
+// seen, 2 weight loads issued, 3 h records read, 4 adds issued; combine:
+// 1 rows written
 // Byte layout of that hand-over memory (a context's own allocation, or the
 // library's static scratch in lt_noalloc.hip): launch counters, 8 logit
 // copies, h record lines, partial-output lines, the XCD probe's ids, and

@@ -69,7 +69,7 @@ EXPORTS = [
     "lt_init", "lt_destroy", "lt_last_error", "lt_sync", "lt_stream", "lt_tensor_upload", "lt_tensor_read", "lt_tensor_clone",
     "lt_tensor_free", "lt_tensor_bytes", "lt_matvec", "lt_ffn_dense", "lt_moe_router_topk", "lt_expert_gate_up_id",
     "lt_expert_down_id", "lt_moe_forward", "lt_moe_forward_noalloc", "lt_moe_prefill", "lt_rmsnorm", "lt_add_rmsnorm",
-    "lt_rmsnorm_weighted_raw_scaled", "lt_moe_tail", "lt_gemma4_moe_block",
+    "lt_rmsnorm_weighted_raw_scaled", "lt_moe_tail", "lt_gemma4_moe_block", "lt_profile_report",
 ]
 
 _lib = None
@@ -107,6 +107,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "lt_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, u32, u32, C.c_float, u32]),
         "lt_rmsnorm_weighted_raw_scaled": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, u32, C.c_float, u32]),
         "lt_moe_tail": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, u32, C.c_float, u32]),
+        "lt_profile_report": (sz, [vp, vp, sz]),
         "lt_gemma4_moe_block": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_float, C.c_float, u32, u32,
                                       u32, u32, vp, vp]),
     }
@@ -196,6 +197,15 @@ class Context:
 
     def sync(self):
         self._check(self.lib.lt_sync(self.ptr))
+
+    def profile_report(self) -> str:
+        """lt_profile_report: the LT_PROFILE tables ("" when profiling is off)."""
+        n = int(self.lib.lt_profile_report(self.ptr, None, 0))
+        if n == 0:
+            return ""
+        buf = C.create_string_buffer(n + 1)
+        self.lib.lt_profile_report(self.ptr, buf, n + 1)
+        return buf.value.decode(errors="replace")
 
     @property
     def stream(self) -> int:

@@ -490,6 +490,49 @@ def test_gpu_first_fused_call_not_capturable(cfg3):
             t.free()
 
 
+def test_gpu_profile_timeline(cfg3):
+    # LT_PROFILE=timeline (read by lt_init): call spans and the phase stamps
+    # of the single-launch kernel; the phases of one launch come in the order
+    # the hand-overs impose, and the results are those of an unprofiled context
+    c, _ = cfg3
+    w = c["weights"]
+    os.environ["LT_PROFILE"] = "timeline"
+    try:
+        cp = lt.Context(0)
+    finally:
+        del os.environ["LT_PROFILE"]
+    try:
+        tens = lt.upload_moe(cp, w)
+        with lt.Context(0) as c0:
+            t0 = lt.upload_moe(c0, w)
+            for i in range(6):
+                x = synth.config3_x(700 + i)
+                a, b = np.zeros(w.d_model, np.float32), np.zeros(w.d_model, np.float32)
+                cp.moe_forward(a, x, *tens, 8, w.d_expert, norm_topk=True, deterministic=True)
+                c0.moe_forward(b, x, *t0, 8, w.d_expert, norm_topk=True, deterministic=True)
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+            for t in t0:
+                t.free()
+        rep = cp.profile_report()
+        print(rep)
+        assert "lt_moe_forward" in rep and "6 launches" in rep
+
+        def med(role, phase):
+            line = next(l for l in rep.splitlines() if l.startswith(role) and phase in l)
+            return float(line.split()[-2])
+
+        published = med("router", "logit published")
+        seen = med("gate/up", "logits seen")
+        known = med("gate/up", "expert known")
+        hpub = med("gate/up", "h record published")
+        adds = med("down", "adds issued")
+        assert 0 < published < seen <= known < hpub < adds < 1000, rep
+        for t in tens:
+            t.free()
+    finally:
+        cp.close()
+
+
 def test_gpu_errors(ctx):
     with pytest.raises(UnsupportedError):
         ctx.upload(np.zeros(64, np.uint8), ggml.F16, 1, 32)
