@@ -38,7 +38,7 @@ struct SpanStat {
     size_t n = 0;
     double total_ms = 0, min_ms = 1e30, max_ms = 0;
 };
-constexpr int kRoles = 5, kPhases = lt::kStamps - 1;
+constexpr int kRoles = 7, kPhases = lt::kStamps - 1;
 struct Profile {
     int mode = 0;  // 0 off, 1 spans, 2 spans + timeline
     std::vector<PendingSpan> pending;
@@ -50,6 +50,8 @@ struct Profile {
     // per launch: median and largest time of each (role, phase) over blocks, us
     std::vector<float> med[kRoles][kPhases], last[kRoles][kPhases];
     std::vector<float> slot_last[2][16];  // per slot: gate/up h published, down adds issued
+    size_t split = 0;                     // launches with a group (bid % 8) spread over XCDs
+    size_t rot[8] = {};                   // launches by XCD of block 0
 };
 
 }  // namespace
@@ -219,6 +221,13 @@ void prof_harvest(lt_ctx *ctx) {
     if (t0 == ~0ull) return;
     std::vector<float> v[kRoles][kPhases];
     std::vector<float> sl[2][16];
+    bool split = false;
+    for (int b = 0; b < lt::kFusedBlocks; b++) {
+        const uint64_t w = st[(size_t)b * lt::kStamps + lt::kStamps - 1], w0 = st[(size_t)(b & 7) * lt::kStamps + lt::kStamps - 1];
+        split |= ((w >> 16) & 15) != ((w0 >> 16) & 15);
+    }
+    P.split += split;
+    P.rot[(st[lt::kStamps - 1] >> 16) & 7]++;
     for (int b = 0; b < lt::kFusedBlocks; b++) {
         const uint64_t *t = &st[(size_t)b * lt::kStamps];
         const int role = (int)(t[lt::kStamps - 1] & 0xff), slot = (int)((t[lt::kStamps - 1] >> 8) & 15);
@@ -381,11 +390,16 @@ int check_fused_err(lt_ctx *ctx) {
     if (!ctx->fused_err) return LT_OK;
     const uint32_t v = __atomic_exchange_n(ctx->fused_err, 0u, __ATOMIC_SEQ_CST);
     if (!v) return LT_OK;
+    uint32_t d[5];  // first timed-out wait: block + 1, site, index, tag or count seen, epoch expected
+    for (int i = 0; i < 5; i++) d[i] = __atomic_exchange_n(ctx->fused_err + 2 + i, 0u, __ATOMIC_SEQ_CST);
     // Later launches publish h through memory (agent scope) instead of an
     // XCD's L2, in case the placement the one-time probe saw has changed.
     ctx->xcd_local = ctx->fsc.xcd_local = ctx->na_fsc.xcd_local = 0;
-    return fail(ctx, LT_ERR_DEVICE, "fused MoE kernel: a hand-over wait timed out (code %u); outputs of that call are NaN",
-                v);
+    return fail(ctx, LT_ERR_DEVICE,
+                "fused MoE kernel: a hand-over wait timed out (code 0x%x: 1 gate/up logits, 2 down logits, 4 down h "
+                "records, 8 combine, 0x10 shared-FFN logits or last h word, 0x20 shared-FFN h; first recorded: block %d, site "
+                "0x%x, index %u, saw %u, expected epoch %u); outputs of that call are NaN",
+                v, (int)d[0] - 1, d[1], d[2], d[3], d[4]);
 }
 
 int matvec_dev(lt_ctx *ctx, const DevTensor &W, const float *x, float *y) {
@@ -855,33 +869,82 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
 
 namespace {
 
+// A Q8_0 dense FFN the fused kernel computes itself: gate and up [S][D],
+// down [D][S] (no padding of the down rows).
+bool shared_fusable(const DevTensor &G, const DevTensor &U, const DevTensor &Dn) {
+    return G.type == LT_TYPE_Q8_0 && U.type == LT_TYPE_Q8_0 && Dn.type == LT_TYPE_Q8_0 &&
+           Dn.cols == G.total_rows && G.total_rows <= (size_t)lt::kFusedMaxShared;
+}
+
+// The fused kernel's description of a layer (sg null: no shared FFN; R, GU,
+// Dn null and k 0: the dense FFN alone).
+lt::FusedLayer fused_layer(const DevTensor &R, const DevTensor &GU, const DevTensor &Dn, const lt_tensor *sg,
+                           const lt_tensor *su, const lt_tensor *sd, uint32_t k, uint32_t d_expert, uint32_t flags) {
+    lt::FusedLayer L{};
+    L.det = (flags & LT_MOE_DETERMINISTIC) ? 1 : 0;
+    L.R = &R;
+    L.GU = &GU;
+    L.Dn = &Dn;
+    L.E = (int)R.total_rows;
+    L.D = (int)GU.cols;
+    L.F = (int)d_expert;
+    L.Kd = (int)Dn.cols;
+    L.k = (int)k;
+    if (sg) {
+        L.SG = &sg->t;
+        L.SU = &su->t;
+        L.SD = &sd->t;
+        L.S = (int)sg->t.total_rows;
+    }
+    return L;
+}
+
 // The decode MoE layer on device pointers.
 int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const float *bias, const DevTensor &GU,
             const DevTensor &D, const lt_tensor *sh_gate, const lt_tensor *sh_up, const lt_tensor *sh_down,
             uint32_t k, uint32_t d_expert, uint32_t act, uint32_t flags) {
     int rc;
-    const float *base = nullptr;
-    if (sh_gate) {
-        if ((rc = ensure(ctx, ctx->shared, D.rows * 4))) return rc;
-        if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p))) return rc;
-        base = (const float *)ctx->shared.p;
-    }
     const size_t Kd = D.cols;
-    if (!(flags & LT_MOE_UNFUSED) && R.type == LT_TYPE_F32 && GU.type == LT_TYPE_Q4_K && D.type == LT_TYPE_Q4_K) {
-        const lt::FusedPlan pl = lt::plan_moe_fused((int)R.total_rows, (int)GU.cols, (int)d_expert, (int)Kd, (int)k);
+    const bool fusable = !(flags & LT_MOE_UNFUSED) && (R.type == LT_TYPE_F32 || R.type == LT_TYPE_Q8_0) &&
+                         GU.type == LT_TYPE_Q4_K && D.type == LT_TYPE_Q4_K;
+    // the shared FFN inside the same launch: Q8_0, unpadded down, atomic combine
+    bool sh_in = fusable && sh_gate && shared_fusable(sh_gate->t, sh_up->t, sh_down->t) &&
+                 !(flags & LT_MOE_DETERMINISTIC);
+    if (fusable) {
+        lt::FusedPlan pl = lt::plan_moe_fused(fused_layer(R, GU, D, sh_in ? sh_gate : nullptr, sh_up, sh_down, k,
+                                                          d_expert, flags));
+        if (!pl.ok && sh_in) {  // no room for the shared FFN's blocks: it runs first, as the base
+            sh_in = false;
+            pl = lt::plan_moe_fused(fused_layer(R, GU, D, nullptr, nullptr, nullptr, k, d_expert, flags));
+        }
         if (pl.ok) {
+            const float *base = nullptr;
+            if (sh_gate && !sh_in) {
+                if ((rc = ensure(ctx, ctx->shared, D.rows * 4))) return rc;
+                if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p)))
+                    return rc;
+                base = (const float *)ctx->shared.p;
+            }
             if ((rc = ensure_fused(ctx)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
                 (rc = ensure(ctx, ctx->w, kMaxK * 4)))
                 return rc;
             ctx->prof.stamps_pending = ctx->prof.stamps != nullptr;
             return launch_rc(ctx,
-                             lt::launch_moe_fused(pl, R, bias, GU, D, x, (int)k, (int)d_expert, act,
-                                                  (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, base,
+                             lt::launch_moe_fused(pl,
+                                                  fused_layer(R, GU, D, sh_in ? sh_gate : nullptr, sh_up, sh_down,
+                                                              k, d_expert, flags),
+                                                  bias, x, act, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, base,
                                                   (flags & LT_MOE_ACCUMULATE) ? 1 : 0,
                                                   (flags & LT_MOE_DETERMINISTIC) ? 1 : 0, out, (uint32_t *)ctx->ids.p,
                                                   (float *)ctx->w.p, ctx->fsc, ctx->stream),
                              "moe_fused");
         }
+    }
+    const float *base = nullptr;
+    if (sh_gate) {
+        if ((rc = ensure(ctx, ctx->shared, D.rows * 4))) return rc;
+        if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p))) return rc;
+        base = (const float *)ctx->shared.p;
     }
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
@@ -963,30 +1026,38 @@ extern "C" int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, c
                     "allocation-free MoE: flags 0x%x not allowed (device pointers only: no LT_HOST_IO; no "
                     "LT_MOE_UNFUSED)",
                     flags & ~(uint32_t)(LT_MOE_NORM_TOPK | LT_MOE_ACCUMULATE | LT_MOE_DETERMINISTIC));
-    if (sh_gate || sh_up || sh_down)
-        return fail(ctx, LT_ERR_UNSUPPORTED, "allocation-free MoE: no shared FFN (it needs context scratch)");
     const size_t d_model = gate_up->t.cols;
     int rc;
     if ((rc = check_router(ctx, router, d_model, k))) return rc;
     if ((rc = check_experts(ctx, gate_up, down, d_model, d_expert, router->t.total_rows, k))) return rc;
+    const bool shared = sh_gate || sh_up || sh_down;
+    if (shared) {
+        if (!sh_gate || !sh_up || !sh_down) return fail(ctx, LT_ERR_INVALID, "shared FFN needs gate, up and down");
+        if ((rc = check_ffn(ctx, sh_gate, sh_up, sh_down, d_model))) return rc;
+        if (!shared_fusable(sh_gate->t, sh_up->t, sh_down->t) || (flags & LT_MOE_DETERMINISTIC))
+            return fail(ctx, LT_ERR_UNSUPPORTED,
+                        "allocation-free MoE: a shared FFN must be Q8_0 with down K == d_ffn <= %d, and the "
+                        "combine atomic (no LT_MOE_DETERMINISTIC)",
+                        lt::kFusedMaxShared);
+    }
     if (!aligned16(x)) return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
     const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
-    if (R.type != LT_TYPE_F32 || GU.type != LT_TYPE_Q4_K || D.type != LT_TYPE_Q4_K)
+    if ((R.type != LT_TYPE_F32 && R.type != LT_TYPE_Q8_0) || GU.type != LT_TYPE_Q4_K || D.type != LT_TYPE_Q4_K)
         return fail(ctx, LT_ERR_UNSUPPORTED,
-                    "allocation-free MoE: single-launch kernel only (F32 router, Q4_K gate_up and down)");
-    const lt::FusedPlan pl = lt::plan_moe_fused((int)R.total_rows, (int)GU.cols, (int)d_expert, (int)D.cols, (int)k);
+                    "allocation-free MoE: single-launch kernel only (F32 or Q8_0 router, Q4_K gate_up and down)");
+    const lt::FusedLayer L = fused_layer(R, GU, D, shared ? sh_gate : nullptr, sh_up, sh_down, k, d_expert, flags);
+    const lt::FusedPlan pl = lt::plan_moe_fused(L);
     if (!pl.ok)
         return fail(ctx, LT_ERR_UNSUPPORTED,
                     "allocation-free MoE: shape beyond the static scratch's kernel (d_model %zu, %zu experts, "
-                    "d_expert %u, down K %zu, k %u; limits: d_model 256..2048 in steps of 256, down K <= 1024, "
-                    "<= 256 experts, k <= 16)",
-                    GU.cols, R.total_rows, d_expert, D.cols, k);
+                    "d_expert %u, down K %zu, k %u%s; limits: d_model 256..4096 in steps of 256, down K <= 1024, "
+                    "<= 256 experts, k <= 16, and the grid's room for the shared FFN)",
+                    GU.cols, R.total_rows, d_expert, D.cols, k, shared ? ", shared FFN" : "");
     ctx->prof.stamps_pending = ctx->prof.stamps != nullptr;
     uint32_t *ids_dev = (uint32_t *)(ctx->na_base + lt::kFusedIdsOff);
     float *w_dev = (float *)(ctx->na_base + lt::kFusedWOff);
     rc = launch_rc(ctx,
-                   lt::launch_moe_fused(pl, R, router_bias, GU, D, x, (int)k, (int)d_expert, act,
-                                        (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, nullptr,
+                   lt::launch_moe_fused(pl, L, router_bias, x, act, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, nullptr,
                                         (flags & LT_MOE_ACCUMULATE) ? 1 : 0, (flags & LT_MOE_DETERMINISTIC) ? 1 : 0,
                                         out, ids_dev, w_dev, ctx->na_fsc, ctx->stream),
                    "moe_fused (allocation-free)");
@@ -1310,13 +1381,15 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                  "us from the first block's start; median over launches of the block median / the last block\n",
                  P.launches);
         o += line;
-        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine"};
+        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "sh.g/u", "sh.down"};
         static const char *phases[kRoles][kPhases] = {
             {},
             {"block start", "first row chunk in", "logit published"},
             {"block start", "logits seen", "expert known", "dot products done", "h record published"},
             {"block start", "logits seen", "weight loads issued", "h records read", "adds issued"},
-            {"block start", "rows written"}};
+            {"block start", "rows written"},
+            {"block start", "h rows published"},
+            {"block start", "h staged", "adds issued"}};
         snprintf(line, sizeof line, "%-9s %-22s %10s %10s\n", "role", "phase", "median", "last");
         o += line;
         for (int r = 1; r < kRoles; r++)
@@ -1335,6 +1408,15 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                 }
             o += "\n";
         }
+        snprintf(line, sizeof line, "XCD of block 0 per launch:");
+        o += line;
+        for (int q = 0; q < 8; q++)
+            if (P.rot[q]) {
+                snprintf(line, sizeof line, " %d:%zu", q, P.rot[q]);
+                o += line;
+            }
+        snprintf(line, sizeof line, "; launches with a group (block index %% 8) on more than one XCD: %zu\n", P.split);
+        o += line;
     }
     if (buf && len) {
         const size_t n = o.size() < len - 1 ? o.size() : len - 1;

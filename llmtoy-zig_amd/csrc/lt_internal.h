@@ -328,8 +328,9 @@ hipError_t launch_expert_down_q4k(const DevTensor &D, const float *h, const uint
                                   uint32_t k, const float *base, int accumulate, float *out, hipStream_t s,
                                   const float *dscale = nullptr);
 
-// The whole decode MoE layer in one launch (lt_moe_fused.hip): F32 router,
-// Q4_K gate_up and down.  The grid is always kFusedBlocks workgroups, which
+// The whole decode MoE layer in one launch (lt_moe_fused.hip): F32 or Q8_0
+// router, Q4_K gate_up and down, optionally a Q8_0 shared dense FFN -- or a
+// Q8_0 dense FFN alone.  The grid is always kFusedBlocks workgroups, which
 // keeps the per-block launch counters equal.
 constexpr int kFusedBlocks = 1024;
 constexpr int kFusedMaxRouterBlocks = 64;  // E <= 256, 4 logits per block
@@ -337,13 +338,28 @@ constexpr int kLgCopy = kFusedMaxRouterBlocks * 16;  // words per copy of the lo
 struct FusedPlan {
     bool ok;     // the shape fits the fused kernel
     int per;     // logits per lane in the top-k wavefront (2 or 4)
+    int wide;    // expert gate/up rows of 9-16 super-blocks (two positions per lane)
+    int qrouter; // Q8_0 router (dotQ8_0 order), else F32
     int NRg;     // router blocks per XCD group
     int rb;      // logit rows per router block (2, or 4 when the grid is full)
     int SPG;     // slots per XCD group (ceil(k / 8))
     int G;       // h groups of 16 per slot (down K / 16)
     int NDg;     // down blocks per slot
-    int NCg;     // combining blocks per XCD group
+    int NCg;     // combining blocks per XCD group (deterministic combine only)
+    int NSG;     // shared-FFN gate/up blocks per XCD group
+    int NSD;     // shared-FFN down blocks per XCD group
+    int sg_rows; // row pairs per shared gate/up block
+    int sd_rows; // output rows per shared down block
     size_t lds;  // dynamic LDS bytes per block
+};
+// A layer for the fused kernel.  MoE: R, GU, Dn set (E experts, k > 0),
+// optionally a shared FFN SG, SU, SD (Q8_0, S rows) added to the experts'
+// combine.  Dense FFN alone: R, GU, Dn null, k = 0, SG, SU, SD set.
+struct FusedLayer {
+    const DevTensor *R, *GU, *Dn;
+    const DevTensor *SG, *SU, *SD;
+    int E, D, F, Kd, k, S;
+    int det;  // slot-order combine (combining blocks; no shared FFN)
 };
 // Device memory the fused kernel hands results over through; zeroed once
 // when allocated and never cleared again (words carry launch epochs).
@@ -355,17 +371,20 @@ struct FusedScratch {
     uint32_t *err;       // host-mapped error word (device address)
     int xcd_local;       // blocks with equal index % 8 share an XCD (probe_xcd_groups)
     uint64_t *stamps = nullptr;  // LT_PROFILE=timeline: [kFusedBlocks][kStamps] phase stamps, else null
+    uint64_t *shh = nullptr;     // shared FFN h words [kFusedMaxShared]
 };
 // Phase stamps of one launch (LT_PROFILE=timeline): thread 0 of block b
 // writes stamps[b * kStamps + i], wall-clock ticks (100 MHz) at the end of
 // phase i of its role, and stamps[b * kStamps + kStamps - 1] = role | slot
-// << 8 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine).
+// << 8 | XCD << 16 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine,
+// 5 shared-FFN gate/up, 6 shared-FFN down).
 constexpr int kStamps = 8;
 enum : int { kStampStart = 0 };
 // router: 1 first row chunk in, 2 logit published; gate/up: 1 logits seen,
 // 2 expert known, 3 dot products done, 4 h record published; down: 1 logits
 // seen, 2 weight loads issued, 3 h records read, 4 adds issued; combine:
-// 1 rows written
+// 1 rows written; shared gate/up: 1 h rows published; shared down: 1 h
+// staged, 2 adds issued
 // Byte layout of that hand-over memory (a context's own allocation, or the
 // library's static scratch in lt_noalloc.hip): launch counters, 8 logit
 // copies, h record lines, partial-output lines, the XCD probe's ids, and
@@ -377,7 +396,11 @@ constexpr size_t kFusedPlOff = kFusedHlOff + (size_t)kFusedBlocks * 16 * 8;
 constexpr size_t kFusedXccOff = kFusedPlOff + (size_t)kFusedBlocks * 4 * 16 * 8;
 constexpr size_t kFusedIdsOff = kFusedXccOff + (size_t)kFusedBlocks * 4;
 constexpr size_t kFusedWOff = kFusedIdsOff + 256;
-constexpr size_t kFusedScratchBytes = kFusedWOff + 256;  // 729,600 B
+// The shared FFN's h values ([S] hand-over words, S <= kFusedMaxShared)
+// follow.
+constexpr int kFusedMaxShared = 8192;
+constexpr size_t kFusedShOff = kFusedWOff + 256;
+constexpr size_t kFusedScratchBytes = kFusedShOff + (size_t)kFusedMaxShared * 8;  // 795,136 B
 // counters, lg, hl, pl at base; err and xcd_local are the caller's
 inline FusedScratch fused_scratch_at(uint8_t *base, uint32_t *err, int xcd_local) {
     FusedScratch s;
@@ -387,6 +410,7 @@ inline FusedScratch fused_scratch_at(uint8_t *base, uint32_t *err, int xcd_local
     s.pl = reinterpret_cast<uint64_t *>(base + kFusedPlOff);
     s.err = err;
     s.xcd_local = xcd_local;
+    s.shh = reinterpret_cast<uint64_t *>(base + kFusedShOff);
     return s;
 }
 // Device address of this GPU's copy of the static scratch of lt_noalloc.hip
@@ -398,9 +422,8 @@ hipError_t noalloc_scratch(int device, uint8_t **base);
 // of block b % 8 (the round-robin placement the fused kernel's same-XCD
 // hand-overs rely on for speed).
 hipError_t probe_xcd_groups(uint32_t *dev_ids, hipStream_t s, int *local);
-FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k);
-hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
-                            const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,
-                            const float *base, int accumulate, int deterministic, float *out, uint32_t *ids_out,
-                            float *w_out, const FusedScratch &sc, hipStream_t s);
+FusedPlan plan_moe_fused(const FusedLayer &L);
+hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const float *bias, const float *x,
+                            uint32_t act, uint32_t norm, const float *base, int accumulate, int deterministic,
+                            float *out, uint32_t *ids_out, float *w_out, const FusedScratch &sc, hipStream_t s);
 }  // namespace lt

@@ -14,13 +14,18 @@
 // in-group index i = bid / 8 picks the role:
 //
 //   i < NRg                 router: logit rows 2*bid + [0, 2), dotf32 order
-//                           (4*bid + [0, 4) when the grid has no room)
+//                           (4*bid + [0, 4) when the grid has no room), or
+//                           dotQ8_0 order for a Q8_0 router
+//   next NSG                shared FFN gate/up: rows 8u + x of sg_rows each
 //   next SPG*G              gate/up: slot x + 8u, h group jg (16 values)
+//   next NSD                shared FFN down: rows 8u + x of sd_rows each
 //   next SPG*NDg            down: slot x + 8u, rows 64j + [0, 64)
 //   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
 //
-// (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = NCg = ceil(D /
-// 64)).  Every hand-over is coherent across XCDs except the h records when
+// (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = ceil(D / 64),
+// NCg = NDg with the deterministic combine, else 0; NSG = NSD = 0 without a
+// shared FFN, which otherwise takes the rest of the group's blocks).  With no
+// experts (k = 0) only the shared FFN roles run: a Q8_0 dense FFN alone.  Every hand-over is coherent across XCDs except the h records when
 // local is set: those are workgroup-scope stores that only the writer's L2
 // holds, correct only while the round-robin placement holds (probed once per
 // context by probe_xcd_groups).  Were it to change, the down blocks' bounded
@@ -68,6 +73,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace lt {
 
 namespace {
@@ -92,8 +99,14 @@ struct FusedArgs {
     uint64_t *lg;        // logits, 8 copies of kLgCopy words (logit r = word r)
     uint64_t *hl;        // h record lines [k*G][16]
     uint64_t *pl;        // partial-output lines [k*NDg*4][16]
-    uint32_t *err;       // host-mapped error word
+    uint32_t *err;       // host-mapped error word (bit mask of the waits that timed out)
     uint64_t *stamps;    // phase stamps (LT_PROFILE=timeline) or null
+    const uint8_t *rq;   // Q8_0 router: quant plane [E][nb][32] (qrouter)
+    const uint16_t *rd;  //   and f16 scale plane [E][nb]
+    const uint8_t *sgq, *suq, *sdq;   // shared FFN (Q8_0) quant planes: gate, up [S][D/32], down [D][S/32]
+    const uint16_t *sgd, *sud, *sdd;  //   and their scale planes
+    uint64_t *shh;       // shared FFN h [S], hand-over words
+    int qrouter, S, NSG, NSD, sg_rows, sd_rows;
     int E, D, nsb, F, nsbd, k, norm, act, accumulate, det, local;
     int dn_delay;  // wall-clock ticks from seeing the logits to the down weight loads
     int rb;        // logit rows per router block: 2 or 4
@@ -122,6 +135,20 @@ __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t ep) { return (uint32
 
 __device__ __forceinline__ void report_timeout(uint32_t *err, uint32_t code) {
     __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// The first timed-out wait of a call also leaves what it saw in err[2..6]:
+// block + 1, site code, the word index, the word's epoch tag (or count)
+// seen, and the epoch expected.
+__device__ __forceinline__ void report_detail(uint32_t *err, int bid, uint32_t code, uint32_t index, uint32_t seen,
+                                              uint32_t ep) {
+    uint32_t zero = 0;
+    if (__hip_atomic_compare_exchange_strong(err + 2, &zero, (uint32_t)bid + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_SYSTEM)) {
+        __hip_atomic_store(err + 3, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(err + 4, index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(err + 5, seen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(err + 6, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 }
 
 // Phase stamps of thread 0 (LT_PROFILE=timeline; `on` = a.stamps != null,
@@ -332,6 +359,21 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Atomic combine: the start values of out (0, the base, or out + base).
+// Router block c < nvalid = ceil(E / rb) -- the blocks that publish logits
+// -- stores rows 256 c + tid + 256 nvalid i with coherent stores, and every
+// router block waits for their acknowledgement (s_waitcnt) and a block
+// barrier before any of its logits goes out: a reader that has seen any
+// logit of block c may add to the rows c stores.
+__device__ __forceinline__ void store_starts(const FusedArgs &a, int bid, int tid) {
+    const int nvalid = (a.E + a.rb - 1) / a.rb;
+    if (a.det || bid >= nvalid || (a.accumulate && !a.base)) return;
+    for (int orow = bid * kThreads + tid; orow < a.D; orow += nvalid * kThreads) {
+        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
+        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, int bid, int tid, int wave,
                                             int lane, Stamps &S) {
 #pragma clang fp contract(off)
@@ -339,15 +381,10 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
     const int row = bid * 4 + wave;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
-    // atomic combine: output row bid * 256 + tid starts at base, 0, or out +
-    // base (the router blocks cover 8 * NRg * 256 >= 2048 >= D rows).  The
-    // store goes out before the router loads: stores count in vmcnt until
-    // acknowledged, and it is acknowledged long before the loads return.
-    const int orow = bid * kThreads + tid;
-    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
-        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
-        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // the start values go out before the router loads: stores count in
+    // vmcnt until acknowledged, and they are acknowledged long before the
+    // loads return
+    store_starts(a, bid, tid);
     // every load unconditional (chunk indices clamped), so that the waits
     // for chunk i count only the loads issued after it
     float4 wv[8], xv[8];
@@ -387,9 +424,10 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
 #pragma unroll
     for (int l = 1; l < 8; l++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), l));
     if (a.bias) sum = sum + bias;
-    // this wavefront's output-row stores are acknowledged (memory-side)
-    // before the logit that lets down blocks start adding
+    // the block's output-row stores are acknowledged (memory-side) before
+    // the logits that let down blocks start adding
     if (!a.det) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
     S.mark(2, tid);
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
@@ -414,49 +452,47 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
     const int row = 2 * bid + rl;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
-    // atomic combine: output rows start values, as in role_router
-    const int orow = bid * kThreads + tid;
-    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
-        const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
-        __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // every load unconditional (stride clamped), so that the wait for load
-    // q counts only the loads issued after it
-    float4 wv[4], xv[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        int it = 16 * q + (lane >> 2);
-        it = it < nit ? it : nit - 1;
-        const int e = 32 * it + 16 * h + 4 * (lane & 3);
-        wv[q] = *reinterpret_cast<const float4 *>(wr + e);
-        xv[q] = *reinterpret_cast<const float4 *>(a.x + e);
-    }
+    store_starts(a, bid, tid);
     const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
     const uint32_t c0 = epoch_peek(a.counters, bid);
     float acc = 0.0f;
+    // loads in batches of 4 (64 strides: D <= 2048 in one batch, 4096 in two)
+    for (int qb = 0; 16 * qb < nit; qb += 4) {
+        // every load unconditional (stride clamped), so that the wait for load
+        // q counts only the loads issued after it
+        float4 wv[4], xv[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        if (16 * q < nit) {
-            float4 pr;
-            pr.x = wv[q].x * xv[q].x;
-            pr.y = wv[q].y * xv[q].y;
-            pr.z = wv[q].z * xv[q].z;
-            pr.w = wv[q].w * xv[q].w;
-            float *buf = prod + (q & 1) * 256;
-            *reinterpret_cast<float4 *>(buf + 4 * lane) = pr;
-            if (q == 0) S.mark(1, tid);
-            wave_lds_sync();
-            // n = 8 or 16 strides in this load; reads past n stay inside the
-            // buffer and are not added
-            const int n = nit - 16 * q < 16 ? nit - 16 * q : 16;
-            float v[16];
+        for (int q = 0; q < 4; q++) {
+            int it = 16 * (qb + q) + (lane >> 2);
+            it = it < nit ? it : nit - 1;
+            const int e = 32 * it + 16 * h + 4 * (lane & 3);
+            wv[q] = *reinterpret_cast<const float4 *>(wr + e);
+            xv[q] = *reinterpret_cast<const float4 *>(a.x + e);
+        }
 #pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = buf[u * 16 + (lane & 15)];
+        for (int q = 0; q < 4; q++) {
+            if (16 * (qb + q) < nit) {
+                float4 pr;
+                pr.x = wv[q].x * xv[q].x;
+                pr.y = wv[q].y * xv[q].y;
+                pr.z = wv[q].z * xv[q].z;
+                pr.w = wv[q].w * xv[q].w;
+                float *buf = prod + (q & 1) * 256;
+                *reinterpret_cast<float4 *>(buf + 4 * lane) = pr;
+                if (q == 0) S.mark(1, tid);
+                wave_lds_sync();
+                // n = 8 or 16 strides in this load; reads past n stay inside the
+                // buffer and are not added
+                const int n = nit - 16 * (qb + q) < 16 ? nit - 16 * (qb + q) : 16;
+                float v[16];
 #pragma unroll
-            for (int u0 = 0; u0 < 16; u0 += 8)
-                if (u0 < n)
+                for (int u = 0; u < 16; u++) v[u] = buf[u * 16 + (lane & 15)];
 #pragma unroll
-                    for (int u = 0; u < 8; u++) acc = acc + v[u0 + u];
+                for (int u0 = 0; u0 < 16; u0 += 8)
+                    if (u0 < n)
+#pragma unroll
+                        for (int u = 0; u < 8; u++) acc = acc + v[u0 + u];
+            }
         }
     }
     // lanes l < 8: chains 16h + l and 16h + l + 8
@@ -478,6 +514,272 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
+// ---------------------------------------------------------------- Q8_0 router
+// Rows 2 bid + [0, 2) of a Q8_0 router: thread t of half h = t >> 7 takes
+// block b = t & 127 (b < nb = D / 32 <= 128) of row 2 bid + h and computes
+// dotQ8_0's block term (quant/dequant.zig:59-78: 8 lane accumulators over 4
+// groups of 8 products, the ordered 8-lane sum, times d); thread 0 of each
+// half adds the nb terms in block order (the reference's running total) and
+// the bias, and lanes 0-7 of its wavefront publish the logit's 8 copies.
+__device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem, int bid, int tid, int lane,
+                                               Stamps &S) {
+#pragma clang fp contract(off)
+    float *terms = reinterpret_cast<float *>(smem);  // [2][128]
+    const int h = tid >> 7, b = tid & 127;
+    const int nb = a.D >> 5;
+    const int row = 2 * bid + h;
+    const bool valid = row < a.E;
+    store_starts(a, bid, tid);
+    // every load unconditional (clamped row and block)
+    const size_t blk = (size_t)(valid ? row : 0) * nb + (b < nb ? b : nb - 1);
+    const uint4 q0 = ld16(a.rq + blk * 32), q1 = ld16(a.rq + blk * 32 + 16);
+    const uint32_t d16 = a.rd[blk];
+    float xv[32];
+    {
+        const float4 *xp = reinterpret_cast<const float4 *>(a.x + (b < nb ? b : nb - 1) * 32);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 v4 = xp[t];
+            xv[4 * t] = v4.x;
+            xv[4 * t + 1] = v4.y;
+            xv[4 * t + 2] = v4.z;
+            xv[4 * t + 3] = v4.w;
+        }
+    }
+    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    float acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) acc[l] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const int e = 8 * j + l;
+            const float p = (float)(int)(int8_t)(qw[e >> 2] >> (8 * (e & 3))) * xv[e];
+            acc[l] = acc[l] + p;
+        }
+    float r = acc[0];
+#pragma unroll
+    for (int l = 1; l < 8; l++) r = r + acc[l];
+    if (b < nb) terms[h * 128 + b] = r * f16_bits_to_f32(d16);
+    S.mark(1, tid);
+    // this thread's output-row store is acknowledged before the logits
+    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (b < 64) {  // wavefronts 0 and 2: one row each
+        float total = 0.0f;
+        if (lane == 0) {
+            for (int bb = 0; bb < nb; bb++) total = total + terms[h * 128 + bb];
+            if (a.bias) total = total + bias;
+        }
+        total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(total), 0));
+        if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(total), c0 + 1u);
+        S.mark(2, tid);
+    }
+    if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
+}
+
+// ---------------------------------------------------------------- shared FFN
+// A Q8_0 dense FFN (the shared expert, gemma4/forward.zig:392-397, or the
+// dense FFN alone, model/forward.zig:304-307) inside the same launch.
+// sum over 16 quants of q * x (the half block's share of a Q8_0 block)
+__device__ __forceinline__ float q8_half_sum(uint4 q, const float *xv) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        a0 = fmaf((float)(int8_t)(w[t] & 0xffu), xv[4 * t], a0);
+        a1 = fmaf((float)(int8_t)((w[t] >> 8) & 0xffu), xv[4 * t + 1], a1);
+        a0 = fmaf((float)(int8_t)((w[t] >> 16) & 0xffu), xv[4 * t + 2], a0);
+        a1 = fmaf((float)(int8_t)(w[t] >> 24), xv[4 * t + 3], a1);
+    }
+    return a0 + a1;
+}
+
+__device__ __forceinline__ void lds_x16(const float *p, float (&xv)[16]) {
+#pragma unroll
+    for (int t = 0; t < 16; t += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(p + t);
+        xv[t] = v.x;
+        xv[t + 1] = v.y;
+        xv[t + 2] = v.z;
+        xv[t + 3] = v.w;
+    }
+}
+
+// The shared FFN's down product is split along K by XCD group: group x owns
+// the Q8_0 blocks [x nb / 8, (x + 1) nb / 8) of each down row (nb = S / 32),
+// i.e. the h rows 32 x nb / 8 ... of the same slice.  Its gate/up blocks
+// compute exactly those h rows and its down blocks read only them, so h
+// never crosses an XCD (the words are handed over like the experts' h
+// records); the 8 groups' partial rows meet in out through float atomics.
+__device__ __forceinline__ void sh_slice(const FusedArgs &a, int x, int &kb0, int &kb1) {
+    const int nb = a.S >> 5;
+    kb0 = (x * nb) >> 3;
+    kb1 = ((x + 1) * nb) >> 3;
+}
+
+// Gate/up: block u of group x takes h rows [lo + u R, lo + u R + R) of its
+// group's slice (R = sg_rows); wavefront w takes rows w + 4 i; lane l takes
+// the half blocks v = l + 64 m of a row (m < 4: D <= 4096), x from LDS.
+// Each row's act(gate . x) * (up . x) goes out as a hand-over word for the
+// group's down blocks.
+__device__ __forceinline__ void role_sh_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int x, int u,
+                                                int bid, int tid, int wave, int lane, Stamps &S) {
+    float *xs = reinterpret_cast<float *>(smem);
+    const int nb = a.D >> 5, nu = 2 * nb, mu = (nu + 63) >> 6;
+    int kb0, kb1;
+    sh_slice(a, x, kb0, kb1);
+    const int j0 = 32 * kb0 + u * a.sg_rows, j1 = min(32 * kb1, j0 + a.sg_rows);
+    uint4 qg[4], qu[4];
+    uint32_t dg[4], du[4];
+    auto load_row = [&](int j) {
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            if (m < mu) {
+                int v = lane + 64 * m;
+                v = v < nu ? v : nu - 1;
+                const size_t blk = (size_t)j * nb + (v >> 1);
+                qg[m] = ld16(a.sgq + blk * 32 + (v & 1) * 16);
+                qu[m] = ld16(a.suq + blk * 32 + (v & 1) * 16);
+                dg[m] = a.sgd[blk];
+                du[m] = a.sud[blk];
+            }
+        }
+    };
+    int j = j0 + wave;
+    if (j < j1) load_row(j);  // the first row's weights before x is staged
+    for (int i = tid * 4; i < a.D; i += kThreads * 4)
+        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.x + i);
+    // the epoch reaches the other wavefronts through LDS: a wavefront that
+    // read the counter after thread 0's increment would see the next epoch
+    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
+    __syncthreads();
+    const uint32_t ep = *s_ep;
+    const bool first = p32_first(lane);
+    for (; j < j1; j += 4) {
+        float g = 0.0f, up = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int v = lane + 64 * m;
+            if (m < mu && v < nu) {
+                float xv[16];
+                lds_x16(xs + v * 16, xv);
+                g = fmaf(f16_bits_to_f32(dg[m]), q8_half_sum(qg[m], xv), g);
+                up = fmaf(f16_bits_to_f32(du[m]), q8_half_sum(qu[m], xv), up);
+            }
+        }
+        if (j + 4 < j1) load_row(j + 4);
+        g = group_sum_dpp<64>(g, first);
+        up = group_sum_dpp<64>(up, first);
+        if (lane == 0) hand_put_group(a.shh + j, __float_as_uint(act_apply((uint32_t)a.act, g) * up), ep, a.local);
+    }
+    S.mark(1, tid);
+}
+
+// Down: block u of group x takes output rows [u R, u R + R) (R = sd_rows)
+// over its group's K slice (nk = kb1 - kb0 <= 32 blocks: S <= 8192);
+// wavefront w takes rows 4 w + 16 i + (l >> 4), 16 lanes per row, lane l
+// the slice's half blocks v = (l & 15) + 16 m (m < 4).  The first step's
+// weights are loaded while thread 0 waits, in a MoE layer, for one logit of
+// each router block that stored start values of its rows, and for the
+// slice's last h word; then the slice of h is read (every word's epoch
+// checked, as the experts' h records are) into LDS.  Partial rows are added
+// into out with float atomics.
+__device__ __forceinline__ void role_sh_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int *s_fail, int x,
+                                             int u, int bid, int tid, int wave, int lane, Stamps &S) {
+    float *hs = reinterpret_cast<float *>(smem);
+    const int nb = a.S >> 5;
+    int kb0, kb1;
+    sh_slice(a, x, kb0, kb1);
+    const int nv = 2 * (kb1 - kb0), mv = (nv + 15) >> 4;
+    const int r0 = u * a.sd_rows, r1 = min(a.D, r0 + a.sd_rows);
+    const int l16 = lane & 15;
+    uint4 qw[4];
+    uint32_t dw[4];
+    auto load_step = [&](int r) {
+        r = min(r, r1 - 1);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            if (m < mv) {
+                int v = l16 + 16 * m;
+                v = v < nv ? v : nv - 1;
+                const size_t blk = (size_t)r * nb + kb0 + (v >> 1);
+                qw[m] = ld16(a.sdq + blk * 32 + (v & 1) * 16);
+                dw[m] = a.sdd[blk];
+            }
+        }
+    };
+    int rb = r0 + 4 * wave + (lane >> 4);
+    if (r0 + 4 * wave < r1) load_step(rb);
+    if (tid == 0) {
+        const uint32_t ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
+        *s_ep = ep;
+        const uint64_t t0 = wall_clock64();
+        bool ok = true;
+        if (a.k > 0 && !(a.accumulate && !a.base) && r0 < r1) {
+            const int nvalid = (a.E + a.rb - 1) / a.rb;
+            const uint64_t *lg = a.lg + (size_t)x * kLgCopy;
+            for (int w = r0 >> 8; w <= (r1 - 1) >> 8 && ok; w++)  // each 256-row window's router block
+                ok = probe_wait(lg + (size_t)a.rb * (w % nvalid), ep, t0);
+            if (!ok) report_detail(a.err, bid, 0x10u, r0, 0, ep);
+        }
+        if (ok && kb1 > kb0) {
+            ok = probe_wait(a.shh + 32 * kb1 - 1, ep, t0);
+            if (!ok) report_detail(a.err, bid, 0x10u, 32 * kb1 - 1, 0, ep);
+        }
+        if (!ok) *s_fail = 1;
+    }
+    __syncthreads();
+    const uint32_t ep = *s_ep;  // from thread 0, as in role_sh_gate_up
+    {
+        const uint64_t t0 = wall_clock64();
+        bool ok = *s_fail == 0;
+        const int n = 32 * (kb1 - kb0);
+        for (int i = tid; i < n && ok; i += kThreads) {
+            uint64_t w = hand_get(a.shh + 32 * kb0 + i);
+            while (!tag_is(w, ep)) {
+                if (wall_clock64() - t0 > kWaitTicks) {
+                    ok = false;
+                    report_detail(a.err, bid, 0x20u, (uint32_t)(32 * kb0 + i), (uint32_t)(w >> 32), ep);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                w = hand_get(a.shh + 32 * kb0 + i);
+            }
+            hs[i] = __uint_as_float((uint32_t)w);
+        }
+        if (!ok) atomicOr(s_fail, 2);
+    }
+    __syncthreads();
+    S.mark(1, tid);
+    const bool fail = *s_fail != 0;
+    for (int rw = r0 + 4 * wave; rw < r1; rw += 16) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int v = l16 + 16 * m;
+            if (m < mv && v < nv) {
+                float xv[16];
+                lds_x16(hs + v * 16, xv);
+                acc = fmaf(f16_bits_to_f32(dw[m]), q8_half_sum(qw[m], xv), acc);
+            }
+        }
+        if (rw + 16 < r1) load_step(rw + 16 + (lane >> 4));
+        acc = group_sum_dpp<16>(acc, false);
+        const int row = rw + (lane >> 4);
+        if (l16 == 0 && row < r1) {
+            const float val = fail ? __int_as_float(0x7fc00000) : acc;
+            if (a.k > 0)
+                (void)__hip_atomic_fetch_add(a.out + row, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (tid == 0 && fail) report_timeout(a.err, (uint32_t)*s_fail << 4);  // 0x10 logits / last h word, 0x20 h
+    S.mark(2, tid);
+}
+
 // ---------------------------------------------------------------- gate/up
 // Block: slot s, h indices j0 = 16 jg + [0, 16), jg < G = Kd/16 (indices
 // >= F are the zero padding of the down K); its record is line s*G + jg.
@@ -485,7 +787,10 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
 // 32-63 the up row; lane & 31 = (super-block, sub-block pair) position, so
 // a lane reads 32 bytes of quants per row and one header word (the quad's
 // four words are shared over DPP).
-template <int PER>
+// WIDE (rows of 9-16 super-blocks): lane position pos covers pos and pos
+// + 32; the second position's weights are loaded as the first's products
+// finish, its x limbs are read from LDS after them.
+template <int PER, int WIDE>
 __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
                                              int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
                                              Stamps &S) {
@@ -503,9 +808,9 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     uint32_t *lb = la + a.D / 4;
     float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
     float *lxs = lsp + a.D / 16;
-    if (tid < a.D / 8) {
-        const float4 f0 = *reinterpret_cast<const float4 *>(a.x + 8 * tid);
-        const float4 f1 = *reinterpret_cast<const float4 *>(a.x + 8 * tid + 4);
+    for (int t8 = tid; t8 < a.D / 8; t8 += kThreads) {  // one pass for D <= 2048
+        const float4 f0 = *reinterpret_cast<const float4 *>(a.x + 8 * t8);
+        const float4 f1 = *reinterpret_cast<const float4 *>(a.x + 8 * t8 + 4);
         const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
         float m = 0.0f;
 #pragma unroll
@@ -525,18 +830,16 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
             pa[i >> 2] |= ((uint32_t)(int)fa & 0xffu) << (8 * (i & 3));
             pb[i >> 2] |= ((uint32_t)(int)fb & 0xffu) << (8 * (i & 3));
         }
-        *reinterpret_cast<uint2 *>(la + 2 * tid) = make_uint2(pa[0], pa[1]);
-        *reinterpret_cast<uint2 *>(lb + 2 * tid) = make_uint2(pb[0], pb[1]);
-        if ((tid & 1) == 0) {
-            lsp[tid >> 1] = sp;
-            lxs[tid >> 1] = xs;
+        *reinterpret_cast<uint2 *>(la + 2 * t8) = make_uint2(pa[0], pa[1]);
+        *reinterpret_cast<uint2 *>(lb + 2 * t8) = make_uint2(pb[0], pb[1]);
+        if ((t8 & 1) == 0) {
+            lsp[t8 >> 1] = sp;
+            lxs[t8 >> 1] = xs;
         }
     }
     if (tid == 0) *s_ep = epoch_commit(a.counters, bid, c0);
     __syncthreads();  // limbs (and s_ep)
-    Limbs xl;
-    {
-        const int gi = lane_on ? sb * 16 + 4 * p : 0;  // first of the window's 4 groups
+    auto read_limbs = [&](Limbs &xl, int gi) {  // gi: first of the window's 4 groups
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const uint4 va = *reinterpret_cast<const uint4 *>(la + (gi + g) * 4);
@@ -549,7 +852,9 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
         xl.sp[0] = sp4.x; xl.sp[1] = sp4.y; xl.sp[2] = sp4.z; xl.sp[3] = sp4.w;
         xl.xs_lo = xs4.x + xs4.y;
         xl.xs_hi = xs4.z + xs4.w;
-    }
+    };
+    Limbs xl;
+    read_limbs(xl, lane_on ? sb * 16 + 4 * p : 0);
     const uint32_t ep = *s_ep;
     if (wave == 0) {  // only this slot's expert: s + 1 selection rounds, no softmax
         float lv[PER];
@@ -580,6 +885,11 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
             hw[r] = *reinterpret_cast<const uint32_t *>(a.gu_hdr + blk * 16 + 4 * (lane & 3));
         }
     }
+    // second position (WIDE): super-block sb + 8 (clamped to the first
+    // when the row has none there: the products are then not added); its
+    // loads reuse row r's registers once row r's first products are done
+    const bool lane_on2 = WIDE && pos + 32 < 4 * a.nsb;
+    const int sb2 = lane_on2 ? sb + 8 : sb;
     float v[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -588,6 +898,26 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
         const PairScale ps = pair_scale(h0, h1, h2, h3, p);
         const uint32_t w8[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
         v[r] = (lane_on && jb + r < a.F) ? q4k_pair_dot(w8, ps, xl) : 0.0f;
+        if (WIDE) {
+            const int jr = jb + r < a.F ? jb + r : a.F - 1;
+            const size_t row = (size_t)e * 2 * a.F + (size_t)half * a.F + jr;
+            const size_t blk = row * a.nsb + sb2;
+            q0[r] = ld16(a.gu_qs + blk * 128 + 32 * p);
+            q1[r] = ld16(a.gu_qs + blk * 128 + 32 * p + 16);
+            hw[r] = *reinterpret_cast<const uint32_t *>(a.gu_hdr + blk * 16 + 4 * (lane & 3));
+        }
+    }
+    if (WIDE) {
+        read_limbs(xl, sb2 * 16 + 4 * p);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            uint32_t h0, h1, h2, h3;
+            quad_header(hw[r], h0, h1, h2, h3);
+            const PairScale ps = pair_scale(h0, h1, h2, h3, p);
+            const uint32_t w8[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            const float d2 = q4k_pair_dot(w8, ps, xl);
+            if (lane_on2 && jb + r < a.F) v[r] += d2;
+        }
     }
     S.mark(3, tid);
     const float t = half_sum4(v, lane);
@@ -765,7 +1095,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     // the slot's h records: thread 0 waits for one record line, then thread
     // q*10 + wl (q < 25) reads word wl of lines q + 25 m, all loads of a
     // pass in flight at once
-    if (tid == 0 && !probe_wait(a.hl + ((size_t)s * G + (size_t)(j % G)) * 16, ep, wall_clock64())) *s_fail = 1;
+    if (tid == 0 && !probe_wait(a.hl + ((size_t)s * G + (size_t)(j % G)) * 16, ep, wall_clock64())) *s_fail = 2;
     __syncthreads();
     bool ok = true;
     {
@@ -807,7 +1137,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
             if (!ok) break;
         }
     }
-    if (!ok) atomicOr(s_fail, 1);
+    if (!ok) atomicOr(s_fail, 2);
     __syncthreads();  // records, s_ids / s_w
     S.mark(3, tid);
     if (s == 0 && j == 0 && tid < a.k) {  // the routing, for the caller
@@ -902,13 +1232,13 @@ __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep,
     if (a.base) acc = a.base[row] + acc;
     if (!ok) {
         acc = __int_as_float(0x7fc00000);
-        report_timeout(a.err, 1u);
+        report_timeout(a.err, 8u);
     }
     a.out[row] = acc;
     S.mark(1, tid);
 }
 
-template <int PER>
+template <int PER, int WIDE>
 __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_ep;
@@ -924,25 +1254,35 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     S.mark(kStampStart, tid);
     uint32_t role = 0;
     if (tid == 0) s_fail = 0;
+    // in-group order: router, shared gate/up, expert gate/up, shared down,
+    // expert down, combine -- every role waits only for earlier ones
     int u = i;
     if (u < a.NRg) {
-        if (a.rb == 2)
+        if (a.qrouter)
+            role_router_q8(a, smem, bid, tid, lane, S);
+        else if (a.rb == 2)
             role_router_pair(a, smem, bid, tid, wave, lane, S);
         else
             role_router(a, smem, bid, tid, wave, lane, S);
         role = 1;
-    } else if ((u -= a.NRg) < a.SPG * a.G) {
+    } else if ((u -= a.NRg) < a.NSG) {
+        role_sh_gate_up(a, smem, &s_ep, x, u, bid, tid, wave, lane, S);
+        role = 5;
+    } else if ((u -= a.NSG) < a.SPG * a.G) {
         const int s = x + 8 * (u / a.G);
         if (s < a.k) {
-            role_gate_up<PER>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
-            if (tid == 0 && s_fail) report_timeout(a.err, 1u);
+            role_gate_up<PER, WIDE>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            if (tid == 0 && s_fail) report_timeout(a.err, 1u);  // logits
             role = 2u | (uint32_t)s << 8;
         }
-    } else if ((u -= a.SPG * a.G) < a.SPG * a.NDg) {
+    } else if ((u -= a.SPG * a.G) < a.NSD) {
+        role_sh_down(a, smem, &s_ep, &s_fail, x, u, bid, tid, wave, lane, S);
+        role = 6;
+    } else if ((u -= a.NSD) < a.SPG * a.NDg) {
         const int s = x + 8 * (u / a.NDg);
         if (s < a.k) {
             role_down<PER, 4>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane, S);
-            if (tid == 0 && s_fail) report_timeout(a.err, 1u);
+            if (tid == 0 && s_fail) report_timeout(a.err, (uint32_t)s_fail << 1);  // 2 logits, 4 h records
             role = 3u | (uint32_t)s << 8;
         }
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
@@ -952,7 +1292,9 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     // no role in this configuration: keep the counter in step
     if (role == 0 && tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     if (S.on && tid == 0) {
-        S.t[kStamps - 1] = role;
+        uint32_t xcc;  // the XCD this block ran on
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        S.t[kStamps - 1] = role | (uint64_t)(xcc & 0xfu) << 16;
 #pragma unroll
         for (int q = 0; q < kStamps; q++) a.stamps[(size_t)bid * kStamps + q] = S.t[q];
     }
@@ -982,55 +1324,102 @@ hipError_t probe_xcd_groups(uint32_t *dev_ids, hipStream_t s, int *local) {
     return hipSuccess;
 }
 
-FusedPlan plan_moe_fused(int E, int D, int F, int Kd, int k) {
+FusedPlan plan_moe_fused(const FusedLayer &L) {
     FusedPlan pl{};
     pl.ok = false;
-    if (D % 256 != 0 || D > 2048 || D < 256) return pl;
-    if (Kd % 256 != 0 || Kd < F || Kd > 1024) return pl;  // 16 lanes = 4 super-blocks x 4 pairs
-    if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return pl;
-    pl.per = E <= 128 ? 2 : 4;
-    // two logit rows per router block where the grid has room, else four
-    pl.rb = 2;
-    pl.NRg = (E + 15) / 16;
-    pl.SPG = (k + 7) / 8;
-    pl.G = Kd / 16;
-    pl.NDg = (D + kDownRows - 1) / kDownRows;
-    pl.NCg = pl.NDg;
-    if (8 * (pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg) > kFusedBlocks) {
-        pl.rb = 4;
-        pl.NRg = (E + 31) / 32;
+    const bool moe = L.k > 0, sh = L.SG != nullptr;
+    const int D = L.D;
+    if (!moe && !sh) return pl;
+    if (D < 256 || D > 4096 || D % (moe ? 256 : 32) != 0) return pl;
+    int used = 0;
+    if (moe) {
+        const int E = L.E, k = L.k, Kd = L.Kd;
+        if (!L.R || !L.GU || !L.Dn) return pl;
+        if (Kd % 256 != 0 || Kd < L.F || Kd > 1024) return pl;  // 16 lanes = 4 super-blocks x 4 pairs
+        if (E < 1 || E > 256 || k > 16 || k > E) return pl;
+        pl.per = E <= 128 ? 2 : 4;
+        pl.wide = D > 2048;
+        pl.qrouter = L.R->type == 8u;  // GGML Q8_0 (else F32)
+        pl.SPG = (k + 7) / 8;
+        pl.G = Kd / 16;
+        pl.NDg = (D + kDownRows - 1) / kDownRows;
+        if (sh && L.det) return pl;  // the shared FFN's rows join the atomic combine only
+        pl.NCg = L.det ? pl.NDg : 0;
+        // two logit rows per router block where the grid has room, else four
+        pl.rb = 2;
+        pl.NRg = (E + 15) / 16;
+        used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
+        // (the four-row F32 router reads rows of at most 2048)
+        if (8 * (used + (sh ? 2 : 0)) > kFusedBlocks && !pl.qrouter && D <= 2048) {
+            pl.rb = 4;
+            pl.NRg = (E + 31) / 32;
+            used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
+        }
+        if (8 * used > kFusedBlocks) return pl;
+        if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;            // h record lines
+        if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;  // partial lines
+    } else {
+        pl.per = 2;
+        pl.rb = 2;
     }
-    if (8 * (pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg) > kFusedBlocks) return pl;
-    if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;                 // h record lines
-    if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;       // partial lines
-    const size_t lds_router = (size_t)(4 * 512 + 16) * 4;
-    const size_t lds_down = (size_t)pl.G * 40;
-    const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
-    pl.lds = lds_router > lds_down ? lds_router : lds_down;
-    if (lds_gu > pl.lds) pl.lds = lds_gu;
-    if (pl.lds < 64) pl.lds = 64;
-    if (pl.lds > 64 * 1024) return pl;
+    if (sh) {
+        const int S = L.S;
+        if (!L.SU || !L.SD || S < 32 || S % 32 != 0 || S > kFusedMaxShared) return pl;
+        // the rest of each group's blocks, shared gate/up : down = 2 : 1 (their bytes)
+        const int left = kFusedBlocks / 8 - used;
+        if (left < 2) return pl;
+        pl.NSG = (2 * left + 1) / 3;
+        pl.NSD = left - pl.NSG;
+        const int slice = 32 * ((S / 32 + 7) / 8);  // h rows of the largest group slice
+        pl.sg_rows = (slice + pl.NSG - 1) / pl.NSG;
+        pl.sd_rows = (D + pl.NSD - 1) / pl.NSD;
+        if (!moe) return pl;  // a dense FFN alone: not in the single launch yet
+    }
+    size_t lds = 64;
+    if (moe) {
+        const size_t lds_router = pl.qrouter ? (size_t)2 * 128 * 4 : (size_t)(4 * 512 + 16) * 4;
+        const size_t lds_down = (size_t)pl.G * 40;
+        const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
+        lds = std::max(lds, std::max(lds_router, std::max(lds_down, lds_gu)));
+    }
+    if (sh) lds = std::max(lds, std::max((size_t)D * 4, (size_t)128 * ((L.S / 32 + 7) / 8)));
+    if (lds > 64 * 1024) return pl;
+    pl.lds = lds;
     pl.ok = true;
     return pl;
 }
 
-template <int PER>
+template <int PER, int WIDE>
 static hipError_t launch_fused_t(const FusedArgs &fa, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((k_moe_fused<PER>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
+    hipLaunchKernelGGL((k_moe_fused<PER, WIDE>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float *bias, const DevTensor &GU,
-                            const DevTensor &Dn, const float *x, int k, int F, uint32_t act, uint32_t norm,
-                            const float *base, int accumulate, int deterministic, float *out, uint32_t *ids_out,
-                            float *w_out, const FusedScratch &sc, hipStream_t s) {
-    FusedArgs fa;
-    fa.router = reinterpret_cast<const float *>(R.p0);
+hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const float *bias, const float *x,
+                            uint32_t act, uint32_t norm, const float *base, int accumulate, int deterministic,
+                            float *out, uint32_t *ids_out, float *w_out, const FusedScratch &sc, hipStream_t s) {
+    FusedArgs fa{};
+    const bool moe = L.k > 0;
+    if (moe) {
+        fa.router = reinterpret_cast<const float *>(L.R->p0);
+        fa.rq = L.R->p0;
+        fa.rd = reinterpret_cast<const uint16_t *>(L.R->p1);
+        fa.gu_hdr = L.GU->p0;
+        fa.gu_qs = L.GU->p1;
+        fa.dn_hdr = L.Dn->p0;
+        fa.dn_qs = L.Dn->p1;
+        fa.nsb = (int)L.GU->blocks_per_row;
+        fa.nsbd = (int)L.Dn->blocks_per_row;
+    }
+    if (L.SG) {
+        fa.sgq = L.SG->p0;
+        fa.sgd = reinterpret_cast<const uint16_t *>(L.SG->p1);
+        fa.suq = L.SU->p0;
+        fa.sud = reinterpret_cast<const uint16_t *>(L.SU->p1);
+        fa.sdq = L.SD->p0;
+        fa.sdd = reinterpret_cast<const uint16_t *>(L.SD->p1);
+    }
     fa.bias = bias;
-    fa.gu_hdr = GU.p0;
-    fa.gu_qs = GU.p1;
-    fa.dn_hdr = Dn.p0;
-    fa.dn_qs = Dn.p1;
     fa.x = x;
     fa.base = base;
     fa.out = out;
@@ -1042,12 +1431,17 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     fa.pl = sc.pl;
     fa.err = sc.err;
     fa.stamps = sc.stamps;
-    fa.E = (int)R.total_rows;
-    fa.D = (int)GU.cols;
-    fa.nsb = (int)GU.blocks_per_row;
-    fa.F = F;
-    fa.nsbd = (int)Dn.blocks_per_row;
-    fa.k = k;
+    fa.shh = sc.shh;
+    fa.qrouter = pl.qrouter;
+    fa.S = L.S;
+    fa.NSG = pl.NSG;
+    fa.NSD = pl.NSD;
+    fa.sg_rows = pl.sg_rows;
+    fa.sd_rows = pl.sd_rows;
+    fa.E = moe ? L.E : 0;
+    fa.D = L.D;
+    fa.F = L.F;
+    fa.k = L.k;
     fa.norm = (int)norm;
     fa.act = (int)act;
     fa.accumulate = accumulate;
@@ -1058,7 +1452,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     // measured for this stream) after the logits are seen, in 10 ns ticks;
     // tuned on config 3 (14.2 MB: 296 ticks; 200 or 360 are 0.2-0.4 us
     // slower per layer).
-    const double gu_bytes = (double)k * 2.0 * F * fa.nsb * 144.0;
+    const double gu_bytes = (double)L.k * 2.0 * L.F * fa.nsb * 144.0;
     fa.dn_delay = 70 + (int)(0.8 * gu_bytes / 50000.0);
     fa.NRg = pl.NRg;
     fa.rb = pl.rb;
@@ -1070,7 +1464,8 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const DevTensor &R, const float
     // blocks' share of the grid (atomic combine) measured 0.15 us slower per
     // layer -- more h record reads and atomics -- though each block's
     // products halve
-    return pl.per == 2 ? launch_fused_t<2>(fa, pl.lds, s) : launch_fused_t<4>(fa, pl.lds, s);
+    if (pl.wide) return pl.per == 2 ? launch_fused_t<2, 1>(fa, pl.lds, s) : launch_fused_t<4, 1>(fa, pl.lds, s);
+    return pl.per == 2 ? launch_fused_t<2, 0>(fa, pl.lds, s) : launch_fused_t<4, 0>(fa, pl.lds, s);
 }
 
 }  // namespace lt

@@ -275,16 +275,17 @@ class Context:
         return out
 
     def moe_forward_noalloc(self, out, x, router: Tensor, gate_up: Tensor, down: Tensor, k: int, d_expert: int,
-                            act=ACT_SILU, norm_topk=False, accumulate=False, bias=None, out_ids=None, out_w=None,
-                            deterministic=False):
+                            act=ACT_SILU, norm_topk=False, accumulate=False, bias=None, shared=None, out_ids=None,
+                            out_w=None, deterministic=False):
         """lt_moe_forward_noalloc: moe_forward on the library's static scratch
         (no device allocation); device arrays only."""
         fl = (LT_MOE_NORM_TOPK if norm_topk else 0) | (LT_MOE_ACCUMULATE if accumulate else 0)
         fl |= LT_MOE_DETERMINISTIC if deterministic else 0
         if self._io(out, x, bias, out_ids, out_w):
             raise InvalidError("moe_forward_noalloc takes device arrays only")
+        sg, su, sd = (t.handle for t in shared) if shared else (None, None, None)
         self._check(self.lib.lt_moe_forward_noalloc(self.ptr, _ptr(out)[0], _ptr(x)[0], router.handle, _ptr(bias)[0],
-                                                    gate_up.handle, down.handle, None, None, None, k, d_expert, act,
+                                                    gate_up.handle, down.handle, sg, su, sd, k, d_expert, act,
                                                     fl, _ptr(out_ids)[0], _ptr(out_w)[0]))
         return out
 

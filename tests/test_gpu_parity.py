@@ -339,6 +339,64 @@ def test_gpu_config4_gemma_like(ctx, pool):
         t.free()
 
 
+def test_gpu_config4_single_launch_vs_unfused(ctx, pool):
+    """Config 4 in the single launch (Q8_0 router role, shared FFN roles,
+    two positions per gate/up lane) against the separate launches and, with
+    LT_MOE_DETERMINISTIC (shared FFN first, then the slot-order kernel), bit
+    for bit run to run; accumulate adds onto out."""
+    c = synth.config4()
+    w = c["weights"]
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    D, S = w.d_model, c["d_shared"]
+    sh = (ctx.upload(c["sh_gate"], ggml.Q8_0, S, D), ctx.upload(c["sh_up"], ggml.Q8_0, S, D),
+          ctx.upload(c["sh_down"], ggml.Q8_0, D, S))
+    x = synth.normal(synth.stream(4, 411), (D,))
+    kw = dict(act=lt.ACT_GELU_TANH, shared=sh)
+    ref, rids, rw = orc.moe_layer_shared(w, x, 8, c["sh_gate"], c["sh_up"], c["sh_down"], S, pool=pool)
+    outs = {}
+    for name, extra in (("fused", {}), ("unfused", {"unfused": True}), ("det", {"deterministic": True}),
+                        ("det2", {"deterministic": True})):
+        out = np.zeros(D, np.float32)
+        ids = np.zeros(8, np.uint32)
+        ctx.moe_forward(out, x, router, gate_up, down, 8, w.d_expert, out_ids=ids, **kw, **extra)
+        assert np.array_equal(ids, rids), (name, ids, rids)
+        assert rel_l2(out, ref) <= REL_L2, name
+        outs[name] = out
+    assert rel_l2(outs["fused"], outs["unfused"]) <= 1e-5
+    assert np.array_equal(outs["det"].view(np.uint32), outs["det2"].view(np.uint32))
+    base = synth.normal(synth.stream(4, 412), (D,))
+    acc = base.copy()
+    ctx.moe_forward(acc, x, router, gate_up, down, 8, w.d_expert, accumulate=True, **kw)
+    assert rel_l2(acc - base, ref) <= REL_L2
+    for t in (router, gate_up, down) + sh:
+        t.free()
+
+
+@pytest.mark.parametrize("D,E,F,k", [(2304, 8, 256, 2), (4096, 16, 512, 4), (2560, 200, 256, 8)])
+def test_gpu_single_launch_wide_rows(ctx, pool, D, E, F, k):
+    """d_model above 2048 in the single launch (two positions per gate/up
+    lane), with few experts (the start values of out spread over the router
+    blocks that publish logits) or many (four logits per lane), with and
+    without accumulate, against the oracle and the separate launches."""
+    w = synth.moe_weights(70 + E, D, E, F)
+    x = synth.normal(synth.stream(70, D + E), (D,))
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    ref, rids, _, agree = orc.moe_forward(w, x, k, pool=pool)
+    assert agree
+    for unfused in (False, True):
+        out = np.zeros(D, np.float32)
+        ids = np.zeros(k, np.uint32)
+        ctx.moe_forward(out, x, router, gate_up, down, k, F, out_ids=ids, unfused=unfused)
+        assert np.array_equal(ids, rids), (unfused, ids, rids)
+        assert rel_l2(out, ref) <= REL_L2, unfused
+    base = synth.normal(synth.stream(71, D), (D,))
+    acc = base.copy()
+    ctx.moe_forward(acc, x, router, gate_up, down, k, F, accumulate=True)
+    assert rel_l2(acc - base, ref) <= REL_L2
+    for t in (router, gate_up, down):
+        t.free()
+
+
 # ------------------------------------------------------------------ edge cases
 @pytest.mark.parametrize("E,k", [(128, 1), (128, 16), (100, 8), (1000, 4), (16, 16)])
 def test_gpu_moe_expert_counts_and_k(ctx, pool, E, k):

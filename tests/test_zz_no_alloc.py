@@ -7,7 +7,7 @@ import pytest
 
 import llmtoy_amd as lt
 import pyoracle as orc
-from llmtoy_amd import synth
+from llmtoy_amd import ggml, synth
 from llmtoy_amd.hip import DeviceArray
 from llmtoy_amd.lib import InvalidError, UnsupportedError
 
@@ -56,6 +56,60 @@ def test_noalloc_matches_moe_forward_two_calls(det):
                 t.free()
 
 
+def _upload_shared(ctx, c):
+    D, S = c["weights"].d_model, c["d_shared"]
+    return (ctx.upload(c["sh_gate"], ggml.Q8_0, S, D), ctx.upload(c["sh_up"], ggml.Q8_0, S, D),
+            ctx.upload(c["sh_down"], ggml.Q8_0, D, S))
+
+
+def test_noalloc_config4_shared_two_calls():
+    """The Gemma4-like layer (Q8_0 router, Q8_0 shared FFN, Q4_K experts,
+    d_model 2816) in the single launch, then the config-3 layer, on the same
+    static scratch."""
+    c = synth.config4()
+    w4 = c["weights"]
+    with lt.Context(0) as ctx, orc.Pool(8) as pool:
+        tens = lt.upload_moe(ctx, w4)
+        sh = _upload_shared(ctx, c)
+        D = w4.d_model
+        for i in range(2):
+            x = c["x"] if i == 0 else synth.normal(synth.stream(4, 500), (D,))
+            xd, od = DeviceArray.from_numpy(x), DeviceArray((D,), np.float32)
+            idd, wd = DeviceArray((8,), np.uint32), DeviceArray((8,), np.float32)
+            ctx.moe_forward_noalloc(od, xd, *tens, 8, w4.d_expert, act=lt.ACT_GELU_TANH, shared=sh, out_ids=idd,
+                                    out_w=wd)
+            ctx.sync()
+            want = np.zeros(D, np.float32)
+            wids = np.zeros(8, np.uint32)
+            ctx.moe_forward(want, x, *tens, 8, w4.d_expert, act=lt.ACT_GELU_TANH, shared=sh, out_ids=wids)
+            ref, rids, rw = orc.moe_layer_shared(w4, x, 8, c["sh_gate"], c["sh_up"], c["sh_down"], c["d_shared"],
+                                                 pool=pool)
+            assert np.array_equal(idd.numpy(), rids) and np.array_equal(wids, rids), (i, idd.numpy(), rids)
+            assert np.allclose(wd.numpy(), rw, rtol=1e-5)
+            assert _rel(od.numpy(), want) <= 1e-6, i
+            assert _rel(od.numpy(), ref) <= 1e-3, i
+            for a in (xd, od, idd, wd):
+                a.free()
+        with pytest.raises(UnsupportedError, match="shared FFN"):
+            xd, od = DeviceArray.from_numpy(c["x"]), DeviceArray((D,), np.float32)
+            try:
+                ctx.moe_forward_noalloc(od, xd, *tens, 8, w4.d_expert, act=lt.ACT_GELU_TANH, shared=sh,
+                                        deterministic=True)
+            finally:
+                xd.free()
+                od.free()
+        # a smaller layer next on the same scratch
+        w = synth.config3()["weights"]
+        x = synth.normal(synth.stream(3, 77), (w.d_model,))
+        t3 = lt.upload_moe(ctx, w)
+        got = _run(ctx, ctx.moe_forward_noalloc, t3, x, 8, w.d_expert, False, True)
+        ref, rids, _, agree = orc.moe_forward(w, x, 8, norm_topk=True, pool=pool)
+        assert agree and np.array_equal(got[1], rids)
+        assert _rel(got[0], ref) <= 1e-3
+        for t in list(tens) + list(sh) + list(t3):
+            t.free()
+
+
 def test_noalloc_rejects_what_it_cannot_run():
     w = synth.moe_weights(42, 512, 16, 256)
     x = synth.normal(synth.stream(42, 7), (512,))
@@ -64,9 +118,9 @@ def test_noalloc_rejects_what_it_cannot_run():
         xd, od = DeviceArray.from_numpy(x), DeviceArray((512,), np.float32)
         with pytest.raises(InvalidError, match="device arrays only"):
             ctx.moe_forward_noalloc(np.zeros(512, np.float32), x, *tens, 2, 256)
-        big = synth.moe_weights(43, 4096, 8, 256)
+        big = synth.moe_weights(43, 4352, 8, 256)  # d_model above 4096
         tb = lt.upload_moe(ctx, big)
-        xb, ob = DeviceArray((4096,), np.float32), DeviceArray((4096,), np.float32)
+        xb, ob = DeviceArray((4352,), np.float32), DeviceArray((4352,), np.float32)
         with pytest.raises(UnsupportedError, match="beyond the static scratch"):
             ctx.moe_forward_noalloc(ob, xb, *tb, 2, 256)
         ctx.moe_forward_noalloc(od, xd, *tens, 2, 256)  # still usable
