@@ -706,6 +706,47 @@ def bench_cfg4(args):
         for t in cp:
             t.free()
     ctx.close()
+    if args.timeline:
+        timeline_cfg4(args, c, w, xs)
+
+
+def timeline_cfg4(args, c, w, xs, n=200):
+    """The config-4 layer's phase timeline: n eager launches in a context
+    created with LT_PROFILE=timeline (rotated weight copies, x pool), each
+    followed by lt_sync; writes lt_profile_report's text to args.timeline."""
+    import llmtoy_amd as lt
+    from llmtoy_amd import ggml
+    from llmtoy_amd.hip import DeviceArray
+    import numpy as np
+    os.environ["LT_PROFILE"] = "timeline"
+    try:
+        ctx = lt.Context(0)
+    finally:
+        del os.environ["LT_PROFILE"]
+    Dm, S = w.d_model, c["d_shared"]
+    base = lt.upload_moe(ctx, w) + (ctx.upload(c["sh_gate"], ggml.Q8_0, S, Dm),
+                                    ctx.upload(c["sh_up"], ggml.Q8_0, S, Dm),
+                                    ctx.upload(c["sh_down"], ggml.Q8_0, Dm, S))
+    copies = [base] + [tuple(t.clone() for t in base) for _ in range(args.copies - 1)]
+    X = DeviceArray.from_numpy(np.asarray(xs))
+    out = DeviceArray((Dm,), np.float32)
+    for i in range(n):
+        t = copies[i % args.copies]
+        ctx.moe_forward(out, X.row(i % len(xs)), *t[:3], K, G4_F, act=lt.ACT_GELU_TANH, shared=t[3:])
+        ctx.sync()
+    rep = ctx.profile_report()
+    head = (f"Command (GPU box, repo root): python bench.py --workload cfg4 --no-cpu --timeline {args.timeline}\n"
+            f"Workload: config-4 layer (shared FFN in the same launch), {n} eager launches, {args.copies} weight "
+            f"copies rotated, x pool of {len(xs)}; LT_PROFILE=timeline adds one store per workgroup at its end.\n\n")
+    with open(args.timeline, "w") as f:
+        f.write(head + rep)
+    log("timeline report:\n" + rep)
+    X.free()
+    out.free()
+    for cp in copies:
+        for t in cp:
+            t.free()
+    ctx.close()
 
 
 # ------------------------------------------------------------------ config 5

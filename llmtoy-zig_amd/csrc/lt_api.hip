@@ -50,6 +50,7 @@ struct Profile {
     // per launch: median and largest time of each (role, phase) over blocks, us
     std::vector<float> med[kRoles][kPhases], last[kRoles][kPhases];
     std::vector<float> slot_last[2][16];  // per slot: gate/up h published, down adds issued
+    std::vector<float> last_stamp;        // per launch: the last stamp of any block, us
     size_t split = 0;                     // launches with a group (bid % 8) spread over XCDs
     size_t rot[8] = {};                   // launches by XCD of block 0
 };
@@ -221,6 +222,7 @@ void prof_harvest(lt_ctx *ctx) {
     if (t0 == ~0ull) return;
     std::vector<float> v[kRoles][kPhases];
     std::vector<float> sl[2][16];
+    uint64_t tmax = t0;
     bool split = false;
     for (int b = 0; b < lt::kFusedBlocks; b++) {
         const uint64_t w = st[(size_t)b * lt::kStamps + lt::kStamps - 1], w0 = st[(size_t)(b & 7) * lt::kStamps + lt::kStamps - 1];
@@ -233,7 +235,10 @@ void prof_harvest(lt_ctx *ctx) {
         const int role = (int)(t[lt::kStamps - 1] & 0xff), slot = (int)((t[lt::kStamps - 1] >> 8) & 15);
         if (role <= 0 || role >= kRoles) continue;
         for (int ph = 0; ph < kPhases; ph++)
-            if (t[ph] >= t0) v[role][ph].push_back((float)(t[ph] - t0) * 0.01f);  // 100 MHz ticks -> us
+            if (t[ph] >= t0) {
+                v[role][ph].push_back((float)(t[ph] - t0) * 0.01f);  // 100 MHz ticks -> us
+                tmax = std::max(tmax, t[ph]);
+            }
         if ((role == 2 || role == 3) && t[4] >= t0) sl[role - 2][slot].push_back((float)(t[4] - t0) * 0.01f);
     }
     for (int r = 0; r < kRoles; r++)
@@ -245,6 +250,7 @@ void prof_harvest(lt_ctx *ctx) {
     for (int r = 0; r < 2; r++)
         for (int q = 0; q < 16; q++)
             if (!sl[r][q].empty()) P.slot_last[r][q].push_back(*std::max_element(sl[r][q].begin(), sl[r][q].end()));
+    P.last_stamp.push_back((float)(tmax - t0) * 0.01f);
     P.launches++;
 }
 
@@ -1407,6 +1413,10 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                     o += line;
                 }
             o += "\n";
+        }
+        if (!P.last_stamp.empty()) {
+            snprintf(line, sizeof line, "last stamp of any block (median over launches): %.2f us\n", median_of(P.last_stamp));
+            o += line;
         }
         snprintf(line, sizeof line, "XCD of block 0 per launch:");
         o += line;

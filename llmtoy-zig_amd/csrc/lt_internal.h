@@ -346,6 +346,7 @@ struct FusedPlan {
     int G;       // h groups of 16 per slot (down K / 16)
     int NDg;     // down blocks per slot
     int NCg;     // combining blocks per XCD group (deterministic combine only)
+    int Ewait;   // logit rows published and waited for (>= E: placeholders cover start-value blocks)
     int NSG;     // shared-FFN gate/up blocks per XCD group
     int NSD;     // shared-FFN down blocks per XCD group
     int sg_rows; // row pairs per shared gate/up block

@@ -101,16 +101,18 @@ struct FusedArgs {
     uint64_t *pl;        // partial-output lines [k*NDg*4][16]
     uint32_t *err;       // host-mapped error word (bit mask of the waits that timed out)
     uint64_t *stamps;    // phase stamps (LT_PROFILE=timeline) or null
+    int E, D, nsb, F, nsbd, k, norm, act, accumulate, det, local;
+    int dn_delay;  // wall-clock ticks from seeing the logits to the down weight loads
+    int rb;        // logit rows per router block: 2 or 4
+    int NRg, SPG, G, NDg, NCg;
+    int Ewait;  // logit rows published and waited for: E, or more placeholders (store_starts)
+    // the Gemma-style instance (SH) only
     const uint8_t *rq;   // Q8_0 router: quant plane [E][nb][32] (qrouter)
     const uint16_t *rd;  //   and f16 scale plane [E][nb]
     const uint8_t *sgq, *suq, *sdq;   // shared FFN (Q8_0) quant planes: gate, up [S][D/32], down [D][S/32]
     const uint16_t *sgd, *sud, *sdd;  //   and their scale planes
     uint64_t *shh;       // shared FFN h [S], hand-over words
     int qrouter, S, NSG, NSD, sg_rows, sd_rows;
-    int E, D, nsb, F, nsbd, k, norm, act, accumulate, det, local;
-    int dn_delay;  // wall-clock ticks from seeing the logits to the down weight loads
-    int rb;        // logit rows per router block: 2 or 4
-    int NRg, SPG, G, NDg, NCg;
 };
 
 __device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
@@ -291,7 +293,7 @@ __device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], in
 #pragma unroll
         for (int j = 0; j < PER; j++) {
             const int r = lane + 64 * j;
-            wv[j] = r < a.E ? hand_get(lg + r) : ((uint64_t)ep << 32);
+            wv[j] = r < a.Ewait ? hand_get(lg + r) : ((uint64_t)ep << 32);
         }
         bool good = true;
 #pragma unroll
@@ -360,15 +362,16 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Atomic combine: the start values of out (0, the base, or out + base).
-// Router block c < nvalid = ceil(E / rb) -- the blocks that publish logits
-// -- stores rows 256 c + tid + 256 nvalid i with coherent stores, and every
+// Router block c stores rows 256 c + [0, 256) with coherent stores (the
+// plan gives the grid at least ceil(D / 256) router blocks), and every
 // router block waits for their acknowledgement (s_waitcnt) and a block
-// barrier before any of its logits goes out: a reader that has seen any
-// logit of block c may add to the rows c stores.
+// barrier before any of its logits goes out.  Every block with start values
+// publishes its logit rows, rows >= E included (placeholders that the
+// readers wait for but do not rank: rows < Ewait), so a reader that has
+// seen the logits of block c may add to the rows c stores.
 __device__ __forceinline__ void store_starts(const FusedArgs &a, int bid, int tid) {
-    const int nvalid = (a.E + a.rb - 1) / a.rb;
-    if (a.det || bid >= nvalid || (a.accumulate && !a.base)) return;
-    for (int orow = bid * kThreads + tid; orow < a.D; orow += nvalid * kThreads) {
+    const int orow = bid * kThreads + tid;
+    if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
         const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
         __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -428,7 +431,7 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
     // the logits that let down blocks start adding
     if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
+    if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
     S.mark(2, tid);
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
@@ -453,14 +456,12 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
     store_starts(a, bid, tid);
-    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
-    const uint32_t c0 = epoch_peek(a.counters, bid);
-    float acc = 0.0f;
-    // loads in batches of 4 (64 strides: D <= 2048 in one batch, 4096 in two)
-    for (int qb = 0; 16 * qb < nit; qb += 4) {
-        // every load unconditional (stride clamped), so that the wait for load
-        // q counts only the loads issued after it
-        float4 wv[4], xv[4];
+    // loads in batches of 4 (64 strides: D <= 2048 in one batch, 4096 in
+    // two); every load unconditional (stride clamped), so that the wait for
+    // load q counts only the loads issued after it.  The first batch goes
+    // out before the bias and counter loads.
+    float4 wv[4], xv[4];
+    auto load_batch = [&](int qb) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             int it = 16 * (qb + q) + (lane >> 2);
@@ -469,6 +470,13 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
             wv[q] = *reinterpret_cast<const float4 *>(wr + e);
             xv[q] = *reinterpret_cast<const float4 *>(a.x + e);
         }
+    };
+    load_batch(0);
+    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    float acc = 0.0f;
+    for (int qb = 0; 16 * qb < nit; qb += 4) {
+        if (qb > 0) load_batch(qb);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             if (16 * (qb + q) < nit) {
@@ -508,7 +516,77 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
 #pragma unroll
         for (int l = 1; l < 8; l++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), l));
         if (a.bias) sum = sum + bias;
-        if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
+        if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
+        S.mark(2, tid);
+    }
+    if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
+}
+
+// The same for rows of at most 2048 (one batch of loads).
+__device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t *smem, int bid, int tid, int wave,
+                                                     int lane, Stamps &S) {
+#pragma clang fp contract(off)
+    const int nit = a.D >> 5;                                       // strides per chain
+    float *prod = reinterpret_cast<float *>(smem) + wave * 512;    // two [16][16] chunk buffers
+    float *xch = reinterpret_cast<float *>(smem) + 4 * 512;        // [2][8]
+    const int h = wave & 1, rl = wave >> 1;
+    const int row = 2 * bid + rl;
+    const bool valid = row < a.E;
+    const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
+    store_starts(a, bid, tid);
+    // every load unconditional (stride clamped), so that the wait for load
+    // q counts only the loads issued after it
+    float4 wv[4], xv[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int it = 16 * q + (lane >> 2);
+        it = it < nit ? it : nit - 1;
+        const int e = 32 * it + 16 * h + 4 * (lane & 3);
+        wv[q] = *reinterpret_cast<const float4 *>(wr + e);
+        xv[q] = *reinterpret_cast<const float4 *>(a.x + e);
+    }
+    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (16 * q < nit) {
+            float4 pr;
+            pr.x = wv[q].x * xv[q].x;
+            pr.y = wv[q].y * xv[q].y;
+            pr.z = wv[q].z * xv[q].z;
+            pr.w = wv[q].w * xv[q].w;
+            float *buf = prod + (q & 1) * 256;
+            *reinterpret_cast<float4 *>(buf + 4 * lane) = pr;
+            if (q == 0) S.mark(1, tid);
+            wave_lds_sync();
+            // n = 8 or 16 strides in this load; reads past n stay inside the
+            // buffer and are not added
+            const int n = nit - 16 * q < 16 ? nit - 16 * q : 16;
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = buf[u * 16 + (lane & 15)];
+#pragma unroll
+            for (int u0 = 0; u0 < 16; u0 += 8)
+                if (u0 < n)
+#pragma unroll
+                    for (int u = 0; u < 8; u++) acc = acc + v[u0 + u];
+        }
+    }
+    // lanes l < 8: chains 16h + l and 16h + l + 8
+    const float s2 = acc + dpp<0x128>(acc);
+    if (h == 1 && lane < 8) xch[rl * 8 + lane] = s2;
+    // every wavefront's output-row stores are acknowledged (memory-side)
+    // before the logits that let down blocks start adding
+    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (h == 0) {
+        const float a8 = s2 + xch[rl * 8 + (lane & 7)];
+        float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), 0));
+#pragma unroll
+        for (int l = 1; l < 8; l++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), l));
+        if (a.bias) sum = sum + bias;
+        if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
         S.mark(2, tid);
     }
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
@@ -575,7 +653,7 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
             if (a.bias) total = total + bias;
         }
         total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(total), 0));
-        if (lane < 8 && valid) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(total), c0 + 1u);
+        if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(total), c0 + 1u);
         S.mark(2, tid);
     }
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
@@ -720,10 +798,9 @@ __device__ __forceinline__ void role_sh_down(const FusedArgs &a, uint8_t *smem, 
         const uint64_t t0 = wall_clock64();
         bool ok = true;
         if (a.k > 0 && !(a.accumulate && !a.base) && r0 < r1) {
-            const int nvalid = (a.E + a.rb - 1) / a.rb;
             const uint64_t *lg = a.lg + (size_t)x * kLgCopy;
             for (int w = r0 >> 8; w <= (r1 - 1) >> 8 && ok; w++)  // each 256-row window's router block
-                ok = probe_wait(lg + (size_t)a.rb * (w % nvalid), ep, t0);
+                ok = probe_wait(lg + (size_t)a.rb * w, ep, t0);
             if (!ok) report_detail(a.err, bid, 0x10u, r0, 0, ep);
         }
         if (ok && kb1 > kb0) {
@@ -1238,7 +1315,11 @@ __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep,
     S.mark(1, tid);
 }
 
-template <int PER, int WIDE>
+// SH: the Gemma-style instance (Q8_0 router role, shared-FFN roles); the
+// others hold only the F32 router roles and the experts' roles, and WIDE
+// (rows over 2048) only the router variants those rows use: less code per
+// instance (the roles of a CU's four workgroups share its instruction cache).
+template <int PER, int WIDE, int SH>
 __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_ep;
@@ -1256,29 +1337,32 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     if (tid == 0) s_fail = 0;
     // in-group order: router, shared gate/up, expert gate/up, shared down,
     // expert down, combine -- every role waits only for earlier ones
+    const int nsg = SH ? a.NSG : 0, nsd = SH ? a.NSD : 0;
     int u = i;
     if (u < a.NRg) {
-        if (a.qrouter)
+        if (SH && a.qrouter)
             role_router_q8(a, smem, bid, tid, lane, S);
-        else if (a.rb == 2)
+        else if (!WIDE && a.rb == 2)
+            role_router_pair_one(a, smem, bid, tid, wave, lane, S);
+        else if (WIDE)
             role_router_pair(a, smem, bid, tid, wave, lane, S);
         else
             role_router(a, smem, bid, tid, wave, lane, S);
         role = 1;
-    } else if ((u -= a.NRg) < a.NSG) {
-        role_sh_gate_up(a, smem, &s_ep, x, u, bid, tid, wave, lane, S);
+    } else if (SH && u - a.NRg < nsg) {
+        role_sh_gate_up(a, smem, &s_ep, x, u - a.NRg, bid, tid, wave, lane, S);
         role = 5;
-    } else if ((u -= a.NSG) < a.SPG * a.G) {
+    } else if ((u -= a.NRg + nsg) < a.SPG * a.G) {
         const int s = x + 8 * (u / a.G);
         if (s < a.k) {
             role_gate_up<PER, WIDE>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, 1u);  // logits
             role = 2u | (uint32_t)s << 8;
         }
-    } else if ((u -= a.SPG * a.G) < a.NSD) {
-        role_sh_down(a, smem, &s_ep, &s_fail, x, u, bid, tid, wave, lane, S);
+    } else if (SH && u - a.SPG * a.G < nsd) {
+        role_sh_down(a, smem, &s_ep, &s_fail, x, u - a.SPG * a.G, bid, tid, wave, lane, S);
         role = 6;
-    } else if ((u -= a.NSD) < a.SPG * a.NDg) {
+    } else if ((u -= a.SPG * a.G + nsd) < a.SPG * a.NDg) {
         const int s = x + 8 * (u / a.NDg);
         if (s < a.k) {
             role_down<PER, 4>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane, S);
@@ -1346,15 +1430,20 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         if (sh && L.det) return pl;  // the shared FFN's rows join the atomic combine only
         pl.NCg = L.det ? pl.NDg : 0;
         // two logit rows per router block where the grid has room, else four
+        // router blocks: the logit rows, and at least one per 256 output rows
+        // (store_starts)
+        const int nstart = (D + kThreads - 1) / kThreads;
         pl.rb = 2;
-        pl.NRg = (E + 15) / 16;
+        pl.NRg = std::max((E + 15) / 16, (nstart + 7) / 8);
         used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
         // (the four-row F32 router reads rows of at most 2048)
         if (8 * (used + (sh ? 2 : 0)) > kFusedBlocks && !pl.qrouter && D <= 2048) {
             pl.rb = 4;
-            pl.NRg = (E + 31) / 32;
+            pl.NRg = std::max((E + 31) / 32, (nstart + 7) / 8);
             used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
         }
+        pl.Ewait = std::max(E, pl.rb * nstart);
+        if (pl.Ewait > 64 * pl.per) return pl;
         if (8 * used > kFusedBlocks) return pl;
         if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;            // h record lines
         if ((size_t)k * pl.NDg * 4 > (size_t)kFusedBlocks * 4) return pl;  // partial lines
@@ -1389,9 +1478,9 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
     return pl;
 }
 
-template <int PER, int WIDE>
+template <int PER, int WIDE, int SH>
 static hipError_t launch_fused_t(const FusedArgs &fa, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((k_moe_fused<PER, WIDE>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
+    hipLaunchKernelGGL((k_moe_fused<PER, WIDE, SH>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
     return hipGetLastError();
 }
 
@@ -1460,12 +1549,18 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     fa.G = pl.G;
     fa.NDg = pl.NDg;
     fa.NCg = pl.NCg;
+    fa.Ewait = pl.Ewait;
     // 64 down rows per block (RPG 4): 32-row blocks using the combining
     // blocks' share of the grid (atomic combine) measured 0.15 us slower per
     // layer -- more h record reads and atomics -- though each block's
     // products halve
-    if (pl.wide) return pl.per == 2 ? launch_fused_t<2, 1>(fa, pl.lds, s) : launch_fused_t<4, 1>(fa, pl.lds, s);
-    return pl.per == 2 ? launch_fused_t<2, 0>(fa, pl.lds, s) : launch_fused_t<4, 0>(fa, pl.lds, s);
+    const bool sh = pl.NSG > 0 || pl.qrouter;
+    if (pl.wide) {
+        if (sh) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl.lds, s) : launch_fused_t<4, 1, 1>(fa, pl.lds, s);
+        return pl.per == 2 ? launch_fused_t<2, 1, 0>(fa, pl.lds, s) : launch_fused_t<4, 1, 0>(fa, pl.lds, s);
+    }
+    if (sh) return pl.per == 2 ? launch_fused_t<2, 0, 1>(fa, pl.lds, s) : launch_fused_t<4, 0, 1>(fa, pl.lds, s);
+    return pl.per == 2 ? launch_fused_t<2, 0, 0>(fa, pl.lds, s) : launch_fused_t<4, 0, 0>(fa, pl.lds, s);
 }
 
 }  // namespace lt
