@@ -196,11 +196,11 @@ int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_tensor *rou
  * arguments and results as lt_moe_forward, on the single-launch kernel only:
  * F32 or Q8_0 router, Q4_K gate_up and down, d_model 256..4096 (a multiple
  * of 256), down K <= 1024, <= 256 experts, k <= 16, optionally a Q8_0 shared
- * FFN with down K == d_ffn <= 8192 (then without LT_MOE_DETERMINISTIC),
+ * FFN with down K == d_ffn in 256..4096 (then without LT_MOE_DETERMINISTIC),
  * device pointers only (flags: LT_MOE_NORM_TOPK, LT_MOE_ACCUMULATE,
  * LT_MOE_DETERMINISTIC); any other shape, type or flag returns
  * LT_ERR_UNSUPPORTED or LT_ERR_INVALID.  Its scratch is the library's static
- * device array of 795,136 bytes per GPU (held until the process ends, set up
+ * device array of 762,368 bytes per GPU (held until the process ends, set up
  * by lt_init): all calls on one GPU share it, so calls that overlap on one
  * GPU (several streams or contexts at once) race. */
 int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, const lt_tensor *router,

@@ -38,7 +38,7 @@ struct SpanStat {
     size_t n = 0;
     double total_ms = 0, min_ms = 1e30, max_ms = 0;
 };
-constexpr int kRoles = 7, kPhases = lt::kStamps - 1;
+constexpr int kRoles = 5, kPhases = lt::kStamps - 1;
 struct Profile {
     int mode = 0;  // 0 off, 1 spans, 2 spans + timeline
     std::vector<PendingSpan> pending;
@@ -876,10 +876,10 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
 namespace {
 
 // A Q8_0 dense FFN the fused kernel computes itself: gate and up [S][D],
-// down [D][S] (no padding of the down rows).
+// down [D][S] (no padding of the down rows), 256 <= S <= 4096.
 bool shared_fusable(const DevTensor &G, const DevTensor &U, const DevTensor &Dn) {
     return G.type == LT_TYPE_Q8_0 && U.type == LT_TYPE_Q8_0 && Dn.type == LT_TYPE_Q8_0 &&
-           Dn.cols == G.total_rows && G.total_rows <= (size_t)lt::kFusedMaxShared;
+           Dn.cols == G.total_rows && G.total_rows >= 256 && G.total_rows <= (size_t)lt::kFusedMaxShared;
 }
 
 // The fused kernel's description of a layer (sg null: no shared FFN; R, GU,
@@ -1042,8 +1042,8 @@ extern "C" int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, c
         if ((rc = check_ffn(ctx, sh_gate, sh_up, sh_down, d_model))) return rc;
         if (!shared_fusable(sh_gate->t, sh_up->t, sh_down->t) || (flags & LT_MOE_DETERMINISTIC))
             return fail(ctx, LT_ERR_UNSUPPORTED,
-                        "allocation-free MoE: a shared FFN must be Q8_0 with down K == d_ffn <= %d, and the "
-                        "combine atomic (no LT_MOE_DETERMINISTIC)",
+                        "allocation-free MoE: a shared FFN must be Q8_0 with down K == d_ffn in 256..%d, and "
+                        "the combine atomic (no LT_MOE_DETERMINISTIC)",
                         lt::kFusedMaxShared);
     }
     if (!aligned16(x)) return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
@@ -1387,15 +1387,15 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                  "us from the first block's start; median over launches of the block median / the last block\n",
                  P.launches);
         o += line;
-        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "sh.g/u", "sh.down"};
+        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine"};
         static const char *phases[kRoles][kPhases] = {
             {},
             {"block start", "first row chunk in", "logit published"},
-            {"block start", "logits seen", "expert known", "dot products done", "h record published"},
-            {"block start", "logits seen", "weight loads issued", "h records read", "adds issued"},
-            {"block start", "rows written"},
-            {"block start", "h rows published"},
-            {"block start", "h staged", "adds issued"}};
+            {"block start", "logits seen", "expert known", "dot products done", "h record published",
+             "shared h rows out"},
+            {"block start", "logits seen", "weight loads issued", "h records read", "adds issued", nullptr,
+             "shared rows added"},
+            {"block start", "rows written"}};
         snprintf(line, sizeof line, "%-9s %-22s %10s %10s\n", "role", "phase", "median", "last");
         o += line;
         for (int r = 1; r < kRoles; r++)

@@ -347,10 +347,8 @@ struct FusedPlan {
     int NDg;     // down blocks per slot
     int NCg;     // combining blocks per XCD group (deterministic combine only)
     int Ewait;   // logit rows published and waited for (>= E: placeholders cover start-value blocks)
-    int NSG;     // shared-FFN gate/up blocks per XCD group
-    int NSD;     // shared-FFN down blocks per XCD group
-    int sg_rows; // row pairs per shared gate/up block
-    int sd_rows; // output rows per shared down block
+    int shared;  // a shared FFN in the launch (filler work of the experts' blocks)
+    int sg_rows; // shared h rows per gate/up-position block
     size_t lds;  // dynamic LDS bytes per block
 };
 // A layer for the fused kernel.  MoE: R, GU, Dn set (E experts, k > 0),
@@ -377,15 +375,14 @@ struct FusedScratch {
 // Phase stamps of one launch (LT_PROFILE=timeline): thread 0 of block b
 // writes stamps[b * kStamps + i], wall-clock ticks (100 MHz) at the end of
 // phase i of its role, and stamps[b * kStamps + kStamps - 1] = role | slot
-// << 8 | XCD << 16 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine,
-// 5 shared-FFN gate/up, 6 shared-FFN down).
+// << 8 | XCD << 16 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine).
 constexpr int kStamps = 8;
 enum : int { kStampStart = 0 };
 // router: 1 first row chunk in, 2 logit published; gate/up: 1 logits seen,
 // 2 expert known, 3 dot products done, 4 h record published; down: 1 logits
 // seen, 2 weight loads issued, 3 h records read, 4 adds issued; combine:
-// 1 rows written; shared gate/up: 1 h rows published; shared down: 1 h
-// staged, 2 adds issued
+// 1 rows written; with a shared FFN, gate/up 5: its shared h rows out,
+// down 6: its shared rows added
 // Byte layout of that hand-over memory (a context's own allocation, or the
 // library's static scratch in lt_noalloc.hip): launch counters, 8 logit
 // copies, h record lines, partial-output lines, the XCD probe's ids, and
@@ -399,9 +396,9 @@ constexpr size_t kFusedIdsOff = kFusedXccOff + (size_t)kFusedBlocks * 4;
 constexpr size_t kFusedWOff = kFusedIdsOff + 256;
 // The shared FFN's h values ([S] hand-over words, S <= kFusedMaxShared)
 // follow.
-constexpr int kFusedMaxShared = 8192;
+constexpr int kFusedMaxShared = 4096;
 constexpr size_t kFusedShOff = kFusedWOff + 256;
-constexpr size_t kFusedScratchBytes = kFusedShOff + (size_t)kFusedMaxShared * 8;  // 795,136 B
+constexpr size_t kFusedScratchBytes = kFusedShOff + (size_t)kFusedMaxShared * 8;  // 762,368 B
 // counters, lg, hl, pl at base; err and xcd_local are the caller's
 inline FusedScratch fused_scratch_at(uint8_t *base, uint32_t *err, int xcd_local) {
     FusedScratch s;

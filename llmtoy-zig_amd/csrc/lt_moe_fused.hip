@@ -16,16 +16,18 @@
 //   i < NRg                 router: logit rows 2*bid + [0, 2), dotf32 order
 //                           (4*bid + [0, 4) when the grid has no room), or
 //                           dotQ8_0 order for a Q8_0 router
-//   next NSG                shared FFN gate/up: rows 8u + x of sg_rows each
-//   next SPG*G              gate/up: slot x + 8u, h group jg (16 values)
-//   next NSD                shared FFN down: rows 8u + x of sd_rows each
-//   next SPG*NDg            down: slot x + 8u, rows 64j + [0, 64)
+//   next SPG*G              gate/up: slot x + 8u, h group jg (16 values);
+//                           first sg_rows shared-FFN h rows (sh_gate_up_fill,
+//                           as the blocks without a role)
+//   next SPG*NDg            down: slot x + 8u, rows 64j + [0, 64); the first
+//                           NDg first add the shared FFN's rows 64j + [0, 64)
+//                           over the group's K slice (sh_down_fill)
 //   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
 //
 // (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = ceil(D / 64),
-// NCg = NDg with the deterministic combine, else 0; NSG = NSD = 0 without a
-// shared FFN, which otherwise takes the rest of the group's blocks).  With no
-// experts (k = 0) only the shared FFN roles run: a Q8_0 dense FFN alone.  Every hand-over is coherent across XCDs except the h records when
+// NCg = NDg with the deterministic combine, else 0; NRg also covers one
+// router block per 256 output rows, store_starts).  Every hand-over is
+// coherent across XCDs except the h records (and the shared FFN's h) when
 // local is set: those are workgroup-scope stores that only the writer's L2
 // holds, correct only while the round-robin placement holds (probed once per
 // context by probe_xcd_groups).  Were it to change, the down blocks' bounded
@@ -112,7 +114,7 @@ struct FusedArgs {
     const uint8_t *sgq, *suq, *sdq;   // shared FFN (Q8_0) quant planes: gate, up [S][D/32], down [D][S/32]
     const uint16_t *sgd, *sud, *sdd;  //   and their scale planes
     uint64_t *shh;       // shared FFN h [S], hand-over words
-    int qrouter, S, NSG, NSD, sg_rows, sd_rows;
+    int qrouter, S, sg_rows;  // S = 0: no shared FFN
 };
 
 __device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
@@ -155,11 +157,21 @@ __device__ __forceinline__ void report_detail(uint32_t *err, int bid, uint32_t c
 
 // Phase stamps of thread 0 (LT_PROFILE=timeline; `on` = a.stamps != null,
 // uniform): kept in registers and stored once at the end of the block.
+// Phase stamps (LT_PROFILE=timeline), thread 0's: held in registers and
+// written at the block's end, or (wt, the Gemma-style instance, which needs
+// those registers) written straight to the block's row, cleared at its
+// start.  wt is a constant of each kernel instance.
 struct Stamps {
+    bool wt;
     bool on;
+    uint64_t *row;  // stamps + bid * kStamps, or null
     uint64_t t[kStamps];
     __device__ __forceinline__ void mark(int i, int tid) {
-        if (on && tid == 0) t[i] = wall_clock64();
+        if (wt) {
+            if (row && tid == 0) row[i] = wall_clock64();
+        } else if (on && tid == 0) {
+            t[i] = wall_clock64();
+        }
     }
 };
 
@@ -641,18 +653,24 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
     float r = acc[0];
 #pragma unroll
     for (int l = 1; l < 8; l++) r = r + acc[l];
-    if (b < nb) terms[h * 128 + b] = r * f16_bits_to_f32(d16);
+    const float term = b < nb ? r * f16_bits_to_f32(d16) : 0.0f;
+    if (b >= 64) terms[h * 128 + b] = term;  // blocks 64..127 cross to the row's first wavefront
     S.mark(1, tid);
     // this thread's output-row store is acknowledged before the logits
     if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b < 64) {  // wavefronts 0 and 2: one row each
+        // the ordered sum over the nb block terms, lane by lane from
+        // registers (term b in lane b of t0, block 64 + l in lane l of t1)
+        const float t0 = term, t1 = terms[h * 128 + 64 + lane];
         float total = 0.0f;
-        if (lane == 0) {
-            for (int bb = 0; bb < nb; bb++) total = total + terms[h * 128 + bb];
-            if (a.bias) total = total + bias;
-        }
-        total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(total), 0));
+#pragma unroll
+        for (int l = 0; l < 64; l++)
+            if (l < nb) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t0), l));
+#pragma unroll
+        for (int l = 0; l < 64; l++)
+            if (64 + l < nb) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1), l));
+        if (a.bias) total = total + bias;
         if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(total), c0 + 1u);
         S.mark(2, tid);
     }
@@ -687,57 +705,86 @@ __device__ __forceinline__ void lds_x16(const float *p, float (&xv)[16]) {
     }
 }
 
-// The shared FFN's down product is split along K by XCD group: group x owns
-// the Q8_0 blocks [x nb / 8, (x + 1) nb / 8) of each down row (nb = S / 32),
-// i.e. the h rows 32 x nb / 8 ... of the same slice.  Its gate/up blocks
-// compute exactly those h rows and its down blocks read only them, so h
-// never crosses an XCD (the words are handed over like the experts' h
-// records); the 8 groups' partial rows meet in out through float atomics.
+// The shared FFN runs in the time the experts' blocks would otherwise spend
+// waiting: each gate/up block first computes a few of the shared FFN's h
+// rows (while the router works), each down block first adds a part of the
+// shared down product (while the experts' gate/up works).  The down product
+// is split along K by XCD group: group x owns the Q8_0 blocks
+// [x nb / 8, (x + 1) nb / 8) of each down row (nb = S / 32), i.e. the h
+// rows 32 x nb / 8 ... of the same slice; its gate/up blocks compute
+// exactly those h rows and its down blocks read only them, so h never
+// crosses an XCD (handed over like the experts' h records), and the 8
+// groups' partial rows meet in out through float atomics.
 __device__ __forceinline__ void sh_slice(const FusedArgs &a, int x, int &kb0, int &kb1) {
     const int nb = a.S >> 5;
     kb0 = (x * nb) >> 3;
     kb1 = ((x + 1) * nb) >> 3;
 }
 
-// Gate/up: block u of group x takes h rows [lo + u R, lo + u R + R) of its
-// group's slice (R = sg_rows); wavefront w takes rows w + 4 i; lane l takes
-// the half blocks v = l + 64 m of a row (m < 4: D <= 4096), x from LDS.
-// Each row's act(gate . x) * (up . x) goes out as a hand-over word for the
-// group's down blocks.
-__device__ __forceinline__ void role_sh_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int x, int u,
-                                                int bid, int tid, int wave, int lane, Stamps &S) {
-    float *xs = reinterpret_cast<float *>(smem);
+// The launch epoch without committing it (the block's own role commits
+// later; nobody else writes the counter): thread 0 reads it, LDS hands it
+// to the other wavefronts -- a wavefront that read the counter after the
+// commit would see the next epoch.
+__device__ __forceinline__ uint32_t fill_epoch(const FusedArgs &a, uint32_t *s_ep, int bid, int tid) {
+    if (tid == 0) *s_ep = epoch_peek(a.counters, bid) + 1u;
+    __syncthreads();
+    return *s_ep;
+}
+
+// Shared gate/up rows of filler block q of group x (the gate/up-position
+// blocks, then the blocks without a role): h rows [lo + q R, lo + q R + R)
+// of the group's slice (R = sg_rows <= 4), one per wavefront; lane l takes
+// the half blocks v = l + 64 m of the row (m < 4: D <= 4096).  This
+// thread's share of x is loaded first, then the row's weights, then x goes
+// to LDS: loads complete in order, so the LDS stores wait only for x.  The
+// row's act(gate . x) * (up . x) goes out as a hand-over word for the
+// group's down-position blocks.
+// x in LDS after the experts' gate/up limb area (64 + 2.5 D bytes), so
+// that role_gate_up converts it from there (no second read of x)
+__device__ __forceinline__ float *sh_xs(const FusedArgs &a, uint8_t *smem) {
+    return reinterpret_cast<float *>(smem + 64 + (size_t)a.D / 4 * 10);
+}
+
+__device__ __forceinline__ void sh_gate_up_fill(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int x, int q,
+                                                bool stage_x, int bid, int tid, int wave, int lane, Stamps &S) {
+    float *xs = sh_xs(a, smem);
     const int nb = a.D >> 5, nu = 2 * nb, mu = (nu + 63) >> 6;
     int kb0, kb1;
     sh_slice(a, x, kb0, kb1);
-    const int j0 = 32 * kb0 + u * a.sg_rows, j1 = min(32 * kb1, j0 + a.sg_rows);
+    const int j0 = 32 * kb0 + q * a.sg_rows, j1 = min(32 * kb1, j0 + a.sg_rows);
+    if (j0 >= j1 && !stage_x) return;  // (the whole block)
+    // four named values, not an array (an array held across the barrier
+    // below ends up in scratch memory); every load unconditional (clamped)
+    auto xat = [&](int t) { return *reinterpret_cast<const float4 *>(a.x + min((tid + kThreads * t) * 4, a.D - 4)); };
+    const float4 x0 = xat(0), x1 = xat(1), x2 = xat(2), x3 = xat(3);
+    __builtin_amdgcn_sched_barrier(0);  // keeps the x loads ahead of the weight loads
+    const int j = j0 + wave;
+    // every weight load unconditional (row and half block clamped): with no
+    // branch around them, the LDS stores below wait for x only
     uint4 qg[4], qu[4];
     uint32_t dg[4], du[4];
-    auto load_row = [&](int j) {
+    {
+        const int jl = min(j, j1 - 1);
 #pragma unroll
         for (int m = 0; m < 4; m++) {
-            if (m < mu) {
-                int v = lane + 64 * m;
-                v = v < nu ? v : nu - 1;
-                const size_t blk = (size_t)j * nb + (v >> 1);
-                qg[m] = ld16(a.sgq + blk * 32 + (v & 1) * 16);
-                qu[m] = ld16(a.suq + blk * 32 + (v & 1) * 16);
-                dg[m] = a.sgd[blk];
-                du[m] = a.sud[blk];
-            }
+            const int v = min(lane + 64 * m, nu - 1);
+            const size_t blk = (size_t)jl * nb + (v >> 1);
+            qg[m] = ld16(a.sgq + blk * 32 + (v & 1) * 16);
+            qu[m] = ld16(a.suq + blk * 32 + (v & 1) * 16);
+            dg[m] = a.sgd[blk];
+            du[m] = a.sud[blk];
         }
-    };
-    int j = j0 + wave;
-    if (j < j1) load_row(j);  // the first row's weights before x is staged
-    for (int i = tid * 4; i < a.D; i += kThreads * 4)
-        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.x + i);
-    // the epoch reaches the other wavefronts through LDS: a wavefront that
-    // read the counter after thread 0's increment would see the next epoch
-    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
-    __syncthreads();
-    const uint32_t ep = *s_ep;
-    const bool first = p32_first(lane);
-    for (; j < j1; j += 4) {
+    }
+    {
+        const int i = tid * 4;
+        if (i < a.D) *reinterpret_cast<float4 *>(xs + i) = x0;
+        if (i + 4 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 4 * kThreads) = x1;
+        if (i + 8 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 8 * kThreads) = x2;
+        if (i + 12 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 12 * kThreads) = x3;
+    }
+    const uint32_t ep = fill_epoch(a, s_ep, bid, tid);  // (its barrier also covers xs)
+    if (j < j1) {
+        const bool first = p32_first(lane);
         float g = 0.0f, up = 0.0f;
 #pragma unroll
         for (int m = 0; m < 4; m++) {
@@ -749,68 +796,65 @@ __device__ __forceinline__ void role_sh_gate_up(const FusedArgs &a, uint8_t *sme
                 up = fmaf(f16_bits_to_f32(du[m]), q8_half_sum(qu[m], xv), up);
             }
         }
-        if (j + 4 < j1) load_row(j + 4);
         g = group_sum_dpp<64>(g, first);
         up = group_sum_dpp<64>(up, first);
         if (lane == 0) hand_put_group(a.shh + j, __float_as_uint(act_apply((uint32_t)a.act, g) * up), ep, a.local);
     }
-    S.mark(1, tid);
+    S.mark(5, tid);
 }
 
-// Down: block u of group x takes output rows [u R, u R + R) (R = sd_rows)
-// over its group's K slice (nk = kb1 - kb0 <= 32 blocks: S <= 8192);
-// wavefront w takes rows 4 w + 16 i + (l >> 4), 16 lanes per row, lane l
-// the slice's half blocks v = (l & 15) + 16 m (m < 4).  The first step's
-// weights are loaded while thread 0 waits, in a MoE layer, for one logit of
-// each router block that stored start values of its rows, and for the
-// slice's last h word; then the slice of h is read (every word's epoch
-// checked, as the experts' h records are) into LDS.  Partial rows are added
-// into out with float atomics.
-__device__ __forceinline__ void role_sh_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int *s_fail, int x,
-                                             int u, int bid, int tid, int wave, int lane, Stamps &S) {
+// Shared down rows of down-position block u (< NDg) of group x: output rows
+// [64 u, 64 u + 64) over the group's K slice (nk = kb1 - kb0 <= 16 blocks:
+// S <= 4096); 16 lanes per row, four rows per wavefront and step.  Thread 0
+// waits for the logit of the router block that stored these rows' start
+// values and for the slice's last h word (the weight loads go out after
+// it, so that they do not compete with the router's and the shared gate/up
+// rows'); then all four steps' weights are loaded while the slice of h is
+// read (every word's epoch checked) into LDS, and the partial rows are
+// added into out with float atomics.  A wait that times out turns the rows NaN (error word 0x10 /
+// 0x20).
+__device__ __forceinline__ void sh_down_fill(const FusedArgs &a, uint8_t *smem, uint32_t ep, int x, int u, int bid,
+                                             int tid, int wave, int lane, Stamps &S) {
+    __shared__ int f_fail;
+    int *s_fail = &f_fail;
     float *hs = reinterpret_cast<float *>(smem);
     const int nb = a.S >> 5;
     int kb0, kb1;
     sh_slice(a, x, kb0, kb1);
     const int nv = 2 * (kb1 - kb0), mv = (nv + 15) >> 4;
-    const int r0 = u * a.sd_rows, r1 = min(a.D, r0 + a.sd_rows);
+    const int r0 = u * kDownRows, r1 = min(a.D, r0 + kDownRows);
     const int l16 = lane & 15;
-    uint4 qw[4];
-    uint32_t dw[4];
-    auto load_step = [&](int r) {
-        r = min(r, r1 - 1);
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            if (m < mv) {
-                int v = l16 + 16 * m;
-                v = v < nv ? v : nv - 1;
-                const size_t blk = (size_t)r * nb + kb0 + (v >> 1);
-                qw[m] = ld16(a.sdq + blk * 32 + (v & 1) * 16);
-                dw[m] = a.sdd[blk];
-            }
-        }
-    };
-    int rb = r0 + 4 * wave + (lane >> 4);
-    if (r0 + 4 * wave < r1) load_step(rb);
     if (tid == 0) {
-        const uint32_t ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
-        *s_ep = ep;
+        *s_fail = 0;
         const uint64_t t0 = wall_clock64();
         bool ok = true;
-        if (a.k > 0 && !(a.accumulate && !a.base) && r0 < r1) {
-            const uint64_t *lg = a.lg + (size_t)x * kLgCopy;
-            for (int w = r0 >> 8; w <= (r1 - 1) >> 8 && ok; w++)  // each 256-row window's router block
-                ok = probe_wait(lg + (size_t)a.rb * w, ep, t0);
+        if (!(a.accumulate && !a.base)) {
+            ok = probe_wait(a.lg + (size_t)x * kLgCopy + (size_t)a.rb * (r0 >> 8), ep, t0);
             if (!ok) report_detail(a.err, bid, 0x10u, r0, 0, ep);
         }
-        if (ok && kb1 > kb0) {
+        if (ok) {
             ok = probe_wait(a.shh + 32 * kb1 - 1, ep, t0);
             if (!ok) report_detail(a.err, bid, 0x10u, 32 * kb1 - 1, 0, ep);
         }
         if (!ok) *s_fail = 1;
     }
     __syncthreads();
-    const uint32_t ep = *s_ep;  // from thread 0, as in role_sh_gate_up
+    uint4 qw[4][2];
+    uint32_t dw[4][2];
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+        const int r = min(r0 + 16 * st + 4 * wave + (lane >> 4), r1 - 1);
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            if (m < mv) {
+                int v = l16 + 16 * m;
+                v = v < nv ? v : nv - 1;
+                const size_t blk = (size_t)r * nb + kb0 + (v >> 1);
+                qw[st][m] = ld16(a.sdq + blk * 32 + (v & 1) * 16);
+                dw[st][m] = a.sdd[blk];
+            }
+        }
+    }
     {
         const uint64_t t0 = wall_clock64();
         bool ok = *s_fail == 0;
@@ -831,30 +875,28 @@ __device__ __forceinline__ void role_sh_down(const FusedArgs &a, uint8_t *smem, 
         if (!ok) atomicOr(s_fail, 2);
     }
     __syncthreads();
-    S.mark(1, tid);
     const bool fail = *s_fail != 0;
-    for (int rw = r0 + 4 * wave; rw < r1; rw += 16) {
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
         float acc = 0.0f;
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
+        for (int m = 0; m < 2; m++) {
             const int v = l16 + 16 * m;
             if (m < mv && v < nv) {
                 float xv[16];
                 lds_x16(hs + v * 16, xv);
-                acc = fmaf(f16_bits_to_f32(dw[m]), q8_half_sum(qw[m], xv), acc);
+                acc = fmaf(f16_bits_to_f32(dw[st][m]), q8_half_sum(qw[st][m], xv), acc);
             }
         }
-        if (rw + 16 < r1) load_step(rw + 16 + (lane >> 4));
         acc = group_sum_dpp<16>(acc, false);
-        const int row = rw + (lane >> 4);
-        if (l16 == 0 && row < r1) {
-            const float val = fail ? __int_as_float(0x7fc00000) : acc;
-            if (a.k > 0)
-                (void)__hip_atomic_fetch_add(a.out + row, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        const int row = r0 + 16 * st + 4 * wave + (lane >> 4);
+        if (l16 == 0 && row < r1)
+            (void)__hip_atomic_fetch_add(a.out + row, fail ? __int_as_float(0x7fc00000) : acc, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (tid == 0 && fail) report_timeout(a.err, (uint32_t)*s_fail << 4);  // 0x10 logits / last h word, 0x20 h
-    S.mark(2, tid);
+    if (tid == 0 && fail) report_timeout(a.err, (uint32_t)*s_fail << 4);  // 0x10 logit / last h word, 0x20 h
+    S.mark(6, tid);
+    __syncthreads();  // hs is free for the block's own role
 }
 
 // ---------------------------------------------------------------- gate/up
@@ -867,7 +909,8 @@ __device__ __forceinline__ void role_sh_down(const FusedArgs &a, uint8_t *smem, 
 // WIDE (rows of 9-16 super-blocks): lane position pos covers pos and pos
 // + 32; the second position's weights are loaded as the first's products
 // finish, its x limbs are read from LDS after them.
-template <int PER, int WIDE>
+// XL: x is already in LDS (sh_xs, staged by sh_gate_up_fill).
+template <int PER, int WIDE, int XL>
 __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
                                              int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
                                              Stamps &S) {
@@ -886,8 +929,9 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
     float *lxs = lsp + a.D / 16;
     for (int t8 = tid; t8 < a.D / 8; t8 += kThreads) {  // one pass for D <= 2048
-        const float4 f0 = *reinterpret_cast<const float4 *>(a.x + 8 * t8);
-        const float4 f1 = *reinterpret_cast<const float4 *>(a.x + 8 * t8 + 4);
+        const float *xsrc = XL ? sh_xs(a, smem) : a.x;
+        const float4 f0 = *reinterpret_cast<const float4 *>(xsrc + 8 * t8);
+        const float4 f1 = *reinterpret_cast<const float4 *>(xsrc + 8 * t8 + 4);
         const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
         float m = 0.0f;
 #pragma unroll
@@ -1095,7 +1139,10 @@ __device__ __forceinline__ float group16_sum_transposed(const float (&v)[V], int
 // partials over DPP, and the rows, times the slot weight, are added into out
 // (float atomics) or, with det (RPG = 4), wavefront w writes rows 16w +
 // [0, 16) as one line of partial-output words.
-template <int PER, int RPG>
+// FILL: the block also adds shared-FFN rows (sh_down_fill) in the time its
+// down weight loads wait (measured 2.8 us better on config 4 than before
+// the logit poll, where the filler delays the block's own role).
+template <int PER, int RPG, int FILL>
 __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, float *s_w,
                                           uint32_t *s_ep, int *s_fail, int bid, int s, int j, int tid, int wave,
                                           int lane, Stamps &S) {
@@ -1130,6 +1177,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     __syncthreads();
     uint32_t e = s_ids[s];
     if (e >= (uint32_t)a.E) e = 0;
+    if (FILL && a.S > 0 && s < 8) sh_down_fill(a, smem, ep, bid & 7, j, bid, tid, wave, lane, S);
     {
         const uint64_t t_go = s_seen + (uint64_t)a.dn_delay;
         while (wall_clock64() < t_go) __builtin_amdgcn_s_sleep(4);
@@ -1329,15 +1377,21 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     const int bid = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int x = bid & 7, i = bid >> 3;
     Stamps S;
+    S.wt = SH;
     S.on = a.stamps != nullptr;
+    S.row = a.stamps ? a.stamps + (size_t)bid * kStamps : nullptr;
+    if (SH) {
+        if (S.row && tid == 0)
+            for (int q = 1; q < kStamps; q++) S.row[q] = 0;
+    } else {
 #pragma unroll
-    for (int q = 0; q < kStamps; q++) S.t[q] = 0;
+        for (int q = 0; q < kStamps; q++) S.t[q] = 0;
+    }
     S.mark(kStampStart, tid);
     uint32_t role = 0;
     if (tid == 0) s_fail = 0;
-    // in-group order: router, shared gate/up, expert gate/up, shared down,
-    // expert down, combine -- every role waits only for earlier ones
-    const int nsg = SH ? a.NSG : 0, nsd = SH ? a.NSD : 0;
+    // in-group order: router, gate/up, down, combine -- every role waits
+    // only for earlier ones (the shared FFN's filler work too)
     int u = i;
     if (u < a.NRg) {
         if (SH && a.qrouter)
@@ -1349,38 +1403,45 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
         else
             role_router(a, smem, bid, tid, wave, lane, S);
         role = 1;
-    } else if (SH && u - a.NRg < nsg) {
-        role_sh_gate_up(a, smem, &s_ep, x, u - a.NRg, bid, tid, wave, lane, S);
-        role = 5;
-    } else if ((u -= a.NRg + nsg) < a.SPG * a.G) {
+    } else if ((u -= a.NRg) < a.SPG * a.G) {
         const int s = x + 8 * (u / a.G);
+        const bool fill = SH && a.S > 0;
+        if (fill) sh_gate_up_fill(a, smem, &s_ep, x, u, s < a.k, bid, tid, wave, lane, S);
         if (s < a.k) {
-            role_gate_up<PER, WIDE>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            if (fill)
+                role_gate_up<PER, WIDE, 1>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            else
+                role_gate_up<PER, WIDE, 0>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, 1u);  // logits
             role = 2u | (uint32_t)s << 8;
         }
-    } else if (SH && u - a.SPG * a.G < nsd) {
-        role_sh_down(a, smem, &s_ep, &s_fail, x, u - a.SPG * a.G, bid, tid, wave, lane, S);
-        role = 6;
-    } else if ((u -= a.SPG * a.G + nsd) < a.SPG * a.NDg) {
+    } else if ((u -= a.SPG * a.G) < a.SPG * a.NDg) {
         const int s = x + 8 * (u / a.NDg);
         if (s < a.k) {
-            role_down<PER, 4>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane, S);
+            role_down<PER, 4, SH>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, (uint32_t)s_fail << 1);  // 2 logits, 4 h records
             role = 3u | (uint32_t)s << 8;
+        } else if (SH && a.S > 0 && u < a.NDg) {  // a group without a slot still adds its shared rows
+            sh_down_fill(a, smem, fill_epoch(a, &s_ep, bid, tid), x, u, bid, tid, wave, lane, S);
         }
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
         role_combine(a, &s_ep, bid, 8 * u + x, tid, S);
         role = 4;
+    } else if (SH && a.S > 0) {  // no role: shared gate/up rows after the gate/up-position blocks'
+        sh_gate_up_fill(a, smem, &s_ep, x, a.SPG * a.G + (u - a.NCg), false, bid, tid, wave, lane, S);
     }
     // no role in this configuration: keep the counter in step
     if (role == 0 && tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
-    if (S.on && tid == 0) {
+    if (S.row && tid == 0) {
         uint32_t xcc;  // the XCD this block ran on
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        S.t[kStamps - 1] = role | (uint64_t)(xcc & 0xfu) << 16;
+        if (SH) {
+            S.row[kStamps - 1] = role | (uint64_t)(xcc & 0xfu) << 16;
+        } else {
+            S.t[kStamps - 1] = role | (uint64_t)(xcc & 0xfu) << 16;
 #pragma unroll
-        for (int q = 0; q < kStamps; q++) a.stamps[(size_t)bid * kStamps + q] = S.t[q];
+            for (int q = 0; q < kStamps; q++) S.row[q] = S.t[q];
+        }
     }
 }
 
@@ -1437,7 +1498,7 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         pl.NRg = std::max((E + 15) / 16, (nstart + 7) / 8);
         used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
         // (the four-row F32 router reads rows of at most 2048)
-        if (8 * (used + (sh ? 2 : 0)) > kFusedBlocks && !pl.qrouter && D <= 2048) {
+        if (8 * used > kFusedBlocks && !pl.qrouter && D <= 2048) {
             pl.rb = 4;
             pl.NRg = std::max((E + 31) / 32, (nstart + 7) / 8);
             used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
@@ -1452,17 +1513,15 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         pl.rb = 2;
     }
     if (sh) {
+        // the shared FFN as filler work of the experts' gate/up and down
+        // blocks (a dense FFN alone is not in the single launch)
         const int S = L.S;
-        if (!L.SU || !L.SD || S < 32 || S % 32 != 0 || S > kFusedMaxShared) return pl;
-        // the rest of each group's blocks, shared gate/up : down = 2 : 1 (their bytes)
-        const int left = kFusedBlocks / 8 - used;
-        if (left < 2) return pl;
-        pl.NSG = (2 * left + 1) / 3;
-        pl.NSD = left - pl.NSG;
+        if (!moe || !L.SU || !L.SD || S % 32 != 0 || S < 256 || S > 4096) return pl;
         const int slice = 32 * ((S / 32 + 7) / 8);  // h rows of the largest group slice
-        pl.sg_rows = (slice + pl.NSG - 1) / pl.NSG;
-        pl.sd_rows = (D + pl.NSD - 1) / pl.NSD;
-        if (!moe) return pl;  // a dense FFN alone: not in the single launch yet
+        const int nfill = kFusedBlocks / 8 - used + pl.SPG * pl.G;  // gate/up-position and idle blocks
+        pl.sg_rows = (slice + nfill - 1) / nfill;
+        if (pl.sg_rows > 4) return pl;  // one row per wavefront
+        pl.shared = 1;
     }
     size_t lds = 64;
     if (moe) {
@@ -1471,7 +1530,7 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
         lds = std::max(lds, std::max(lds_router, std::max(lds_down, lds_gu)));
     }
-    if (sh) lds = std::max(lds, std::max((size_t)D * 4, (size_t)128 * ((L.S / 32 + 7) / 8)));
+    if (sh) lds = std::max(lds, std::max(64 + (size_t)D / 4 * 10 + (size_t)D * 4, (size_t)128 * ((L.S / 32 + 7) / 8)));  // limbs + x, h slice
     if (lds > 64 * 1024) return pl;
     pl.lds = lds;
     pl.ok = true;
@@ -1522,11 +1581,8 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     fa.stamps = sc.stamps;
     fa.shh = sc.shh;
     fa.qrouter = pl.qrouter;
-    fa.S = L.S;
-    fa.NSG = pl.NSG;
-    fa.NSD = pl.NSD;
+    fa.S = pl.shared ? L.S : 0;
     fa.sg_rows = pl.sg_rows;
-    fa.sd_rows = pl.sd_rows;
     fa.E = moe ? L.E : 0;
     fa.D = L.D;
     fa.F = L.F;
@@ -1554,7 +1610,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // blocks' share of the grid (atomic combine) measured 0.15 us slower per
     // layer -- more h record reads and atomics -- though each block's
     // products halve
-    const bool sh = pl.NSG > 0 || pl.qrouter;
+    const bool sh = pl.shared || pl.qrouter;
     if (pl.wide) {
         if (sh) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl.lds, s) : launch_fused_t<4, 1, 1>(fa, pl.lds, s);
         return pl.per == 2 ? launch_fused_t<2, 1, 0>(fa, pl.lds, s) : launch_fused_t<4, 1, 0>(fa, pl.lds, s);
