@@ -143,7 +143,12 @@ int lt_matvec(lt_ctx *ctx, float *out, const lt_tensor *W, const float *x, uint3
 
 /* Dense gated FFN: out[d_model] = Wd * (act(Wg x) * (Wu x)).
  * Replaces the dense-FFN matvec chain (model/forward.zig:301-308,
- * gemma4/forward.zig:392-397; GPU: runLayerDenseFfnQ8_1, gpu_weights.zig). */
+ * gemma4/forward.zig:392-397; GPU: runLayerDenseFfnQ8_1, gpu_weights.zig).
+ * Q8_0 weights with d_model <= 2048 and d_ffn <= 8192 (multiples of 32,
+ * down K == d_ffn) run as one launch whose 8 partial sums per output row
+ * meet through float atomics (last bits may vary run to run); LT_MOE_UNFUSED
+ * runs gate/up and down as two launches instead.  flags: LT_HOST_IO,
+ * LT_MOE_UNFUSED. */
 int lt_ffn_dense(lt_ctx *ctx, float *out, const lt_tensor *Wg, const lt_tensor *Wu, const lt_tensor *Wd,
                  const float *x, uint32_t act, uint32_t flags);
 

@@ -82,6 +82,9 @@ struct lt_ctx {
     // lt_moe_forward_noalloc
     uint8_t *na_base = nullptr;
     lt::FusedScratch na_fsc{};
+    // hand-over memory of the single-launch dense FFN (allocated by lt_init)
+    void *ffn = nullptr;
+    lt::FfnScratch ffsc{};
     Profile prof;
     // pinned + device staging of tensor uploads and read-backs (allocated on first use)
     lt::UploadStaging up{};
@@ -375,6 +378,9 @@ hipError_t init_device_state(lt_ctx *ctx) {
     if (agent && agent[0] == '1') local = 0;
     ctx->xcd_local = local;
     ctx->na_fsc = lt::fused_scratch_at(ctx->na_base, ctx->err_dev, local);
+    if ((e = hipMalloc(&ctx->ffn, lt::kFfnScratchBytes)) != hipSuccess) return e;
+    if ((e = hipMemset(ctx->ffn, 0, lt::kFfnScratchBytes)) != hipSuccess) return e;
+    ctx->ffsc = lt::ffn_scratch_at((uint8_t *)ctx->ffn, ctx->err_dev, local);
     // LT_PROFILE: "timeline" = spans + phase stamps of the fused kernel;
     // any other non-empty value except "0" = spans
     const char *prof = getenv("LT_PROFILE");
@@ -400,11 +406,12 @@ int check_fused_err(lt_ctx *ctx) {
     for (int i = 0; i < 5; i++) d[i] = __atomic_exchange_n(ctx->fused_err + 2 + i, 0u, __ATOMIC_SEQ_CST);
     // Later launches publish h through memory (agent scope) instead of an
     // XCD's L2, in case the placement the one-time probe saw has changed.
-    ctx->xcd_local = ctx->fsc.xcd_local = ctx->na_fsc.xcd_local = 0;
+    ctx->xcd_local = ctx->fsc.xcd_local = ctx->na_fsc.xcd_local = ctx->ffsc.xcd_local = 0;
     return fail(ctx, LT_ERR_DEVICE,
-                "fused MoE kernel: a hand-over wait timed out (code 0x%x: 1 gate/up logits, 2 down logits, 4 down h "
-                "records, 8 combine, 0x10 shared-FFN logits or last h word, 0x20 shared-FFN h; first recorded: block %d, site "
-                "0x%x, index %u, saw %u, expected epoch %u); outputs of that call are NaN",
+                "single-launch kernel: a hand-over wait timed out (code 0x%x: 1 gate/up logits, 2 down logits, 4 down "
+                "h records, 8 combine, 0x10 shared-FFN logits or last h word, 0x20 shared-FFN h, 0x40 dense-FFN h, "
+                "0x80 dense-FFN start values; first recorded: block %d, site 0x%x, index %u, saw %u, expected epoch "
+                "%u); outputs of that call are NaN",
                 v, (int)d[0] - 1, d[1], d[2], d[3], d[4]);
 }
 
@@ -456,6 +463,7 @@ extern "C" int lt_init(int device, lt_ctx **out_ctx) {
         if (ctx->ticket) (void)hipFree(ctx->ticket);
         if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
         if (ctx->prof.stamps) (void)hipFree(ctx->prof.stamps);
+        if (ctx->ffn) (void)hipFree(ctx->ffn);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return e == hipErrorOutOfMemory ? LT_ERR_OOM : LT_ERR_DEVICE;
@@ -482,6 +490,7 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     if (ctx->prof.stamps) (void)hipFree(ctx->prof.stamps);
     if (ctx->ticket) (void)hipFree(ctx->ticket);
     if (ctx->fused) (void)hipFree(ctx->fused);
+    if (ctx->ffn) (void)hipFree(ctx->ffn);
     if (ctx->fused_err) (void)hipHostFree(ctx->fused_err);
     lt::free_staging(ctx->up);
     (void)hipStreamDestroy(ctx->stream);
@@ -607,10 +616,17 @@ __global__ void k_act_mul(const float *g, const float *u, int n, int n_out, uint
     else if (i < n_out) h[i] = 0.f;
 }
 
-// out = Wd * (act(Wg x) * (Wu x)), all device pointers.
+// out = Wd * (act(Wg x) * (Wu x)), all device pointers.  Q8_0 weights of a
+// shape the single-launch kernel takes run there (unless unfused); others as
+// a gate/up launch and a down matvec.
 int ffn_dense_dev(lt_ctx *ctx, const DevTensor &G, const DevTensor &U, const DevTensor &D, const float *x,
-                  uint32_t act, float *out) {
+                  uint32_t act, float *out, bool unfused = false) {
     const size_t F = G.total_rows, Kd = D.cols;
+    const bool q8 = G.type == LT_TYPE_Q8_0 && U.type == LT_TYPE_Q8_0 && D.type == LT_TYPE_Q8_0 && Kd == F;
+    if (q8 && !unfused) {
+        const lt::FfnPlan pl = lt::plan_ffn_fused((int)G.cols, (int)F);
+        if (pl.ok) return launch_rc(ctx, lt::launch_ffn_fused(pl, G, U, D, x, act, out, ctx->ffsc, ctx->stream), "ffn_fused");
+    }
     int rc = ensure(ctx, ctx->h, Kd * 4);
     if (rc) return rc;
     float *h = (float *)ctx->h.p;
@@ -661,7 +677,7 @@ extern "C" int lt_ffn_dense(lt_ctx *ctx, float *out, const lt_tensor *Wg, const 
     } else if (!aligned16(x)) {
         return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
     }
-    if ((rc = ffn_dense_dev(ctx, Wg->t, Wu->t, Wd->t, dx, act, dy))) return rc;
+    if ((rc = ffn_dense_dev(ctx, Wg->t, Wu->t, Wd->t, dx, act, dy, (flags & LT_MOE_UNFUSED) != 0))) return rc;
     if (host) {
         LT_HIP(ctx, hipMemcpyAsync(out, dy, D * 4, hipMemcpyDeviceToHost, ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -949,7 +965,9 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
     const float *base = nullptr;
     if (sh_gate) {
         if ((rc = ensure(ctx, ctx->shared, D.rows * 4))) return rc;
-        if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p))) return rc;
+        if ((rc = ffn_dense_dev(ctx, sh_gate->t, sh_up->t, sh_down->t, x, act, (float *)ctx->shared.p,
+                                (flags & LT_MOE_UNFUSED) != 0)))
+            return rc;
         base = (const float *)ctx->shared.p;
     }
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;

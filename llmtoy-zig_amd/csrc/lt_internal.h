@@ -238,6 +238,61 @@ __device__ __forceinline__ float act_apply(uint32_t act, float g) {
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ __forceinline__ float4 ldg16f(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
+// ---------------------------------------------------------------- hand-over words
+// The single-launch kernels (lt_moe_fused.hip, lt_ffn_fused.hip) pass
+// results between workgroups as 64-bit words, a 32-bit payload beside the
+// 32-bit launch epoch, written and read with relaxed atomics: a reader waits
+// until every word it needs carries the current epoch, so the memory never
+// needs clearing between launches.
+__device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
+    __hip_atomic_store(p, (uint64_t)v | ((uint64_t)ep << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A word read only by blocks of the writer's own group.  With local set
+// (blocks with equal bid % 8 share an XCD: checked once per context by
+// probe_xcd_groups), a workgroup-scope store leaves it dirty in that XCD's
+// L2, where the readers' agent-scope loads find it: about 0.2 us instead
+// of the 0.6 us a round trip through memory takes.  Otherwise agent scope.
+__device__ __forceinline__ void hand_put_group(uint64_t *p, uint32_t v, uint32_t ep, int local) {
+    const uint64_t w = (uint64_t)v | ((uint64_t)ep << 32);
+    if (local)
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t hand_get(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t ep) { return (uint32_t)(w >> 32) == ep; }
+
+__device__ __forceinline__ void report_timeout(uint32_t *err, uint32_t code) {
+    __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// The first timed-out wait of a call also leaves what it saw in err[2..6]:
+// block + 1, site code, the word index, the word's epoch tag (or count)
+// seen, and the epoch expected.
+__device__ __forceinline__ void report_detail(uint32_t *err, int bid, uint32_t code, uint32_t index, uint32_t seen,
+                                              uint32_t ep) {
+    uint32_t zero = 0;
+    if (__hip_atomic_compare_exchange_strong(err + 2, &zero, (uint32_t)bid + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_SYSTEM)) {
+        __hip_atomic_store(err + 3, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(err + 4, index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(err + 5, seen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(err + 6, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+// The launch counter of block bid: epoch_peek reads it (issued early, its
+// value used late), epoch_commit stores the incremented value; the new value
+// is the launch epoch.
+__device__ __forceinline__ uint32_t epoch_peek(const uint32_t *counters, int bid) {
+    return __hip_atomic_load(counters + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t epoch_commit(uint32_t *counters, int bid, uint32_t c) {
+    __hip_atomic_store(counters + bid, c + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return c + 1u;
+}
+
 }  // namespace lt
 
 namespace lt {
@@ -421,6 +476,39 @@ hipError_t noalloc_scratch(int device, uint8_t **base);
 // hand-overs rely on for speed).
 hipError_t probe_xcd_groups(uint32_t *dev_ids, hipStream_t s, int *local);
 FusedPlan plan_moe_fused(const FusedLayer &L);
+// A Q8_0 dense FFN (gate, up [S][D], down [D][S]) in one launch
+// (lt_ffn_fused.hip): D <= 2048, S <= kFfnMaxS, both multiples of 32.
+constexpr int kFfnMaxS = 8192;
+constexpr int kFfnFlags = 128;
+struct FfnPlan {
+    bool ok;
+    int P, Q;    // gate/up passes (4 h rows each), down steps (16 rows each) per block
+    int NG, ND;  // gate/up and down blocks per XCD group
+    int cu;      // 64-unit spans of a gate/up row per lane
+    size_t lds;
+};
+// Hand-over memory of that kernel: launch counters [kFusedBlocks], h words
+// [kFfnMaxS], start-value flags [kFfnFlags]; zeroed once when allocated.
+struct FfnScratch {
+    uint32_t *counters;
+    uint64_t *hw;
+    uint64_t *flags;
+    uint32_t *err;  // the context's host-mapped error word (device address)
+    int xcd_local;
+};
+constexpr size_t kFfnScratchBytes = (size_t)kFusedBlocks * 4 + (size_t)kFfnMaxS * 8 + (size_t)kFfnFlags * 8;
+inline FfnScratch ffn_scratch_at(uint8_t *base, uint32_t *err, int xcd_local) {
+    FfnScratch s;
+    s.counters = reinterpret_cast<uint32_t *>(base);
+    s.hw = reinterpret_cast<uint64_t *>(base + (size_t)kFusedBlocks * 4);
+    s.flags = s.hw + kFfnMaxS;
+    s.err = err;
+    s.xcd_local = xcd_local;
+    return s;
+}
+FfnPlan plan_ffn_fused(int D, int S);
+hipError_t launch_ffn_fused(const FfnPlan &pl, const DevTensor &G, const DevTensor &U, const DevTensor &Dn,
+                            const float *x, uint32_t act, float *out, const FfnScratch &sc, hipStream_t s);
 hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const float *bias, const float *x,
                             uint32_t act, uint32_t norm, const float *base, int accumulate, int deterministic,
                             float *out, uint32_t *ids_out, float *w_out, const FusedScratch &sc, hipStream_t s);

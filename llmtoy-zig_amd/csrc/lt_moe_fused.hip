@@ -117,46 +117,6 @@ struct FusedArgs {
     int qrouter, S, sg_rows;  // S = 0: no shared FFN
 };
 
-__device__ __forceinline__ void hand_put(uint64_t *p, uint32_t v, uint32_t ep) {
-    __hip_atomic_store(p, (uint64_t)v | ((uint64_t)ep << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// A word read only by blocks of the writer's own group.  With local set
-// (blocks with equal bid % 8 share an XCD: checked once per context by
-// probe_xcd_groups), a workgroup-scope store leaves it dirty in that XCD's
-// L2, where the readers' agent-scope loads find it: about 0.2 us instead
-// of the 0.6 us a round trip through memory takes.  Otherwise agent scope.
-__device__ __forceinline__ void hand_put_group(uint64_t *p, uint32_t v, uint32_t ep, int local) {
-    const uint64_t w = (uint64_t)v | ((uint64_t)ep << 32);
-    if (local)
-        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    else
-        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t hand_get(const uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t ep) { return (uint32_t)(w >> 32) == ep; }
-
-__device__ __forceinline__ void report_timeout(uint32_t *err, uint32_t code) {
-    __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-// The first timed-out wait of a call also leaves what it saw in err[2..6]:
-// block + 1, site code, the word index, the word's epoch tag (or count)
-// seen, and the epoch expected.
-__device__ __forceinline__ void report_detail(uint32_t *err, int bid, uint32_t code, uint32_t index, uint32_t seen,
-                                              uint32_t ep) {
-    uint32_t zero = 0;
-    if (__hip_atomic_compare_exchange_strong(err + 2, &zero, (uint32_t)bid + 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_SYSTEM)) {
-        __hip_atomic_store(err + 3, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(err + 4, index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(err + 5, seen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(err + 6, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-}
-
-// Phase stamps of thread 0 (LT_PROFILE=timeline; `on` = a.stamps != null,
-// uniform): kept in registers and stored once at the end of the block.
 // Phase stamps (LT_PROFILE=timeline), thread 0's: held in registers and
 // written at the block's end, or (wt, the Gemma-style instance, which needs
 // those registers) written straight to the block's row, cleared at its
@@ -317,17 +277,6 @@ __device__ bool poll_logits(const FusedArgs &a, uint32_t ep, float (&v)[PER], in
         if (wall_clock64() - t0 > kWaitTicks) return false;
         __builtin_amdgcn_s_sleep(1);
     }
-}
-
-// The launch counter of block bid: epoch_peek reads it (issued early, its
-// value used late), epoch_commit stores the incremented value; the new value
-// is the launch epoch.
-__device__ __forceinline__ uint32_t epoch_peek(const uint32_t *counters, int bid) {
-    return __hip_atomic_load(counters + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t epoch_commit(uint32_t *counters, int bid, uint32_t c) {
-    __hip_atomic_store(counters + bid, c + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return c + 1u;
 }
 
 // Sum of 4 values per lane over each 32-lane half, transposed: returns in

@@ -136,6 +136,14 @@ static hipError_t launch_q8_any(const DevTensor &A, const DevTensor *B, const fl
     case 6: return launch_q8_t<64, 6, DUAL>(A, B, x, y, act, s);
     case 7: return launch_q8_t<64, 7, DUAL>(A, B, x, y, act, s);
     case 8: return launch_q8_t<64, 8, DUAL>(A, B, x, y, act, s);
+    case 9: return launch_q8_t<64, 9, DUAL>(A, B, x, y, act, s);
+    case 10: return launch_q8_t<64, 10, DUAL>(A, B, x, y, act, s);
+    case 11: return launch_q8_t<64, 11, DUAL>(A, B, x, y, act, s);
+    case 12: return launch_q8_t<64, 12, DUAL>(A, B, x, y, act, s);
+    case 13: return launch_q8_t<64, 13, DUAL>(A, B, x, y, act, s);
+    case 14: return launch_q8_t<64, 14, DUAL>(A, B, x, y, act, s);
+    case 15: return launch_q8_t<64, 15, DUAL>(A, B, x, y, act, s);
+    case 16: return launch_q8_t<64, 16, DUAL>(A, B, x, y, act, s);
     default: return hipErrorInvalidValue;  // K > 16384: rejected by the API layer
     }
 }

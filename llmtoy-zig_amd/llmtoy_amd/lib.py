@@ -231,8 +231,9 @@ class Context:
         self._check(self.lib.lt_matvec(self.ptr, _ptr(out)[0], W.handle, _ptr(x)[0], fl))
         return out
 
-    def ffn_dense(self, out, Wg: Tensor, Wu: Tensor, Wd: Tensor, x, act=ACT_SILU):
-        fl = self._io(out, x)
+    def ffn_dense(self, out, Wg: Tensor, Wu: Tensor, Wd: Tensor, x, act=ACT_SILU, unfused=False):
+        """unfused: gate/up and down as two launches instead of the single-launch kernel."""
+        fl = self._io(out, x) | (LT_MOE_UNFUSED if unfused else 0)
         self._check(self.lib.lt_ffn_dense(self.ptr, _ptr(out)[0], Wg.handle, Wu.handle, Wd.handle, _ptr(x)[0],
                                           act, fl))
         return out

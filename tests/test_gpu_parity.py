@@ -5,6 +5,7 @@ relative L2 of the oracle (fp32 accumulation); router logits bit-exact.
 Matvec fuzz cases also hold the reference's own fuzz bound,
 max|d| / max|ref| < 1e-4 for fp32 activations (gpu/matvec.zig:4618).
 """
+import dataclasses
 import os
 import sys
 
@@ -245,11 +246,43 @@ def test_gpu_config1_dense_ffn_q8_0(ctx):
     wg = ctx.upload(c["w_gate"], ggml.Q8_0, F, D)
     wu = ctx.upload(c["w_up"], ggml.Q8_0, F, D)
     wd = ctx.upload(c["w_down"], ggml.Q8_0, D, F)
-    out = np.zeros(D, np.float32)
-    ctx.ffn_dense(out, wg, wu, wd, c["x"], act=lt.ACT_SILU)
     with orc.Pool(16) as p:
         ref = orc.ffn_dense(c["w_gate"], c["w_up"], c["w_down"], orc.Q8_0, c["x"], D, F, pool=p)
-    assert rel_l2(out, ref) <= REL_L2
+    for unfused in (False, True):  # single launch, then gate/up + down launches
+        out = np.zeros(D, np.float32)
+        ctx.ffn_dense(out, wg, wu, wd, c["x"], act=lt.ACT_SILU, unfused=unfused)
+        assert rel_l2(out, ref) <= REL_L2, (unfused, rel_l2(out, ref))
+        assert rel_l2(out, ref) <= 1e-5, (unfused, rel_l2(out, ref))  # fp32 arithmetic throughout
+    for t in (wg, wu, wd):
+        t.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D,S,act", [
+    (64, 256, 0),       # smallest: one Q8_0 block per h row slice
+    (512, 288, 1),      # S / 32 = 9 down-K blocks: slices of 1 and 2 blocks, GELU
+    (1024, 2112, 0),    # the Gemma4 shared-FFN width
+    (2048, 8192, 1),    # the largest single-launch shape: 2 units per lane, 4 passes
+    (2048, 8224, 0),    # past it: two launches
+])
+def test_gpu_ffn_dense_shapes(ctx, pool, D, S, act):
+    # the single-launch dense FFN (one h slice per XCD group, partial rows
+    # through float atomics) against the oracle and the two-launch path;
+    # several calls in a row (launch epochs) with changing x
+    g = synth.stream(120, D + S)
+    wg_b = synth.q8_0_matrix(g, S, D)
+    wu_b = synth.q8_0_matrix(g, S, D)
+    wd_b = synth.q8_0_matrix(g, D, S)
+    wg, wu, wd = ctx.upload(wg_b, ggml.Q8_0, S, D), ctx.upload(wu_b, ggml.Q8_0, S, D), ctx.upload(wd_b, ggml.Q8_0, D, S)
+    for i in range(3):
+        x = synth.normal(synth.stream(121, 10 * D + i), (D,))
+        ref = orc.ffn_dense(wg_b, wu_b, wd_b, orc.Q8_0, x, D, S, act=act, pool=pool)
+        a = np.zeros(D, np.float32)
+        b = np.zeros(D, np.float32)
+        ctx.ffn_dense(a, wg, wu, wd, x, act=act)
+        ctx.ffn_dense(b, wg, wu, wd, x, act=act, unfused=True)
+        assert rel_l2(a, ref) <= 1e-5, (i, rel_l2(a, ref))
+        assert rel_l2(b, ref) <= 1e-5, (i, rel_l2(b, ref))
     for t in (wg, wu, wd):
         t.free()
 
@@ -713,6 +746,38 @@ def test_gpu_fused_layer_matches_oracle_and_unfused(ctx, pool, D, E, F, Kd, k, a
             assert rel_l2(res[mode][0], ref) <= 2e-4, (mode, rel_l2(res[mode][0], ref))
         assert rel_l2(res["atomic"][0], res["deterministic"][0]) <= 1e-6
     for t in (router, gate_up, down):
+        t.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pattern", ["pairs", "period16", "all_equal"])
+def test_gpu_fused_tied_logits(ctx, pool, pattern):
+    # Equal router rows give bit-equal logits.  The single-launch kernel
+    # selects from the logits at or above a group-maximum threshold (or by
+    # serial rounds when more than 64 reach it: all_equal) and must keep the
+    # tie rule, the lower index first (ops/moe.zig:87).
+    D, E, F, k = 512, 128, 256, 8
+    w = synth.moe_weights(91, D, E, F)
+    pick = {"pairs": np.arange(E) // 2, "period16": np.arange(E) % 16, "all_equal": None}[pattern]
+    router = np.zeros_like(w.router) if pick is None else w.router[pick]
+    w = dataclasses.replace(w, router=np.ascontiguousarray(router))
+    router_t, gate_up, down = lt.upload_moe(ctx, w)
+    for i in range(2):
+        x = synth.normal(synth.stream(92, i), (D,))
+        ref, rids, rw, agree = orc.moe_forward(w, x, k, norm_topk=True, pool=pool)
+        assert agree
+        if pattern == "all_equal":
+            assert rids.tolist() == list(range(k))
+        for mode in ("atomic", "deterministic"):
+            out = np.zeros(D, np.float32)
+            ids = np.zeros(k, np.uint32)
+            wt = np.zeros(k, np.float32)
+            ctx.moe_forward(out, x, router_t, gate_up, down, k, F, norm_topk=True, out_ids=ids, out_w=wt,
+                            deterministic=mode == "deterministic")
+            assert np.array_equal(ids, rids), (pattern, mode, i, ids, rids)
+            assert np.allclose(wt, rw, rtol=1e-5, atol=0), (pattern, mode, i)
+            assert rel_l2(out, ref) <= 2e-4, (pattern, mode, i, rel_l2(out, ref))
+    for t in (router_t, gate_up, down):
         t.free()
 
 
