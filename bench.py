@@ -588,14 +588,14 @@ def bench_ffn(args):
     us, dev_us, steps = timer.graph_steps(step, n_steps, 64)
     mean = timer.launches(step, args.kernel_iters)
     algo = CFG1_BYTES
-    log(f"cfg1: {us:.2f} us wall / {dev_us:.2f} device per FFN; {mean:.2f} us per call (2 launches)")
+    log(f"cfg1: {us:.2f} us wall / {dev_us:.2f} device per FFN; {mean:.2f} us per call (one launch)")
     result = base_record(
         args, "Dense FFN decode µs/token + achieved HBM GB/s at batch 1 (Q8_0, 896 -> 4864 -> 896)",
         round(us, 3), "us/token", steps, False, "Q8_0 weights x fp32 activations, fp32 accumulation",
         {"workload": "dense_ffn_q8_0_cfg1", "d_model": Dm, "d_ffn": Ff, "act": "silu", "batch": 1,
          "weight_copies": len(copies), "graph_steps": 64},
         {"device_us_per_step": round(dev_us, 3),
-         "roofline": roofline("k_gate_up_q8_0 + k_matvec_q8_0 (one FFN call)", algo, mean, "dense_ffn_cfg1",
+         "roofline": roofline("k_ffn_fused", algo, mean, "dense_ffn_cfg1",
                               args.kernel_iters), "parity": parity})
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_record(

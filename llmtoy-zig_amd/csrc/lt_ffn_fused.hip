@@ -270,8 +270,11 @@ FfnPlan plan_ffn_fused(int D, int S) {
     const int rows_max = 32 * ((nbS + 7) / 8);  // the largest group slice
     if (2 * ((nbS + 7) / 8) > 16 * kMV) return pl;
     pl.cu = (2 * (D / 32) + 63) / 64;
-    for (int P = 1; P <= kPMax && !pl.ok; P++)
-        for (int Q = 1; Q <= kQMax && !pl.ok; Q++) {
+    // fewest down steps first, then fewest gate/up passes (measured on
+    // config 1: 3 passes / 1 step 7.3 us, 2 / 2 7.4, 4 / 1 8.4; a 2048-block
+    // grid with 1 / 1 7.6)
+    for (int Q = 1; Q <= kQMax && !pl.ok; Q++)
+        for (int P = 1; P <= kPMax && !pl.ok; P++) {
             const int NG = (rows_max + 4 * P - 1) / (4 * P), ND = (D + 16 * Q - 1) / (16 * Q);
             if (NG + ND <= kFusedBlocks / 8 && ND <= kFfnFlags) {
                 pl.P = P;
