@@ -690,7 +690,7 @@ def bench_cfg4(args):
          "x_pool": args.xpool, "graph_steps": G},
         {"device_us_per_step": round(dev_us, 3), "deterministic_us_per_token": round(det_us, 3),
          "deterministic_device_us_per_token": round(det_dev_us, 3),
-         "roofline": roofline("lt_moe_forward with shared FFN (whole call)", CFG4_BYTES, mean, "moe_cfg4",
+         "roofline": roofline("lt_moe_forward with shared FFN (whole call)", CFG4_BYTES, mean, "moe_fused_cfg4",
                               args.kernel_iters), "parity": parity})
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_record(
@@ -934,6 +934,50 @@ def bench_formats(args):
     ctx.close()
 
 
+def bench_stream(args):
+    """The read ceiling of one launch: lt_stream_read (16-byte loads, every
+    load in flight before any is used, nothing else) over each config's
+    algorithmic byte count, cold (each launch reads a fresh region of a 4 GiB
+    buffer, far past the 256 MB Infinity Cache) and hot (the same region
+    every launch).  Timed like the roofline figures of the other workloads:
+    back-to-back launches between one HIP event pair, and graph replay."""
+    from llmtoy_amd.hip import DeviceArray, check, hip
+    import llmtoy_amd as lt
+    import numpy as np
+
+    ctx = lt.Context(0)
+    timer = Timer(ctx.stream)
+    total = 4 << 30
+    buf = DeviceArray((total,), np.uint8)
+    check(hip().hipMemset(buf.ptr, 1, total), "hipMemset")
+    sizes = {"cfg2": 9469952, "cfg1": 13976576, "cfg3": FUSED_BYTES, "cfg4": CFG4_BYTES, "cfg2b": 128238080}
+    rows = {}
+    for name, nb in sizes.items():
+        nb = nb // 256 * 256
+        nreg = total // nb
+        for mode in ("cold", "hot"):
+            def step(i, nb=nb, nreg=nreg, mode=mode):
+                off = ((i * 7 + 3) % nreg) * nb if mode == "cold" else 0
+                ctx.stream_read(buf.ptr + off, nb)
+            mean = timer.launches(step, args.kernel_iters)
+            wall, dev, _ = timer.graph_steps(step, timed_steps(args), 64)
+            rows[f"{name}_{mode}"] = {"bytes": nb, "mean_launch_us": round(mean, 3), "graph_us": round(dev, 3),
+                                      "gbps": round(nb / (mean * 1e-6) / 1e9, 1),
+                                      "frac_of_8tbs": round(nb / (mean * 1e-6) / 1e9 / PEAK_GBPS, 4)}
+            log(f"stream {name} {mode}: {nb} B {mean:.3f} us per launch, {rows[f'{name}_{mode}']['gbps']} GB/s")
+    big = rows["cfg2b_cold"]
+    result = base_record(
+        args, "read ceiling of one launch: GB/s of a streaming read kernel (lt_stream_read)", big["gbps"], "GB/s",
+        args.kernel_iters, True, "u8 (16-byte loads, no arithmetic)",
+        {"workload": "stream_read", "buffer_bytes": total, "sizes": {k: v for k, v in sizes.items()}},
+        {"rows": rows, "roofline": {"bound": "hbm", "achieved": big["gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
+                                    "frac": big["frac_of_8tbs"], "traffic": None, "kernel": "k_stream_read",
+                                    "algorithmic_bytes": big["bytes"], "mean_launch_us": big["mean_launch_us"]}})
+    print(json.dumps(result), flush=True)
+    buf.free()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -949,7 +993,8 @@ def main():
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF file load + upload check")
     ap.add_argument("--apex", action="store_true",
                     help="--workload gemma4 with the APEX expert formats (Q3_K gate/up, IQ4_NL down)")
-    ap.add_argument("--workload", choices=["decode", "cfg1", "cfg2", "cfg2b", "cfg4", "prefill", "gemma4", "formats"],
+    ap.add_argument("--workload", choices=["decode", "cfg1", "cfg2", "cfg2b", "cfg4", "prefill", "gemma4", "formats",
+                                           "stream"],
                     default="decode")
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
@@ -965,7 +1010,7 @@ def main():
     if args.warmup is None:
         args.warmup = 5 if args.workload == "prefill" else 64
     {"decode": bench_decode, "cfg1": bench_ffn, "cfg2": bench_matvec, "cfg2b": bench_matvec, "cfg4": bench_cfg4,
-     "prefill": bench_prefill, "gemma4": bench_gemma4, "formats": bench_formats}[args.workload](args)
+     "prefill": bench_prefill, "gemma4": bench_gemma4, "formats": bench_formats, "stream": bench_stream}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -132,6 +132,11 @@ int lt_tensor_read(lt_ctx *ctx, const lt_tensor *t, void *host_bytes, size_t nby
  * rotate weight copies so that timing is not served from the 256 MB cache. */
 int lt_tensor_clone(lt_ctx *ctx, const lt_tensor *src, lt_tensor **out_tensor);
 int lt_tensor_free(lt_ctx *ctx, lt_tensor *t);
+/* Read nbytes (a positive multiple of 16) of device memory at buf (16-byte
+ * aligned) once, with a streaming kernel of 16-byte loads, on the context's
+ * stream.  No counterpart in the reference: bench.py times it as the read
+ * ceiling of one launch that the decode kernels' streams are set against. */
+int lt_stream_read(lt_ctx *ctx, const void *buf, size_t nbytes);
 /* Device bytes held by the tensor (equal to the GGUF byte count). */
 size_t lt_tensor_bytes(const lt_tensor *t);
 

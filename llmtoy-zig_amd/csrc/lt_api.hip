@@ -62,7 +62,7 @@ struct lt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // context-owned device scratch, grown on demand
-    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh, pf, nrm;
+    DevBuf x, out, logits, h, ids, w, shared, g, u, ids_io, w_io, bias, eh, pf, nrm, sink;
     // buffers replaced by larger ones; a HIP graph captured earlier may still
     // reference them, so they are released only by lt_destroy
     std::vector<void *> retired;
@@ -478,7 +478,7 @@ extern "C" void lt_destroy(lt_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     DevBuf *bufs[] = {&ctx->x, &ctx->out, &ctx->logits, &ctx->h, &ctx->ids, &ctx->w,
                       &ctx->shared, &ctx->g, &ctx->u, &ctx->ids_io, &ctx->w_io, &ctx->bias, &ctx->eh, &ctx->pf,
-                      &ctx->nrm};
+                      &ctx->nrm, &ctx->sink};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     for (void *p : ctx->retired) (void)hipFree(p);
@@ -569,6 +569,15 @@ extern "C" int lt_tensor_clone(lt_ctx *ctx, const lt_tensor *src, lt_tensor **ou
     set_planes(t->t);
     *out_tensor = t;
     return LT_OK;
+}
+
+extern "C" int lt_stream_read(lt_ctx *ctx, const void *buf, size_t nbytes) {
+    if (!ctx || !buf) return fail(ctx, LT_ERR_INVALID, "null argument");
+    if (nbytes == 0 || nbytes % 16 != 0 || ((uintptr_t)buf & 15) != 0)
+        return fail(ctx, LT_ERR_INVALID, "nbytes must be a positive multiple of 16 and buf 16-byte aligned");
+    int rc = ensure(ctx, ctx->sink, 256);
+    if (rc) return rc;
+    return launch_rc(ctx, lt::launch_stream_read(buf, nbytes, (uint32_t *)ctx->sink.p, ctx->stream), "stream_read");
 }
 
 extern "C" int lt_tensor_free(lt_ctx *ctx, lt_tensor *t) {

@@ -507,6 +507,8 @@ inline FfnScratch ffn_scratch_at(uint8_t *base, uint32_t *err, int xcd_local) {
     return s;
 }
 FfnPlan plan_ffn_fused(int D, int S);
+// Reads nbytes (a multiple of 16) at buf once (lt_probe.hip).
+hipError_t launch_stream_read(const void *buf, size_t nbytes, uint32_t *sink, hipStream_t s);
 hipError_t launch_ffn_fused(const FfnPlan &pl, const DevTensor &G, const DevTensor &U, const DevTensor &Dn,
                             const float *x, uint32_t act, float *out, const FfnScratch &sc, hipStream_t s);
 hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const float *bias, const float *x,

@@ -24,6 +24,7 @@ def hip() -> C.CDLL:
             ("hipFree", C.c_int, [vp]),
             ("hipMemcpy", C.c_int, [vp, vp, sz, C.c_int]),
             ("hipMemcpyAsync", C.c_int, [vp, vp, sz, C.c_int, vp]),
+            ("hipMemset", C.c_int, [vp, C.c_int, sz]),
             ("hipDeviceSynchronize", C.c_int, []),
             ("hipStreamSynchronize", C.c_int, [vp]),
             ("hipEventCreate", C.c_int, [C.POINTER(vp)]),

@@ -67,7 +67,7 @@ _ERRS = {LT_ERR_UNSUPPORTED: UnsupportedError, LT_ERR_INVALID: InvalidError, LT_
 
 EXPORTS = [
     "lt_init", "lt_destroy", "lt_last_error", "lt_sync", "lt_stream", "lt_tensor_upload", "lt_tensor_read", "lt_tensor_clone",
-    "lt_tensor_free", "lt_tensor_bytes", "lt_matvec", "lt_ffn_dense", "lt_moe_router_topk", "lt_expert_gate_up_id",
+    "lt_tensor_free", "lt_tensor_bytes", "lt_stream_read", "lt_matvec", "lt_ffn_dense", "lt_moe_router_topk", "lt_expert_gate_up_id",
     "lt_expert_down_id", "lt_moe_forward", "lt_moe_forward_noalloc", "lt_moe_prefill", "lt_rmsnorm", "lt_add_rmsnorm",
     "lt_rmsnorm_weighted_raw_scaled", "lt_moe_tail", "lt_gemma4_moe_block", "lt_profile_report",
 ]
@@ -95,6 +95,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "lt_tensor_clone": (i32, [vp, vp, C.POINTER(vp)]),
         "lt_tensor_free": (i32, [vp, vp]),
         "lt_tensor_bytes": (sz, [vp]),
+        "lt_stream_read": (i32, [vp, vp, sz]),
         "lt_matvec": (i32, [vp, vp, vp, vp, u32]),
         "lt_ffn_dense": (i32, [vp, vp, vp, vp, vp, vp, u32, u32]),
         "lt_moe_router_topk": (i32, [vp, vp, vp, vp, u32, u32, vp, vp, vp]),
@@ -230,6 +231,10 @@ class Context:
         fl = self._io(out, x)
         self._check(self.lib.lt_matvec(self.ptr, _ptr(out)[0], W.handle, _ptr(x)[0], fl))
         return out
+
+    def stream_read(self, ptr: int, nbytes: int):
+        """Enqueue one read of nbytes of device memory at ptr (the read-ceiling probe)."""
+        self._check(self.lib.lt_stream_read(self.ptr, C.c_void_p(ptr), nbytes))
 
     def ffn_dense(self, out, Wg: Tensor, Wu: Tensor, Wd: Tensor, x, act=ACT_SILU, unfused=False):
         """unfused: gate/up and down as two launches instead of the single-launch kernel."""

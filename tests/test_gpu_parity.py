@@ -880,3 +880,18 @@ def test_gpu_fused_accumulate_and_alternating_shapes(ctx, cfg3, pool):
         assert rel_l2(so, sref) <= REL_L2, i
     for t in (sr, sg, sd):
         t.free()
+
+
+@pytest.mark.gpu
+def test_gpu_stream_read(ctx):
+    # the read-ceiling probe: enqueues, reads, and rejects what it cannot take
+    from llmtoy_amd.hip import DeviceArray
+    buf = DeviceArray((1 << 20,), np.uint8)
+    for nb in (16, 4096, 1 << 20):
+        ctx.stream_read(buf.ptr, nb)
+    ctx.sync()
+    with pytest.raises(InvalidError):
+        ctx.stream_read(buf.ptr, 24)
+    with pytest.raises(InvalidError):
+        ctx.stream_read(buf.ptr + 8, 16)
+    buf.free()
