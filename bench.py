@@ -787,7 +787,7 @@ def bench_prefill(args):
     us, dev_us, steps = timer.graph_steps(call, steps_req, 16)
     result = base_record(
         args, "MoE-layer batched prefill tokens/s (config 5, 512 tokens)", round(512 / (us * 1e-6)), "tokens/s",
-        steps, True, "bf16 MFMA (Q4_K dequantised to bf16 in LDS), fp32 accumulation",
+        steps, True, "f16 MFMA (Q4_K dequantised to f16 in LDS; X per-row power-of-two scaled to f16), fp32 accumulation",
         {"workload": "qwen3_moe_prefill_cfg5", "tokens": 512, "d_model": D, "n_experts": E, "d_expert": F,
          "top_k": K, "router_bias": "zipf(1.1)", "graph_steps": 16},
         {"ms_per_step": round(us / 1e3, 4), "us_per_call": round(us, 2), "device_us_per_call": round(dev_us, 2),

@@ -7,13 +7,14 @@
 //   2. dispatch: one block counts tokens per expert, lays out per-expert
 //      row ranges ("sorted rows"), cuts each range into chunks of at most
 //      MC = 128 rows, and scatters (token, slot) assignments into them;
-//      X is converted to bf16 once (k_prefill_x_bf16);
+//      X is converted to f16 once (k_prefill_x_f16), each row scaled by a
+//      power of two that keeps it far inside f16's range;
 //   3. grouped gate/up GEMM: one block per (chunk, 64 output columns); its
-//      128 weight rows (64 gate + 64 up) are dequantised from Q4_K to bf16
+//      128 weight rows (64 gate + 64 up) are dequantised from Q4_K to f16
 //      in LDS once per K stage and shared by the chunk's 4 token tiles (one
-//      32-row tile per wavefront, v_mfma_f32_32x32x16_bf16, fp32
+//      32-row tile per wavefront, v_mfma_f32_32x32x16_f16, fp32
 //      accumulation); gate and up of an output column sit in the same
-//      wavefront, so the epilogue act(gate) * up -> H (bf16) needs no
+//      wavefront, so the epilogue act(gate) * up -> H (f16) needs no
 //      exchange;
 //   4. grouped down GEMM: one block per (chunk, 128 output rows), the same
 //      scheme with H as the A operand -> Y (fp32, sorted rows);
@@ -25,18 +26,29 @@
 // A row's result does not depend on which chunk position it lands in, so
 // the atomically assigned positions leave the output bit-identical run to
 // run.
+//
+// f16 rather than bf16 tiles: a Q4_K nibble q becomes the exact f16 1024 + q
+// (or 1024 + 16 q) with one v_and_or (its bits in the mantissa under 1024's
+// exponent), two such values per dword, so the dequantisation is a packed
+// f16 subtract of 1024 and a packed f16 fma (d sc) q - dmin mn per pair of
+// weights, with no conversion or packing step -- and f16 keeps 3 more
+// mantissa bits than bf16.  The pairs come out as elements (0, 2) and (1, 3) of each aligned
+// group of 4, so every K dimension is stored with the middle two of each 4
+// swapped (kperm): X and H are written in that order, and the MFMA sums the
+// same products.
 #include "lt_internal.h"
 
 namespace lt {
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 namespace {
 
 constexpr int MC = 128;       // sorted rows per chunk: 4 wavefronts x 32
 constexpr int KS = 128;       // K per stage: half a Q4_K super-block
-constexpr int LDK = KS + 8;   // padded LDS row (bf16 elements)
+constexpr int LDK = KS + 8;   // padded LDS row (f16 elements)
 constexpr int NB = 128;       // weight rows per block (gate/up: 64 gate + 64 up)
 constexpr int BN1 = 64;       // gate/up output columns per block
 constexpr int BN2 = 128;      // down output rows (= output columns of Y) per block
@@ -52,8 +64,9 @@ struct Ws {
     int *n_chunks;  // [1]
     int *perm;      // [T*k] token of each sorted row
     int *pos;       // [T*k] sorted row of assignment t*k + s
-    __bf16 *Xb;     // [T][D] X in bf16
-    __bf16 *H;      // [T*k][Kd]
+    float *rs;      // [T] row scales: X row t = rs[t] * Xh row t
+    _Float16 *Xh;   // [T][D] X / rs in f16, columns in kperm order
+    _Float16 *H;    // [T*k][Kd], columns in kperm order
     float *Y;       // [T*k][D]
 };
 
@@ -71,65 +84,68 @@ Ws carve(void *base, int T, int k, int E, int Kd, int D) {
     w.n_chunks = (int *)p; p += 256;
     w.perm = (int *)p; p += align256(TK * 4);
     w.pos = (int *)p; p += align256(TK * 4);
-    w.Xb = (__bf16 *)p; p += align256((size_t)T * D * 2);
-    w.H = (__bf16 *)p; p += align256(TK * Kd * 2);
+    w.rs = (float *)p; p += align256((size_t)T * 4);
+    w.Xh = (_Float16 *)p; p += align256((size_t)T * D * 2);
+    w.H = (_Float16 *)p; p += align256(TK * Kd * 2);
     w.Y = (float *)p; p += align256(TK * D * 4);
     return w;
 }
 
-typedef float float2v __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+// The K order of every f16 operand: within each aligned group of 4 the
+// middle two elements are swapped (an involution).
+__host__ __device__ __forceinline__ int kperm(int c) { return (c & ~3) | ((c & 1) << 1) | ((c >> 1) & 1); }
 
-// Two fp32 values -> a packed bf16 pair (round to nearest even; one
-// v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    const float2v v = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
-}
-
-// 16 fp32 values -> 16 bf16 as two 16-byte words.
-__device__ __forceinline__ void store_bf16x16(__bf16 *dst, const float (&v)[16]) {
-    uint4 a, b;
-    a.x = pack_bf16x2(v[0], v[1]);
-    a.y = pack_bf16x2(v[2], v[3]);
-    a.z = pack_bf16x2(v[4], v[5]);
-    a.w = pack_bf16x2(v[6], v[7]);
-    b.x = pack_bf16x2(v[8], v[9]);
-    b.y = pack_bf16x2(v[10], v[11]);
-    b.z = pack_bf16x2(v[12], v[13]);
-    b.w = pack_bf16x2(v[14], v[15]);
-    *reinterpret_cast<uint4 *>(dst) = a;
-    *reinterpret_cast<uint4 *>(dst + 8) = b;
+// 4 packed words of (1024 + q 2^j) pairs -> (scale q + neg_min) pairs
+// (scale already divided by 2^j), stored as 8 f16 at dst.
+__device__ __forceinline__ void q4_pairs_to_f16(const uint32_t (&v)[4], half2v sc, half2v nm, _Float16 *dst) {
+    const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2v q = __builtin_bit_cast(half2v, v[i]) - k1024;  // exact: q 2^j, q in 0..15
+        o[i] = __builtin_bit_cast(uint32_t, q * sc + nm);
+    }
+    *reinterpret_cast<uint4 *>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Q4_K 16-byte chunk cc (0..7) of a super-block with header hdr, dequantised
-// (quant/dequant.zig:157-187: (d*sc)*q - dmin*mn) and stored as bf16:
-// elements 64p + 16(cc&1) + [0, 16) at lo, the same + 32 at hi (p = cc / 2).
-__device__ __forceinline__ void q4k_chunk_to_bf16(uint4 hdr, uint4 q, int cc, __bf16 *lo_dst, __bf16 *hi_dst) {
+// (quant/dequant.zig:157-187: (d*sc)*q - dmin*mn) to f16: elements 64p +
+// 16(cc&1) + [0, 16) at lo_dst, the same + 32 at hi_dst (p = cc / 2), each
+// run in kperm order.  Quant byte j holds element j of the low run in its
+// low nibble and of the high run in its high nibble.  Under f16's exponent
+// of 1024 (0x6400) a nibble in mantissa bits 0-3 reads 1024 + q and one in
+// bits 4-7 reads 1024 + 16 q, both exact, so (w & 0x000f000f) | 0x64006400
+// is the low-run pair (e0, e2) of the word's bytes 0 and 2, (w & 0x00f000f0)
+// | 0x64006400 the high-run pair, and the same of w >> 8 gives (e1, e3):
+// one v_and_or per pair (the masks kept in registers so that the compiler
+// forms it), the high run's scale divided by 16.
+__device__ __forceinline__ void q4k_chunk_to_f16(uint4 hdr, uint4 q, int cc, _Float16 *lo_dst, _Float16 *hi_dst) {
     const float d = f16_bits_to_f32(hdr.x), dmin = f16_bits_to_f32(hdr.x >> 16);
     const int p = cc >> 1;
     const int sh = (p & 1) * 16;
     const uint32_t ys = hdr.y >> sh, zs = hdr.z >> sh, ws = hdr.w >> sh;
     const uint32_t scp = opaque(p < 2 ? (ys & 0x3f3fu) : ((ws & 0x0f0fu) | ((ys >> 2) & 0x3030u)));
     const uint32_t mnp = opaque(p < 2 ? (zs & 0x3f3fu) : (((ws >> 4) & 0x0f0fu) | ((zs >> 2) & 0x3030u)));
-    const float d1 = d * (float)(scp & 0xffu), m1 = dmin * (float)(mnp & 0xffu);
-    const float d2 = d * (float)((scp >> 8) & 0xffu), m2 = dmin * (float)((mnp >> 8) & 0xffu);
+    const _Float16 d1 = (_Float16)(d * (float)(scp & 0xffu)), m1 = (_Float16)(-(dmin * (float)(mnp & 0xffu)));
+    const _Float16 d2 = (_Float16)(d * (float)((scp >> 8) & 0xffu) * 0.0625f);
+    const _Float16 m2 = (_Float16)(-(dmin * (float)((mnp >> 8) & 0xffu)));
+    const uint32_t ml = opaque(0x000f000fu), mh = opaque(0x00f000f0u), ex = opaque(0x64006400u);
     const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
-    float lo[16], hi[16];
+    uint32_t lo[8], hi[8];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const uint32_t l = opaque(wv[t] & 0x0f0f0f0fu), h = opaque((wv[t] >> 4) & 0x0f0f0f0fu);
-        lo[4 * t + 0] = d1 * (float)(l & 0xffu) - m1;
-        lo[4 * t + 1] = d1 * (float)((l >> 8) & 0xffu) - m1;
-        lo[4 * t + 2] = d1 * (float)((l >> 16) & 0xffu) - m1;
-        lo[4 * t + 3] = d1 * (float)(l >> 24) - m1;
-        hi[4 * t + 0] = d2 * (float)(h & 0xffu) - m2;
-        hi[4 * t + 1] = d2 * (float)((h >> 8) & 0xffu) - m2;
-        hi[4 * t + 2] = d2 * (float)((h >> 16) & 0xffu) - m2;
-        hi[4 * t + 3] = d2 * (float)(h >> 24) - m2;
+        const uint32_t w = wv[t], w8 = w >> 8;
+        lo[2 * t] = (w & ml) | ex;
+        lo[2 * t + 1] = (w8 & ml) | ex;
+        hi[2 * t] = (w & mh) | ex;
+        hi[2 * t + 1] = (w8 & mh) | ex;
     }
-    store_bf16x16(lo_dst, lo);
-    store_bf16x16(hi_dst, hi);
+    const uint32_t lo0[4] = {lo[0], lo[1], lo[2], lo[3]}, lo1[4] = {lo[4], lo[5], lo[6], lo[7]};
+    const uint32_t hi0[4] = {hi[0], hi[1], hi[2], hi[3]}, hi1[4] = {hi[4], hi[5], hi[6], hi[7]};
+    q4_pairs_to_f16(lo0, half2v{d1, d1}, half2v{m1, m1}, lo_dst);
+    q4_pairs_to_f16(lo1, half2v{d1, d1}, half2v{m1, m1}, lo_dst + 8);
+    q4_pairs_to_f16(hi0, half2v{d2, d2}, half2v{m2, m2}, hi_dst);
+    q4_pairs_to_f16(hi1, half2v{d2, d2}, half2v{m2, m2}, hi_dst + 8);
 }
 
 // One thread's share of a K stage's weight tile: 2 units of (weight row r,
@@ -151,12 +167,12 @@ __device__ __forceinline__ void stage_load(StageRegs &R, const uint8_t *hdr, con
 
 // Stage ks's chunk cc = 4 (ks & 1) + c lands at local K 64 (c / 2) + 16 (c & 1)
 // (low nibbles) and +32 (high nibbles).
-__device__ __forceinline__ void stage_dequant(const StageRegs &R, __bf16 (*Bs)[LDK], int r0, int ks, int c) {
+__device__ __forceinline__ void stage_dequant(const StageRegs &R, _Float16 (*Bs)[LDK], int r0, int ks, int c) {
     const int cc = (ks & 1) * 4 + c, local = 64 * (c >> 1) + 16 * (c & 1);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        __bf16 *row = Bs[r0 + 64 * j];
-        q4k_chunk_to_bf16(R.h[j], R.q[j], cc, row + local, row + local + 32);
+        _Float16 *row = Bs[r0 + 64 * j];
+        q4k_chunk_to_f16(R.h[j], R.q[j], cc, row + local, row + local + 32);
     }
 }
 
@@ -169,13 +185,13 @@ __device__ __forceinline__ void stage_dequant(const StageRegs &R, __bf16 (*Bs)[L
 // keeps all four wavefronts' MFMA pipes busy.  arow points at this lane's A
 // row (row 32 t + lane % 32 of the chunk) plus its K half (lane / 32) * 8.
 template <int S>
-__device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], __bf16 (*Bs)[NB][LDK], const uint8_t *hdr,
+__device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[NB][LDK], const uint8_t *hdr,
                                              const uint8_t *qs, int nsb, const size_t (&wrow)[2], int NS,
-                                             const __bf16 *arow, bool wave_on, int kb, int tid, int lane) {
+                                             const _Float16 *arow, bool wave_on, int kb, int tid, int lane) {
     constexpr int NK = 8 / S;
     const int c = tid & 3, r0 = tid >> 2;
     StageRegs R0, R1;
-    bf16x8 a0[NK], a1[NK];
+    f16x8 a0[NK], a1[NK];
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[i] = floatx16{};
     // Every wavefront issues the same loads on every path (stage indices
@@ -186,7 +202,7 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], __bf16 (*Bs)[NB
     stage_load(R0, hdr, qs, nsb, wrow, 0, c);
     stage_load(R1, hdr, qs, nsb, wrow, 1, c);  // NS = 2 * super-blocks >= 2
 #pragma unroll
-    for (int i = 0; i < NK; i++) a0[i] = *reinterpret_cast<const bf16x8 *>(arow + (kb + i) * 16);
+    for (int i = 0; i < NK; i++) a0[i] = *reinterpret_cast<const f16x8 *>(arow + (kb + i) * 16);
     stage_dequant(R0, Bs[0], r0, 0, c);
     stage_load(R0, hdr, qs, nsb, wrow, min(2, NS - 1), c);
     __syncthreads();
@@ -198,20 +214,20 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], __bf16 (*Bs)[NB
         for (int half = 0; half < 2; half++) {
             const int st = ks + half;
             StageRegs &Rn = half ? R0 : R1;   // stage st + 1
-            bf16x8(&acur)[NK] = half ? a1 : a0;
-            bf16x8(&anext)[NK] = half ? a0 : a1;
+            f16x8(&acur)[NK] = half ? a1 : a0;
+            f16x8(&anext)[NK] = half ? a0 : a1;
             const size_t sa = (size_t)min(st + 1, NS - 1) * KS;
 #pragma unroll
-            for (int i = 0; i < NK; i++) anext[i] = *reinterpret_cast<const bf16x8 *>(arow + sa + (kb + i) * 16);
+            for (int i = 0; i < NK; i++) anext[i] = *reinterpret_cast<const f16x8 *>(arow + sa + (kb + i) * 16);
             if (wave_on) {
-                __bf16(*B)[LDK] = Bs[st & 1];
+                _Float16(*B)[LDK] = Bs[st & 1];
 #pragma unroll
                 for (int i = 0; i < NK; i++)
 #pragma unroll
                     for (int ct = 0; ct < 4; ct++) {
-                        const bf16x8 b = *reinterpret_cast<const bf16x8 *>(
+                        const f16x8 b = *reinterpret_cast<const f16x8 *>(
                             &B[32 * ct + (lane & 31)][(kb + i) * 16 + (lane >> 5) * 8]);
-                        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(acur[i], b, acc[ct], 0, 0, 0);
+                        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(acur[i], b, acc[ct], 0, 0, 0);
                     }
             }
             if (st + 1 < NS) stage_dequant(Rn, Bs[(st + 1) & 1], r0, st + 1, c);
@@ -228,14 +244,14 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], __bf16 (*Bs)[NB
 // on timing.  acc element i of a 32x32 tile is C[(i / 4) * 8 + (lane / 32) *
 // 4 + i % 4][lane % 32].
 template <int S, typename Row, typename Epi>
-__device__ __forceinline__ void run_block(__bf16 (*Bs)[NB][LDK], const uint8_t *hdr, const uint8_t *qs, int nsb,
+__device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t *hdr, const uint8_t *qs, int nsb,
                                           const size_t (&wrow)[2], int NS, int mc, Row row_ptr, Epi epi, int tid,
                                           int wave, int lane) {
     constexpr int NT = 4 / S;  // token tiles handled side by side
     const int t = wave % NT, q = wave / NT;
     const int mrow = 32 * t + (lane & 31);
     const bool wave_on = 32 * t < mc;
-    const __bf16 *arow = row_ptr(mrow < mc ? mrow : 0) + (lane >> 5) * 8;
+    const _Float16 *arow = row_ptr(mrow < mc ? mrow : 0) + (lane >> 5) * 8;
     floatx16 acc[4];
     grouped_gemm<S>(acc, Bs, hdr, qs, nsb, wrow, NS, arow, wave_on, q * (8 / S), tid, lane);
     if (S == 1) {
@@ -343,16 +359,43 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
     }
 }
 
-// X (fp32) -> bf16, 8 elements per thread; n % 8 == 0.
-__global__ void __launch_bounds__(256) k_prefill_x_bf16(const float *__restrict__ X, __bf16 *__restrict__ Xb,
-                                                        size_t n8) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n8) return;
-    const float4 a = ldg16f(X + 8 * i), b = ldg16f(X + 8 * i + 4);
-    bf16x8 o;
-    o[0] = (__bf16)a.x; o[1] = (__bf16)a.y; o[2] = (__bf16)a.z; o[3] = (__bf16)a.w;
-    o[4] = (__bf16)b.x; o[5] = (__bf16)b.y; o[6] = (__bf16)b.z; o[7] = (__bf16)b.w;
-    *reinterpret_cast<bf16x8 *>(Xb + 8 * i) = o;
+// X (fp32) -> f16, one block per token row: the row is divided by rs =
+// 2^e, the smallest power of two (e >= 0) that brings max |x| to at most
+// 2^14 (exact; f16's range ends near 2^16), and stored in kperm order.  D %
+// 8 == 0; the fp32 row is read twice (max, then values).
+__global__ void __launch_bounds__(256) k_prefill_x_f16(const float *__restrict__ X, _Float16 *__restrict__ Xh,
+                                                       float *__restrict__ rs, int D) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *xr = X + (size_t)t * D;
+    float m = 0.0f;
+    for (int i = 4 * tid; i < D; i += 4 * 256) {
+        const float4 v = ldg16f(xr + i);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    __shared__ float s_m[4];
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 8, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    if ((tid & 63) == 0) s_m[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    int e = 0;
+    if (m > 16384.0f) e = ilogbf(m) - 13;  // m / 2^e < 2^14
+    if (!(m <= 3.0e38f)) e = 0;             // inf / NaN rows pass through unscaled
+    const float inv = ldexpf(1.0f, -e);
+    if (tid == 0) rs[t] = ldexpf(1.0f, e);
+    _Float16 *hr = Xh + (size_t)t * D;
+    for (int i = 8 * tid; i < D; i += 8 * 256) {
+        const float4 a = ldg16f(xr + i), b = ldg16f(xr + i + 4);
+        // kperm within each 4: positions (0, 1, 2, 3) take elements (0, 2, 1, 3)
+        f16x8 o;
+        o[0] = (_Float16)(a.x * inv); o[1] = (_Float16)(a.z * inv); o[2] = (_Float16)(a.y * inv); o[3] = (_Float16)(a.w * inv);
+        o[4] = (_Float16)(b.x * inv); o[5] = (_Float16)(b.z * inv); o[6] = (_Float16)(b.y * inv); o[7] = (_Float16)(b.w * inv);
+        *reinterpret_cast<f16x8 *>(hr + i) = o;
+    }
 }
 
 // ---------------------------------------------------------------- gate/up
@@ -362,17 +405,18 @@ __global__ void __launch_bounds__(256) k_prefill_x_bf16(const float *__restrict_
 // up), so h = act(gate) * up is formed in registers.
 __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restrict__ hdr,
                                                          const uint8_t *__restrict__ qs, int nsb, int F,
-                                                         const __bf16 *__restrict__ Xb, int D,
+                                                         const _Float16 *__restrict__ Xh,
+                                                         const float *__restrict__ rs, int D,
                                                          const int *__restrict__ chunks,
                                                          const int *__restrict__ n_chunks,
                                                          const int *__restrict__ offsets,
                                                          const int *__restrict__ perm, uint32_t act,
-                                                         __bf16 *__restrict__ H, int Kd) {
+                                                         _Float16 *__restrict__ H, int Kd) {
     if ((int)blockIdx.y >= *n_chunks) return;
     const int e = chunks[3 * blockIdx.y], m0 = chunks[3 * blockIdx.y + 1], mc = chunks[3 * blockIdx.y + 2];
     const int base = offsets[e];
     const int n0 = blockIdx.x * BN1;
-    __shared__ __attribute__((aligned(16))) __bf16 Bs[2][NB][LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     size_t wrow[2];
 #pragma unroll
@@ -381,14 +425,19 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
         wrow[j] = (size_t)e * 2 * F + (r < BN1 ? n0 + r : F + n0 + (r - BN1));
     }
     const int *prow = perm + base + m0;
-    auto row_ptr = [&](int m) { return Xb + (size_t)prow[m] * D; };
-    // ct 0, 1 = gate columns n0 + [0, 64), ct 2, 3 = the matching up columns
+    auto row_ptr = [&](int m) { return Xh + (size_t)prow[m] * D; };
+    // ct 0, 1 = gate columns n0 + [0, 64), ct 2, 3 = the matching up columns;
+    // the row scale brings gate and up back to X's scale; h is stored in
+    // kperm order (the down GEMM's K), clamped to f16's finite range
     auto epi = [&](int t, int i, const float (&v)[4]) {
         const int m = 32 * t + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
         if (m < mc) {
-            __bf16 *hrow = H + (size_t)(base + m0 + m) * Kd + n0 + (lane & 31);
-            hrow[0] = (__bf16)(act_apply(act, v[0]) * v[2]);
-            hrow[32] = (__bf16)(act_apply(act, v[1]) * v[3]);
+            const float r = rs[prow[m]];
+            _Float16 *hrow = H + (size_t)(base + m0 + m) * Kd;
+            const int c0 = n0 + (lane & 31);
+            const float h0 = act_apply(act, v[0] * r) * (v[2] * r), h1 = act_apply(act, v[1] * r) * (v[3] * r);
+            hrow[kperm(c0)] = (_Float16)fminf(fmaxf(h0, -65504.0f), 65504.0f);
+            hrow[kperm(c0 + 32)] = (_Float16)fminf(fmaxf(h1, -65504.0f), 65504.0f);
         }
     };
     const int nt = (mc + 31) / 32, NS = 2 * nsb;
@@ -401,27 +450,27 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
     if (blockIdx.x == 0 && Kd > F)  // zero K padding of the down product
         for (int i = tid; i < mc * (Kd - F); i += 256) {
             const int m = i / (Kd - F), col = F + i % (Kd - F);
-            H[(size_t)(base + m0 + m) * Kd + col] = (__bf16)0.f;
+            H[(size_t)(base + m0 + m) * Kd + col] = (_Float16)0.f;  // (kperm keeps [F, Kd): F % 4 == 0)
         }
 }
 
 // ---------------------------------------------------------------- down
 // Block: chunk x output rows [n0, n0 + 128) of the expert's down matrix
-// (= columns of Y); wavefront w computes token tile w, A = H rows (bf16).
+// (= columns of Y); wavefront w computes token tile w, A = H rows (f16).
 __global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict__ hdr, const uint8_t *__restrict__ qs,
-                                                      int nsb, int D, const __bf16 *__restrict__ H, int Kd,
+                                                      int nsb, int D, const _Float16 *__restrict__ H, int Kd,
                                                       const int *__restrict__ chunks, const int *__restrict__ n_chunks,
                                                       const int *__restrict__ offsets, float *__restrict__ Y) {
     if ((int)blockIdx.y >= *n_chunks) return;
     const int e = chunks[3 * blockIdx.y], m0 = chunks[3 * blockIdx.y + 1], mc = chunks[3 * blockIdx.y + 2];
     const int base = offsets[e];
     const int n0 = blockIdx.x * BN2;
-    __shared__ __attribute__((aligned(16))) __bf16 Bs[2][NB][LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     size_t wrow[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) wrow[j] = (size_t)e * D + n0 + (tid >> 2) + 64 * j;
-    const __bf16 *hbase = H + (size_t)(base + m0) * Kd;
+    const _Float16 *hbase = H + (size_t)(base + m0) * Kd;
     auto row_ptr = [&](int m) { return hbase + (size_t)m * Kd; };
     auto epi = [&](int t, int i, const float (&v)[4]) {
         const int m = 32 * t + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
@@ -457,7 +506,7 @@ __global__ void __launch_bounds__(256) k_prefill_combine(const float *__restrict
 size_t prefill_workspace_bytes(int T, int k, int E, int Kd, int D) {
     const size_t TK = (size_t)T * k;
     return align256((size_t)T * E * 4) + 2 * align256(TK * 4) + align256((size_t)(E + 1) * 4) +
-           align256((size_t)max_chunks((int)TK, E) * 12) + 256 + 2 * align256(TK * 4) +
+           align256((size_t)max_chunks((int)TK, E) * 12) + 256 + 2 * align256(TK * 4) + align256((size_t)T * 4) +
            align256((size_t)T * D * 2) + align256(TK * Kd * 2) + align256(TK * D * 4);
 }
 
@@ -472,12 +521,11 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
     hipLaunchKernelGGL(k_prefill_dispatch, dim3(1), dim3(1024), 0, s, w.ids, TK, k, E, w.offsets, w.chunks,
                        w.n_chunks, w.perm, w.pos);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const size_t n8 = (size_t)T * D / 8;
-    hipLaunchKernelGGL(k_prefill_x_bf16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, X, w.Xb, n8);
+    hipLaunchKernelGGL(k_prefill_x_f16, dim3((unsigned)T), dim3(256), 0, s, X, w.Xh, w.rs, D);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int mc = max_chunks(TK, E);
     hipLaunchKernelGGL(k_prefill_gate_up, dim3(F / BN1, mc), dim3(256), 0, s, GU.p0, GU.p1, (int)GU.blocks_per_row,
-                       F, w.Xb, D, w.chunks, w.n_chunks, w.offsets, w.perm, act, w.H, Kd);
+                       F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm, act, w.H, Kd);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_prefill_down, dim3(D / BN2, mc), dim3(256), 0, s, Dn.p0, Dn.p1, (int)Dn.blocks_per_row, D,
                        w.H, Kd, w.chunks, w.n_chunks, w.offsets, w.Y);

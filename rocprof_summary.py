@@ -7,8 +7,12 @@
       mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the kernel, and the
       same counters on the 256 MiB device copies bench.py --calibrate runs,
       giving the scale factors bench.py applies (counter KiB / true KiB).
+  counters <out.md> <kernel-substring> <db>=<command> [<db>=<command> ...]
+      mean value per dispatch of every counter each database holds, for the
+      kernels whose name contains the substring.
   mfma <db> <out.md> "<command>"
-      MFMA utilisation per kernel from rocprofv3's MfmaUtil / MfmaFlopsBF16.
+      MFMA utilisation per kernel from rocprofv3's MfmaUtil and the f16 MFMA
+      operation count SQ_INSTS_VALU_MFMA_MOPS_F16.
 """
 import json
 import sqlite3
@@ -25,6 +29,20 @@ def kernel_rows(db):
 
 
 def short(name):
+    """Readable kernel name: the demangled name without its arguments, or,
+    for a name the profiler left mangled (_ZN<len><id>...E...), its
+    namespace path."""
+    if name.startswith("_ZN"):
+        parts, i = [], 3
+        while i < len(name) and name[i].isdigit():
+            j = i
+            while name[j].isdigit():
+                j += 1
+            n = int(name[i:j])
+            parts.append(name[j:j + n])
+            i = j + n
+        if parts:
+            return "::".join(p for p in parts if not p.startswith("_GLOBAL__N"))
     return name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
 
 
@@ -95,8 +113,9 @@ def traffic(fetch_db, write_db, kernel, out, fetch_cmd, write_cmd):
 
 
 def mfma(db, out, cmd):
-    """rocprofv3's derived counters MfmaUtil (= sum of SQ_VALU_MFMA_BUSY_CYCLES
-    / (max GRBM_GUI_ACTIVE x SIMDs) x 100) and MfmaFlopsBF16, per kernel."""
+    """rocprofv3's derived counter MfmaUtil (= sum of SQ_VALU_MFMA_BUSY_CYCLES
+    / (max GRBM_GUI_ACTIVE x SIMDs) x 100) and the f16 MFMA FLOPs
+    (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512), per kernel."""
     con = sqlite3.connect(db)
     rows = con.execute("select dispatch_id, kernel_name, counter_name, value from counters_collection").fetchall()
     per = {}
@@ -109,16 +128,35 @@ def mfma(db, out, cmd):
     lines = ["# MFMA utilisation: batched prefill (config 5)", "", "Command (GPU box, repo root):", "", "```", cmd,
              "```", "",
              "MfmaUtil (rocprofv3 derived counter) = sum over the GPU of SQ_VALU_MFMA_BUSY_CYCLES / (max",
-             "GRBM_GUI_ACTIVE x SIMDs) x 100; MfmaFlopsBF16 = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 (bf16 MFMA FLOPs",
+             "GRBM_GUI_ACTIVE x SIMDs) x 100; f16 MFMA FLOPs = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 (f16 MFMA FLOPs",
              "issued, padding rows included).", "",
-             "| kernel | dispatches | mean MfmaUtil % | mean bf16 MFMA GFLOP |", "|---|---:|---:|---:|"]
+             "| kernel | dispatches | mean MfmaUtil % | mean f16 MFMA GFLOP |", "|---|---:|---:|---:|"]
     for k, v in sorted(by.items()):
         util = [c["MfmaUtil"] for c in v if "MfmaUtil" in c]
-        fl = [c["MfmaFlopsBF16"] for c in v if "MfmaFlopsBF16" in c]
+        fl = [c["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512 for c in v if "SQ_INSTS_VALU_MFMA_MOPS_F16" in c]
         if not util:
             continue
         lines.append(f"| `{k}` | {len(v)} | {statistics.mean(util):.2f} | "
                      f"{statistics.mean(fl) / 1e9 if fl else float('nan'):.2f} |")
+    open(out, "w").write("\n".join(lines) + "\n")
+
+
+def counters(out, kernel, pairs):
+    rows = {}
+    cmds = []
+    for pair in pairs:
+        db, cmd = pair.split("=", 1)
+        cmds.append(cmd)
+        con = sqlite3.connect(db)
+        for name, cname, val in con.execute("select kernel_name, counter_name, value from counters_collection"):
+            k = short(name)
+            if kernel in k:
+                rows.setdefault((k, cname), []).append(val)
+    lines = [f"# Counters: {out.split('/')[-1].rsplit('.', 1)[0]}", "", "Commands (GPU box, repo root):", "", "```"]
+    lines += cmds + ["```", "", "Mean per dispatch (rocprofv3's aggregation over the GPU).", "",
+                     "| kernel | counter | dispatches | mean |", "|---|---|---:|---:|"]
+    for (k, c), v in sorted(rows.items()):
+        lines.append(f"| `{k}` | {c} | {len(v)} | {statistics.mean(v):,.0f} |")
     open(out, "w").write("\n".join(lines) + "\n")
 
 
@@ -128,6 +166,8 @@ if __name__ == "__main__":
         trace(*sys.argv[2:5])
     elif mode == "traffic":
         traffic(*sys.argv[2:8])
+    elif mode == "counters":
+        counters(sys.argv[2], sys.argv[3], sys.argv[4:])
     elif mode == "mfma":
         mfma(*sys.argv[2:5])
     else:
