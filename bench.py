@@ -529,7 +529,9 @@ def bench_matvec(args):
         f"{algo / (mean * 1e-6) / 1e9:.0f} GB/s")
     result = base_record(
         args, f"{ggml.NAMES[gtype]} matvec µs + achieved HBM GB/s at batch 1 ({rows} x {cols})", round(us, 3),
-        "us/matvec", steps, False, f"{ggml.NAMES[gtype]} weights x fp32 activations, fp32 accumulation",
+        "us/matvec", steps, False,
+        f"{ggml.NAMES[gtype]} weights x fp32 activations split into two int8 limbs per 16-element group "
+        "(v_dot4 int32 dots), fp32 scales and accumulation",
         {"workload": wl, "rows": rows, "cols": cols, "valid_cols": c.get("valid_cols", cols), "batch": 1,
          "weight_copies": len(copies), "graph_steps": G},
         {"device_us_per_step": round(dev_us, 3), "gbps_tensor_bytes": round(nb / (mean * 1e-6) / 1e9, 1),
@@ -925,7 +927,8 @@ def bench_formats(args):
         t0.free()
         t1.free()
     result = {"metric": "dense matvec GB/s per GGUF format (131072 x 4096, batch 1)", "unit": "GB/s",
-              "value": per["Q3_K"]["gbps"], "higher_is_better": True, "n_gpus": 1, "dtype": "fp32 activations",
+              "value": per["Q3_K"]["gbps"], "higher_is_better": True, "n_gpus": 1,
+              "dtype": "fp32 activations (Q4_K: int8-limb pairs on v_dot4)",
               "data": "synthetic", "config": {"workload": "matvec_formats", "rows": rows, "cols": cols},
               "per_format": per}
     print(json.dumps(result), flush=True)
@@ -950,7 +953,8 @@ def bench_stream(args):
     total = 4 << 30
     buf = DeviceArray((total,), np.uint8)
     check(hip().hipMemset(buf.ptr, 1, total), "hipMemset")
-    sizes = {"cfg2": 9469952, "cfg1": 13976576, "cfg3": FUSED_BYTES, "cfg4": CFG4_BYTES, "cfg2b": 128238080}
+    sizes = {"cfg2": 9469952, "cfg1": 13976576, "cfg3": FUSED_BYTES, "cfg4": CFG4_BYTES, "cfg2b": 128238080,
+             "q4k_131072x4096": 131072 * 16 * 144}
     rows = {}
     for name, nb in sizes.items():
         nb = nb // 256 * 256

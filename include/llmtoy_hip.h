@@ -140,7 +140,13 @@ int lt_stream_read(lt_ctx *ctx, const void *buf, size_t nbytes);
 /* Device bytes held by the tensor (equal to the GGUF byte count). */
 size_t lt_tensor_bytes(const lt_tensor *t);
 
-/* out[rows] = W[rows x cols] * x[cols], fp32 activations and accumulation.
+/* out[rows] = W[rows x cols] * x[cols], fp32 accumulation.  Activations are
+ * fp32, except for Q4_K and Q6_K rows of 1, 2, 4, 8 or 16 super-blocks
+ * (cols 256..4096, powers of two): there each group of 16 activations is
+ * split into two int8 limbs, x ~= sp * (256 a + b) with sp = max|x| / 32512
+ * (|error| <= max|x| / 65024 per element, about 2e-5 rel-L2 on the dot
+ * product), which meet the weight codes in v_dot4; a group holding a NaN or
+ * an infinity makes every output NaN.
  * Replaces quantMatvec / quantMatvecPar (ops/math.zig:133-171, 277-320) and
  * MatvecSession.run / runQ8_1Mv (gpu/matvec.zig:497-647,
  * gemma4/gpu_weights.zig:1573-1607).  W must be a 2-D tensor. */

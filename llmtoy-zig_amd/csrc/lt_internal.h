@@ -237,6 +237,14 @@ __device__ __forceinline__ float act_apply(uint32_t act, float g) {
 
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ __forceinline__ float4 ldg16f(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+// 16-byte load with the non-temporal hint (global_load_dwordx4 ... nt), for
+// weight streams that a launch reads once (the Q6_K stream: 23.6 -> 22.7 us
+// on 128 MB).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg16_nt(const uint8_t *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // ---------------------------------------------------------------- hand-over words
 // The single-launch kernels (lt_moe_fused.hip, lt_ffn_fused.hip) pass

@@ -72,6 +72,7 @@
 // already in this limb form.
 #include "lt_internal.h"
 #include "lt_topk.h"
+#include "lt_limbs.h"
 
 #include <math.h>
 
@@ -134,105 +135,6 @@ struct Stamps {
         }
     }
 };
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dppw(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
-}
-
-struct Limbs {
-    uint32_t a[4][4];  // a[g][m]: bytes = limb a of elements 16g + 4m + 0..3
-    uint32_t b[4][4];
-    float sp[4];
-    float xs_lo, xs_hi;  // exact sums of groups 0+1 and 2+3
-};
-
-// Q4_K scale decode of sub-block pair p (2p, 2p+1) from the header words
-// (h0 = d | dmin << 16, h1..h3 = scales[0..11]): get_scale_min_k4,
-// quant/dequant.zig:289-300.  Returns d*sc and dmin*mn of both sub-blocks.
-struct PairScale {
-    float dsc0, dsc1, dmn0, dmn1;
-};
-
-__device__ __forceinline__ PairScale pair_scale(uint32_t h0, uint32_t h1, uint32_t h2, uint32_t h3, int p) {
-    const float d = f16_bits_to_f32(h0);
-    const float dmin = f16_bits_to_f32(h0 >> 16);
-    const int sh = (p & 1) * 16;
-    const uint32_t ys = h1 >> sh, zs = h2 >> sh, ws = h3 >> sh;
-    const uint32_t scp = p < 2 ? (ys & 0x3f3fu) : ((ws & 0x0f0fu) | ((ys >> 2) & 0x3030u));
-    const uint32_t mnp = p < 2 ? (zs & 0x3f3fu) : (((ws >> 4) & 0x0f0fu) | ((zs >> 2) & 0x3030u));
-    PairScale s;
-    s.dsc0 = d * (float)(scp & 0xffu);
-    s.dsc1 = d * (float)((scp >> 8) & 0xffu);
-    s.dmn0 = dmin * (float)(mnp & 0xffu);
-    s.dmn1 = dmin * (float)((mnp >> 8) & 0xffu);
-    return s;
-}
-
-// The four header words of a (row, super-block) from the one word each lane
-// of an aligned quad loaded (lane & 3 = word index).
-__device__ __forceinline__ void quad_header(uint32_t mine, uint32_t &h0, uint32_t &h1, uint32_t &h2,
-                                            uint32_t &h3) {
-    h0 = dppw<0x00>(mine);
-    h1 = dppw<0x55>(mine);
-    h2 = dppw<0xAA>(mine);
-    h3 = dppw<0xFF>(mine);
-}
-
-// Dot of one Q4_K sub-block pair (64 weights: qs bytes 32p..32p+31 of a
-// super-block, w[0..7]) with the limbs of the matching 64 activations; the
-// _nib form takes the nibbles already unpacked (lo[m] = w[m] & 0x0f0f0f0f,
-// hi[m] = (w[m] >> 4) & 0x0f0f0f0f).
-// First product of an accumulator chain: the three-operand v_dot4_i32_i8
-// with an inline 0 (the compiler's choice, v_dot4c, needs a v_mov of 0
-// first: 8 of the pair's ~56 VALU instructions).
-__device__ __forceinline__ int sdot4_first(int a, int b) {
-    int r;
-    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-
-__device__ __forceinline__ float q4k_pair_dot_nib(const uint32_t (&lo)[8], const uint32_t (&hi)[8], const PairScale &s,
-                                                  const Limbs &x) {
-    int A[4], B[4];
-    A[0] = sdot4_first((int)lo[0], (int)x.a[0][0]);
-    B[0] = sdot4_first((int)lo[0], (int)x.b[0][0]);
-    A[1] = sdot4_first((int)lo[4], (int)x.a[1][0]);
-    B[1] = sdot4_first((int)lo[4], (int)x.b[1][0]);
-    A[2] = sdot4_first((int)hi[0], (int)x.a[2][0]);
-    B[2] = sdot4_first((int)hi[0], (int)x.b[2][0]);
-    A[3] = sdot4_first((int)hi[4], (int)x.a[3][0]);
-    B[3] = sdot4_first((int)hi[4], (int)x.b[3][0]);
-#pragma unroll
-    for (int m = 1; m < 4; m++) {
-        const uint32_t lo0 = lo[m], hi0 = hi[m];
-        const uint32_t lo1 = lo[4 + m], hi1 = hi[4 + m];
-        A[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.a[0][m], A[0], false);
-        B[0] = __builtin_amdgcn_sdot4((int)lo0, (int)x.b[0][m], B[0], false);
-        A[1] = __builtin_amdgcn_sdot4((int)lo1, (int)x.a[1][m], A[1], false);
-        B[1] = __builtin_amdgcn_sdot4((int)lo1, (int)x.b[1][m], B[1], false);
-        A[2] = __builtin_amdgcn_sdot4((int)hi0, (int)x.a[2][m], A[2], false);
-        B[2] = __builtin_amdgcn_sdot4((int)hi0, (int)x.b[2][m], B[2], false);
-        A[3] = __builtin_amdgcn_sdot4((int)hi1, (int)x.a[3][m], A[3], false);
-        B[3] = __builtin_amdgcn_sdot4((int)hi1, (int)x.b[3][m], B[3], false);
-    }
-    float c[4];
-#pragma unroll
-    for (int g = 0; g < 4; g++) c[g] = (float)((A[g] << 8) + B[g]);  // |.| < 2^23: exact
-    const float t_lo = x.sp[0] * c[0] + x.sp[1] * c[1];
-    const float t_hi = x.sp[2] * c[2] + x.sp[3] * c[3];
-    return (s.dsc0 * t_lo - s.dmn0 * x.xs_lo) + (s.dsc1 * t_hi - s.dmn1 * x.xs_hi);
-}
-
-__device__ __forceinline__ float q4k_pair_dot(const uint32_t (&w)[8], const PairScale &s, const Limbs &x) {
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int m = 0; m < 8; m++) {
-        lo[m] = w[m] & 0x0f0f0f0fu;
-        hi[m] = (w[m] >> 4) & 0x0f0f0f0fu;
-    }
-    return q4k_pair_dot_nib(lo, hi, s, x);
-}
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 

@@ -20,6 +20,7 @@
 // oracle's element-wise dequant then dotf32).
 #include "lt_internal.h"
 #include "lt_topk.h"
+#include "lt_limbs.h"
 
 namespace lt {
 
@@ -157,24 +158,43 @@ __global__ void __launch_bounds__(256) k_matvec_q4k(const uint8_t *__restrict__ 
 
 // ------------------------------------------------------------------------
 // Streaming matvec for rows of NSB = 1, 2, 4, 8 or 16 super-blocks (config 2
-// is NSB = 16).  Persistent waves as in k_matvec_q6k_stream: lane L takes
-// chunks c = L % LPR + LPR j (j < UPL) of rows RPS apart (LPR = min(64, 8
-// NSB) lanes per row, UPL = 8 NSB / LPR chunks per lane), so its x values
-// are loop-invariant registers; slab i + 1 is loaded while slab i is
-// computed, from two static buffers; DPP row sums.
+// is NSB = 16).  Work unit of a lane: one sub-block pair (p = 0..3) of a
+// super-block, 64 weights: qs bytes 32p..32p+31 (two 16-byte loads) and
+// header word p, the quad of lanes holding pairs 0..3 of one super-block
+// sharing the header through DPP.  Lane L takes pairs u = L % LPR + LPR j
+// (j < UPL) of rows RPS apart (LPR = min(64, 4 NSB) lanes per row, UPL =
+// 4 NSB / LPR), so its 64 UPL activations are loop-invariant registers,
+// held as int8 limbs (lt_limbs.h; the block converts x once through LDS):
+// a pair costs 24 bit operations, 32 v_dot4 and one scale decode instead
+// of 64 conversions and 64 fma.  Persistent waves, each with ND row slabs
+// in flight: the ND buffers are loaded between the load and the
+// conversion of x, and each is reloaded ND slabs ahead as soon as it has
+// been used; DPP row sums (at NSB = 16, where a row is one slab, the ND
+// slabs' sums in one transposed reduction).  NSB <= 16: x fits one group
+// per thread.
 template <int UPL>
 struct Q4Regs {
-    uint4 h[UPL], q[UPL];
+    uint4 q0[UPL], q1[UPL];
+    uint32_t h[UPL];
 };
 
-template <int NSB>
-__global__ void __launch_bounds__(256) k_matvec_q4k_stream(const uint8_t *__restrict__ hdr,
-                                                           const uint8_t *__restrict__ qs,
-                                                           const float *__restrict__ x, float *__restrict__ y,
-                                                           int row0, int nrows) {
-    constexpr int LPR = 8 * NSB < 64 ? 8 * NSB : 64, UPL = 8 * NSB / LPR, RPS = 64 / LPR;
+// Waves per SIMD the streaming kernel is compiled for (its VGPR budget: 128
+// at 4, 168 at 3) and hence its workgroups per CU.
+constexpr int q4k_stream_waves(int nd) { return nd <= 4 ? 4 : 3; }
+
+// Row slabs in flight per wave on large matrices.
+constexpr int kQ4StreamND = 4;
+
+template <int NSB, int ND>
+__global__ void __launch_bounds__(256, q4k_stream_waves(ND)) k_matvec_q4k_stream(const uint8_t *hdr, const uint8_t *qs,
+                                                                                 const float *x, float *y, int row0,
+                                                                                 int nrows) {
+    constexpr int PPR = 4 * NSB, LPR = PPR < 64 ? PPR : 64, UPL = PPR / LPR, RPS = 64 / LPR;
+    __shared__ uint32_t la[64 * NSB], lb[64 * NSB];
+    __shared__ float lsp[16 * NSB], lxs[16 * NSB];
     const int lane = threadIdx.x & 63;
     const int l = lane % LPR, rs = lane / LPR;
+    const int p = l & 3;  // the same pair index for every j (LPR % 4 == 0)
     const int stride = gridDim.x * 4 * RPS;
     int base = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPS;
     const bool first = p32_first(lane);
@@ -184,59 +204,88 @@ __global__ void __launch_bounds__(256) k_matvec_q4k_stream(const uint8_t *__rest
         const size_t b0 = (size_t)(row0 + row) * NSB;
 #pragma unroll
         for (int j = 0; j < UPL; j++) {
-            const int c = l + LPR * j;
-            w.h[j] = ldg16(hdr + (b0 + (c >> 3)) * 16);
-            w.q[j] = ldg16(qs + (b0 + (c >> 3)) * 128 + (c & 7) * 16);
+            const size_t blk = b0 + ((l + LPR * j) >> 2);
+            w.q0[j] = ldg16(qs + blk * 128 + 32 * p);
+            w.q1[j] = ldg16(qs + blk * 128 + 32 * p + 16);
+            w.h[j] = *reinterpret_cast<const uint32_t *>(hdr + blk * 16 + 4 * p);
         }
     };
-    Q4Regs<UPL> a, b;
-    ld(a, base);
-    XChunk xc[UPL];
+    float xv[16];
+    stage_x_load(x, 256 * NSB, xv);  // x first: its wait does not include the weights
+    asm volatile("" ::: "memory");  // keep the x loads ahead of the weight loads
+    Q4Regs<UPL> w[ND];
 #pragma unroll
-    for (int j = 0; j < UPL; j++) {
-        const int c = l + LPR * j;
-        const float *p = x + (c >> 3) * 256 + 64 * ((c & 7) >> 1) + 16 * (c & 1);
+    for (int i = 0; i < ND; i++) ld(w[i], base + i * stride);
+    __builtin_amdgcn_sched_barrier(0);  // the weight loads issued before the conversion
+    stage_limbs_store(xv, 256 * NSB, la, lb, lsp, lxs);
+    Limbs xl[UPL];
 #pragma unroll
-        for (int t = 0; t < 16; t += 4) {
-            const float4 lo = *reinterpret_cast<const float4 *>(p + t);
-            const float4 hi = *reinterpret_cast<const float4 *>(p + 32 + t);
-            xc[j].lo[t] = lo.x; xc[j].lo[t + 1] = lo.y; xc[j].lo[t + 2] = lo.z; xc[j].lo[t + 3] = lo.w;
-            xc[j].hi[t] = hi.x; xc[j].hi[t + 1] = hi.y; xc[j].hi[t + 2] = hi.z; xc[j].hi[t + 3] = hi.w;
-        }
-        sum_xchunk(xc[j]);
-    }
-    auto step = [&](const Q4Regs<UPL> &w, int rb) {
+    for (int j = 0; j < UPL; j++) read_pair_limbs(la, lb, lsp, lxs, 4 * (l + LPR * j), xl[j]);
+    auto lane_dot = [&](const Q4Regs<UPL> &r) {
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < UPL; j++) acc += q4k_chunk_dot(w.h[j], w.q[j], (l + LPR * j) & 7, xc[j]);
-        const float v = group_sum_dpp<LPR>(acc, first);
-        const int row = rb + rs;
-        if (l == 0 && row < nrows) y[row] = v;
+        for (int j = 0; j < UPL; j++) {
+            uint32_t h0, h1, h2, h3;
+            quad_header(r.h[j], h0, h1, h2, h3);
+            const PairScale ps = pair_scale(h0, h1, h2, h3, p);
+            const uint32_t w8[8] = {r.q0[j].x, r.q0[j].y, r.q0[j].z, r.q0[j].w,
+                                    r.q1[j].x, r.q1[j].y, r.q1[j].z, r.q1[j].w};
+            acc += q4k_pair_dot(w8, ps, xl[j]);
+        }
+        return acc;
     };
     // loads stay unconditional (clamped rows); the math of a slab past the
     // last row is skipped (wave-uniform branch)
-    for (; base < nrows; base += 2 * stride) {
-        ld(b, base + stride);
-        step(a, base);
-        ld(a, base + 2 * stride);
-        if (base + stride < nrows) step(b, base + stride);
+    if constexpr (LPR == 64) {
+        // one row per slab: the ND slabs' row sums in one transposed
+        // reduction, lane 64 i / ND storing slab i's row
+        constexpr int SH = ND == 2 ? 5 : ND == 4 ? 4 : 3;
+        for (; base < nrows; base += ND * stride) {
+            float acc[ND];
+#pragma unroll
+            for (int i = 0; i < ND; i++) {
+                acc[i] = (i == 0 || base + i * stride < nrows) ? lane_dot(w[i]) : 0.f;
+                ld(w[i], base + (i + ND) * stride);
+            }
+            const float t = wave_sum_transposed<ND>(acc, lane, first);
+            const int row = base + (lane >> SH) * stride;
+            if ((lane & ((1 << SH) - 1)) == 0 && row < nrows) y[row] = t;
+        }
+    } else {
+        for (; base < nrows; base += ND * stride) {
+#pragma unroll
+            for (int i = 0; i < ND; i++) {
+                if (i == 0 || base + i * stride < nrows) {
+                    const float v = group_sum_dpp<LPR>(lane_dot(w[i]), first);
+                    const int row = base + i * stride + rs;
+                    if (l == 0 && row < nrows) y[row] = v;
+                }
+                ld(w[i], base + (i + ND) * stride);
+            }
+        }
     }
 }
 
 template <int NSB>
 static hipError_t launch_q4k_stream(const DevTensor &W, size_t row0, size_t nrows, const float *x, float *y,
                                     hipStream_t s) {
-    constexpr int LPR = 8 * NSB < 64 ? 8 * NSB : 64, RPS = 64 / LPR;
-    // 8 workgroups per CU fit below 64 VGPRs (NSB <= 8), 4 at NSB = 16
-    constexpr size_t cap = NSB <= 8 ? 2 * kStreamBlocks : kStreamBlocks;
-    // at least two row slabs per wave: the second slab's loads overlap the
-    // first one's math and x is loaded once for both (one slab per wave
-    // made config 2, 4096 rows, 7.3 us instead of 5.6)
+    constexpr int LPR = 4 * NSB < 64 ? 4 * NSB : 64, RPS = 64 / LPR;
     const size_t slabs = (nrows + RPS - 1) / RPS;
-    size_t nblk = (slabs + 7) / 8;
-    if (nblk > cap) nblk = cap;
-    hipLaunchKernelGGL((k_matvec_q4k_stream<NSB>), dim3((unsigned)nblk), dim3(256), 0, s, W.p0, W.p1, x, y,
-                       (int)row0, (int)nrows);
+    // Small matrices: two slabs per wave, both in flight from the start
+    // (one slab per wave made config 2, 4096 rows, 7.3 us instead of 5.6).
+    // Large ones: every workgroup resident (256 CUs x its waves per SIMD)
+    // with kQ4StreamND slabs in flight per wave.
+    constexpr size_t nblk_big = (size_t)256 * q4k_stream_waves(kQ4StreamND);
+    if (slabs >= nblk_big * 4 * 2 * kQ4StreamND) {
+        hipLaunchKernelGGL((k_matvec_q4k_stream<NSB, kQ4StreamND>), dim3((unsigned)nblk_big), dim3(256), 0, s, W.p0,
+                           W.p1, x, y, (int)row0, (int)nrows);
+    } else {
+        constexpr size_t cap2 = (size_t)256 * q4k_stream_waves(2);
+        size_t nblk = (slabs + 7) / 8;
+        if (nblk > cap2) nblk = cap2;
+        hipLaunchKernelGGL((k_matvec_q4k_stream<NSB, 2>), dim3((unsigned)nblk), dim3(256), 0, s, W.p0, W.p1, x, y,
+                           (int)row0, (int)nrows);
+    }
     return hipGetLastError();
 }
 

@@ -240,6 +240,50 @@ def test_gpu_config2_q6k_151936(ctx):
     assert max_rel(y, ref) < FUZZ_MAX_REL
 
 
+def _limb_case_x(kind, cols, g):
+    x = g.standard_normal(cols).astype(np.float32)
+    if kind == "group_magnitudes":  # each 16-element group at its own scale, 1e-6 .. 1e6
+        x *= (10.0 ** np.repeat(np.arange(cols // 16) % 13 - 6, 16)).astype(np.float32)
+    elif kind == "spike":  # one large element inside otherwise unit groups
+        x[5::37] *= 1e4
+    elif kind == "tiny":  # group maxima below 2^-100 (scaled before the division)
+        x *= np.float32(2.0 ** -110)
+    return x
+
+
+@pytest.mark.parametrize("gtype,rows,cols", [
+    (ggml.Q4_K, 300, 256), (ggml.Q4_K, 257, 2048), (ggml.Q4_K, 4100, 4096),
+    (ggml.Q4_K, 33000, 4096),  # past 32768 row slabs: four slabs in flight per wave, ragged tail
+    (ggml.Q6_K, 129, 1024), (ggml.Q6_K, 999, 4096),
+    (ggml.Q6_K, 99000, 1024)])  # past 24576 row slabs of 4 rows: three slabs in flight per wave
+@pytest.mark.parametrize("kind", ["normal", "group_magnitudes", "spike", "tiny"])
+def test_gpu_matvec_limb_ranges(ctx, pool, gtype, rows, cols, kind):
+    # The streaming Q4_K / Q6_K matvecs carry each group of 16 activations as
+    # two int8 limbs scaled by the group's largest magnitude: groups of very
+    # different scales, a spike inside a group and groups near 2^-110 stay
+    # within the fp32-activation fuzz bound against the oracle's fp32 dot.
+    g = np.random.default_rng(rows + cols)
+    w = synth.q4k_matrix(g, rows, cols) if gtype == ggml.Q4_K else synth.q6k_matrix(g, rows, cols)
+    x = _limb_case_x(kind, cols, g)
+    print(f"limb ranges {ggml.NAMES[gtype]} {rows}x{cols} {kind}", flush=True)
+    y = gpu_matvec(ctx, w, gtype, rows, cols, x)
+    ref = orc.quant_matvec(w, gtype, x, rows, cols, pool=pool)
+    assert rel_l2(y, ref) <= REL_L2, rel_l2(y, ref)
+    assert max_rel(y, ref) < FUZZ_MAX_REL, max_rel(y, ref)
+
+
+@pytest.mark.parametrize("gtype,cols", [(ggml.Q4_K, 4096), (ggml.Q6_K, 1024)])
+def test_gpu_matvec_limb_nan(ctx, gtype, cols):
+    # a NaN activation makes every output NaN, as in the fp32 dot
+    g = np.random.default_rng(cols)
+    rows = 70
+    w = synth.q4k_matrix(g, rows, cols) if gtype == ggml.Q4_K else synth.q6k_matrix(g, rows, cols)
+    x = g.standard_normal(cols).astype(np.float32)
+    x[cols // 3] = np.nan
+    y = gpu_matvec(ctx, w, gtype, rows, cols, x)
+    assert np.isnan(y).all()
+
+
 def test_gpu_config1_dense_ffn_q8_0(ctx):
     c = synth.config1()
     D, F = c["d_model"], c["d_ffn"]
