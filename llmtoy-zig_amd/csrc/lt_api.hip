@@ -38,7 +38,7 @@ struct SpanStat {
     size_t n = 0;
     double total_ms = 0, min_ms = 1e30, max_ms = 0;
 };
-constexpr int kRoles = 5, kPhases = lt::kStamps - 1;
+constexpr int kRoles = 6, kPhases = lt::kStamps - 1;
 struct Profile {
     int mode = 0;  // 0 off, 1 spans, 2 spans + timeline
     std::vector<PendingSpan> pending;
@@ -1414,15 +1414,16 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                  "us from the first block's start; median over launches of the block median / the last block\n",
                  P.launches);
         o += line;
-        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine"};
+        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "filler"};
         static const char *phases[kRoles][kPhases] = {
             {},
-            {"block start", "first row chunk in", "logit published"},
+            {"block start", "first row chunk in", "logit published", "all row terms in"},
             {"block start", "logits seen", "expert known", "dot products done", "h record published",
              "shared h rows out"},
-            {"block start", "logits seen", "weight loads issued", "h records read", "adds issued", nullptr,
-             "shared rows added"},
-            {"block start", "rows written"}};
+            {"block start", "logits seen", "weight loads issued", "h records read", "adds issued",
+             "shared h seen", "shared rows added"},
+            {"block start", "rows written"},
+            {"block start", nullptr, nullptr, nullptr, nullptr, "shared h rows out", "shared rows added"}};
         snprintf(line, sizeof line, "%-9s %-22s %10s %10s\n", "role", "phase", "median", "last");
         o += line;
         for (int r = 1; r < kRoles; r++)

@@ -438,14 +438,16 @@ struct FusedScratch {
 // Phase stamps of one launch (LT_PROFILE=timeline): thread 0 of block b
 // writes stamps[b * kStamps + i], wall-clock ticks (100 MHz) at the end of
 // phase i of its role, and stamps[b * kStamps + kStamps - 1] = role | slot
-// << 8 | XCD << 16 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine).
+// << 8 | XCD << 16 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine,
+// 5 shared-FFN filler work only).
 constexpr int kStamps = 8;
 enum : int { kStampStart = 0 };
-// router: 1 first row chunk in, 2 logit published; gate/up: 1 logits seen,
-// 2 expert known, 3 dot products done, 4 h record published; down: 1 logits
-// seen, 2 weight loads issued, 3 h records read, 4 adds issued; combine:
-// 1 rows written; with a shared FFN, gate/up 5: its shared h rows out,
-// down 6: its shared rows added
+// router: 1 first row chunk in, 2 logit published, 3 all row terms in (Q8_0
+// router); gate/up: 1 logits seen, 2 expert known, 3 dot products done, 4 h
+// record published; down: 1 logits seen, 2 weight loads issued, 3 h records
+// read, 4 adds issued; combine: 1 rows written; with a shared FFN, gate/up
+// and filler 5: shared h rows out, down 5: the slice's shared h seen, down
+// and filler 6: shared rows added
 // Byte layout of that hand-over memory (a context's own allocation, or the
 // library's static scratch in lt_noalloc.hip): launch counters, 8 logit
 // copies, h record lines, partial-output lines, the XCD probe's ids, and

@@ -23,6 +23,8 @@
 //                           NDg first add the shared FFN's rows 64j + [0, 64)
 //                           over the group's K slice (sh_down_fill)
 //   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
+//   the rest (no role)      shared-FFN h rows after the gate/up-position
+//                           blocks' (sh_gate_up_fill)
 //
 // (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = ceil(D / 64),
 // NCg = NDg with the deterministic combine, else 0; NRg also covers one
@@ -36,10 +38,10 @@
 //
 // Combine.  By default the down blocks add their slot's weighted rows
 // straight into out with float atomics (agent scope): the router blocks
-// first set out to its starting value (0, the shared FFN output, or out +
-// that when accumulating) with coherent stores, and every router wavefront
-// waits for their acknowledgement before it publishes its logit, so each
-// add lands after the start value.  The order of the k adds to a row
+// set out to its starting value (0, the shared FFN output, or out + that
+// when accumulating) with coherent stores after their logits and flag them
+// once acknowledged; every block waits for its rows' flag before adding,
+// so each add lands after the start value.  The order of the k adds to a row
 // varies, so the result's last bits may differ run to run.  With det set,
 // the down blocks publish per-slot partial rows instead and the combining
 // blocks add them in slot order (moeForward's order, ops/moe.zig:67-76):
@@ -108,7 +110,7 @@ struct FusedArgs {
     int dn_delay;  // wall-clock ticks from seeing the logits to the down weight loads
     int rb;        // logit rows per router block: 2 or 4
     int NRg, SPG, G, NDg, NCg;
-    int Ewait;  // logit rows published and waited for: E, or more placeholders (store_starts)
+    int Ewait;  // logit rows published and waited for (E)
     // the Gemma-style instance (SH) only
     const uint8_t *rq;   // Q8_0 router: quant plane [E][nb][32] (qrouter)
     const uint16_t *rd;  //   and f16 scale plane [E][nb]
@@ -226,18 +228,37 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Atomic combine: the start values of out (0, the base, or out + base).
 // Router block c stores rows 256 c + [0, 256) with coherent stores (the
-// plan gives the grid at least ceil(D / 256) router blocks), and every
-// router block waits for their acknowledgement (s_waitcnt) and a block
-// barrier before any of its logits goes out.  Every block with start values
-// publishes its logit rows, rows >= E included (placeholders that the
-// readers wait for but do not rank: rows < Ewait), so a reader that has
-// seen the logits of block c may add to the rows c stores.
+// plan gives the grid at least ceil(D / 256) router blocks) after its
+// logits, and flags them once acknowledged (flag_starts).
 __device__ __forceinline__ void store_starts(const FusedArgs &a, int bid, int tid) {
     const int orow = bid * kThreads + tid;
     if (!a.det && orow < a.D && !(a.accumulate && !a.base)) {
         const float start = a.accumulate ? a.out[orow] + a.base[orow] : (a.base ? a.base[orow] : 0.0f);
         __hip_atomic_store(a.out + orow, start, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// Router block b < ceil(D / 256) stores the start values of out rows 256 b
+// + [0, 256) after publishing its logits, and once the stores are
+// acknowledged sets word kStartFlagOff + b of every logit copy; every block
+// adding into out waits for the flag of its rows first.  (Stores count in
+// vmcnt with the loads, in order: stored before the router's loads, or
+// acknowledged before its logits, they delayed the logits by the time an
+// acknowledgement takes while the weight streams fill the memory system,
+// up to 3 us.)
+constexpr int kStartFlagOff = kLgCopy - 16;
+__device__ __forceinline__ bool starts_stored_by_router(const FusedArgs &a) {
+    return !a.det && !(a.accumulate && !a.base);
+}
+__device__ __forceinline__ void flag_starts(const FusedArgs &a, int bid, int tid, uint32_t ep) {
+    if (!starts_stored_by_router(a) || bid * kThreads >= a.D) return;  // (uniform over the block)
+    store_starts(a, bid, tid);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's start store acknowledged
+    __syncthreads();
+    if (tid < 8) hand_put(a.lg + (size_t)tid * kLgCopy + kStartFlagOff + bid, 1u, ep);
+}
+__device__ __forceinline__ const uint64_t *start_flag(const FusedArgs &a, int x, int row) {
+    return a.lg + (size_t)x * kLgCopy + kStartFlagOff + (row >> 8);
 }
 
 __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, int bid, int tid, int wave,
@@ -247,10 +268,6 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
     const int row = bid * 4 + wave;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
-    // the start values go out before the router loads: stores count in
-    // vmcnt until acknowledged, and they are acknowledged long before the
-    // loads return
-    store_starts(a, bid, tid);
     // every load unconditional (chunk indices clamped), so that the waits
     // for chunk i count only the loads issued after it
     float4 wv[8], xv[8];
@@ -290,12 +307,10 @@ __device__ __forceinline__ void role_router(const FusedArgs &a, uint8_t *smem, i
 #pragma unroll
     for (int l = 1; l < 8; l++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a8), l));
     if (a.bias) sum = sum + bias;
-    // the block's output-row stores are acknowledged (memory-side) before
-    // the logits that let down blocks start adding
-    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
     S.mark(2, tid);
+    flag_starts(a, bid, tid, c0 + 1u);
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
@@ -318,7 +333,6 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
     const int row = 2 * bid + rl;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
-    store_starts(a, bid, tid);
     // loads in batches of 4 (64 strides: D <= 2048 in one batch, 4096 in
     // two); every load unconditional (stride clamped), so that the wait for
     // load q counts only the loads issued after it.  The first batch goes
@@ -369,9 +383,6 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
     // lanes l < 8: chains 16h + l and 16h + l + 8
     const float s2 = acc + dpp<0x128>(acc);
     if (h == 1 && lane < 8) xch[rl * 8 + lane] = s2;
-    // every wavefront's output-row stores are acknowledged (memory-side)
-    // before the logits that let down blocks start adding
-    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (h == 0) {
         const float a8 = s2 + xch[rl * 8 + (lane & 7)];
@@ -382,6 +393,7 @@ __device__ __forceinline__ void role_router_pair(const FusedArgs &a, uint8_t *sm
         if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
         S.mark(2, tid);
     }
+    flag_starts(a, bid, tid, c0 + 1u);
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
@@ -396,7 +408,6 @@ __device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t
     const int row = 2 * bid + rl;
     const bool valid = row < a.E;
     const float *wr = a.router + (size_t)(valid ? row : 0) * a.D;
-    store_starts(a, bid, tid);
     // every load unconditional (stride clamped), so that the wait for load
     // q counts only the loads issued after it
     float4 wv[4], xv[4];
@@ -439,9 +450,6 @@ __device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t
     // lanes l < 8: chains 16h + l and 16h + l + 8
     const float s2 = acc + dpp<0x128>(acc);
     if (h == 1 && lane < 8) xch[rl * 8 + lane] = s2;
-    // every wavefront's output-row stores are acknowledged (memory-side)
-    // before the logits that let down blocks start adding
-    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (h == 0) {
         const float a8 = s2 + xch[rl * 8 + (lane & 7)];
@@ -452,6 +460,7 @@ __device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t
         if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(sum), c0 + 1u);  // copy lane
         S.mark(2, tid);
     }
+    flag_starts(a, bid, tid, c0 + 1u);
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
@@ -459,9 +468,9 @@ __device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t
 // Rows 2 bid + [0, 2) of a Q8_0 router: thread t of half h = t >> 7 takes
 // block b = t & 127 (b < nb = D / 32 <= 128) of row 2 bid + h and computes
 // dotQ8_0's block term (quant/dequant.zig:59-78: 8 lane accumulators over 4
-// groups of 8 products, the ordered 8-lane sum, times d); thread 0 of each
-// half adds the nb terms in block order (the reference's running total) and
-// the bias, and lanes 0-7 of its wavefront publish the logit's 8 copies.
+// groups of 8 products, the ordered 8-lane sum, times d) into LDS; the first
+// wavefront of each half adds the nb terms in block order (the reference's
+// running total) and the bias, and lanes 0-7 publish the logit's 8 copies.
 __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem, int bid, int tid, int lane,
                                                Stamps &S) {
 #pragma clang fp contract(off)
@@ -470,7 +479,6 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
     const int nb = a.D >> 5;
     const int row = 2 * bid + h;
     const bool valid = row < a.E;
-    store_starts(a, bid, tid);
     // every load unconditional (clamped row and block)
     const size_t blk = (size_t)(valid ? row : 0) * nb + (b < nb ? b : nb - 1);
     const uint4 q0 = ld16(a.rq + blk * 32), q1 = ld16(a.rq + blk * 32 + 16);
@@ -504,27 +512,33 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
     float r = acc[0];
 #pragma unroll
     for (int l = 1; l < 8; l++) r = r + acc[l];
-    const float term = b < nb ? r * f16_bits_to_f32(d16) : 0.0f;
-    if (b >= 64) terms[h * 128 + b] = term;  // blocks 64..127 cross to the row's first wavefront
+    // past the row's nb blocks the term is -0, which leaves any sum as it is
+    // (x + -0 = x, also for x = +0 and -0): the ordered sum below runs over
+    // whole chunks of 16 without a branch per term
+    terms[h * 128 + b] = b < nb ? r * f16_bits_to_f32(d16) : -0.0f;
     S.mark(1, tid);
-    // this thread's output-row store is acknowledged before the logits
-    if (!a.det) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    S.mark(3, tid);
     if (b < 64) {  // wavefronts 0 and 2: one row each
-        // the ordered sum over the nb block terms, lane by lane from
-        // registers (term b in lane b of t0, block 64 + l in lane l of t1)
-        const float t0 = term, t1 = terms[h * 128 + 64 + lane];
+        // the ordered sum over the block terms (every lane the same, LDS
+        // broadcast reads of 16 terms at a time)
+        const float *tr = terms + h * 128;
         float total = 0.0f;
+        for (int c = 0; c < nb; c += 16) {
+            float t16[16];
 #pragma unroll
-        for (int l = 0; l < 64; l++)
-            if (l < nb) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t0), l));
+            for (int i = 0; i < 16; i += 4) {
+                const float4 v4 = *reinterpret_cast<const float4 *>(tr + c + i);
+                t16[i] = v4.x; t16[i + 1] = v4.y; t16[i + 2] = v4.z; t16[i + 3] = v4.w;
+            }
 #pragma unroll
-        for (int l = 0; l < 64; l++)
-            if (64 + l < nb) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1), l));
+            for (int i = 0; i < 16; i++) total = total + t16[i];
+        }
         if (a.bias) total = total + bias;
         if (lane < 8 && row < a.Ewait) hand_put(a.lg + (size_t)lane * kLgCopy + row, __float_as_uint(total), c0 + 1u);
         S.mark(2, tid);
     }
+    flag_starts(a, bid, tid, c0 + 1u);
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
@@ -633,6 +647,9 @@ __device__ __forceinline__ void sh_gate_up_fill(const FusedArgs &a, uint8_t *sme
         if (i + 8 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 8 * kThreads) = x2;
         if (i + 12 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 12 * kThreads) = x3;
     }
+    // the epoch read after the weight loads are issued; s_ep keeps it for
+    // the block's own role, which then reads the counter no more (a load
+    // issued under the weight streams waits microseconds)
     const uint32_t ep = fill_epoch(a, s_ep, bid, tid);  // (its barrier also covers xs)
     if (j < j1) {
         const bool first = p32_first(lane);
@@ -679,8 +696,8 @@ __device__ __forceinline__ void sh_down_fill(const FusedArgs &a, uint8_t *smem, 
         *s_fail = 0;
         const uint64_t t0 = wall_clock64();
         bool ok = true;
-        if (!(a.accumulate && !a.base)) {
-            ok = probe_wait(a.lg + (size_t)x * kLgCopy + (size_t)a.rb * (r0 >> 8), ep, t0);
+        if (starts_stored_by_router(a)) {
+            ok = probe_wait(start_flag(a, x, r0), ep, t0);
             if (!ok) report_detail(a.err, bid, 0x10u, r0, 0, ep);
         }
         if (ok) {
@@ -690,6 +707,7 @@ __device__ __forceinline__ void sh_down_fill(const FusedArgs &a, uint8_t *smem, 
         if (!ok) *s_fail = 1;
     }
     __syncthreads();
+    S.mark(5, tid);
     uint4 qw[4][2];
     uint32_t dw[4][2];
 #pragma unroll
@@ -771,7 +789,8 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
     const bool lane_on = pos < 4 * a.nsb;
     const bool first = p32_first(lane);
-    const uint32_t c0 = epoch_peek(a.counters, bid);
+    // (after the shared gate/up filler s_ep holds this launch's epoch)
+    const uint32_t c0 = XL ? *s_ep - 1u : epoch_peek(a.counters, bid);
     // activation limbs, once per block: thread t converts elements 8t + [0, 8)
     // (half of group t / 2) into LDS; each lane then reads its window's 4
     // groups.  LDS: limb-a words [D/4], limb-b words [D/4], sp [D/16], xs [D/16].
@@ -1071,6 +1090,8 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     // the slot's h records: thread 0 waits for one record line, then thread
     // q*10 + wl (q < 25) reads word wl of lines q + 25 m, all loads of a
     // pass in flight at once
+    if (tid == 0 && !a.det && starts_stored_by_router(a) && !probe_wait(start_flag(a, bid & 7, row0), ep, wall_clock64()))
+        *s_fail = 1;  // (reported as the logit wait: the start values come with the routing)
     if (tid == 0 && !probe_wait(a.hl + ((size_t)s * G + (size_t)(j % G)) * 16, ep, wall_clock64())) *s_fail = 2;
     __syncthreads();
     bool ok = true;
@@ -1274,15 +1295,17 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
             role = 3u | (uint32_t)s << 8;
         } else if (SH && a.S > 0 && u < a.NDg) {  // a group without a slot still adds its shared rows
             sh_down_fill(a, smem, fill_epoch(a, &s_ep, bid, tid), x, u, bid, tid, wave, lane, S);
+            role = 5;
         }
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
         role_combine(a, &s_ep, bid, 8 * u + x, tid, S);
         role = 4;
     } else if (SH && a.S > 0) {  // no role: shared gate/up rows after the gate/up-position blocks'
         sh_gate_up_fill(a, smem, &s_ep, x, a.SPG * a.G + (u - a.NCg), false, bid, tid, wave, lane, S);
+        role = 5;
     }
-    // no role in this configuration: keep the counter in step
-    if (role == 0 && tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
+    // no role in this configuration (or filler work only): keep the counter in step
+    if ((role == 0 || role == 5) && tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     if (S.row && tid == 0) {
         uint32_t xcc;  // the XCD this block ran on
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -1354,7 +1377,7 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
             pl.NRg = std::max((E + 31) / 32, (nstart + 7) / 8);
             used = pl.NRg + pl.SPG * pl.G + pl.SPG * pl.NDg + pl.NCg;
         }
-        pl.Ewait = std::max(E, pl.rb * nstart);
+        pl.Ewait = E;  // (the start values have flags of their own: flag_starts)
         if (pl.Ewait > 64 * pl.per) return pl;
         if (8 * used > kFusedBlocks) return pl;
         if ((size_t)k * pl.G > (size_t)kFusedBlocks) return pl;            // h record lines
