@@ -231,7 +231,8 @@ int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, const lt_ten
  * one token at a time through the decode path (main.zig:1916-1922); results
  * match per-token lt_moe_forward to f16 tolerance.  X rows are scaled by
  * powers of two into f16's range; the expert activations between the two
- * GEMMs saturate at +-65504. */
+ * GEMMs saturate at +-65504.  Device pointers X and out must be 16-byte
+ * aligned. */
 int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt_tensor *router,
                    const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
                    uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);

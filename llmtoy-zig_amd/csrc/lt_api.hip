@@ -1130,8 +1130,8 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
         dout = (float *)ctx->out.p;
         dids = nullptr;  // copied from the workspace below
         dw = nullptr;
-    } else if (!aligned16(X)) {
-        return fail(ctx, LT_ERR_INVALID, "X must be 16-byte aligned");
+    } else if (!aligned16(X) || !aligned16(out)) {
+        return fail(ctx, LT_ERR_INVALID, "X and out must be 16-byte aligned");
     }
     if ((rc = stage_bias(ctx, router_bias, E, host, &dbias))) return rc;
     const size_t wsb = lt::prefill_workspace_bytes((int)T, (int)k, E, Kd, (int)D);

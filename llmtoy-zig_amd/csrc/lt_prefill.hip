@@ -149,9 +149,12 @@ __device__ __forceinline__ void q4k_chunk_to_f16(uint4 hdr, uint4 q, int cc, _Fl
 }
 
 // One thread's share of a K stage's weight tile: 2 units of (weight row r,
-// 16-byte chunk c): r = tid / 4 + 64 j, c = tid % 4.
+// 16-byte chunk c): r = tid / 4 + 64 j, c = tid % 4.  The four threads of a
+// row (an aligned quad) each load one word of the row's 16-byte header and
+// share them over DPP, so a stage in flight holds 10 registers, not 16.
 struct StageRegs {
-    uint4 h[2], q[2];
+    uint32_t h[2];
+    uint4 q[2];
 };
 
 __device__ __forceinline__ void stage_load(StageRegs &R, const uint8_t *hdr, const uint8_t *qs, int nsb,
@@ -160,9 +163,14 @@ __device__ __forceinline__ void stage_load(StageRegs &R, const uint8_t *hdr, con
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const size_t blk = wrow[j] * nsb + sb;
-        R.h[j] = ldg16(hdr + blk * 16);
+        R.h[j] = *reinterpret_cast<const uint32_t *>(hdr + blk * 16 + 4 * c);
         R.q[j] = ldg16(qs + blk * 128 + cc * 16);
     }
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_word(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
 }
 
 // Stage ks's chunk cc = 4 (ks & 1) + c lands at local K 64 (c / 2) + 16 (c & 1)
@@ -172,7 +180,9 @@ __device__ __forceinline__ void stage_dequant(const StageRegs &R, _Float16 (*Bs)
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         _Float16 *row = Bs[r0 + 64 * j];
-        q4k_chunk_to_f16(R.h[j], R.q[j], cc, row + local, row + local + 32);
+        const uint4 h = make_uint4(quad_word<0x00>(R.h[j]), quad_word<0x55>(R.h[j]), quad_word<0xAA>(R.h[j]),
+                                   quad_word<0xFF>(R.h[j]));
+        q4k_chunk_to_f16(h, R.q[j], cc, row + local, row + local + 32);
     }
 }
 
@@ -190,32 +200,36 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
                                              const _Float16 *arow, bool wave_on, int kb, int tid, int lane) {
     constexpr int NK = 8 / S;
     const int c = tid & 3, r0 = tid >> 2;
-    StageRegs R0, R1;
-    f16x8 a0[NK], a1[NK];
+    StageRegs R[3];
+    f16x8 a[2][NK];
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[i] = floatx16{};
     // Every wavefront issues the same loads on every path (stage indices
     // past the end are clamped and their data left unused; a wavefront
     // without a token tile loads a valid row it does not use): the memory
     // counter waits the compiler derives then cover only the data a step
-    // needs, not the prefetches behind it.
-    stage_load(R0, hdr, qs, nsb, wrow, 0, c);
-    stage_load(R1, hdr, qs, nsb, wrow, 1, c);  // NS = 2 * super-blocks >= 2
+    // needs, not the prefetches behind it.  Three stages' weights are in
+    // flight ahead of the one being dequantised.
+    stage_load(R[0], hdr, qs, nsb, wrow, 0, c);
+    stage_load(R[1], hdr, qs, nsb, wrow, 1, c);  // NS = 2 * super-blocks >= 2
+    stage_load(R[2], hdr, qs, nsb, wrow, min(2, NS - 1), c);
 #pragma unroll
-    for (int i = 0; i < NK; i++) a0[i] = *reinterpret_cast<const f16x8 *>(arow + (kb + i) * 16);
-    stage_dequant(R0, Bs[0], r0, 0, c);
-    stage_load(R0, hdr, qs, nsb, wrow, min(2, NS - 1), c);
+    for (int i = 0; i < NK; i++) a[0][i] = *reinterpret_cast<const f16x8 *>(arow + (kb + i) * 16);
+    stage_dequant(R[0], Bs[0], r0, 0, c);
+    stage_load(R[0], hdr, qs, nsb, wrow, min(3, NS - 1), c);
     __syncthreads();
-    // Two stages per trip (NS is even) so the register sets alternate
-    // without copies: entering stage ks, Bs[ks & 1] holds it, R1 holds
-    // ks + 1 and R0 holds ks + 2.
-    for (int ks = 0; ks < NS; ks += 2) {
+    // Six stages per trip, so that the A buffers (stage parity) and the
+    // weight register sets (stage mod 3) have fixed names: entering stage
+    // st, Bs[st & 1] holds it and R[(st + 1) % 3], R[(st + 2) % 3],
+    // R[st % 3] hold stages st + 1, st + 2, st + 3.
+    for (int ks = 0; ks < NS; ks += 6) {
 #pragma unroll
-        for (int half = 0; half < 2; half++) {
-            const int st = ks + half;
-            StageRegs &Rn = half ? R0 : R1;   // stage st + 1
-            f16x8(&acur)[NK] = half ? a1 : a0;
-            f16x8(&anext)[NK] = half ? a0 : a1;
+        for (int u = 0; u < 6; u++) {
+            const int st = ks + u;
+            if (st >= NS) break;  // (uniform over the block)
+            StageRegs &Rn = R[(u + 1) % 3];  // stage st + 1
+            f16x8(&acur)[NK] = a[u & 1];
+            f16x8(&anext)[NK] = a[(u + 1) & 1];
             const size_t sa = (size_t)min(st + 1, NS - 1) * KS;
 #pragma unroll
             for (int i = 0; i < NK; i++) anext[i] = *reinterpret_cast<const f16x8 *>(arow + sa + (kb + i) * 16);
@@ -231,7 +245,7 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
                     }
             }
             if (st + 1 < NS) stage_dequant(Rn, Bs[(st + 1) & 1], r0, st + 1, c);
-            stage_load(Rn, hdr, qs, nsb, wrow, min(st + 3, NS - 1), c);
+            stage_load(Rn, hdr, qs, nsb, wrow, min(st + 4, NS - 1), c);
             __syncthreads();
         }
     }
@@ -490,17 +504,35 @@ __global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict_
 }
 
 // ---------------------------------------------------------------- combine
+// Thread: 4 consecutive elements of one token's row (D % 4 == 0); every
+// slot's Y row is read with one 16-byte load per thread, all k loads in
+// flight before the sum, which runs in slot order.
 __global__ void __launch_bounds__(256) k_prefill_combine(const float *__restrict__ Y, const int *__restrict__ pos,
                                                          const float *__restrict__ w, int k, int D,
                                                          float *__restrict__ out) {
-    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y, i = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (i >= D) return;
-    float acc = 0.f;
-    for (int s = 0; s < k; s++) {
-        const int p = pos[t * k + s];
-        if (p >= 0) acc += w[t * k + s] * Y[(size_t)p * D + i];
+    float4 v[16];
+    float ws[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        if (s < k) {
+            const int p = pos[t * k + s];
+            ws[s] = p >= 0 ? w[t * k + s] : 0.0f;
+            v[s] = ldg16f(Y + (size_t)(p >= 0 ? p : 0) * D + i);
+        }
     }
-    out[(size_t)t * D + i] = acc;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        if (s < k && pos[t * k + s] >= 0) {
+            acc.x += ws[s] * v[s].x;
+            acc.y += ws[s] * v[s].y;
+            acc.z += ws[s] * v[s].z;
+            acc.w += ws[s] * v[s].w;
+        }
+    }
+    *reinterpret_cast<float4 *>(out + (size_t)t * D + i) = acc;
 }
 
 size_t prefill_workspace_bytes(int T, int k, int E, int Kd, int D) {
@@ -530,7 +562,7 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
     hipLaunchKernelGGL(k_prefill_down, dim3(D / BN2, mc), dim3(256), 0, s, Dn.p0, Dn.p1, (int)Dn.blocks_per_row, D,
                        w.H, Kd, w.chunks, w.n_chunks, w.offsets, w.Y);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_prefill_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, w.Y, w.pos, w.w, k, D, out);
+    hipLaunchKernelGGL(k_prefill_combine, dim3((D / 4 + 255) / 256, T), dim3(256), 0, s, w.Y, w.pos, w.w, k, D, out);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (out_ids) {
         if ((e = hipMemcpyAsync(out_ids, w.ids, (size_t)TK * 4, hipMemcpyDefault, s)) != hipSuccess) return e;
