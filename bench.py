@@ -862,7 +862,7 @@ def bench_gemma4(args):
     log(f"gemma4 block: {us:.2f} us/token wall, {dev_us:.2f} us/token device, {gbps:.0f} GB/s")
     result = base_record(
         args, "Gemma4 MoE block decode us/token (config-4 layer + router-input prep + MoE tail)", round(us, 3),
-        "us/token", steps, False, "expert weights x fp32 activations (int8-limb dots for Q4_K); fp32 norms",
+        "us/token", steps, False, "expert weights x fp32 activations in int8-limb pairs (v_dot4), Q8_0 router x fp32 activations; fp32 norms",
         {"workload": "gemma4_moe_block_cfg4", "d_model": G4_D, "n_experts": G4_E, "d_expert": G4_F,
          "down_cols": w.down_cols, "top_k": K, "router": "Q8_0",
          "experts": f"{ggml.NAMES[w.gate_up_type]} gate/up, {ggml.NAMES[w.down_type]} down",
@@ -928,7 +928,7 @@ def bench_formats(args):
         t1.free()
     result = {"metric": "dense matvec GB/s per GGUF format (131072 x 4096, batch 1)", "unit": "GB/s",
               "value": per["Q3_K"]["gbps"], "higher_is_better": True, "n_gpus": 1,
-              "dtype": "fp32 activations (Q4_K: int8-limb pairs on v_dot4)",
+              "dtype": "weights x fp32 activations split into two int8 limbs per 16-element group (v_dot4 int32 dots), fp32 scales and accumulation",
               "data": "synthetic", "config": {"workload": "matvec_formats", "rows": rows, "cols": cols},
               "per_format": per}
     print(json.dumps(result), flush=True)

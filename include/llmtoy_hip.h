@@ -181,14 +181,16 @@ int lt_moe_router_topk(lt_ctx *ctx, const lt_tensor *router, const float *x, con
 /* Expert-indexed gate/up: h[s][j] = act(G_e x)[j] * (U_e x)[j] for slot s,
  * e = ids[s], j < d_expert; h rows are padded with zeros to down_cols.
  * gate_up is the flattened [E, 2*d_expert, d_model] tensor (gate rows then
- * up rows per expert, ops/moe.zig:55-73).  h is [k, down_cols] fp32.
+ * up rows per expert, ops/moe.zig:55-73).  h is [k, down_cols] fp32.  A
+ * device pointer x must be 16-byte aligned.
  * Replaces ExpertGateUpIdPipeline (gpu/matvec.zig:1348-1460). */
 int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const float *x, const uint32_t *ids, uint32_t k,
                          uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, uint32_t flags);
 
 /* Expert-indexed down with the weighted combine fused:
  * out[i] = sum_{s<k, in slot order} weights[s] * (D_{ids[s]} h[s])[i]
- * (plus the previous out[i] with LT_MOE_ACCUMULATE).
+ * (plus the previous out[i] with LT_MOE_ACCUMULATE).  A device pointer h
+ * must be 16-byte aligned.
  * Replaces ExpertDownIdPipeline + AccumPipeline (gpu/matvec.zig:1465-1610,
  * 833-1008). */
 int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float *h, const uint32_t *ids,

@@ -849,6 +849,8 @@ extern "C" int lt_expert_gate_up_id(lt_ctx *ctx, const lt_tensor *gate_up, const
         if ((rc = stage_in(ctx, ctx->ids_io, ids, k * 4, (const void **)&dids))) return rc;
         if ((rc = ensure(ctx, ctx->out, (size_t)k * down_cols * 4))) return rc;
         dh = (float *)ctx->out.p;
+    } else if (!aligned16(x)) {
+        return fail(ctx, LT_ERR_INVALID, "x must be 16-byte aligned");
     }
     if ((rc = gate_up_dev(ctx, GU, dx, dids, k, d_expert, down_cols, act, dh))) return rc;
     if (host) {
@@ -887,6 +889,8 @@ extern "C" int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float
             return rc;
         }
         dout = (float *)ctx->out.p;
+    } else if (!aligned16(h)) {
+        return fail(ctx, LT_ERR_INVALID, "h must be 16-byte aligned");
     }
     if ((rc = down_dev(ctx, D, dh, dids, dw, k, nullptr, (flags & LT_MOE_ACCUMULATE) ? 1 : 0, nullptr, dout)))
         return rc;

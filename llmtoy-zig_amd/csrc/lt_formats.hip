@@ -16,11 +16,17 @@
 // Work unit: one 32-element block (Q5_0/Q5_1/IQ4_NL) or one 32-element
 // group of a Q3_K super-block (one scale pair).  A wavefront takes 1-8 rows
 // at a time (lanes striding over each row's units) and the workgroups walk
-// all rows, so x is staged in LDS once per workgroup.  fp32 accumulation in an
-// order of our own: parity with the reference's quantMatvec is to tolerance
-// (its GPU matvec fuzz bound, 1e-4 of max |y|), not bit-exact.
+// all rows, so x is staged in LDS once per workgroup, as two int8 limbs per
+// 16-element group (lt_limbs.h: x ~= sp (256 a + b), error <= max |x| /
+// 65024 of the group) with the group's fp32 sum: the codes (unsigned 5-bit
+// for Q5_0 / Q5_1, the signed IQ4_NL table values, unsigned 3-bit for Q3_K)
+// meet both limbs in v_dot4_i32_i8, exact int32 sums per group, and the
+// formats' offsets (-16, m, -4) come back through the group sums.  fp32
+// accumulation in an order of our own: parity with the reference's
+// quantMatvec is to tolerance (its GPU matvec fuzz bound, 1e-4 of max |y|),
+// not bit-exact.
 #include "llmtoy_hip.h"
-#include "lt_internal.h"
+#include "lt_limbs.h"
 
 namespace lt {
 
@@ -28,13 +34,80 @@ namespace {
 
 constexpr int kFmtWaves = 4;  // rows per workgroup
 
-// Length of the x runs whose sums are staged beside x: one Q3_K scale's 16
-// elements, or one 32-element block.
-template <int T>
-constexpr int kSumLen = T == LT_TYPE_Q3_K ? 16 : 32;
+// Staged activations: n elements (n % 16 == 0) as limb words la [n / 4],
+// lb [n / 4] (word i: elements 4i..4i+3), then per 16-element group its
+// scale lsp [n / 16] and fp32 sum lxs [n / 16].
+size_t lds_bytes(size_t n) { return n * 2 + n / 4 * 2; }
 
-template <int T>
-size_t lds_floats(size_t n) { return n + n / kSumLen<T>; }
+struct LimbView {
+    const uint32_t *la, *lb;
+    const float *lsp, *lxs;
+};
+
+__device__ __forceinline__ LimbView limb_view(const uint32_t *base, int n) {
+    return LimbView{base, base + n / 4, reinterpret_cast<const float *>(base + n / 2),
+                    reinterpret_cast<const float *>(base + n / 2 + n / 16)};
+}
+
+// Block-wide: src[0..n) into limbs at base, one 16-element group per thread
+// and pass, then a barrier.
+__device__ __forceinline__ void stage_limbs(uint32_t *base, const float *src, int n) {
+    uint32_t *la = base, *lb = base + n / 4;
+    float *lsp = reinterpret_cast<float *>(base + n / 2), *lxs = lsp + n / 16;
+    for (int g = threadIdx.x; g < n / 16; g += blockDim.x) {
+        float v[16];
+#pragma unroll
+        for (int t = 0; t < 16; t += 4) {
+            const float4 f = ldg16f(src + 16 * g + t);
+            v[t] = f.x; v[t + 1] = f.y; v[t + 2] = f.z; v[t + 3] = f.w;
+        }
+        uint32_t a[4], b[4];
+        float sp, xs;
+        limbs16(v, a, b, sp, xs);
+        *reinterpret_cast<uint4 *>(la + 4 * g) = make_uint4(a[0], a[1], a[2], a[3]);
+        *reinterpret_cast<uint4 *>(lb + 4 * g) = make_uint4(b[0], b[1], b[2], b[3]);
+        lsp[g] = sp;
+        lxs[g] = xs;
+    }
+    __syncthreads();
+}
+
+// The activations of one 32-element unit: groups 0 (elements 0..15) and 1.
+struct UnitX {
+    uint32_t a[8], b[8];  // a[4g + m]: limb a of elements 16g + 4m + 0..3
+    float sp[2], xs[2];
+};
+
+__device__ __forceinline__ UnitX load_ux(const LimbView &v, int u) {
+    UnitX x;
+    const uint4 *pa = reinterpret_cast<const uint4 *>(v.la + 8 * u);
+    const uint4 *pb = reinterpret_cast<const uint4 *>(v.lb + 8 * u);
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        const uint4 qa = pa[g], qb = pb[g];
+        x.a[4 * g] = qa.x; x.a[4 * g + 1] = qa.y; x.a[4 * g + 2] = qa.z; x.a[4 * g + 3] = qa.w;
+        x.b[4 * g] = qb.x; x.b[4 * g + 1] = qb.y; x.b[4 * g + 2] = qb.z; x.b[4 * g + 3] = qb.w;
+    }
+    const float2 sp = *reinterpret_cast<const float2 *>(v.lsp + 2 * u);
+    const float2 xs = *reinterpret_cast<const float2 *>(v.lxs + 2 * u);
+    x.sp[0] = sp.x; x.sp[1] = sp.y;
+    x.xs[0] = xs.x; x.xs[1] = xs.y;
+    return x;
+}
+
+// Sum over group g of code * x for 16 codes (signed bytes, words c[0..3]):
+// sp (256 A + B) with A, B the exact int32 dots against the two limbs
+// (|256 A + B| < 2^27 for codes of magnitude <= 127, one fp32 rounding).
+__device__ __forceinline__ float group_dot(const uint32_t (&c)[4], const UnitX &x, int g) {
+    int A = sdot4_first((int)c[0], (int)x.a[4 * g]);
+    int B = sdot4_first((int)c[0], (int)x.b[4 * g]);
+#pragma unroll
+    for (int m = 1; m < 4; m++) {
+        A = __builtin_amdgcn_sdot4((int)c[m], (int)x.a[4 * g + m], A, false);
+        B = __builtin_amdgcn_sdot4((int)c[m], (int)x.b[4 * g + m], B, false);
+    }
+    return x.sp[g] * (float)((A << 8) + B);
+}
 
 // Unsigned 5-bit codes of a Q5 block as bytes: word i of the result holds
 // elements 4i..4i+3 (low nibbles of qs word i + high bit 4i..4i+3 of qh) and
@@ -44,35 +117,25 @@ size_t lds_floats(size_t n) { return n + n / kSumLen<T>; }
 // and no two partial products meet.
 __device__ __forceinline__ uint32_t spread4(uint32_t v4) { return (__umul24(v4, 0x204081u) & 0x01010101u) << 4; }
 
-// Byte i of v as a float (one v_cvt_f32_ubyte<i>).
-__device__ __forceinline__ float ubyte_f(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xffu); }
-
-// sum over the block of (code) * x: codes 0..31 as unsigned bytes,
-// converted with v_cvt_f32_ubyte0..3.  x4[i] holds elements 4i..4i+3.
-__device__ __forceinline__ float q5u_block_dot(uint4 qv, uint32_t qh, const float4 *x4) {
+// sum over the block of (code) * x: codes 0..31 as bytes, elements 4i..4i+3
+// of the low half from qs word i's low nibbles and qh bits 4i..4i+3, of the
+// high half from its high nibbles and qh bits 16+4i..
+__device__ __forceinline__ float q5u_block_dot(uint4 qv, uint32_t qh, const UnitX &x) {
     const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
-    float acc = 0.f;
+    uint32_t cl[4], ch[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 lo = x4[i], hi = x4[4 + i];
-        const uint32_t cl = (w[i] & 0x0f0f0f0fu) | spread4((qh >> (4 * i)) & 15u);
-        const uint32_t ch = ((w[i] >> 4) & 0x0f0f0f0fu) | spread4((qh >> (16 + 4 * i)) & 15u);
-        acc += ubyte_f(cl, 0) * lo.x;
-        acc += ubyte_f(cl, 1) * lo.y;
-        acc += ubyte_f(cl, 2) * lo.z;
-        acc += ubyte_f(cl, 3) * lo.w;
-        acc += ubyte_f(ch, 0) * hi.x;
-        acc += ubyte_f(ch, 1) * hi.y;
-        acc += ubyte_f(ch, 2) * hi.z;
-        acc += ubyte_f(ch, 3) * hi.w;
+        cl[i] = (w[i] & 0x0f0f0f0fu) | spread4((qh >> (4 * i)) & 15u);
+        ch[i] = ((w[i] >> 4) & 0x0f0f0f0fu) | spread4((qh >> (16 + 4 * i)) & 15u);
     }
-    return acc;
+    return group_dot(cl, x, 0) + group_dot(ch, x, 1);
 }
 
-// IQ4_NL table + 128 as unsigned bytes (1..241): entries 0-3, 4-7, 8-11, 12-15.
-constexpr uint32_t kIq4T0 = 0x3f2d1801u, kIq4T1 = 0x766a5d4fu, kIq4T2 = 0xa6998d81u, kIq4T3 = 0xf1d9c5b5u;
+// The IQ4_NL table (quant/dequant.zig:607-612) as signed bytes: entries
+// 0-3, 4-7, 8-11, 12-15.
+constexpr uint32_t kIq4T0 = 0xbfad9881u, kIq4T1 = 0xf6eaddcfu, kIq4T2 = 0x26190d01u, kIq4T3 = 0x71594535u;
 
-// table[n] + 128 for the four nibbles in the bytes of n4 (each 0..15):
+// table[n] for the four nibbles in the bytes of n4 (each 0..15):
 // v_perm_b32 picks bytes by 3-bit index from the low and high half tables,
 // bit 3 chooses between them (v_bfi_b32 on a byte mask).
 __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n4) {
@@ -84,23 +147,15 @@ __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n4) {
     return (hi & m) | (lo & ~m);
 }
 
-__device__ __forceinline__ float iq4u_block_dot(uint4 qv, const float4 *x4) {
+__device__ __forceinline__ float iq4_block_dot(uint4 qv, const UnitX &x) {
     const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
-    float acc = 0.f;
+    uint32_t tl[4], th[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 lo = x4[i], hi = x4[4 + i];
-        const uint32_t tl = iq4_lookup4(w[i] & 0x0f0f0f0fu), th = iq4_lookup4((w[i] >> 4) & 0x0f0f0f0fu);
-        acc += ubyte_f(tl, 0) * lo.x;
-        acc += ubyte_f(tl, 1) * lo.y;
-        acc += ubyte_f(tl, 2) * lo.z;
-        acc += ubyte_f(tl, 3) * lo.w;
-        acc += ubyte_f(th, 0) * hi.x;
-        acc += ubyte_f(th, 1) * hi.y;
-        acc += ubyte_f(th, 2) * hi.z;
-        acc += ubyte_f(th, 3) * hi.w;
+        tl[i] = iq4_lookup4(w[i] & 0x0f0f0f0fu);
+        th[i] = iq4_lookup4((w[i] >> 4) & 0x0f0f0f0fu);
     }
-    return acc;
+    return group_dot(tl, x, 0) + group_dot(th, x, 1);
 }
 
 // Q3_K scale i (0..15) from the 12 packed bytes s0, s1, s2 (little-endian
@@ -162,32 +217,13 @@ __device__ __forceinline__ UnitW<T> load_unit(const DevTensor &W, size_t row, in
     return w;
 }
 
-// x of unit u (elements 32 u .. 32 u + 32 of the row's columns, in LDS) into
-// registers, with the sums of its runs (xsum = the run sums staged beside x):
-// s0 = the block's sum, or for Q3_K s0/s1 = the two 16-element halves.
-template <int T>
-__device__ __forceinline__ void load_x(const float *xs, const float *xsum, int u, float4 (&x4)[8], float &s0,
-                                       float &s1) {
-    const float4 *p = reinterpret_cast<const float4 *>(xs + 32 * u);
-#pragma unroll
-    for (int i = 0; i < 8; i++) x4[i] = p[i];
-    if constexpr (T == LT_TYPE_Q3_K) {
-        s0 = xsum[2 * u];
-        s1 = xsum[2 * u + 1];
-    } else {
-        s0 = xsum[u];
-        s1 = 0.f;
-    }
-}
-
 // Group u % 8 = 4 h + j of a Q3_K super-block: elements 128 h + 32 j + [0, 32)
 // (16 from qs[32 h ..] and hmask[0 ..], 16 from qs[32 h + 16 ..] and
 // hmask[16 ..]) against x.  Each element's 3-bit unsigned code
-// c = q2 | hbit << 2 (value c - 4) is built four to a dword and converted
-// with v_cvt_f32_ubyte<i>; the -4 folds into the sums of the group's two
-// 16-element halves of x.
-__device__ __forceinline__ float q3k_group_dot(const UnitW<LT_TYPE_Q3_K> &w, int u, const float4 *x4, float s0,
-                                               float s1) {
+// c = q2 | hbit << 2 (value c - 4) is built four to a dword; the -4 folds
+// into the sums of the group's two 16-element halves of x, which are the
+// two limb groups, each with its own scale.
+__device__ __forceinline__ float q3k_group_dot(const UnitW<LT_TYPE_Q3_K> &w, int u, const UnitX &x) {
     const int h = (u >> 2) & 1, j = u & 3;
     const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
     const uint32_t mw[8] = {w.m0.x, w.m0.y, w.m0.z, w.m0.w, w.m1.x, w.m1.y, w.m1.z, w.m1.w};
@@ -196,31 +232,27 @@ __device__ __forceinline__ float q3k_group_dot(const UnitW<LT_TYPE_Q3_K> &w, int
     float total = 0.f;
 #pragma unroll
     for (int g = 0; g < 2; g++) {
-        float acc = 0.f;
+        uint32_t c[4];
 #pragma unroll
-        for (int w4 = 0; w4 < 4; w4++) {
-            const float4 xv = x4[4 * g + w4];
-            const uint32_t c = ((qw[4 * g + w4] >> qsh) & 0x03030303u) | (((mw[4 * g + w4] >> msh) & 0x01010101u) << 2);
-            acc += ubyte_f(c, 0) * xv.x;
-            acc += ubyte_f(c, 1) * xv.y;
-            acc += ubyte_f(c, 2) * xv.z;
-            acc += ubyte_f(c, 3) * xv.w;
-        }
-        total += (d * (float)(q3k_scale(w.sc[0], w.sc[1], w.sc[2], 8 * h + 2 * j + g) - 32)) * (acc - 4.f * (g ? s1 : s0));
+        for (int w4 = 0; w4 < 4; w4++)
+            c[w4] = ((qw[4 * g + w4] >> qsh) & 0x03030303u) | (((mw[4 * g + w4] >> msh) & 0x01010101u) << 2);
+        const float dot = group_dot(c, x, g);
+        total += (d * (float)(q3k_scale(w.sc[0], w.sc[1], w.sc[2], 8 * h + 2 * j + g) - 32)) * (dot - 4.f * x.xs[g]);
     }
     return total;
 }
 
 // Contribution of unit u of a row from its weight words and its x (the
-// offsets the unsigned codes leave out come back through the run sums).
+// offsets the unsigned codes leave out come back through the group sums).
 template <int T>
-__device__ __forceinline__ float dot_unit(const UnitW<T> &w, int u, const float4 *x4, float s0, float s1) {
+__device__ __forceinline__ float dot_unit(const UnitW<T> &w, int u, const UnitX &x) {
     if constexpr (T == LT_TYPE_Q3_K) {
-        return q3k_group_dot(w, u, x4, s0, s1);
+        return q3k_group_dot(w, u, x);
     } else {
         const float d = f16_bits_to_f32((uint16_t)w.dm);
-        if constexpr (T == LT_TYPE_IQ4_NL) return d * (iq4u_block_dot(w.q, x4) - 128.f * s0);  // table + 128
-        const float dot = q5u_block_dot(w.q, w.qh, x4);
+        if constexpr (T == LT_TYPE_IQ4_NL) return d * iq4_block_dot(w.q, x);
+        const float dot = q5u_block_dot(w.q, w.qh, x);
+        const float s0 = x.xs[0] + x.xs[1];
         if constexpr (T == LT_TYPE_Q5_0) return d * (dot - 16.f * s0);                   // codes - 16
         return d * dot + f16_bits_to_f32((uint16_t)(w.dm >> 16)) * s0;                    // Q5_1: d q + m
     }
@@ -238,22 +270,6 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
-// Stage n floats into LDS and their sums over kSumLen<T> elements
-// (sums[j] = sum of dst[L j .. L j + L)) right after them.
-template <int T>
-__device__ __forceinline__ void stage(float *dst, const float *src, int n) {
-    constexpr int L = kSumLen<T>;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
-    __syncthreads();
-    for (int j = threadIdx.x; j < n / L; j += blockDim.x) {
-        float t = 0.f;
-#pragma unroll 8
-        for (int e = 0; e < L; e++) t += dst[L * j + e];
-        dst[n + j] = t;
-    }
-    __syncthreads();
-}
-
 // Workgroup = kFmtWaves waves; a wave takes RPW groups of R rows at a time
 // (64 / RPW lanes per group, striding over the rows' units; each lane loads
 // a unit's x once and applies it to the R rows) and walks the rows with a
@@ -261,10 +277,10 @@ __device__ __forceinline__ void stage(float *dst, const float *src, int n) {
 template <int T, int RPW, int R>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, const float *__restrict__ x,
                                                                float *__restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + their run sums
+    extern __shared__ __attribute__((aligned(16))) uint32_t xl[];  // x as limbs (lds_bytes(cols))
     constexpr int LPR = kWave / RPW;
-    stage<T>(xs, x, (int)W.cols);
-    const float *xsum = xs + W.cols;
+    stage_limbs(xl, x, (int)W.cols);
+    const LimbView xv = limb_view(xl, (int)W.cols);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int grp = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
@@ -280,11 +296,9 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, cons
                 UnitW<T> w[R];
 #pragma unroll
                 for (int r = 0; r < R; r++) w[r] = load_unit<T>(W, row0 + r < n ? row0 + r : n - 1, u);
-                float4 x4[8];
-                float s0, s1;
-                load_x<T>(xs, xsum, u, x4, s0, s1);
+                const UnitX ux = load_ux(xv, u);
 #pragma unroll
-                for (int r = 0; r < R; r++) acc[r] += dot_unit<T>(w[r], u, x4, s0, s1);
+                for (int r = 0; r < R; r++) acc[r] += dot_unit<T>(w[r], u, ux);
             }
         }
 #pragma unroll
@@ -304,10 +318,10 @@ template <int T, int RPW, int R>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, const float *__restrict__ x,
                                                                   const uint32_t *__restrict__ ids, int F,
                                                                   int down_cols, uint32_t act, float *__restrict__ h) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // cols floats + their run sums
+    extern __shared__ __attribute__((aligned(16))) uint32_t xl[];  // x as limbs (lds_bytes(cols))
     constexpr int LPR = kWave / RPW;
-    stage<T>(xs, x, (int)W.cols);
-    const float *xsum = xs + W.cols;
+    stage_limbs(xl, x, (int)W.cols);
+    const LimbView xv = limb_view(xl, (int)W.cols);
     const int s = blockIdx.y;
     const uint32_t e = __builtin_amdgcn_readfirstlane(ids[s]);
     float *hs = h + (size_t)s * down_cols;
@@ -333,13 +347,11 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, c
                     wg[r] = load_unit<T>(W, g0 + j, u);
                     wu[r] = load_unit<T>(W, g0 + F + j, u);
                 }
-                float4 x4[8];
-                float s0, s1;
-                load_x<T>(xs, xsum, u, x4, s0, s1);
+                const UnitX ux = load_ux(xv, u);
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    ag[r] += dot_unit<T>(wg[r], u, x4, s0, s1);
-                    au[r] += dot_unit<T>(wu[r], u, x4, s0, s1);
+                    ag[r] += dot_unit<T>(wg[r], u, ux);
+                    au[r] += dot_unit<T>(wu[r], u, ux);
                 }
             }
         }
@@ -363,7 +375,7 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
                                                                     const float *__restrict__ wts, int k,
                                                                     const float *base, int accumulate,
                                                                     const float *dscale, float *out) {
-    extern __shared__ __attribute__((aligned(16))) float hsm[];  // k * down_cols floats + their run sums
+    extern __shared__ __attribute__((aligned(16))) uint32_t hl[];  // h [k][down_cols] as limbs
     __shared__ uint32_t s_e[16];
     __shared__ float s_w[16];
     constexpr int LPR = kWave / RPW;
@@ -373,8 +385,8 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
         s_e[threadIdx.x] = e;
         s_w[threadIdx.x] = e < (uint32_t)W.n_experts ? (dscale ? dscale[e] * wts[threadIdx.x] : wts[threadIdx.x]) : 0.f;
     }
-    stage<T>(hsm, h, k * Kd);
-    const float *hsum = hsm + k * Kd;  // run sums: slot s's at hsum + s * (Kd / kSumLen<T>)
+    stage_limbs(hl, h, k * Kd);
+    const LimbView hv = limb_view(hl, k * Kd);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int r = lane / LPR, sub = lane % LPR;
     const int U = units_per_row<T>(W);
@@ -389,10 +401,8 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_down_fmt(DevTensor W,
                 const uint32_t e = s_e[s];
                 if (e < (uint32_t)W.n_experts) {
                     const UnitW<T> w = load_unit<T>(W, (size_t)e * D + i, u);
-                    float4 x4[8];
-                    float s0, s1;
-                    load_x<T>(hsm + s * Kd, hsum + s * (Kd / kSumLen<T>), u, x4, s0, s1);
-                    acc += s_w[s] * dot_unit<T>(w, u, x4, s0, s1);
+                    const UnitX ux = load_ux(hv, s * U + u);  // U = Kd / 32 units per slot
+                    acc += s_w[s] * dot_unit<T>(w, u, ux);
                 }
                 u += LPR;
                 while (u >= U) {
@@ -420,15 +430,15 @@ int pick_rpw(size_t units) {
     return units >= 24 ? 2 : units >= 12 ? 4 : 8;
 }
 
-// Allow the largest staging (16384 floats and their 16-element run sums:
-// 68 KiB of dynamic LDS), once per kernel and device.
+// Allow the largest staging (16384 activations as limbs: 40 KiB of dynamic
+// LDS), once per kernel and device.
 hipError_t allow_lds(const void *fn, bool *set) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     if (set[dev]) return hipSuccess;
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (16384 + 16384 / 16) * 4);
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes(16384));
     if (e == hipSuccess) set[dev] = true;
     return e;
 }
@@ -450,8 +460,7 @@ hipError_t launch_mv(const DevTensor &W, const float *x, float *y, hipStream_t s
     const size_t per = (size_t)kFmtWaves * RPW * R;
     const size_t need = (W.total_rows + per - 1) / per;
     const dim3 grid((unsigned)(need < 2048 ? need : 2048));
-    hipLaunchKernelGGL((k_matvec_fmt<T, RPW, R>), grid, dim3(64 * kFmtWaves), lds_floats<T>(W.cols) * sizeof(float),
-                       s, W, x, y);
+    hipLaunchKernelGGL((k_matvec_fmt<T, RPW, R>), grid, dim3(64 * kFmtWaves), lds_bytes(W.cols), s, W, x, y);
     return hipGetLastError();
 }
 
@@ -466,7 +475,7 @@ hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, in
     const int need = (F + per - 1) / per;
     const dim3 grid((unsigned)(need < 128 ? need : 128), (unsigned)k);  // up to 128 x k workgroups walk the rows
     hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW, R>), grid, dim3(64 * kFmtWaves),
-                       lds_floats<T>(W.cols) * sizeof(float), s, W, x, ids, F, down_cols, act, h);
+                       lds_bytes(W.cols), s, W, x, ids, F, down_cols, act, h);
     return hipGetLastError();
 }
 
@@ -480,7 +489,7 @@ hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, co
     const int need = (D + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const dim3 grid((unsigned)(need < 1024 ? need : 1024));
     hipLaunchKernelGGL((k_expert_down_fmt<T, RPW>), grid, dim3(64 * kFmtWaves),
-                       lds_floats<T>((size_t)k * W.cols) * sizeof(float), s, W, h, ids, w, k, base,
+                       lds_bytes((size_t)k * W.cols), s, W, h, ids, w, k, base,
                        accumulate, dscale, out);
     return hipGetLastError();
 }
