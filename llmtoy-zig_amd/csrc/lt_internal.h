@@ -237,6 +237,28 @@ __device__ __forceinline__ float act_apply(uint32_t act, float g) {
 
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ __forceinline__ float4 ldg16f(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// The prefill's f16 copy of X (X rows scaled into f16's range, K in the
+// order the f16 dequantisation produces): a row with max |x| = m is divided
+// by 2^e, e the smallest value >= 0 with m / 2^e <= 2^14 (exact; f16's range
+// ends near 2^16); rows holding inf or NaN pass unscaled (e = 0).
+__device__ __forceinline__ int prefill_x_exp(float m) {
+    int e = 0;
+    if (m > 16384.0f) e = ilogbf(m) - 13;  // m / 2^e < 2^14
+    if (!(m <= 3.0e38f)) e = 0;
+    return e;
+}
+
+// Elements i..i+7 of a row (i % 8 == 0) times inv as f16 at dst + i, each
+// aligned 4 in the order (0, 2, 1, 3).
+__device__ __forceinline__ void prefill_x_store8(const float *xr, float inv, _Float16 *hr, int i) {
+    typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 h8;
+    const float4 a = ldg16f(xr + i), b = ldg16f(xr + i + 4);
+    h8 o;
+    o[0] = (_Float16)(a.x * inv); o[1] = (_Float16)(a.z * inv); o[2] = (_Float16)(a.y * inv); o[3] = (_Float16)(a.w * inv);
+    o[4] = (_Float16)(b.x * inv); o[5] = (_Float16)(b.z * inv); o[6] = (_Float16)(b.y * inv); o[7] = (_Float16)(b.w * inv);
+    *reinterpret_cast<h8 *>(hr + i) = o;
+}
 // 16-byte load with the non-temporal hint (global_load_dwordx4 ... nt), for
 // weight streams that a launch reads once (the Q6_K stream: 23.6 -> 22.7 us
 // on 128 MB).
@@ -370,8 +392,13 @@ hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, 
                          const RouterPrep *prep = nullptr);
 // Router logits for T tokens (X [T][cols] -> logits [T][rows]) and per-token
 // softmax + top-k (ids, w: [T][k]).
+// Batched router logits and top-k of T tokens (prefill).  With the F32 tile
+// kernel (cols % 256 == 0, at least 32 router rows) the router launch also
+// writes the prefill's f16 X (Xh, row scales rs); *x_done reports whether
+// it did.
 hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, const float *bias, float *logits,
-                                 uint32_t k, uint32_t norm, uint32_t *ids, float *w, hipStream_t s);
+                                 uint32_t k, uint32_t norm, uint32_t *ids, float *w, _Float16 *Xh, float *rs,
+                                 bool *x_done, hipStream_t s);
 // Batched prefill MoE (Q4_K experts), see lt_prefill.hip.  ws: workspace of
 // prefill_workspace_bytes(T, k, E, F, D) bytes.
 size_t prefill_workspace_bytes(int T, int k, int E, int F, int D);

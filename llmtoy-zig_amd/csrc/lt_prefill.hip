@@ -7,8 +7,9 @@
 //   2. dispatch: one block counts tokens per expert, lays out per-expert
 //      row ranges ("sorted rows"), cuts each range into chunks of at most
 //      MC = 128 rows, and scatters (token, slot) assignments into them;
-//      X is converted to f16 once (k_prefill_x_f16), each row scaled by a
-//      power of two that keeps it far inside f16's range;
+//      X is converted to f16 once (by the router kernel, or
+//      k_prefill_x_f16), each row scaled by a power of two that keeps it far
+//      inside f16's range;
 //   3. grouped gate/up GEMM: one block per (chunk, 64 output columns); its
 //      128 weight rows (64 gate + 64 up) are dequantised from Q4_K to f16
 //      in LDS once per K stage and shared by the chunk's 4 token tiles (one
@@ -373,10 +374,10 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
     }
 }
 
-// X (fp32) -> f16, one block per token row: the row is divided by rs =
-// 2^e, the smallest power of two (e >= 0) that brings max |x| to at most
-// 2^14 (exact; f16's range ends near 2^16), and stored in kperm order.  D %
-// 8 == 0; the fp32 row is read twice (max, then values).
+// X (fp32) -> f16, one block per token row (prefill_x_exp, prefill_x_store8:
+// the row divided by rs = 2^e, stored in kperm order), for the router paths
+// that do not write it themselves.  D % 8 == 0; the fp32 row is read twice
+// (max, then values).
 __global__ void __launch_bounds__(256) k_prefill_x_f16(const float *__restrict__ X, _Float16 *__restrict__ Xh,
                                                        float *__restrict__ rs, int D) {
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -396,20 +397,11 @@ __global__ void __launch_bounds__(256) k_prefill_x_f16(const float *__restrict__
     if ((tid & 63) == 0) s_m[tid >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-    int e = 0;
-    if (m > 16384.0f) e = ilogbf(m) - 13;  // m / 2^e < 2^14
-    if (!(m <= 3.0e38f)) e = 0;             // inf / NaN rows pass through unscaled
+    const int e = prefill_x_exp(m);
     const float inv = ldexpf(1.0f, -e);
     if (tid == 0) rs[t] = ldexpf(1.0f, e);
     _Float16 *hr = Xh + (size_t)t * D;
-    for (int i = 8 * tid; i < D; i += 8 * 256) {
-        const float4 a = ldg16f(xr + i), b = ldg16f(xr + i + 4);
-        // kperm within each 4: positions (0, 1, 2, 3) take elements (0, 2, 1, 3)
-        f16x8 o;
-        o[0] = (_Float16)(a.x * inv); o[1] = (_Float16)(a.z * inv); o[2] = (_Float16)(a.y * inv); o[3] = (_Float16)(a.w * inv);
-        o[4] = (_Float16)(b.x * inv); o[5] = (_Float16)(b.z * inv); o[6] = (_Float16)(b.y * inv); o[7] = (_Float16)(b.w * inv);
-        *reinterpret_cast<f16x8 *>(hr + i) = o;
-    }
+    for (int i = 8 * tid; i < D; i += 8 * 256) prefill_x_store8(xr, inv, hr, i);
 }
 
 // ---------------------------------------------------------------- gate/up
@@ -548,13 +540,16 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
     const int E = (int)GU.n_experts, D = (int)GU.cols, Kd = (int)Dn.cols;
     const int TK = T * k;
     Ws w = carve(ws, T, k, E, Kd, D);
-    hipError_t e = launch_router_batched(R, X, T, bias, w.logits, k, norm, w.ids, w.w, s);
+    bool x_done = false;
+    hipError_t e = launch_router_batched(R, X, T, bias, w.logits, k, norm, w.ids, w.w, w.Xh, w.rs, &x_done, s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_prefill_dispatch, dim3(1), dim3(1024), 0, s, w.ids, TK, k, E, w.offsets, w.chunks,
                        w.n_chunks, w.perm, w.pos);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_prefill_x_f16, dim3((unsigned)T), dim3(256), 0, s, X, w.Xh, w.rs, D);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!x_done) {
+        hipLaunchKernelGGL(k_prefill_x_f16, dim3((unsigned)T), dim3(256), 0, s, X, w.Xh, w.rs, D);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     const int mc = max_chunks(TK, E);
     hipLaunchKernelGGL(k_prefill_gate_up, dim3(F / BN1, mc), dim3(256), 0, s, GU.p0, GU.p1, (int)GU.blocks_per_row,
                        F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm, act, w.H, Kd);

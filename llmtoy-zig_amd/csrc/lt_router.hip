@@ -272,18 +272,32 @@ hipError_t launch_router(const DevTensor &R, const float *x, const float *bias, 
 // value used by 4 chains.  The 32 chain totals of a (row, token) then meet
 // in LDS for the (acc0+acc1)+(acc2+acc3) and ordered lane reduce.
 // Requires cols % 256 == 0.
+// With Xh set, the same launch writes the prefill's f16 X (Xh, row scales
+// rs; prefill_x_exp / prefill_x_store8): token t0 + j of the tile is
+// converted by wavefront w of the row block with j = blockIdx.x + gridDim.x
+// * w (gridDim.x >= TB / 4), its max |x| taken from the X chunks as they
+// pass through LDS.  (Running the top-k in the last row block of each token
+// tile as well, behind an arrival ticket, made the launch 70 us instead of
+// 15: the release fences of 512 blocks write back the L2s the f16 rows have
+// filled.)
 constexpr int RT_RB = 8, RT_TB = 16, RT_KC = 256;
 
 __global__ void __launch_bounds__(256) k_router_f32_tile(const float *__restrict__ W, const float *__restrict__ X,
                                                          const float *__restrict__ bias, float *__restrict__ logits,
-                                                         int rows, int cols, int T) {
+                                                         int rows, int cols, int T, _Float16 *__restrict__ Xh,
+                                                         float *__restrict__ rs) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float ws[2][RT_RB][RT_KC];
     __shared__ __attribute__((aligned(16))) float xs[2][RT_TB][RT_KC];
     __shared__ float ch[RT_RB][RT_TB][33];
     const int tid = threadIdx.x, c = tid & 31, g = tid >> 5;
+    const int wave = tid >> 6, lane = tid & 63;
     const int rg = g & 1, tg = g >> 1;  // rows 4 rg + [0, 4), tokens 4 tg + [0, 4)
     const int r0 = blockIdx.x * RT_RB, t0 = blockIdx.y * RT_TB;
+    // this wavefront's token for the f16 X (uniform over the wavefront)
+    const int xj = blockIdx.x + gridDim.x * wave;
+    const bool xconv = Xh && xj < RT_TB && t0 + xj < T;
+    float xmax = 0.0f;
     // stage loads: W tile 8 x 256 = 512 float4 (2 per thread), X tile
     // 16 x 256 = 1024 float4 (4 per thread); rows / tokens past the end
     // re-read the last valid one (never used)
@@ -328,6 +342,10 @@ __global__ void __launch_bounds__(256) k_router_f32_tile(const float *__restrict
 #pragma unroll
             for (int u = 0; u < 4; u++) xr[u] = ldg16f(xsrc[u] + (kc + 1) * RT_KC);
         }
+        if (xconv) {
+            const float4 v = *reinterpret_cast<const float4 *>(&xs[b][xj][4 * lane]);
+            xmax = fmaxf(xmax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
 #pragma unroll
         for (int it = 0; it < RT_KC / 32; it++) {
             float wv[4], xv[4];
@@ -367,6 +385,17 @@ __global__ void __launch_bounds__(256) k_router_f32_tile(const float *__restrict
             logits[(size_t)tok * rows + row] = sum;
         }
     }
+    if (xconv) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) xmax = fmaxf(xmax, __shfl_xor(xmax, off, 64));
+        const int e = prefill_x_exp(xmax);
+        const int tok = t0 + xj;
+        if (lane == 0) rs[tok] = ldexpf(1.0f, e);
+        const float inv = ldexpf(1.0f, -e);
+        const float *xrow = X + (size_t)tok * cols;
+        _Float16 *hrow = Xh + (size_t)tok * cols;
+        for (int i = 8 * lane; i < cols; i += 8 * 64) prefill_x_store8(xrow, inv, hrow, i);
+    }
 }
 
 // Softmax + top-k of token blockIdx.x of a batch of logits rows.
@@ -378,13 +407,17 @@ __global__ void __launch_bounds__(64) k_topk_rows(const float *__restrict__ logi
 }
 
 hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, const float *bias, float *logits,
-                                 uint32_t k, uint32_t norm, uint32_t *ids, float *w, hipStream_t s) {
+                                 uint32_t k, uint32_t norm, uint32_t *ids, float *w, _Float16 *Xh, float *rs,
+                                 bool *x_done, hipStream_t s) {
     const TopkArgs none{nullptr, 0, 0, nullptr, nullptr, nullptr};
     const int rows = (int)R.total_rows;
-    if (R.type == 0 && R.cols % RT_KC == 0)
-        hipLaunchKernelGGL(k_router_f32_tile, dim3((rows + RT_RB - 1) / RT_RB, (T + RT_TB - 1) / RT_TB), dim3(256), 0,
-                           s, (const float *)R.p0, X, bias, logits, rows, (int)R.cols, T);
-    else if (R.type == 0)
+    *x_done = false;
+    if (R.type == 0 && R.cols % RT_KC == 0) {
+        const int gx = (rows + RT_RB - 1) / RT_RB;
+        *x_done = Xh && 4 * gx >= RT_TB;  // every token of a tile has a wavefront to convert it
+        hipLaunchKernelGGL(k_router_f32_tile, dim3(gx, (T + RT_TB - 1) / RT_TB), dim3(256), 0, s,
+                           (const float *)R.p0, X, bias, logits, rows, (int)R.cols, T, *x_done ? Xh : nullptr, rs);
+    } else if (R.type == 0)
         hipLaunchKernelGGL(k_router_f32<64>, dim3((rows + 1) / 2, T), dim3(64), 0, s, (const float *)R.p0, X, bias,
                            logits, rows, (int)R.cols, none);
     else
