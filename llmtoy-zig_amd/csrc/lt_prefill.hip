@@ -312,14 +312,30 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
     // positions of its chunks in a list ordered by token tiles, largest
     // first: the blocks with the most MFMA work are dispatched first and
     // the short ones fill in behind them.
+    // Up to kIdsPer ids per thread are loaded once, all in flight together,
+    // and kept for the scatter; longer batches read them again.
+    constexpr int kIdsPer = 8;
     __shared__ int cnt[1024], cur[1024];
     __shared__ int scan[2][6][1024];
     const int e = threadIdx.x;
+    const bool cached = TK <= kIdsPer * (int)blockDim.x;
+    uint32_t xc[kIdsPer];
+#pragma unroll
+    for (int j = 0; j < kIdsPer; j++) {
+        const int i = threadIdx.x + j * blockDim.x;
+        xc[j] = cached && i < TK ? ids[i] : 0xffffffffu;
+    }
     if (e < E) cnt[e] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < TK; i += blockDim.x) {
-        const uint32_t x = ids[i];
-        if (x < (uint32_t)E) atomicAdd(&cnt[x], 1);
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < kIdsPer; j++)
+            if (xc[j] < (uint32_t)E) atomicAdd(&cnt[xc[j]], 1);
+    } else {
+        for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+            const uint32_t x = ids[i];
+            if (x < (uint32_t)E) atomicAdd(&cnt[x], 1);
+        }
     }
     __syncthreads();
     const int n = e < E ? cnt[e] : 0, full = n / MC, rem = n % MC, cls = rem ? (rem + 31) / 32 : 0;
@@ -362,8 +378,7 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < TK; i += blockDim.x) {
-        const uint32_t x = ids[i];
+    auto place = [&](int i, uint32_t x) {
         if (x < (uint32_t)E) {
             const int p = atomicAdd(&cur[x], 1);
             perm[p] = i / k;
@@ -371,6 +386,15 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
         } else {
             pos[i] = -1;
         }
+    };
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < kIdsPer; j++) {
+            const int i = threadIdx.x + j * blockDim.x;
+            if (i < TK) place(i, xc[j]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < TK; i += blockDim.x) place(i, ids[i]);
     }
 }
 
