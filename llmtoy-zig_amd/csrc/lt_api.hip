@@ -783,6 +783,24 @@ int gate_up_dev(lt_ctx *ctx, const DevTensor &GU, const float *x, const uint32_t
                      "expert_gate_up_fmt");
 }
 
+// gate/up that selects the experts itself from the router logits in
+// ctx->logits and leaves the selection in ctx->ids / ctx->w
+int gate_up_routed_dev(lt_ctx *ctx, const DevTensor &GU, const float *x, uint32_t k, uint32_t norm,
+                       uint32_t d_expert, uint32_t Kd, uint32_t act, float *h) {
+    const float *logits = (const float *)ctx->logits.p;
+    uint32_t *ids = (uint32_t *)ctx->ids.p;
+    float *w = (float *)ctx->w.p;
+    if (GU.type == LT_TYPE_Q4_K)
+        return launch_rc(ctx,
+                         lt::launch_expert_gate_up_q4k_routed(GU, x, logits, k, norm, d_expert, Kd, act, h, ids, w,
+                                                              ctx->stream),
+                         "expert_gate_up_routed");
+    return launch_rc(ctx,
+                     lt::launch_expert_gate_up_fmt_routed(GU, x, logits, k, norm, d_expert, Kd, act, h, ids, w,
+                                                          ctx->stream),
+                     "expert_gate_up_fmt_routed");
+}
+
 int down_dev(lt_ctx *ctx, const DevTensor &D, const float *h, const uint32_t *ids, const float *w, uint32_t k,
              const float *base, int accumulate, const float *dscale, float *out) {
     if (D.type == LT_TYPE_Q4_K)
@@ -985,15 +1003,10 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
     }
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
-    if (GU.type == LT_TYPE_Q4_K && R.total_rows <= kRoutedGateUpMaxExperts) {
+    if (R.total_rows <= kRoutedGateUpMaxExperts) {
         // logits only; each gate/up block selects its expert from them
         if ((rc = router_dev(ctx, R, x, bias, 0, flags))) return rc;
-        rc = launch_rc(ctx,
-                       lt::launch_expert_gate_up_q4k_routed(GU, x, (const float *)ctx->logits.p, k,
-                                                            (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, d_expert,
-                                                            (uint32_t)Kd, act, h, (uint32_t *)ctx->ids.p,
-                                                            (float *)ctx->w.p, ctx->stream),
-                       "expert_gate_up_routed");
+        rc = gate_up_routed_dev(ctx, GU, x, k, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, d_expert, (uint32_t)Kd, act, h);
     } else {
         if ((rc = router_dev(ctx, R, x, bias, k, flags))) return rc;
         rc = gate_up_dev(ctx, GU, x, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act, h);
@@ -1367,13 +1380,9 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     if ((rc = ensure(ctx, ctx->eh, (size_t)k * Kd * 4))) return rc;
     float *h = (float *)ctx->eh.p;
     const uint32_t norm = (flags & LT_MOE_NORM_TOPK) ? 1u : 0u;
-    if (GU.type == LT_TYPE_Q4_K && E <= kRoutedGateUpMaxExperts) {
+    if (E <= kRoutedGateUpMaxExperts) {
         if ((rc = router_dev(ctx, R, rin, nullptr, 0, flags, nullptr, fuse_prep ? &prep : nullptr))) return rc;
-        rc = launch_rc(ctx,
-                       lt::launch_expert_gate_up_q4k_routed(GU, moe_in, (const float *)ctx->logits.p, k, norm,
-                                                            d_expert, (uint32_t)Kd, act, h, (uint32_t *)ctx->ids.p,
-                                                            (float *)ctx->w.p, ctx->stream),
-                       "expert_gate_up_routed");
+        rc = gate_up_routed_dev(ctx, GU, moe_in, k, norm, d_expert, (uint32_t)Kd, act, h);
     } else {
         if ((rc = router_dev(ctx, R, rin, nullptr, k, flags, nullptr, fuse_prep ? &prep : nullptr))) return rc;
         rc = gate_up_dev(ctx, GU, moe_in, (const uint32_t *)ctx->ids.p, k, d_expert, (uint32_t)Kd, act, h);

@@ -27,6 +27,7 @@
 // not bit-exact.
 #include "llmtoy_hip.h"
 #include "lt_limbs.h"
+#include "lt_topk.h"
 
 namespace lt {
 
@@ -309,21 +310,50 @@ __global__ __launch_bounds__(64 * kFmtWaves) void k_matvec_fmt(DevTensor W, cons
     }
 }
 
+// Routing done by the gate/up blocks themselves (ROUTE = PER > 0): wave 0 of
+// every block runs softmax + top-k over the router logits (PER per lane)
+// while the block stages x, and block (0, 0) publishes the selection for
+// the down kernel -- instead of the router's last block doing it behind an
+// arrival ticket and two fences.
+struct FmtRoute {
+    const float *logits;  // [n_experts]
+    int k;
+    int norm;
+    uint32_t *ids_out;    // [k]
+    float *w_out;         // [k]
+};
+
 // Expert-indexed gate/up (ops/moe.zig:55-73): slot s = blockIdx.y, expert
-// e = ids[s]; row pair j = (gate row e 2F + j, up row e 2F + F + j);
-// h[s][j] = act(gate . x) * (up . x), h[s][F, down_cols) = 0.  A lane group
-// takes R row pairs at a time (one x load per unit for 2 R rows); waves walk
-// the row pairs of their slot with a stride of gridDim.x * kFmtWaves * RPW * R.
-template <int T, int RPW, int R>
+// e = ids[s] (or the block's own selection); row pair j = (gate row e 2F +
+// j, up row e 2F + F + j); h[s][j] = act(gate . x) * (up . x), h[s][F,
+// down_cols) = 0.  A lane group takes R row pairs at a time (one x load per
+// unit for 2 R rows); waves walk the row pairs of their slot with a stride
+// of gridDim.x * kFmtWaves * RPW * R.
+template <int T, int RPW, int R, int ROUTE>
 __global__ __launch_bounds__(64 * kFmtWaves) void k_expert_gu_fmt(DevTensor W, const float *__restrict__ x,
                                                                   const uint32_t *__restrict__ ids, int F,
-                                                                  int down_cols, uint32_t act, float *__restrict__ h) {
+                                                                  int down_cols, uint32_t act, float *__restrict__ h,
+                                                                  FmtRoute ra) {
     extern __shared__ __attribute__((aligned(16))) uint32_t xl[];  // x as limbs (lds_bytes(cols))
     constexpr int LPR = kWave / RPW;
-    stage_limbs(xl, x, (int)W.cols);
-    const LimbView xv = limb_view(xl, (int)W.cols);
     const int s = blockIdx.y;
-    const uint32_t e = __builtin_amdgcn_readfirstlane(ids[s]);
+    uint32_t e;
+    if constexpr (ROUTE > 0) {
+        __shared__ uint32_t s_ids[16];
+        __shared__ float s_w[16];
+        if (threadIdx.x < kWave)
+            topk_softmax_wave<ROUTE>(ra.logits, (int)W.n_experts, ra.k, ra.norm, s_ids, s_w, nullptr, threadIdx.x);
+        stage_limbs(xl, x, (int)W.cols);  // (its barrier also publishes s_ids / s_w)
+        if (blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < ra.k) {
+            ra.ids_out[threadIdx.x] = s_ids[threadIdx.x];
+            ra.w_out[threadIdx.x] = s_w[threadIdx.x];
+        }
+        e = __builtin_amdgcn_readfirstlane(s_ids[s]);
+    } else {
+        stage_limbs(xl, x, (int)W.cols);
+        e = __builtin_amdgcn_readfirstlane(ids[s]);
+    }
+    const LimbView xv = limb_view(xl, (int)W.cols);
     float *hs = h + (size_t)s * down_cols;
     if (blockIdx.x == 0)
         for (int j = F + threadIdx.x; j < down_cols; j += blockDim.x) hs[j] = 0.f;
@@ -464,18 +494,18 @@ hipError_t launch_mv(const DevTensor &W, const float *x, float *y, hipStream_t s
     return hipGetLastError();
 }
 
-template <int T, int RPW>
+template <int T, int RPW, int ROUTE>
 hipError_t launch_gu(const DevTensor &W, const float *x, const uint32_t *ids, int k, int F, int down_cols,
-                     uint32_t act, float *h, hipStream_t s) {
+                     uint32_t act, float *h, const FmtRoute &ra, hipStream_t s) {
     constexpr int R = kGuPairs<T>;
     static bool set[64] = {};
-    hipError_t e = allow_lds((const void *)k_expert_gu_fmt<T, RPW, R>, set);
+    hipError_t e = allow_lds((const void *)k_expert_gu_fmt<T, RPW, R, ROUTE>, set);
     if (e != hipSuccess) return e;
     const int per = kFmtWaves * RPW * R;
     const int need = (F + per - 1) / per;
     const dim3 grid((unsigned)(need < 128 ? need : 128), (unsigned)k);  // up to 128 x k workgroups walk the rows
-    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW, R>), grid, dim3(64 * kFmtWaves),
-                       lds_bytes(W.cols), s, W, x, ids, F, down_cols, act, h);
+    hipLaunchKernelGGL((k_expert_gu_fmt<T, RPW, R, ROUTE>), grid, dim3(64 * kFmtWaves),
+                       lds_bytes(W.cols), s, W, x, ids, F, down_cols, act, h, ra);
     return hipGetLastError();
 }
 
@@ -504,14 +534,37 @@ hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s)
     }
 }
 
+template <int T, int ROUTE>
+hipError_t launch_gu_r(const DevTensor &W, const float *x, const uint32_t *ids, int k, int F, int down_cols,
+                       uint32_t act, float *h, const FmtRoute &ra, hipStream_t s) {
+    switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
+    case 1: return launch_gu<T, 1, ROUTE>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    case 2: return launch_gu<T, 2, ROUTE>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    case 4: return launch_gu<T, 4, ROUTE>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    default: return launch_gu<T, 8, ROUTE>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    }
+}
+
 template <int T>
 hipError_t launch_gu_t(const DevTensor &W, const float *x, const uint32_t *ids, int k, int F, int down_cols,
-                       uint32_t act, float *h, hipStream_t s) {
-    switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
-    case 1: return launch_gu<T, 1>(W, x, ids, k, F, down_cols, act, h, s);
-    case 2: return launch_gu<T, 2>(W, x, ids, k, F, down_cols, act, h, s);
-    case 4: return launch_gu<T, 4>(W, x, ids, k, F, down_cols, act, h, s);
-    default: return launch_gu<T, 8>(W, x, ids, k, F, down_cols, act, h, s);
+                       uint32_t act, float *h, const FmtRoute &ra, hipStream_t s) {
+    if (!ra.logits) return launch_gu_r<T, 0>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    const int E = (int)W.n_experts;
+    if (E <= 64) return launch_gu_r<T, 1>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    if (E <= 128) return launch_gu_r<T, 2>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    if (E <= 256) return launch_gu_r<T, 4>(W, x, ids, k, F, down_cols, act, h, ra, s);
+    return hipErrorInvalidValue;  // more experts: the caller uses the router's top-k
+}
+
+hipError_t launch_gu_any(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k, uint32_t d_expert,
+                         uint32_t down_cols, uint32_t act, float *h, const FmtRoute &ra, hipStream_t s) {
+    const int K = (int)k, F = (int)d_expert, Kd = (int)down_cols;
+    switch (GU.type) {
+    case LT_TYPE_Q5_0: return launch_gu_t<LT_TYPE_Q5_0>(GU, x, ids, K, F, Kd, act, h, ra, s);
+    case LT_TYPE_Q5_1: return launch_gu_t<LT_TYPE_Q5_1>(GU, x, ids, K, F, Kd, act, h, ra, s);
+    case LT_TYPE_IQ4_NL: return launch_gu_t<LT_TYPE_IQ4_NL>(GU, x, ids, K, F, Kd, act, h, ra, s);
+    case LT_TYPE_Q3_K: return launch_gu_t<LT_TYPE_Q3_K>(GU, x, ids, K, F, Kd, act, h, ra, s);
+    default: return hipErrorInvalidValue;
     }
 }
 
@@ -541,14 +594,15 @@ hipError_t launch_matvec_fmt(const DevTensor &W, const float *x, float *y, hipSt
 
 hipError_t launch_expert_gate_up_fmt(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, hipStream_t s) {
-    const int K = (int)k, F = (int)d_expert, Kd = (int)down_cols;
-    switch (GU.type) {
-    case LT_TYPE_Q5_0: return launch_gu_t<LT_TYPE_Q5_0>(GU, x, ids, K, F, Kd, act, h, s);
-    case LT_TYPE_Q5_1: return launch_gu_t<LT_TYPE_Q5_1>(GU, x, ids, K, F, Kd, act, h, s);
-    case LT_TYPE_IQ4_NL: return launch_gu_t<LT_TYPE_IQ4_NL>(GU, x, ids, K, F, Kd, act, h, s);
-    case LT_TYPE_Q3_K: return launch_gu_t<LT_TYPE_Q3_K>(GU, x, ids, K, F, Kd, act, h, s);
-    default: return hipErrorInvalidValue;
-    }
+    const FmtRoute none{nullptr, 0, 0, nullptr, nullptr};
+    return launch_gu_any(GU, x, ids, k, d_expert, down_cols, act, h, none, s);
+}
+
+hipError_t launch_expert_gate_up_fmt_routed(const DevTensor &GU, const float *x, const float *logits, uint32_t k,
+                                            uint32_t norm, uint32_t d_expert, uint32_t down_cols, uint32_t act,
+                                            float *h, uint32_t *ids_out, float *w_out, hipStream_t s) {
+    const FmtRoute ra{logits, (int)k, (int)norm, ids_out, w_out};
+    return launch_gu_any(GU, x, nullptr, k, d_expert, down_cols, act, h, ra, s);
 }
 
 hipError_t launch_expert_down_fmt(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,

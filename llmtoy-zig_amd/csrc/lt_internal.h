@@ -371,6 +371,12 @@ hipError_t launch_matvec_fmt(const DevTensor &W, const float *x, float *y, hipSt
 // down staging needs k * down_cols * 4 <= 64 KiB, x rows <= 16384 floats.
 hipError_t launch_expert_gate_up_fmt(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h, hipStream_t s);
+// The same, routing for itself: every block runs softmax + top-k over the
+// router logits (n_experts <= 256) and block (0, 0) writes the selection to
+// ids_out / w_out for the down kernel.
+hipError_t launch_expert_gate_up_fmt_routed(const DevTensor &GU, const float *x, const float *logits, uint32_t k,
+                                            uint32_t norm, uint32_t d_expert, uint32_t down_cols, uint32_t act,
+                                            float *h, uint32_t *ids_out, float *w_out, hipStream_t s);
 hipError_t launch_expert_down_fmt(const DevTensor &D, const float *h, const uint32_t *ids, const float *w,
                                   uint32_t k, const float *base, int accumulate, const float *dscale, float *out,
                                   hipStream_t s);
