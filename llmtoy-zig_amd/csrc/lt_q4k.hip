@@ -234,8 +234,8 @@ __global__ void __launch_bounds__(256, q4k_stream_waves(ND)) k_matvec_q4k_stream
         }
         return acc;
     };
-    // loads stay unconditional (clamped rows); the math of a slab past the
-    // last row is skipped (wave-uniform branch)
+    // a slab past the last row is neither reloaded nor computed (wave-uniform
+    // branches; a wave's last reloads would only delay its end)
     if constexpr (LPR == 64) {
         // one row per slab: the ND slabs' row sums in one transposed
         // reduction, lane 64 i / ND storing slab i's row
@@ -245,7 +245,7 @@ __global__ void __launch_bounds__(256, q4k_stream_waves(ND)) k_matvec_q4k_stream
 #pragma unroll
             for (int i = 0; i < ND; i++) {
                 acc[i] = (i == 0 || base + i * stride < nrows) ? lane_dot(w[i]) : 0.f;
-                ld(w[i], base + (i + ND) * stride);
+                if (base + (i + ND) * stride < nrows) ld(w[i], base + (i + ND) * stride);
             }
             const float t = wave_sum_transposed<ND>(acc, lane, first);
             const int row = base + (lane >> SH) * stride;
@@ -260,7 +260,7 @@ __global__ void __launch_bounds__(256, q4k_stream_waves(ND)) k_matvec_q4k_stream
                     const int row = base + i * stride + rs;
                     if (l == 0 && row < nrows) y[row] = v;
                 }
-                ld(w[i], base + (i + ND) * stride);
+                if (base + (i + ND) * stride < nrows) ld(w[i], base + (i + ND) * stride);
             }
         }
     }
@@ -271,8 +271,9 @@ static hipError_t launch_q4k_stream(const DevTensor &W, size_t row0, size_t nrow
                                     hipStream_t s) {
     constexpr int LPR = 4 * NSB < 64 ? 4 * NSB : 64, RPS = 64 / LPR;
     const size_t slabs = (nrows + RPS - 1) / RPS;
-    // Small matrices: two slabs per wave, both in flight from the start
-    // (one slab per wave made config 2, 4096 rows, 7.3 us instead of 5.6).
+    // Small matrices: four slabs per wave, all in flight from the start
+    // (config 2, 4096 rows: 4.49 us per launch; two slabs per wave on twice
+    // the workgroups 4.59, one slab per wave 7.3 with an older kernel).
     // Large ones: every workgroup resident (256 CUs x its waves per SIMD)
     // with kQ4StreamND slabs in flight per wave.
     constexpr size_t nblk_big = (size_t)256 * q4k_stream_waves(kQ4StreamND);
@@ -280,10 +281,10 @@ static hipError_t launch_q4k_stream(const DevTensor &W, size_t row0, size_t nrow
         hipLaunchKernelGGL((k_matvec_q4k_stream<NSB, kQ4StreamND>), dim3((unsigned)nblk_big), dim3(256), 0, s, W.p0,
                            W.p1, x, y, (int)row0, (int)nrows);
     } else {
-        constexpr size_t cap2 = (size_t)256 * q4k_stream_waves(2);
-        size_t nblk = (slabs + 7) / 8;
-        if (nblk > cap2) nblk = cap2;
-        hipLaunchKernelGGL((k_matvec_q4k_stream<NSB, 2>), dim3((unsigned)nblk), dim3(256), 0, s, W.p0, W.p1, x, y,
+        constexpr size_t cap = (size_t)256 * q4k_stream_waves(4);
+        size_t nblk = (slabs + 15) / 16;
+        if (nblk > cap) nblk = cap;
+        hipLaunchKernelGGL((k_matvec_q4k_stream<NSB, 4>), dim3((unsigned)nblk), dim3(256), 0, s, W.p0, W.p1, x, y,
                            (int)row0, (int)nrows);
     }
     return hipGetLastError();
