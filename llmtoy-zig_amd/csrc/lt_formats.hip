@@ -524,8 +524,132 @@ hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, co
     return hipGetLastError();
 }
 
+// Streaming Q3_K matvec for rows of NSB = 1, 2, 4, 8 or 16 super-blocks.  A
+// lane owns quant chunk j (qs bytes 16 j .. 16 j + 15: half h = j / 2,
+// 16-element run g = j % 2, all four bit pairs) of one super-block and the
+// hmask bytes 16 g .. 16 g + 15 those elements need; lanes 0-2 of the
+// aligned quad load scale dwords 0-2 and lane 3 the f16 d, shared over DPP.
+// Per 64 weights that is two 16-byte loads and one small one, where the
+// unit kernel above loads 20 dwords per 32 weights.  The lane's four limb
+// groups (16 sb + 8 h + 2 jp + g, jp = bit pair) stay in registers; each
+// wave keeps ND row slabs in flight (as k_matvec_q4k_stream).
+template <int NSB, int ND>
+__global__ void __launch_bounds__(256, 4) k_matvec_q3k_stream(DevTensor W, const float *x, float *y) {
+    constexpr int LPR = 4 * NSB, RPS = 64 / LPR;
+    __shared__ uint32_t la[64 * NSB], lb[64 * NSB];
+    __shared__ float lsp[16 * NSB], lxs[16 * NSB];
+    const int nrows = (int)W.total_rows;
+    const int lane = threadIdx.x & 63;
+    const int l = lane % LPR, rs = lane / LPR;
+    const int sb = l >> 2, j = l & 3, h = j >> 1, g = j & 1;
+    const int stride = gridDim.x * 4 * RPS;
+    int base = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPS;
+    const bool first = p32_first(lane);
+    struct Regs {
+        uint4 q, m;
+        uint32_t hd;
+    };
+    auto ld = [&](Regs &w, int rb) {
+        int row = rb + rs;
+        row = row < nrows ? row : nrows - 1;
+        const size_t blk = (size_t)row * NSB + sb;
+        w.q = ldg16(W.p0 + blk * 64 + 16 * j);
+        w.m = ldg16(W.p1 + blk * 32 + 16 * g);
+        w.hd = j < 3 ? *reinterpret_cast<const uint32_t *>(W.p2 + blk * 12 + 4 * j)
+                     : (uint32_t)*reinterpret_cast<const uint16_t *>(W.p3 + blk * 2);
+    };
+    float xv[16];
+    stage_x_load(x, 256 * NSB, xv);  // x first: its wait does not include the weights
+    asm volatile("" ::: "memory");  // keep the x loads ahead of the weight loads
+    Regs w[ND];
+#pragma unroll
+    for (int i = 0; i < ND; i++) ld(w[i], base + i * stride);
+    __builtin_amdgcn_sched_barrier(0);  // the weight loads issued before the conversion
+    stage_limbs_store(xv, 256 * NSB, la, lb, lsp, lxs);
+    uint32_t xa[4][4], xb[4][4];
+    float xsp[4], xsum[4];
+#pragma unroll
+    for (int jp = 0; jp < 4; jp++) {
+        const int gi = 16 * sb + 8 * h + 2 * jp + g;
+        read_group_limbs(la, lb, gi, xa[jp], xb[jp]);
+        xsp[jp] = lsp[gi];
+        xsum[jp] = lxs[gi];
+    }
+    auto lane_dot = [&](const Regs &r) {
+        const uint32_t s0 = quad_bcast<0x00>(r.hd), s1 = quad_bcast<0x55>(r.hd), s2 = quad_bcast<0xAA>(r.hd);
+        const float d = f16_bits_to_f32(quad_bcast<0xFF>(r.hd) & 0xffffu);
+        const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, mw[4] = {r.m.x, r.m.y, r.m.z, r.m.w};
+        float acc = 0.f;
+#pragma unroll
+        for (int jp = 0; jp < 4; jp++) {
+            uint32_t c[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                c[m] = ((qw[m] >> (2 * jp)) & 0x03030303u) | (((mw[m] >> (jp + 4 * h)) & 0x01010101u) << 2);
+            int A = sdot4_first((int)c[0], (int)xa[jp][0]);
+            int B = sdot4_first((int)c[0], (int)xb[jp][0]);
+#pragma unroll
+            for (int m = 1; m < 4; m++) {
+                A = __builtin_amdgcn_sdot4((int)c[m], (int)xa[jp][m], A, false);
+                B = __builtin_amdgcn_sdot4((int)c[m], (int)xb[jp][m], B, false);
+            }
+            const float dot = xsp[jp] * (float)((A << 8) + B);
+            const int sc = q3k_scale(s0, s1, s2, 8 * h + 2 * jp + g);
+            acc += (d * (float)(sc - 32)) * (dot - 4.f * xsum[jp]);
+        }
+        return acc;
+    };
+    // a slab past the last row is neither reloaded nor computed
+    if constexpr (LPR == 64) {
+        constexpr int SH = ND == 2 ? 5 : ND == 4 ? 4 : 3;
+        for (; base < nrows; base += ND * stride) {
+            float acc[ND];
+#pragma unroll
+            for (int i = 0; i < ND; i++) {
+                acc[i] = (i == 0 || base + i * stride < nrows) ? lane_dot(w[i]) : 0.f;
+                if (base + (i + ND) * stride < nrows) ld(w[i], base + (i + ND) * stride);
+            }
+            const float t = wave_sum_transposed<ND>(acc, lane, first);
+            const int row = base + (lane >> SH) * stride;
+            if ((lane & ((1 << SH) - 1)) == 0 && row < nrows) y[row] = t;
+        }
+    } else {
+        for (; base < nrows; base += ND * stride) {
+#pragma unroll
+            for (int i = 0; i < ND; i++) {
+                if (i == 0 || base + i * stride < nrows) {
+                    const float v = group_sum_dpp<LPR>(lane_dot(w[i]), first);
+                    const int row = base + i * stride + rs;
+                    if (l == 0 && row < nrows) y[row] = v;
+                }
+                if (base + (i + ND) * stride < nrows) ld(w[i], base + (i + ND) * stride);
+            }
+        }
+    }
+}
+
+template <int NSB>
+hipError_t launch_q3k_stream(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    constexpr int RPS = 64 / (4 * NSB);
+    const size_t slabs = (W.total_rows + RPS - 1) / RPS;
+    size_t nblk = (slabs + 15) / 16;  // four slabs per wave
+    if (nblk > (size_t)kStreamBlocks) nblk = kStreamBlocks;
+    hipLaunchKernelGGL((k_matvec_q3k_stream<NSB, 4>), dim3((unsigned)nblk), dim3(256), 0, s, W, x, y);
+    return hipGetLastError();
+}
+
 template <int T>
 hipError_t launch_t(const DevTensor &W, const float *x, float *y, hipStream_t s) {
+    if constexpr (T == LT_TYPE_Q3_K) {
+        switch (W.cols == 256 * W.blocks_per_row ? W.blocks_per_row : 0) {
+        case 1: return launch_q3k_stream<1>(W, x, y, s);
+        case 2: return launch_q3k_stream<2>(W, x, y, s);
+        case 4: return launch_q3k_stream<4>(W, x, y, s);
+        case 8: return launch_q3k_stream<8>(W, x, y, s);
+        case 16: return launch_q3k_stream<16>(W, x, y, s);
+        default: break;
+        }
+    }
     switch (pick_rpw(T == LT_TYPE_Q3_K ? 8 * W.blocks_per_row : W.blocks_per_row)) {
     case 1: return launch_mv<T, 1>(W, x, y, s);
     case 2: return launch_mv<T, 2>(W, x, y, s);

@@ -33,6 +33,22 @@ def test_gpu_matvec_formats(ctx, gtype, rows, cols):
     assert max_rel(y, ref) < 1e-4
 
 
+# The streaming Q3_K kernel (rows of 1, 2, 4, 8 or 16 super-blocks): ragged
+# slabs, and a matrix large enough that waves loop over several slab sets.
+@pytest.mark.parametrize("rows,cols", [(29, 512), (41, 1024), (19, 2048), (1025, 256), (20000, 4096)])
+def test_gpu_matvec_q3k_stream(ctx, rows, cols):
+    g = np.random.default_rng(rows + 3 * cols)
+    m = synth.quant_matrix(g, ggml.Q3_K, rows, cols)
+    x = ((g.random(cols, dtype=np.float32) - 0.5) * 2).astype(np.float32)
+    print(f"matvec Q3_K stream {rows}x{cols}", flush=True)
+    t = ctx.upload(m, ggml.Q3_K, rows, cols)
+    y = np.zeros(rows, np.float32)
+    ctx.quant_matvec(y, t, x)
+    t.free()
+    ref = orc.quant_matvec(m, ggml.Q3_K, x, rows, cols)
+    assert max_rel(y, ref) < 1e-4
+
+
 @pytest.mark.parametrize("gtype", FMTS)
 def test_gpu_formats_expert_layout_and_large_upload(ctx, gtype):
     # 3-D expert tensors upload as one flat matrix (gemma4/loader.zig:277-292);
