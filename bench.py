@@ -862,7 +862,10 @@ def bench_gemma4(args):
     log(f"gemma4 block: {us:.2f} us/token wall, {dev_us:.2f} us/token device, {gbps:.0f} GB/s")
     result = base_record(
         args, "Gemma4 MoE block decode us/token (config-4 layer + router-input prep + MoE tail)", round(us, 3),
-        "us/token", steps, False, "expert weights x fp32 activations in int8-limb pairs (v_dot4), Q8_0 router x fp32 activations; fp32 norms",
+        "us/token", steps, False,
+        ("expert weights x fp32 activations in int8-limb pairs (v_dot4)" if args.apex else
+         "Q4_K gate/up x fp32 activations in int8-limb pairs (v_dot4), Q4_K down x fp32 h")
+        + ", Q8_0 router x fp32 activations; fp32 accumulation and norms",
         {"workload": "gemma4_moe_block_cfg4", "d_model": G4_D, "n_experts": G4_E, "d_expert": G4_F,
          "down_cols": w.down_cols, "top_k": K, "router": "Q8_0",
          "experts": f"{ggml.NAMES[w.gate_up_type]} gate/up, {ggml.NAMES[w.down_type]} down",

@@ -91,6 +91,46 @@ __device__ __forceinline__ float q4k_chunk_dot(uint4 hdr, uint4 q, int cc, const
     return ((d * sc0) * dl - (dmin * mn0) * xc.slo) + ((d * sc1) * dh - (dmin * mn1) * xc.shi);
 }
 
+// The limbs of one chunk's activations (lt_limbs.h): group 0 = the 16
+// low-nibble partners, group 1 = the 16 high-nibble partners.
+struct ChunkLimbs {
+    uint32_t a[2][4], b[2][4];
+    float sp[2], xs[2];
+};
+
+// q4k_chunk_dot against int8-limb activations: the nibbles meet both limbs
+// in v_dot4 (exact int32 sums per 16-element group), then the group scales.
+__device__ __forceinline__ float q4k_chunk_dot_limbs(uint4 hdr, uint4 q, int cc, const ChunkLimbs &x) {
+    const float d = f16_bits_to_f32(hdr.x);
+    const float dmin = f16_bits_to_f32(hdr.x >> 16);
+    const int p = cc >> 1;
+    const int sh = (p & 1) * 16;
+    const uint32_t ys = hdr.y >> sh, zs = hdr.z >> sh, ws = hdr.w >> sh;
+    const uint32_t scp = opaque(p < 2 ? (ys & 0x3f3fu) : ((ws & 0x0f0fu) | ((ys >> 2) & 0x3030u)));
+    const uint32_t mnp = opaque(p < 2 ? (zs & 0x3f3fu) : (((ws >> 4) & 0x0f0fu) | ((zs >> 2) & 0x3030u)));
+    const float sc0 = (float)(scp & 0xffu), sc1 = (float)((scp >> 8) & 0xffu);
+    const float mn0 = (float)(mnp & 0xffu), mn1 = (float)((mnp >> 8) & 0xffu);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    int A0 = 0, B0 = 0, A1 = 0, B1 = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int lo = (int)(w[t] & 0x0f0f0f0fu), hi = (int)((w[t] >> 4) & 0x0f0f0f0fu);
+        if (t == 0) {
+            A0 = sdot4_first(lo, (int)x.a[0][0]);
+            B0 = sdot4_first(lo, (int)x.b[0][0]);
+            A1 = sdot4_first(hi, (int)x.a[1][0]);
+            B1 = sdot4_first(hi, (int)x.b[1][0]);
+        } else {
+            A0 = __builtin_amdgcn_sdot4(lo, (int)x.a[0][t], A0, false);
+            B0 = __builtin_amdgcn_sdot4(lo, (int)x.b[0][t], B0, false);
+            A1 = __builtin_amdgcn_sdot4(hi, (int)x.a[1][t], A1, false);
+            B1 = __builtin_amdgcn_sdot4(hi, (int)x.b[1][t], B1, false);
+        }
+    }
+    const float dl = x.sp[0] * (float)((A0 << 8) + B0), dh = x.sp[1] * (float)((A1 << 8) + B1);
+    return ((d * sc0) * dl - (dmin * mn0) * x.xs[0]) + ((d * sc1) * dh - (dmin * mn1) * x.xs[1]);
+}
+
 // Stage x[0..n) into LDS with 16-byte loads (n % 4 == 0).
 __device__ __forceinline__ void stage_x(float *xs, const float *x, int n) {
     for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4)
@@ -363,11 +403,22 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int jbase = (blockIdx.x * WPB + wave) * R;
     const int nch = nsb * 8;
-    // x first (L2-resident), so its latency overlaps the routing below
-    XChunk xc[CPL];
+    const int ng = nsb * 16;  // 16-element groups of x
+    // x first (L2-resident), so its latency overlaps the routing below:
+    // thread t holds groups t and t + 256 (nsb <= 32), converted to int8
+    // limbs in LDS once the weight loads are out
+    __shared__ uint32_t la[32 * 64], lb[32 * 64];
+    __shared__ float lsp[32 * 16], lxs[32 * 16];
+    float xv[2][16];
 #pragma unroll
-    for (int i = 0; i < CPL; i++)
-        if (lane + kWave * i < nch) load_xchunk(x, (lane + kWave * i) >> 3, (lane + kWave * i) & 7, xc[i]);
+    for (int u = 0; u < 2; u++) {
+        const int gi = min((int)threadIdx.x + 256 * u, ng - 1);
+#pragma unroll
+        for (int t = 0; t < 16; t += 4) {
+            const float4 f = ldg16f(x + 16 * gi + t);
+            xv[u][t] = f.x; xv[u][t + 1] = f.y; xv[u][t + 2] = f.z; xv[u][t + 3] = f.w;
+        }
+    }
     uint32_t e;
     if constexpr (ROUTE > 0) {
         __shared__ uint32_t s_ids[16];
@@ -410,7 +461,33 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
         }
     }
 #pragma unroll
-    for (int i = 0; i < CPL; i++) sum_xchunk(xc[i]);
+    for (int u = 0; u < 2; u++) {
+        const int gi = (int)threadIdx.x + 256 * u;
+        if (gi < ng) {
+            uint32_t a4[4], b4[4];
+            float sp, xs;
+            limbs16(xv[u], a4, b4, sp, xs);
+            *reinterpret_cast<uint4 *>(la + 4 * gi) = make_uint4(a4[0], a4[1], a4[2], a4[3]);
+            *reinterpret_cast<uint4 *>(lb + 4 * gi) = make_uint4(b4[0], b4[1], b4[2], b4[3]);
+            lsp[gi] = sp;
+            lxs[gi] = xs;
+        }
+    }
+    __syncthreads();
+    // chunk c = 8 sb + cc: low nibbles meet group 16 sb + 4 (cc / 2) + cc % 2,
+    // high nibbles that group + 2
+    ChunkLimbs xc[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = min(lane + kWave * i, nch - 1);
+        const int g0 = 16 * (c >> 3) + 4 * ((c & 7) >> 1) + (c & 1);
+#pragma unroll
+        for (int h2 = 0; h2 < 2; h2++) {
+            read_group_limbs(la, lb, g0 + 2 * h2, xc[i].a[h2], xc[i].b[h2]);
+            xc[i].sp[h2] = lsp[g0 + 2 * h2];
+            xc[i].xs[h2] = lxs[g0 + 2 * h2];
+        }
+    }
     float ag[R], au[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -419,8 +496,8 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
         for (int i = 0; i < CPL; i++) {
             const int c = lane + kWave * i;
             if (c < nch && jbase + r < F) {
-                ag[r] += q4k_chunk_dot(hg[r][i], qg[r][i], c & 7, xc[i]);
-                au[r] += q4k_chunk_dot(hu[r][i], qu[r][i], c & 7, xc[i]);
+                ag[r] += q4k_chunk_dot_limbs(hg[r][i], qg[r][i], c & 7, xc[i]);
+                au[r] += q4k_chunk_dot_limbs(hu[r][i], qu[r][i], c & 7, xc[i]);
             }
         }
     }
