@@ -793,7 +793,13 @@ def bench_prefill(args):
         {"workload": "qwen3_moe_prefill_cfg5", "tokens": 512, "d_model": D, "n_experts": E, "d_expert": F,
          "top_k": K, "router_bias": "zipf(1.1)", "graph_steps": 16},
         {"ms_per_step": round(us / 1e3, 4), "us_per_call": round(us, 2), "device_us_per_call": round(dev_us, 2),
-         "achieved_tflops": round(PREFILL_FLOP / (us * 1e-6) / 1e12, 2), "parity": parity})
+         "achieved_tflops": round(PREFILL_FLOP / (us * 1e-6) / 1e12, 2),
+         "roofline": {"bound": "mfma", "achieved": round(PREFILL_FLOP / (dev_us * 1e-6) / 1e12, 2),
+                      "peak": 2500.0, "unit": "TFLOP/s",
+                      "frac": round(PREFILL_FLOP / (dev_us * 1e-6) / 1e12 / 2500.0, 4), "traffic": None,
+                      "kernel": "whole prefill call (device time per call; f16 dense MFMA peak)",
+                      "algorithmic_flops": PREFILL_FLOP},
+         "parity": parity})
     if args.calibrate:
         calibrate_copy(ctx)
     print(json.dumps(result), flush=True)
