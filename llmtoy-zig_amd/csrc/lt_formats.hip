@@ -536,8 +536,8 @@ hipError_t launch_dn(const DevTensor &W, const float *h, const uint32_t *ids, co
 template <int NSB, int ND>
 __global__ void __launch_bounds__(256, 4) k_matvec_q3k_stream(DevTensor W, const float *x, float *y) {
     constexpr int LPR = 4 * NSB, RPS = 64 / LPR;
-    __shared__ uint32_t la[64 * NSB], lb[64 * NSB];
-    __shared__ float lsp[16 * NSB], lxs[16 * NSB];
+    __shared__ __attribute__((aligned(16))) uint32_t la[64 * NSB], lb[64 * NSB];
+    __shared__ __attribute__((aligned(16))) float lsp[16 * NSB], lxs[16 * NSB];
     const int nrows = (int)W.total_rows;
     const int lane = threadIdx.x & 63;
     const int l = lane % LPR, rs = lane / LPR;
