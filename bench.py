@@ -177,6 +177,10 @@ class Timer:
         return us
 
 
+def rnd(v, n=3):
+    return None if v is None else round(v, n)
+
+
 def timed_steps(args) -> int:
     return max(args.steps or 0, MIN_TIMED_STEPS)
 
@@ -361,8 +365,10 @@ def bench_decode(args):
     n_steps = timed_steps(args)
     us_per_token, dev_us, steps = timer.graph_steps(step, n_steps, G)
     log(f"graph replay ({steps} steps): {us_per_token:.3f} us/token wall, {dev_us:.3f} us/token device")
-    det_us, det_dev_us, _ = timer.graph_steps(lambda i: step(i, True), n_steps, G)
-    log(f"deterministic (slot-order combine): {det_us:.3f} us/token wall, {det_dev_us:.3f} device")
+    det_us = det_dev_us = None
+    if not args.atomic_only:
+        det_us, det_dev_us, _ = timer.graph_steps(lambda i: step(i, True), n_steps, G)
+        log(f"deterministic (slot-order combine): {det_us:.3f} us/token wall, {det_dev_us:.3f} device")
 
     # ---- per-kernel launch durations
     ids_pool = []
@@ -390,11 +396,11 @@ def bench_decode(args):
         ctx.router_topk(r, X.row(i % args.xpool), K, dids, dw, norm_topk=True)
 
     fu_mean = timer.launches(step, args.kernel_iters)
-    fu_det_mean = timer.launches(lambda i: step(i, True), args.kernel_iters)
+    fu_det_mean = None if args.atomic_only else timer.launches(lambda i: step(i, True), args.kernel_iters)
     gu_mean = timer.launches(gu, args.kernel_iters)
     dn_mean = timer.launches(dn, args.kernel_iters)
     rt_mean = timer.launches(rt, args.kernel_iters)
-    log(f"fused layer kernel {fu_mean:.2f} us per launch ({fu_det_mean:.2f} deterministic); three-launch path "
+    log(f"fused layer kernel {fu_mean:.2f} us per launch ({fu_det_mean} deterministic); three-launch path "
         f"kernels alone: gate/up {gu_mean:.2f} us, down {dn_mean:.2f} us, router+topk {rt_mean:.2f} us")
 
     layer_gbps = SELECTED_BYTES / (us_per_token * 1e-6) / 1e9
@@ -408,11 +414,11 @@ def bench_decode(args):
          "hbm_frac_selected_experts": round(layer_gbps / PEAK_GBPS, 4),
          "achieved_gbps_full_layer": round(LAYER_BYTES / (us_per_token * 1e-6) / 1e9, 1),
          "device_us_per_step": round(dev_us, 3),
-         "deterministic_us_per_token": round(det_us, 3),
-         "deterministic_device_us_per_token": round(det_dev_us, 3),
+         "deterministic_us_per_token": rnd(det_us),
+         "deterministic_device_us_per_token": rnd(det_dev_us),
          "eager_us_per_token": round(eager_us, 3),
          "host_io_us_per_token": round(host_io_us, 3),
-         "kernel_us": {"moe_fused": round(fu_mean, 3), "moe_fused_deterministic": round(fu_det_mean, 3)},
+         "kernel_us": {"moe_fused": round(fu_mean, 3), "moe_fused_deterministic": rnd(fu_det_mean)},
          "unfused_kernel_us": {"router_topk": round(rt_mean, 3), "expert_gate_up": round(gu_mean, 3),
                                "expert_down": round(dn_mean, 3)},
          "unfused_kernel_gbps": {"expert_gate_up": round(GATE_UP_BYTES / (gu_mean * 1e-6) / 1e9, 1),
@@ -461,7 +467,7 @@ def timeline_report(args, w, xs, n=200):
         ctx.moe_forward(out, X.row(i % len(xs)), *copies[i % args.copies], K, F, norm_topk=True)
         ctx.sync()
     rep = ctx.profile_report()
-    head = (f"Command (GPU box, repo root): python bench.py --no-cpu --no-gguf --timeline {args.timeline}\n"
+    head = (f"Command (GPU box, repo root): python3 {' '.join(sys.argv)}\n"
             f"Workload: config-3 decode layer, {n} eager launches, {args.copies} weight copies rotated, "
             f"x pool of {len(xs)}; LT_PROFILE=timeline adds one store per workgroup at its end.\n\n")
     with open(args.timeline, "w") as f:
@@ -678,9 +684,11 @@ def bench_cfg4(args):
         G *= 2
     n_steps = timed_steps(args)
     us, dev_us, steps = timer.graph_steps(step, n_steps, G)
-    det_us, det_dev_us, _ = timer.graph_steps(lambda i: step(i, True), n_steps, G)
+    det_us = det_dev_us = None
+    if not args.atomic_only:
+        det_us, det_dev_us, _ = timer.graph_steps(lambda i: step(i, True), n_steps, G)
     mean = timer.launches(step, args.kernel_iters)
-    log(f"cfg4: {us:.2f} us/token wall, {dev_us:.2f} device, {mean:.2f} per call; deterministic {det_us:.2f}")
+    log(f"cfg4: {us:.2f} us/token wall, {dev_us:.2f} device, {mean:.2f} per call; deterministic {det_us}")
     result = base_record(
         args, "Gemma4-A4B-like MoE layer decode µs/token + achieved HBM GB/s at batch 1 (config 4)", round(us, 3),
         "us/token", steps, False,
@@ -690,8 +698,8 @@ def bench_cfg4(args):
          "down_cols": G4_KD, "d_shared": S, "top_k": K, "router": "Q8_0", "shared_ffn": "Q8_0",
          "experts": "Q4_K", "act": "gelu_tanh", "norm_topk": False, "weight_copies": args.copies,
          "x_pool": args.xpool, "graph_steps": G},
-        {"device_us_per_step": round(dev_us, 3), "deterministic_us_per_token": round(det_us, 3),
-         "deterministic_device_us_per_token": round(det_dev_us, 3),
+        {"device_us_per_step": round(dev_us, 3), "deterministic_us_per_token": rnd(det_us),
+         "deterministic_device_us_per_token": rnd(det_dev_us),
          "roofline": roofline("lt_moe_forward with shared FFN (whole call)", CFG4_BYTES, mean, "moe_fused_cfg4",
                               args.kernel_iters), "parity": parity})
     if not args.no_cpu:
@@ -737,7 +745,7 @@ def timeline_cfg4(args, c, w, xs, n=200):
         ctx.moe_forward(out, X.row(i % len(xs)), *t[:3], K, G4_F, act=lt.ACT_GELU_TANH, shared=t[3:])
         ctx.sync()
     rep = ctx.profile_report()
-    head = (f"Command (GPU box, repo root): python bench.py --workload cfg4 --no-cpu --timeline {args.timeline}\n"
+    head = (f"Command (GPU box, repo root): python3 {' '.join(sys.argv)}\n"
             f"Workload: config-4 layer (shared FFN in the same launch), {n} eager launches, {args.copies} weight "
             f"copies rotated, x pool of {len(xs)}; LT_PROFILE=timeline adds one store per workgroup at its end.\n\n")
     with open(args.timeline, "w") as f:
@@ -1004,6 +1012,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF file load + upload check")
+    ap.add_argument("--atomic-only", action="store_true",
+                    help="decode, cfg4: time the default (atomic) combine only, so that a kernel trace of the run holds "
+                         "no slot-order-combine dispatches of the same kernel")
     ap.add_argument("--apex", action="store_true",
                     help="--workload gemma4 with the APEX expert formats (Q3_K gate/up, IQ4_NL down)")
     ap.add_argument("--workload", choices=["decode", "cfg1", "cfg2", "cfg2b", "cfg4", "prefill", "gemma4", "formats",

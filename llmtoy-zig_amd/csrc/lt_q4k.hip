@@ -230,8 +230,8 @@ __global__ void __launch_bounds__(256, q4k_stream_waves(ND)) k_matvec_q4k_stream
                                                                                  const float *x, float *y, int row0,
                                                                                  int nrows) {
     constexpr int PPR = 4 * NSB, LPR = PPR < 64 ? PPR : 64, UPL = PPR / LPR, RPS = 64 / LPR;
-    __shared__ uint32_t la[64 * NSB], lb[64 * NSB];
-    __shared__ float lsp[16 * NSB], lxs[16 * NSB];
+    __shared__ __attribute__((aligned(16))) uint32_t la[64 * NSB], lb[64 * NSB];
+    __shared__ __attribute__((aligned(16))) float lsp[16 * NSB], lxs[16 * NSB];
     const int lane = threadIdx.x & 63;
     const int l = lane % LPR, rs = lane / LPR;
     const int p = l & 3;  // the same pair index for every j (LPR % 4 == 0)
@@ -407,8 +407,8 @@ __global__ void __launch_bounds__(256) k_expert_gate_up_q4k(const uint8_t *__res
     // x first (L2-resident), so its latency overlaps the routing below:
     // thread t holds groups t and t + 256 (nsb <= 32), converted to int8
     // limbs in LDS once the weight loads are out
-    __shared__ uint32_t la[32 * 64], lb[32 * 64];
-    __shared__ float lsp[32 * 16], lxs[32 * 16];
+    __shared__ __attribute__((aligned(16))) uint32_t la[32 * 64], lb[32 * 64];
+    __shared__ __attribute__((aligned(16))) float lsp[32 * 16], lxs[32 * 16];
     float xv[2][16];
 #pragma unroll
     for (int u = 0; u < 2; u++) {

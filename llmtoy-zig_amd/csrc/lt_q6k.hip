@@ -202,8 +202,8 @@ __global__ void __launch_bounds__(256, q6k_stream_waves(ND)) k_matvec_q6k_stream
                                                               const uint16_t *dp, const float *x, float *y,
                                                               int nrows) {
     constexpr int LPR = 4 * NSB, RPS = 64 / LPR;
-    __shared__ uint32_t la[64 * NSB], lb[64 * NSB];
-    __shared__ float lsp[16 * NSB], lxs[16 * NSB];
+    __shared__ __attribute__((aligned(16))) uint32_t la[64 * NSB], lb[64 * NSB];
+    __shared__ __attribute__((aligned(16))) float lsp[16 * NSB], lxs[16 * NSB];
     const int lane = threadIdx.x & 63;
     const int u = lane % LPR, rs = lane / LPR;
     const int sbi = u >> 2, hf = (u >> 1) & 1, l0 = (u & 1) * 16;
