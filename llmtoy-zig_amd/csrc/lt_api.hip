@@ -38,7 +38,7 @@ struct SpanStat {
     size_t n = 0;
     double total_ms = 0, min_ms = 1e30, max_ms = 0;
 };
-constexpr int kRoles = 6, kPhases = lt::kStamps - 1;
+constexpr int kRoles = 7, kPhases = lt::kStamps - 1;
 struct Profile {
     int mode = 0;  // 0 off, 1 spans, 2 spans + timeline
     std::vector<PendingSpan> pending;
@@ -49,6 +49,7 @@ struct Profile {
     size_t launches = 0;
     // per launch: median and largest time of each (role, phase) over blocks, us
     std::vector<float> med[kRoles][kPhases], last[kRoles][kPhases];
+    std::string placement;  // CU placement of XCD group 0's blocks in the first harvested launch
     std::vector<float> slot_last[2][16];  // per slot: gate/up h published, down adds issued
     std::vector<float> last_stamp;        // per launch: the last stamp of any block, us
     size_t split = 0;                     // launches with a group (bid % 8) spread over XCDs
@@ -254,6 +255,27 @@ void prof_harvest(lt_ctx *ctx) {
         for (int q = 0; q < 16; q++)
             if (!sl[r][q].empty()) P.slot_last[r][q].push_back(*std::max_element(sl[r][q].begin(), sl[r][q].end()));
     P.last_stamp.push_back((float)(tmax - t0) * 0.01f);
+    if (P.placement.empty()) {
+        // the first harvested launch: which in-group indices (block / 8) of
+        // XCD group 0 shared a CU (HW_ID bits 8-15: CU, shader array,
+        // engine), with their roles
+        static const char rc[] = "-RGDCsd";
+        std::map<uint32_t, std::string> cu;
+        for (int b = 0; b < lt::kFusedBlocks; b += 8) {
+            const uint64_t w = st[(size_t)b * lt::kStamps + lt::kStamps - 1];
+            const int role = (int)(w & 0xff);
+            char item[24];
+            snprintf(item, sizeof item, " %d%c", b >> 3, role >= 0 && role < 7 ? rc[role] : '?');
+            cu[(uint32_t)(w >> 40) & 0xffu] += item;
+        }
+        P.placement = "placement, XCD group 0, one launch (in-group index + role: R router, G gate/up, D down, "
+                      "C combine, s shared gate/up, d shared down, - none), blocks per CU:\n";
+        for (const auto &kv : cu) {
+            char head[32];
+            snprintf(head, sizeof head, "  CU 0x%02x:", kv.first);
+            P.placement += head + kv.second + "\n";
+        }
+    }
     P.launches++;
 }
 
@@ -1427,16 +1449,16 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                  "us from the first block's start; median over launches of the block median / the last block\n",
                  P.launches);
         o += line;
-        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "filler"};
+        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "sh g/u", "sh down"};
         static const char *phases[kRoles][kPhases] = {
             {},
             {"block start", "first row chunk in", "logit published", "all row terms in"},
-            {"block start", "logits seen", "expert known", "dot products done", "h record published",
-             "shared h rows out"},
+            {"block start", "logits seen", "expert known", "dot products done", "h record published"},
             {"block start", "logits seen", "weight loads issued", "h records read", "adds issued",
-             "shared h seen", "shared rows added"},
+             "shared h slice read", "shared rows added"},
             {"block start", "rows written"},
-            {"block start", nullptr, nullptr, nullptr, nullptr, "shared h rows out", "shared rows added"}};
+            {"block start", "h rows out"},
+            {"block start", nullptr, nullptr, nullptr, nullptr, "h slice read", "rows added"}};
         snprintf(line, sizeof line, "%-9s %-22s %10s %10s\n", "role", "phase", "median", "last");
         o += line;
         for (int r = 1; r < kRoles; r++)
@@ -1468,6 +1490,7 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
             }
         snprintf(line, sizeof line, "; launches with a group (block index %% 8) on more than one XCD: %zu\n", P.split);
         o += line;
+        if (!P.placement.empty()) o += P.placement;
     }
     if (buf && len) {
         const size_t n = o.size() < len - 1 ? o.size() : len - 1;

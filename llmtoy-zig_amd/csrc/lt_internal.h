@@ -443,8 +443,9 @@ struct FusedPlan {
     int NDg;     // down blocks per slot
     int NCg;     // combining blocks per XCD group (deterministic combine only)
     int Ewait;   // logit rows published and waited for (>= E: placeholders cover start-value blocks)
-    int shared;  // a shared FFN in the launch (filler work of the experts' blocks)
-    int sg_rows; // shared h rows per gate/up-position block
+    int shared;  // a shared FFN in the launch (blocks of its own)
+    int NSg;     // shared gate/up blocks per XCD group (the shared down rows are in the down blocks)
+    int sg_rows; // shared h rows per shared gate/up block (<= 32)
     size_t lds;  // dynamic LDS bytes per block
 };
 // A layer for the fused kernel.  MoE: R, GU, Dn set (E experts, k > 0),
@@ -471,16 +472,17 @@ struct FusedScratch {
 // Phase stamps of one launch (LT_PROFILE=timeline): thread 0 of block b
 // writes stamps[b * kStamps + i], wall-clock ticks (100 MHz) at the end of
 // phase i of its role, and stamps[b * kStamps + kStamps - 1] = role | slot
-// << 8 | XCD << 16 (role 0 none, 1 router, 2 gate/up, 3 down, 4 combine,
-// 5 shared-FFN filler work only).
+// << 8 | XCD << 16 | HW_ID << 32 (role 0 none, 1 router, 2 gate/up, 3 down,
+// 4 combine, 5 shared-FFN gate/up, 6 shared-FFN down; HW_ID the hardware
+// register naming the CU, shader array and engine the block ran on).
 constexpr int kStamps = 8;
 enum : int { kStampStart = 0 };
 // router: 1 first row chunk in, 2 logit published, 3 all row terms in (Q8_0
 // router); gate/up: 1 logits seen, 2 expert known, 3 dot products done, 4 h
 // record published; down: 1 logits seen, 2 weight loads issued, 3 h records
-// read, 4 adds issued; combine: 1 rows written; with a shared FFN, gate/up
-// and filler 5: shared h rows out, down 5: the slice's shared h seen, down
-// and filler 6: shared rows added
+// read, 4 adds issued, with a shared FFN 5 its h slice read, 6 its rows
+// added; combine: 1 rows written; shared gate/up: 1 h rows out; shared
+// down only (a group without a slot): 5 h slice read, 6 rows added
 // Byte layout of that hand-over memory (a context's own allocation, or the
 // library's static scratch in lt_noalloc.hip): launch counters, 8 logit
 // copies, h record lines, partial-output lines, the XCD probe's ids, and

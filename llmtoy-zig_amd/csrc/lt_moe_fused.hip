@@ -16,19 +16,19 @@
 //   i < NRg                 router: logit rows 2*bid + [0, 2), dotf32 order
 //                           (4*bid + [0, 4) when the grid has no room), or
 //                           dotQ8_0 order for a Q8_0 router
-//   next SPG*G              gate/up: slot x + 8u, h group jg (16 values);
-//                           first sg_rows shared-FFN h rows (sh_gate_up_fill,
-//                           as the blocks without a role)
+//   next NSg                shared FFN gate/up: sg_rows h rows of the
+//                           group's K slice of the shared down product
+//   next SPG*G              gate/up: slot x + 8u, h group jg (16 values)
 //   next SPG*NDg            down: slot x + 8u, rows 64j + [0, 64); the first
-//                           NDg first add the shared FFN's rows 64j + [0, 64)
-//                           over the group's K slice (sh_down_fill)
+//                           NDg also add the shared FFN's rows 64j + [0, 64)
+//                           over the group's K slice
 //   next NCg                combine: rows 8c + [0, 8), c = 8(i - ...) + x
-//   the rest (no role)      shared-FFN h rows after the gate/up-position
-//                           blocks' (sh_gate_up_fill)
+//   the rest                no role
 //
 // (SPG = slots per group = ceil(k / 8), G = Kd / 16, NDg = ceil(D / 64),
-// NCg = NDg with the deterministic combine, else 0; NRg also covers one
-// router block per 256 output rows, store_starts).  Every hand-over is
+// NCg = NDg with the deterministic combine, else 0, NSg = 0 without a
+// shared FFN; NRg also covers one router block per 256 output rows,
+// store_starts).  Every hand-over is
 // coherent across XCDs except the h records (and the shared FFN's h) when
 // local is set: those are workgroup-scope stores that only the writer's L2
 // holds, correct only while the round-robin placement holds (probed once per
@@ -117,7 +117,9 @@ struct FusedArgs {
     const uint8_t *sgq, *suq, *sdq;   // shared FFN (Q8_0) quant planes: gate, up [S][D/32], down [D][S/32]
     const uint16_t *sgd, *sud, *sdd;  //   and their scale planes
     uint64_t *shh;       // shared FFN h [S], hand-over words
-    int qrouter, S, sg_rows;  // S = 0: no shared FFN
+    int qrouter, S;      // S = 0: no shared FFN
+    int NSg;             // shared gate/up blocks per XCD group
+    int sg_rows;         // shared h rows per shared gate/up block
 };
 
 // Phase stamps (LT_PROFILE=timeline), thread 0's: held in registers and
@@ -570,68 +572,58 @@ __device__ __forceinline__ void lds_x16(const float *p, float (&xv)[16]) {
     }
 }
 
-// The shared FFN runs in the time the experts' blocks would otherwise spend
-// waiting: each gate/up block first computes a few of the shared FFN's h
-// rows (while the router works), each down block first adds a part of the
-// shared down product (while the experts' gate/up works).  The down product
-// is split along K by XCD group: group x owns the Q8_0 blocks
-// [x nb / 8, (x + 1) nb / 8) of each down row (nb = S / 32), i.e. the h
-// rows 32 x nb / 8 ... of the same slice; its gate/up blocks compute
-// exactly those h rows and its down blocks read only them, so h never
-// crosses an XCD (handed over like the experts' h records), and the 8
-// groups' partial rows meet in out through float atomics.
+// The shared FFN has two roles of its own in each XCD group, placed after
+// the router blocks and before the experts' blocks, so that the experts'
+// gate/up blocks poll the logits with no weight stream of their own in
+// flight (a wavefront's loads complete in issue order, so a probe issued
+// behind a stream waits for the stream).  The down product is split along K
+// by XCD group: group x owns the Q8_0 blocks [x nb / 8, (x + 1) nb / 8) of
+// each down row (nb = S / 32), i.e. h rows 32 x nb / 8 ... of the same slice.
+// Its shared gate/up blocks compute exactly those h rows and its shared down
+// blocks read only them, so h never crosses an XCD (handed over like the
+// experts' h records), and the 8 groups' partial rows meet in out through
+// float atomics.  Every wait of these roles is for a block of a smaller
+// index: shared down waits for shared gate/up and for the router's start
+// values.  d_model <= kShMaxD (three 64-lane spans of half blocks per row).
+constexpr int kShMaxD = 3072;
 __device__ __forceinline__ void sh_slice(const FusedArgs &a, int x, int &kb0, int &kb1) {
     const int nb = a.S >> 5;
     kb0 = (x * nb) >> 3;
     kb1 = ((x + 1) * nb) >> 3;
 }
 
-// The launch epoch without committing it (the block's own role commits
-// later; nobody else writes the counter): thread 0 reads it, LDS hands it
-// to the other wavefronts -- a wavefront that read the counter after the
-// commit would see the next epoch.
-__device__ __forceinline__ uint32_t fill_epoch(const FusedArgs &a, uint32_t *s_ep, int bid, int tid) {
-    if (tid == 0) *s_ep = epoch_peek(a.counters, bid) + 1u;
-    __syncthreads();
-    return *s_ep;
-}
-
-// Shared gate/up rows of filler block q of group x (the gate/up-position
-// blocks, then the blocks without a role): h rows [lo + q R, lo + q R + R)
-// of the group's slice (R = sg_rows <= 4), one per wavefront; lane l takes
-// the half blocks v = l + 64 m of the row (m < 4: D <= 4096).  This
-// thread's share of x is loaded first, then the row's weights, then x goes
-// to LDS: loads complete in order, so the LDS stores wait only for x.  The
-// row's act(gate . x) * (up . x) goes out as a hand-over word for the
-// group's down-position blocks.
-// x in LDS after the experts' gate/up limb area (64 + 2.5 D bytes), so
-// that role_gate_up converts it from there (no second read of x)
-__device__ __forceinline__ float *sh_xs(const FusedArgs &a, uint8_t *smem) {
-    return reinterpret_cast<float *>(smem + 64 + (size_t)a.D / 4 * 10);
-}
-
-__device__ __forceinline__ void sh_gate_up_fill(const FusedArgs &a, uint8_t *smem, uint32_t *s_ep, int x, int q,
-                                                bool stage_x, int bid, int tid, int wave, int lane, Stamps &S) {
-    float *xs = sh_xs(a, smem);
-    const int nb = a.D >> 5, nu = 2 * nb, mu = (nu + 63) >> 6;
+// Shared gate/up block q (< NSg) of group x: h rows [j0, j1) = the slice's
+// rows q R + [0, R), R = sg_rows <= 32; wavefront w takes rows j0 + w + 4p,
+// its next row's weights in flight while this row's dots run (two register
+// sets).  Lane l takes the half blocks v = l + 64 m of a row (m < 3: D <=
+// kShMaxD), x comes from LDS.  x is loaded first and the block's launch epoch
+// read before any weight load, so that neither waits behind the stream.
+// The row's act(gate . x) * (up . x) goes out as a hand-over word.
+__device__ __forceinline__ void role_shared_gate_up(const FusedArgs &a, uint8_t *smem, int x, int q, int bid,
+                                                    int tid, int wave, int lane, Stamps &S) {
+    float *xs = reinterpret_cast<float *>(smem);
+    const int nb = a.D >> 5, nu = 2 * nb;
     int kb0, kb1;
     sh_slice(a, x, kb0, kb1);
     const int j0 = 32 * kb0 + q * a.sg_rows, j1 = min(32 * kb1, j0 + a.sg_rows);
-    if (j0 >= j1 && !stage_x) return;  // (the whole block)
-    // four named values, not an array (an array held across the barrier
+    if (j1 <= j0) return;  // no rows left for this block (the whole block)
+    // three named values, not an array (an array held across the barrier
     // below ends up in scratch memory); every load unconditional (clamped)
     auto xat = [&](int t) { return *reinterpret_cast<const float4 *>(a.x + min((tid + kThreads * t) * 4, a.D - 4)); };
-    const float4 x0 = xat(0), x1 = xat(1), x2 = xat(2), x3 = xat(3);
-    __builtin_amdgcn_sched_barrier(0);  // keeps the x loads ahead of the weight loads
-    const int j = j0 + wave;
-    // every weight load unconditional (row and half block clamped): with no
-    // branch around them, the LDS stores below wait for x only
-    uint4 qg[4], qu[4];
-    uint32_t dg[4], du[4];
-    {
-        const int jl = min(j, j1 - 1);
+    const float4 x0 = xat(0), x1 = xat(1), x2 = xat(2);
+    const uint32_t ep = epoch_peek(a.counters, bid) + 1u;
+    __builtin_amdgcn_sched_barrier(0);  // x and the counter ahead of the weight loads
+    const int nr = j1 - j0 > wave ? (j1 - j0 - wave + 3) >> 2 : 0;  // rows of this wavefront
+    const int jlast = j1 - 1;
+    uint4 qg0[3], qu0[3], qg1[3], qu1[3];
+    uint32_t dg0[3], du0[3], dg1[3], du1[3];
+    // every weight load unconditional (row and half block clamped): the
+    // compiler's wait before a row's dots then counts exactly the loads of
+    // the row after it
+    auto load = [&](uint4 (&qg)[3], uint4 (&qu)[3], uint32_t (&dg)[3], uint32_t (&du)[3], int p) {
+        const int jl = min(j0 + wave + 4 * p, jlast);
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
+        for (int m = 0; m < 3; m++) {
             const int v = min(lane + 64 * m, nu - 1);
             const size_t blk = (size_t)jl * nb + (v >> 1);
             qg[m] = ld16(a.sgq + blk * 32 + (v & 1) * 16);
@@ -639,25 +631,16 @@ __device__ __forceinline__ void sh_gate_up_fill(const FusedArgs &a, uint8_t *sme
             dg[m] = a.sgd[blk];
             du[m] = a.sud[blk];
         }
-    }
-    {
-        const int i = tid * 4;
-        if (i < a.D) *reinterpret_cast<float4 *>(xs + i) = x0;
-        if (i + 4 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 4 * kThreads) = x1;
-        if (i + 8 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 8 * kThreads) = x2;
-        if (i + 12 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 12 * kThreads) = x3;
-    }
-    // the epoch read after the weight loads are issued; s_ep keeps it for
-    // the block's own role, which then reads the counter no more (a load
-    // issued under the weight streams waits microseconds)
-    const uint32_t ep = fill_epoch(a, s_ep, bid, tid);  // (its barrier also covers xs)
-    if (j < j1) {
-        const bool first = p32_first(lane);
+    };
+    const bool first = p32_first(lane);
+    auto row = [&](const uint4 (&qg)[3], const uint4 (&qu)[3], const uint32_t (&dg)[3], const uint32_t (&du)[3],
+                   int p) {
+        if (p >= nr) return;  // (uniform over the wavefront)
         float g = 0.0f, up = 0.0f;
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
+        for (int m = 0; m < 3; m++) {
             const int v = lane + 64 * m;
-            if (m < mu && v < nu) {
+            if (v < nu) {
                 float xv[16];
                 lds_x16(xs + v * 16, xv);
                 g = fmaf(f16_bits_to_f32(dg[m]), q8_half_sum(qg[m], xv), g);
@@ -666,106 +649,154 @@ __device__ __forceinline__ void sh_gate_up_fill(const FusedArgs &a, uint8_t *sme
         }
         g = group_sum_dpp<64>(g, first);
         up = group_sum_dpp<64>(up, first);
-        if (lane == 0) hand_put_group(a.shh + j, __float_as_uint(act_apply((uint32_t)a.act, g) * up), ep, a.local);
+        if (lane == 0)
+            hand_put_group(a.shh + j0 + wave + 4 * p, __float_as_uint(act_apply((uint32_t)a.act, g) * up), ep,
+                           a.local);
+    };
+    load(qg0, qu0, dg0, du0, 0);
+    {
+        const int i = tid * 4;
+        if (i < a.D) *reinterpret_cast<float4 *>(xs + i) = x0;
+        if (i + 4 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 4 * kThreads) = x1;
+        if (i + 8 * kThreads < a.D) *reinterpret_cast<float4 *>(xs + i + 8 * kThreads) = x2;
     }
-    S.mark(5, tid);
+    __syncthreads();  // x in LDS
+    // (the loads past the wavefront's last row reload that row: clamped,
+    // and unconditional so that each wait counts only the loads after it)
+    for (int p = 0; p < nr; p += 2) {
+        load(qg1, qu1, dg1, du1, p + 1);
+        row(qg0, qu0, dg0, du0, p);
+        load(qg0, qu0, dg0, du0, p + 2);
+        row(qg1, qu1, dg1, du1, p + 1);
+    }
+    S.mark(1, tid);
 }
 
 // Shared down rows of down-position block u (< NDg) of group x: output rows
 // [64 u, 64 u + 64) over the group's K slice (nk = kb1 - kb0 <= 16 blocks:
-// S <= 4096); 16 lanes per row, four rows per wavefront and step.  Thread 0
-// waits for the logit of the router block that stored these rows' start
-// values and for the slice's last h word (the weight loads go out after
-// it, so that they do not compete with the router's and the shared gate/up
-// rows'); then all four steps' weights are loaded while the slice of h is
-// read (every word's epoch checked) into LDS, and the partial rows are
-// added into out with float atomics.  A wait that times out turns the rows NaN (error word 0x10 /
-// 0x20).
-__device__ __forceinline__ void sh_down_fill(const FusedArgs &a, uint8_t *smem, uint32_t ep, int x, int u, int bid,
-                                             int tid, int wave, int lane, Stamps &S) {
-    __shared__ int f_fail;
-    int *s_fail = &f_fail;
-    float *hs = reinterpret_cast<float *>(smem);
+// S <= 4096, nv = 2 nk half blocks).  When the block starts, wavefronts 1-3
+// load the rows' weights and store them in LDS (sh_stage_*): all 6.3 MB
+// of config 4's shared down weights are then read in the routing phase, and
+// none of them competes with the experts' weight streams later.  The rows
+// are added after the block's own rows (sh_down_add): a CU returns loads
+// in issue order across its wavefronts, so a wait for the shared h issued
+// while the gate/up blocks on the same CU stream their experts' weights
+// lasts until those streams end, and placed before the block's own weight
+// loads or its h records it held them back by 3 us (config 4).  By the time
+// the block's own rows are out the streams are over; the slice of h is read
+// with the block's own h records.  LDS from kShOff:
+// quants [64][nv] x 16 B, f16 scales [64][nk], then the slice of h (fp32).
+constexpr int kShOff = 2560;  // past the down role's h records (G <= 64: 40 G bytes)
+__host__ __device__ inline size_t sh_down_lds(int S) {
+    const int nk = (S / 32 + 7) / 8;  // blocks of the largest slice
+    return (size_t)kShOff + (size_t)kDownRows * 2 * nk * 16 + (size_t)kDownRows * nk * 2 + (size_t)32 * nk * 4;
+}
+// Wavefronts 1-3 issue the loads when the block starts (sh_stage_load) and
+// store the data in LDS while wavefront 0 polls the logits (sh_stage_store):
+// quants chunk c = row * nv + v, 11 per thread at most (64 rows x 32 half
+// blocks over 192 threads), scales 6 per thread; rows past r1 clamped
+// (loaded, never used).
+struct ShStage {
+    uint4 q[11];
+    uint32_t d[6];
+};
+__device__ __forceinline__ void sh_stage_load(const FusedArgs &a, ShStage &w, int x, int u, int tid) {
+    if (tid < 64) return;  // (wavefront 0 polls the logits)
     const int nb = a.S >> 5;
     int kb0, kb1;
     sh_slice(a, x, kb0, kb1);
-    const int nv = 2 * (kb1 - kb0), mv = (nv + 15) >> 4;
+    const int nk = kb1 - kb0, nv = 2 * nk;
+    const int r0 = u * kDownRows, r1 = min(a.D, r0 + kDownRows);
+    const int t = tid - 64;
+#pragma unroll
+    for (int m = 0; m < 11; m++) {
+        const int c = min(t + 192 * m, kDownRows * nv - 1);
+        const int row = min(r0 + c / nv, r1 - 1), v = c % nv;
+        w.q[m] = ld16(a.sdq + ((size_t)row * nb + kb0 + (v >> 1)) * 32 + (v & 1) * 16);
+    }
+#pragma unroll
+    for (int m = 0; m < 6; m++) {
+        const int c = min(t + 192 * m, kDownRows * nk - 1);
+        const int row = min(r0 + c / nk, r1 - 1);
+        w.d[m] = a.sdd[(size_t)row * nb + kb0 + c % nk];
+    }
+}
+__device__ __forceinline__ void sh_stage_store(const FusedArgs &a, uint8_t *smem, const ShStage &w, int x, int tid) {
+    if (tid < 64) return;
+    int kb0, kb1;
+    sh_slice(a, x, kb0, kb1);
+    const int nk = kb1 - kb0, nv = 2 * nk;
+    uint4 *lq = reinterpret_cast<uint4 *>(smem + kShOff);
+    uint16_t *ld = reinterpret_cast<uint16_t *>(lq + kDownRows * nv);
+    const int t = tid - 64;
+#pragma unroll
+    for (int m = 0; m < 11; m++)
+        if (t + 192 * m < kDownRows * nv) lq[t + 192 * m] = w.q[m];
+#pragma unroll
+    for (int m = 0; m < 6; m++)
+        if (t + 192 * m < kDownRows * nk) ld[t + 192 * m] = (uint16_t)w.d[m];
+}
+// The group's slice of the shared h into LDS after the staged weights (every
+// word's epoch checked; the words come from shared gate/up blocks, of smaller
+// index).  The down role reads it in the same pass as its own h records,
+// which it waits for long after the slice was written.  False on timeout
+// (error word 0x20).
+__device__ __forceinline__ float *sh_h_lds(uint8_t *smem, int nk) {
+    return reinterpret_cast<float *>(smem + kShOff + (size_t)kDownRows * 2 * nk * 16 + (size_t)kDownRows * nk * 2);
+}
+__device__ __forceinline__ bool sh_read_h(const FusedArgs &a, uint8_t *smem, uint32_t ep, int x, int bid, int tid) {
+    int kb0, kb1;
+    sh_slice(a, x, kb0, kb1);
+    float *hs = sh_h_lds(smem, kb1 - kb0);
+    const uint64_t t0 = wall_clock64();
+    for (int i = tid; i < 32 * (kb1 - kb0); i += kThreads) {
+        uint64_t hw = hand_get(a.shh + 32 * kb0 + i);
+        while (!tag_is(hw, ep)) {
+            if (wall_clock64() - t0 > kWaitTicks) {
+                report_detail(a.err, bid, 0x20u, (uint32_t)(32 * kb0 + i), (uint32_t)(hw >> 32), ep);
+                return false;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            hw = hand_get(a.shh + 32 * kb0 + i);
+        }
+        hs[i] = __uint_as_float((uint32_t)hw);
+    }
+    return true;
+}
+// The shared down rows [64 u, 64 u + 64) from the staged weights and the
+// slice of h in LDS, added into out with float atomics: 16 lanes per row
+// (lane l16 takes half blocks l16 and l16 + 16), four rows per wavefront and
+// step, four steps.  fail: NaN rows (error word 0x20).
+__device__ __forceinline__ void sh_down_add(const FusedArgs &a, uint8_t *smem, int x, int u, bool fail, int tid,
+                                            int wave, int lane, Stamps &S) {
+    int kb0, kb1;
+    sh_slice(a, x, kb0, kb1);
+    const int nk = kb1 - kb0, nv = 2 * nk;
+    const uint4 *lq = reinterpret_cast<const uint4 *>(smem + kShOff);
+    const uint16_t *ld = reinterpret_cast<const uint16_t *>(lq + kDownRows * nv);
+    const float *hs = sh_h_lds(smem, nk);
     const int r0 = u * kDownRows, r1 = min(a.D, r0 + kDownRows);
     const int l16 = lane & 15;
-    if (tid == 0) {
-        *s_fail = 0;
-        const uint64_t t0 = wall_clock64();
-        bool ok = true;
-        if (starts_stored_by_router(a)) {
-            ok = probe_wait(start_flag(a, x, r0), ep, t0);
-            if (!ok) report_detail(a.err, bid, 0x10u, r0, 0, ep);
-        }
-        if (ok) {
-            ok = probe_wait(a.shh + 32 * kb1 - 1, ep, t0);
-            if (!ok) report_detail(a.err, bid, 0x10u, 32 * kb1 - 1, 0, ep);
-        }
-        if (!ok) *s_fail = 1;
-    }
-    __syncthreads();
-    S.mark(5, tid);
-    uint4 qw[4][2];
-    uint32_t dw[4][2];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
-        const int r = min(r0 + 16 * st + 4 * wave + (lane >> 4), r1 - 1);
-#pragma unroll
-        for (int m = 0; m < 2; m++) {
-            if (m < mv) {
-                int v = l16 + 16 * m;
-                v = v < nv ? v : nv - 1;
-                const size_t blk = (size_t)r * nb + kb0 + (v >> 1);
-                qw[st][m] = ld16(a.sdq + blk * 32 + (v & 1) * 16);
-                dw[st][m] = a.sdd[blk];
-            }
-        }
-    }
-    {
-        const uint64_t t0 = wall_clock64();
-        bool ok = *s_fail == 0;
-        const int n = 32 * (kb1 - kb0);
-        for (int i = tid; i < n && ok; i += kThreads) {
-            uint64_t w = hand_get(a.shh + 32 * kb0 + i);
-            while (!tag_is(w, ep)) {
-                if (wall_clock64() - t0 > kWaitTicks) {
-                    ok = false;
-                    report_detail(a.err, bid, 0x20u, (uint32_t)(32 * kb0 + i), (uint32_t)(w >> 32), ep);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-                w = hand_get(a.shh + 32 * kb0 + i);
-            }
-            hs[i] = __uint_as_float((uint32_t)w);
-        }
-        if (!ok) atomicOr(s_fail, 2);
-    }
-    __syncthreads();
-    const bool fail = *s_fail != 0;
-#pragma unroll
-    for (int st = 0; st < 4; st++) {
+        const int rr = 16 * st + 4 * wave + (lane >> 4);  // row within the block
         float acc = 0.0f;
 #pragma unroll
         for (int m = 0; m < 2; m++) {
             const int v = l16 + 16 * m;
-            if (m < mv && v < nv) {
+            if (v < nv && r0 + rr < r1) {
                 float xv[16];
                 lds_x16(hs + v * 16, xv);
-                acc = fmaf(f16_bits_to_f32(dw[st][m]), q8_half_sum(qw[st][m], xv), acc);
+                acc = fmaf(f16_bits_to_f32(ld[rr * nk + (v >> 1)]), q8_half_sum(lq[rr * nv + v], xv), acc);
             }
         }
         acc = group_sum_dpp<16>(acc, false);
-        const int row = r0 + 16 * st + 4 * wave + (lane >> 4);
-        if (l16 == 0 && row < r1)
-            (void)__hip_atomic_fetch_add(a.out + row, fail ? __int_as_float(0x7fc00000) : acc, __ATOMIC_RELAXED,
+        if (l16 == 0 && r0 + rr < r1)
+            (void)__hip_atomic_fetch_add(a.out + r0 + rr, fail ? __int_as_float(0x7fc00000) : acc, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (tid == 0 && fail) report_timeout(a.err, (uint32_t)*s_fail << 4);  // 0x10 logit / last h word, 0x20 h
+    if (tid == 0 && fail) report_timeout(a.err, 0x20u);
     S.mark(6, tid);
-    __syncthreads();  // hs is free for the block's own role
 }
 
 // ---------------------------------------------------------------- gate/up
@@ -778,8 +809,7 @@ __device__ __forceinline__ void sh_down_fill(const FusedArgs &a, uint8_t *smem, 
 // WIDE (rows of 9-16 super-blocks): lane position pos covers pos and pos
 // + 32; the second position's weights are loaded as the first's products
 // finish, its x limbs are read from LDS after them.
-// XL: x is already in LDS (sh_xs, staged by sh_gate_up_fill).
-template <int PER, int WIDE, int XL>
+template <int PER, int WIDE>
 __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
                                              int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
                                              Stamps &S) {
@@ -789,8 +819,7 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
     const bool lane_on = pos < 4 * a.nsb;
     const bool first = p32_first(lane);
-    // (after the shared gate/up filler s_ep holds this launch's epoch)
-    const uint32_t c0 = XL ? *s_ep - 1u : epoch_peek(a.counters, bid);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
     // activation limbs, once per block: thread t converts elements 8t + [0, 8)
     // (half of group t / 2) into LDS; each lane then reads its window's 4
     // groups.  LDS: limb-a words [D/4], limb-b words [D/4], sp [D/16], xs [D/16].
@@ -799,7 +828,7 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
     float *lxs = lsp + a.D / 16;
     for (int t8 = tid; t8 < a.D / 8; t8 += kThreads) {  // one pass for D <= 2048
-        const float *xsrc = XL ? sh_xs(a, smem) : a.x;
+        const float *xsrc = a.x;
         const float4 f0 = *reinterpret_cast<const float4 *>(xsrc + 8 * t8);
         const float4 f1 = *reinterpret_cast<const float4 *>(xsrc + 8 * t8 + 4);
         const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
@@ -1009,9 +1038,10 @@ __device__ __forceinline__ float group16_sum_transposed(const float (&v)[V], int
 // partials over DPP, and the rows, times the slot weight, are added into out
 // (float atomics) or, with det (RPG = 4), wavefront w writes rows 16w +
 // [0, 16) as one line of partial-output words.
-// FILL: the block also adds shared-FFN rows (sh_down_fill) in the time its
-// down weight loads wait (measured 2.8 us better on config 4 than before
-// the logit poll, where the filler delays the block's own role).
+// FILL: the block also adds the shared FFN's down rows 64 j + [0, 64) over
+// its group's K slice: sh_stage_load when it starts, sh_stage_store during
+// its logit poll, sh_read_h with its h records, sh_down_add after its own
+// rows.
 template <int PER, int RPG, int FILL>
 __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, float *s_w,
                                           uint32_t *s_ep, int *s_fail, int bid, int s, int j, int tid, int wave,
@@ -1025,6 +1055,11 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     uint32_t *rec_b = rec_a + G * 4;
     float *rec_sp = reinterpret_cast<float *>(rec_b + G * 4);
     float *rec_xs = rec_sp + G;
+    const bool fill = FILL && a.S > 0 && s < 8;
+    __shared__ int sh_fail;
+    ShStage sst;
+    if (fill) sh_stage_load(a, sst, bid & 7, j, tid);
+    if (fill && tid == 0) sh_fail = 0;
     if (tid == 0) *s_ep = epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     __syncthreads();
     const uint32_t ep = *s_ep;
@@ -1043,11 +1078,12 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         float my_p;
         topk_softmax_regs<PER>(lv, a.E, a.k, a.norm, s_ids, s_w, key, my_i, my_p, lane);
         if (!ok && lane == 0) *s_fail = 1;
+    } else if (fill) {
+        sh_stage_store(a, smem, sst, bid & 7, tid);
     }
     __syncthreads();
     uint32_t e = s_ids[s];
     if (e >= (uint32_t)a.E) e = 0;
-    if (FILL && a.S > 0 && s < 8) sh_down_fill(a, smem, ep, bid & 7, j, bid, tid, wave, lane, S);
     {
         const uint64_t t_go = s_seen + (uint64_t)a.dn_delay;
         while (wall_clock64() < t_go) __builtin_amdgcn_s_sleep(4);
@@ -1135,7 +1171,8 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         }
     }
     if (!ok) atomicOr(s_fail, 2);
-    __syncthreads();  // records, s_ids / s_w
+    if (fill && !sh_read_h(a, smem, ep, bid & 7, bid, tid)) sh_fail = 1;
+    __syncthreads();  // records, shared h, s_ids / s_w
     S.mark(3, tid);
     if (s == 0 && j == 0 && tid < a.k) {  // the routing, for the caller
         a.ids_out[tid] = s_ids[tid];
@@ -1183,6 +1220,8 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
             (void)__hip_atomic_fetch_add(a.out + row0 + rr, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     S.mark(4, tid);
+    // (the start values of these rows were awaited with the h records)
+    if (fill) sh_down_add(a, smem, bid & 7, j, sh_fail != 0 || *s_fail != 0, tid, wave, lane, S);
 }
 
 // ---------------------------------------------------------------- combine
@@ -1240,7 +1279,9 @@ __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep,
 // (rows over 2048) only the router variants those rows use: less code per
 // instance (the roles of a CU's four workgroups share its instruction cache).
 template <int PER, int WIDE, int SH>
-__global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
+// (SH: at most 128 VGPRs, four blocks per SIMD, for the whole grid to be
+// resident; the others fit without the bound, which costs config 3 0.07 us)
+__global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_ep;
     __shared__ uint32_t s_ids[16];
@@ -1262,8 +1303,10 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
     S.mark(kStampStart, tid);
     uint32_t role = 0;
     if (tid == 0) s_fail = 0;
-    // in-group order: router, gate/up, down, combine -- every role waits
-    // only for earlier ones (the shared FFN's filler work too)
+    // in-group order: router, shared gate/up, gate/up, down, combine --
+    // every role waits only for earlier ones.  (Computing a role code first
+    // and dispatching on it, or reading it from a table in the kernel
+    // arguments, made config 3 0.07-0.45 us slower.)
     int u = i;
     if (u < a.NRg) {
         if (SH && a.qrouter)
@@ -1275,15 +1318,13 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
         else
             role_router(a, smem, bid, tid, wave, lane, S);
         role = 1;
-    } else if ((u -= a.NRg) < a.SPG * a.G) {
+    } else if ((u -= a.NRg) < a.NSg) {
+        if (SH) role_shared_gate_up(a, smem, x, u, bid, tid, wave, lane, S);
+        role = 5;
+    } else if ((u -= a.NSg) < a.SPG * a.G) {
         const int s = x + 8 * (u / a.G);
-        const bool fill = SH && a.S > 0;
-        if (fill) sh_gate_up_fill(a, smem, &s_ep, x, u, s < a.k, bid, tid, wave, lane, S);
         if (s < a.k) {
-            if (fill)
-                role_gate_up<PER, WIDE, 1>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
-            else
-                role_gate_up<PER, WIDE, 0>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            role_gate_up<PER, WIDE>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, 1u);  // logits
             role = 2u | (uint32_t)s << 8;
         }
@@ -1294,25 +1335,34 @@ __global__ void __launch_bounds__(kThreads) k_moe_fused(FusedArgs a) {
             if (tid == 0 && s_fail) report_timeout(a.err, (uint32_t)s_fail << 1);  // 2 logits, 4 h records
             role = 3u | (uint32_t)s << 8;
         } else if (SH && a.S > 0 && u < a.NDg) {  // a group without a slot still adds its shared rows
-            sh_down_fill(a, smem, fill_epoch(a, &s_ep, bid, tid), x, u, bid, tid, wave, lane, S);
-            role = 5;
+            const uint32_t ep = epoch_peek(a.counters, bid) + 1u;
+            ShStage sst;
+            sh_stage_load(a, sst, x, u, tid);
+            sh_stage_store(a, smem, sst, x, tid);
+            if (tid == 0 && starts_stored_by_router(a) && !probe_wait(start_flag(a, x, u * kDownRows), ep, wall_clock64()))
+                s_fail = 1;
+            if (!sh_read_h(a, smem, ep, x, bid, tid)) s_fail = 1;
+            __syncthreads();
+            sh_down_add(a, smem, x, u, s_fail != 0, tid, wave, lane, S);
+            role = 6;
         }
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
         role_combine(a, &s_ep, bid, 8 * u + x, tid, S);
         role = 4;
-    } else if (SH && a.S > 0) {  // no role: shared gate/up rows after the gate/up-position blocks'
-        sh_gate_up_fill(a, smem, &s_ep, x, a.SPG * a.G + (u - a.NCg), false, bid, tid, wave, lane, S);
-        role = 5;
     }
-    // no role in this configuration (or filler work only): keep the counter in step
-    if ((role == 0 || role == 5) && tid == 0) (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
+    // no role in this configuration, or a shared-FFN role: keep the counter in step
+    // (role 5 and 6 carry no slot bits; 2 and 3 do, and commit in their role)
+    if ((role == 0 || role == 5 || role == 6) && tid == 0)
+        (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     if (S.row && tid == 0) {
-        uint32_t xcc;  // the XCD this block ran on
+        uint32_t xcc, hw;  // the XCD and the CU this block ran on
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        const uint64_t w = role | (uint64_t)(xcc & 0xfu) << 16 | (uint64_t)hw << 32;
         if (SH) {
-            S.row[kStamps - 1] = role | (uint64_t)(xcc & 0xfu) << 16;
+            S.row[kStamps - 1] = w;
         } else {
-            S.t[kStamps - 1] = role | (uint64_t)(xcc & 0xfu) << 16;
+            S.t[kStamps - 1] = w;
 #pragma unroll
             for (int q = 0; q < kStamps; q++) S.row[q] = S.t[q];
         }
@@ -1387,14 +1437,17 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         pl.rb = 2;
     }
     if (sh) {
-        // the shared FFN as filler work of the experts' gate/up and down
-        // blocks (a dense FFN alone is not in the single launch)
+        // the shared FFN's gate/up rows in blocks of their own (the group's
+        // blocks the experts leave free, at most 32 h rows each), its down
+        // rows in the experts' down blocks (64 each: NDg * 64 >= D); a dense
+        // FFN alone is not in the single launch
         const int S = L.S;
-        if (!moe || !L.SU || !L.SD || S % 32 != 0 || S < 256 || S > 4096) return pl;
+        if (!moe || !L.SU || !L.SD || S % 32 != 0 || S < 256 || S > 4096 || D > kShMaxD) return pl;
         const int slice = 32 * ((S / 32 + 7) / 8);  // h rows of the largest group slice
-        const int nfill = kFusedBlocks / 8 - used + pl.SPG * pl.G;  // gate/up-position and idle blocks
-        pl.sg_rows = (slice + nfill - 1) / nfill;
-        if (pl.sg_rows > 4) return pl;  // one row per wavefront
+        const int spare = kFusedBlocks / 8 - used;
+        if (spare < 1 || (slice + spare - 1) / spare > 32) return pl;
+        pl.NSg = spare;
+        pl.sg_rows = (slice + spare - 1) / spare;
         pl.shared = 1;
     }
     size_t lds = 64;
@@ -1404,16 +1457,16 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
         lds = std::max(lds, std::max(lds_router, std::max(lds_down, lds_gu)));
     }
-    if (sh) lds = std::max(lds, std::max(64 + (size_t)D / 4 * 10 + (size_t)D * 4, (size_t)128 * ((L.S / 32 + 7) / 8)));  // limbs + x, h slice
-    if (lds > 64 * 1024) return pl;
+    if (sh) lds = std::max(lds, std::max((size_t)D * 4, sh_down_lds(L.S)));  // x; shared down weights + h slice
+    if (lds > 40 * 1024) return pl;  // four blocks per CU (160 KB of LDS): the whole grid resident
     pl.lds = lds;
     pl.ok = true;
     return pl;
 }
 
 template <int PER, int WIDE, int SH>
-static hipError_t launch_fused_t(const FusedArgs &fa, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((k_moe_fused<PER, WIDE, SH>), dim3(kFusedBlocks), dim3(kThreads), lds, s, fa);
+static hipError_t launch_fused_t(const FusedArgs &fa, const FusedPlan &pl, hipStream_t s) {
+    hipLaunchKernelGGL((k_moe_fused<PER, WIDE, SH>), dim3(kFusedBlocks), dim3(kThreads), pl.lds, s, fa);
     return hipGetLastError();
 }
 
@@ -1456,6 +1509,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     fa.shh = sc.shh;
     fa.qrouter = pl.qrouter;
     fa.S = pl.shared ? L.S : 0;
+    fa.NSg = pl.shared ? pl.NSg : 0;
     fa.sg_rows = pl.sg_rows;
     fa.E = moe ? L.E : 0;
     fa.D = L.D;
@@ -1486,11 +1540,11 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // products halve
     const bool sh = pl.shared || pl.qrouter;
     if (pl.wide) {
-        if (sh) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl.lds, s) : launch_fused_t<4, 1, 1>(fa, pl.lds, s);
-        return pl.per == 2 ? launch_fused_t<2, 1, 0>(fa, pl.lds, s) : launch_fused_t<4, 1, 0>(fa, pl.lds, s);
+        if (sh) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl, s) : launch_fused_t<4, 1, 1>(fa, pl, s);
+        return pl.per == 2 ? launch_fused_t<2, 1, 0>(fa, pl, s) : launch_fused_t<4, 1, 0>(fa, pl, s);
     }
-    if (sh) return pl.per == 2 ? launch_fused_t<2, 0, 1>(fa, pl.lds, s) : launch_fused_t<4, 0, 1>(fa, pl.lds, s);
-    return pl.per == 2 ? launch_fused_t<2, 0, 0>(fa, pl.lds, s) : launch_fused_t<4, 0, 0>(fa, pl.lds, s);
+    if (sh) return pl.per == 2 ? launch_fused_t<2, 0, 1>(fa, pl, s) : launch_fused_t<4, 0, 1>(fa, pl, s);
+    return pl.per == 2 ? launch_fused_t<2, 0, 0>(fa, pl, s) : launch_fused_t<4, 0, 0>(fa, pl, s);
 }
 
 }  // namespace lt
