@@ -684,12 +684,15 @@ __device__ __forceinline__ void role_shared_gate_up(const FusedArgs &a, uint8_t 
 // lasts until those streams end, and placed before the block's own weight
 // loads or its h records it held them back by 3 us (config 4).  By the time
 // the block's own rows are out the streams are over; the slice of h is read
-// with the block's own h records.  LDS from kShOff:
-// quants [64][nv] x 16 B, f16 scales [64][nk], then the slice of h (fp32).
+// once the block's own weight loads are issued, and its rows are summed into
+// LDS while the block waits for its own h records.  LDS from kShOff:
+// quants [64][nv] x 16 B, f16 scales [64][nk], the slice of h (fp32), its
+// limbs [nv][2] x 16 B, group scales [nv], row sums [64].
 constexpr int kShOff = 2560;  // past the down role's h records (G <= 64: 40 G bytes)
 __host__ __device__ inline size_t sh_down_lds(int S) {
     const int nk = (S / 32 + 7) / 8;  // blocks of the largest slice
-    return (size_t)kShOff + (size_t)kDownRows * 2 * nk * 16 + (size_t)kDownRows * nk * 2 + (size_t)32 * nk * 4;
+    return (size_t)kShOff + (size_t)kDownRows * 2 * nk * 16 + (size_t)kDownRows * nk * 2 + (size_t)32 * nk * 4 +
+           (size_t)2 * nk * 36 + (size_t)kDownRows * 4;  // + limbs and scales of its 2 nk groups, row sums
 }
 // Wavefronts 1-3 issue the loads when the block starts (sh_stage_load) and
 // store the data in LDS while wavefront 0 polls the logits (sh_stage_store):
@@ -764,18 +767,53 @@ __device__ __forceinline__ bool sh_read_h(const FusedArgs &a, uint8_t *smem, uin
     return true;
 }
 // The shared down rows [64 u, 64 u + 64) from the staged weights and the
-// slice of h in LDS, added into out with float atomics: 16 lanes per row
-// (lane l16 takes half blocks l16 and l16 + 16), four rows per wavefront and
-// step, four steps.  fail: NaN rows (error word 0x20).
-__device__ __forceinline__ void sh_down_add(const FusedArgs &a, uint8_t *smem, int x, int u, bool fail, int tid,
-                                            int wave, int lane, Stamps &S) {
+// slice of h in LDS (sh_down_rows: sums into LDS; sh_down_add: added into
+// out with float atomics).  Each half block's 16 h values become two int8
+// limbs (as the experts' h records: h ~= sp (256 a + b), error <= max|h| /
+// 65024 per element; thread g converts group g), so a Q8_0 half block meets
+// them in 8 v_dot4 instead of 16 conversions and 16 fma.  16 lanes per row
+// (lane l16 takes half blocks l16 and l16 + 16), four rows per wavefront
+// and step, four steps.
+__device__ __forceinline__ float *sh_row_sums(uint8_t *smem, int nk) {
+    return sh_h_lds(smem, nk) + 16 * 2 * nk + 2 * 2 * nk * 4 + 2 * nk;  // after h, limbs and group scales
+}
+__device__ __forceinline__ void sh_down_rows(const FusedArgs &a, uint8_t *smem, int x, int u, int tid, int wave,
+                                             int lane) {
     int kb0, kb1;
     sh_slice(a, x, kb0, kb1);
     const int nk = kb1 - kb0, nv = 2 * nk;
     const uint4 *lq = reinterpret_cast<const uint4 *>(smem + kShOff);
     const uint16_t *ld = reinterpret_cast<const uint16_t *>(lq + kDownRows * nv);
     const float *hs = sh_h_lds(smem, nk);
-    const int r0 = u * kDownRows, r1 = min(a.D, r0 + kDownRows);
+    uint4 *la = reinterpret_cast<uint4 *>(const_cast<float *>(hs) + 16 * nv);  // [nv][2]: limbs a, b
+    float *lsp = reinterpret_cast<float *>(la + 2 * nv);                       // [nv]
+    float *ps = sh_row_sums(smem, nk);                                         // [64]
+    if (tid < nv) {
+        float v[16];
+        lds_x16(hs + tid * 16, v);
+        float m = 0.0f, sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            m = fmaxf(m, fabsf(v[i]));
+            sum += v[i];
+        }
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        float sp = m * (1.0f / 32512.0f);
+        if (!(fabsf(sum) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);  // inf / NaN propagate
+        uint32_t pa[4] = {0u, 0u, 0u, 0u}, pb[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float t = v[i] * inv;
+            const float fa = rintf(t);
+            const float fb = fminf(rintf((t - fa) * 256.0f), 127.0f);
+            pa[i >> 2] |= ((uint32_t)(int)fa & 0xffu) << (8 * (i & 3));
+            pb[i >> 2] |= ((uint32_t)(int)fb & 0xffu) << (8 * (i & 3));
+        }
+        la[2 * tid] = make_uint4(pa[0], pa[1], pa[2], pa[3]);
+        la[2 * tid + 1] = make_uint4(pb[0], pb[1], pb[2], pb[3]);
+        lsp[tid] = sp;
+    }
+    __syncthreads();
     const int l16 = lane & 15;
 #pragma unroll
     for (int st = 0; st < 4; st++) {
@@ -784,17 +822,33 @@ __device__ __forceinline__ void sh_down_add(const FusedArgs &a, uint8_t *smem, i
 #pragma unroll
         for (int m = 0; m < 2; m++) {
             const int v = l16 + 16 * m;
-            if (v < nv && r0 + rr < r1) {
-                float xv[16];
-                lds_x16(hs + v * 16, xv);
-                acc = fmaf(f16_bits_to_f32(ld[rr * nk + (v >> 1)]), q8_half_sum(lq[rr * nv + v], xv), acc);
+            if (v < nv) {
+                const uint4 q = lq[rr * nv + v], ga = la[2 * v], gb = la[2 * v + 1];
+                int ia = sdot4_first((int)q.x, (int)ga.x);
+                ia = __builtin_amdgcn_sdot4((int)q.y, (int)ga.y, ia, false);
+                ia = __builtin_amdgcn_sdot4((int)q.z, (int)ga.z, ia, false);
+                ia = __builtin_amdgcn_sdot4((int)q.w, (int)ga.w, ia, false);
+                int ib = sdot4_first((int)q.x, (int)gb.x);
+                ib = __builtin_amdgcn_sdot4((int)q.y, (int)gb.y, ib, false);
+                ib = __builtin_amdgcn_sdot4((int)q.z, (int)gb.z, ib, false);
+                ib = __builtin_amdgcn_sdot4((int)q.w, (int)gb.w, ib, false);
+                acc = fmaf(f16_bits_to_f32(ld[rr * nk + (v >> 1)]) * lsp[v], (float)(256 * ia + ib), acc);
             }
         }
         acc = group_sum_dpp<16>(acc, false);
-        if (l16 == 0 && r0 + rr < r1)
-            (void)__hip_atomic_fetch_add(a.out + r0 + rr, fail ? __int_as_float(0x7fc00000) : acc, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
+        if (l16 == 0) ps[rr] = acc;
     }
+}
+// (after a barrier that follows sh_down_rows) fail: NaN rows (error word 0x20)
+__device__ __forceinline__ void sh_down_add(const FusedArgs &a, uint8_t *smem, int x, int u, bool fail, int tid,
+                                            Stamps &S) {
+    int kb0, kb1;
+    sh_slice(a, x, kb0, kb1);
+    const float *ps = sh_row_sums(smem, kb1 - kb0);
+    const int r0 = u * kDownRows, r1 = min(a.D, r0 + kDownRows);
+    if (tid < kDownRows && r0 + tid < r1)
+        (void)__hip_atomic_fetch_add(a.out + r0 + tid, fail ? __int_as_float(0x7fc00000) : ps[tid], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0 && fail) report_timeout(a.err, 0x20u);
     S.mark(6, tid);
 }
@@ -1103,6 +1157,15 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
             hw[i] = *reinterpret_cast<const uint32_t *>(a.dn_hdr + blk * 16 + 4 * p);
         }
     }
+    // the shared FFN's rows while these weights are in flight: its slice of
+    // h (written long before; the reads return once this CU's earlier loads
+    // have), summed into LDS
+    if (fill) {
+        if (!sh_read_h(a, smem, ep, bid & 7, bid, tid)) sh_fail = 1;
+        __syncthreads();
+        sh_down_rows(a, smem, bid & 7, j, tid, wave, lane);
+        S.mark(5, tid);
+    }
     // scales decoded, and the nibbles of rows 0-1 unpacked, while the h
     // records are awaited (the dots after their arrival are VALU-bound; all
     // four rows unpacked would exceed 128 VGPRs); the empty asm keeps the
@@ -1171,8 +1234,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         }
     }
     if (!ok) atomicOr(s_fail, 2);
-    if (fill && !sh_read_h(a, smem, ep, bid & 7, bid, tid)) sh_fail = 1;
-    __syncthreads();  // records, shared h, s_ids / s_w
+    __syncthreads();  // records, s_ids / s_w
     S.mark(3, tid);
     if (s == 0 && j == 0 && tid < a.k) {  // the routing, for the caller
         a.ids_out[tid] = s_ids[tid];
@@ -1220,8 +1282,9 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
             (void)__hip_atomic_fetch_add(a.out + row0 + rr, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     S.mark(4, tid);
-    // (the start values of these rows were awaited with the h records)
-    if (fill) sh_down_add(a, smem, bid & 7, j, sh_fail != 0 || *s_fail != 0, tid, wave, lane, S);
+    // (the start values of these rows were awaited with the h records; the
+    // row sums are behind the barrier after the records)
+    if (fill) sh_down_add(a, smem, bid & 7, j, sh_fail != 0 || *s_fail != 0, tid, S);
 }
 
 // ---------------------------------------------------------------- combine
@@ -1343,7 +1406,9 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
                 s_fail = 1;
             if (!sh_read_h(a, smem, ep, x, bid, tid)) s_fail = 1;
             __syncthreads();
-            sh_down_add(a, smem, x, u, s_fail != 0, tid, wave, lane, S);
+            sh_down_rows(a, smem, x, u, tid, wave, lane);
+            __syncthreads();
+            sh_down_add(a, smem, x, u, s_fail != 0, tid, S);
             role = 6;
         }
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
