@@ -231,10 +231,13 @@ int lt_moe_forward_noalloc(lt_ctx *ctx, float *out, const float *x, const lt_ten
  * expert GEMM with f16 MFMA (fp32 accumulation) over Q4_K weights
  * dequantised in LDS, then a combine in slot order.  The reference prefills
  * one token at a time through the decode path (main.zig:1916-1922); results
- * match per-token lt_moe_forward to f16 tolerance.  X rows are scaled by
- * powers of two into f16's range; the expert activations between the two
- * GEMMs saturate at +-65504.  Device pointers X and out must be 16-byte
- * aligned. */
+ * match per-token lt_moe_forward to f16 tolerance.  Each X row is divided by
+ * a power of two 2^e that puts its largest element in [1, 2) and the expert
+ * activations between the two GEMMs are kept divided by 2^(2e) (f16 tiles,
+ * exact rescaling), so rows of any magnitude stay inside f16's range; an
+ * activation that still passes +-65504 saturates there, is counted, and the
+ * call (LT_HOST_IO) or the next lt_sync returns LT_ERR_DEVICE naming the
+ * count.  Device pointers X and out must be 16-byte aligned. */
 int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t T, const lt_tensor *router,
                    const float *router_bias, const lt_tensor *gate_up, const lt_tensor *down, uint32_t k,
                    uint32_t d_expert, uint32_t act, uint32_t flags, uint32_t *out_ids, float *out_w);

@@ -424,6 +424,14 @@ int check_fused_err(lt_ctx *ctx) {
     if (!ctx->fused_err) return LT_OK;
     const uint32_t v = __atomic_exchange_n(ctx->fused_err, 0u, __ATOMIC_SEQ_CST);
     if (!v) return LT_OK;
+    if (v == lt::kErrCodePrefillSat) {
+        const uint32_t n = __atomic_exchange_n(ctx->fused_err + lt::kErrPrefillSat, 0u, __ATOMIC_SEQ_CST);
+        return fail(ctx, LT_ERR_DEVICE,
+                    "batched prefill: %u expert activations between the two GEMMs fell outside f16's range (after "
+                    "the row's power-of-two scaling) and saturated at +-65504; the outputs of that call are inexact",
+                    n);
+    }
+    (void)__atomic_exchange_n(ctx->fused_err + lt::kErrPrefillSat, 0u, __ATOMIC_SEQ_CST);
     uint32_t d[5];  // first timed-out wait: block + 1, site, index, tag or count seen, epoch expected
     for (int i = 0; i < 5; i++) d[i] = __atomic_exchange_n(ctx->fused_err + 2 + i, 0u, __ATOMIC_SEQ_CST);
     // Later launches publish h through memory (agent scope) instead of an
@@ -432,8 +440,8 @@ int check_fused_err(lt_ctx *ctx) {
     return fail(ctx, LT_ERR_DEVICE,
                 "single-launch kernel: a hand-over wait timed out (code 0x%x: 1 gate/up logits, 2 down logits, 4 down "
                 "h records, 8 combine, 0x10 shared-FFN logits or last h word, 0x20 shared-FFN h, 0x40 dense-FFN h, "
-                "0x80 dense-FFN start values; first recorded: block %d, site 0x%x, index %u, saw %u, expected epoch "
-                "%u); outputs of that call are NaN",
+                "0x80 dense-FFN start values, 0x100 prefill f16 saturation; first recorded: block %d, site 0x%x, index "
+                "%u, saw %u, expected epoch %u); outputs of that call are NaN",
                 v, (int)d[0] - 1, d[1], d[2], d[3], d[4]);
 }
 
@@ -1178,7 +1186,7 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
     rc = launch_rc(ctx,
                    lt::launch_moe_prefill(router->t, gate_up->t, down->t, dX, (int)T, dbias, (int)k, (int)d_expert,
                                           act, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, ctx->pf.p, dout, dids, dw,
-                                          ctx->stream),
+                                          ctx->err_dev, ctx->stream),
                    "moe_prefill");
     if (rc) return rc;
     if (host) {
@@ -1194,6 +1202,7 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
                                        ctx->stream));
         LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
         prof_harvest(ctx);
+        return check_fused_err(ctx);
     }
     return LT_OK;
 }

@@ -239,13 +239,16 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_c
 __device__ __forceinline__ float4 ldg16f(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
 // The prefill's f16 copy of X (X rows scaled into f16's range, K in the
-// order the f16 dequantisation produces): a row with max |x| = m is divided
-// by 2^e, e the smallest value >= 0 with m / 2^e <= 2^14 (exact; f16's range
-// ends near 2^16); rows holding inf or NaN pass unscaled (e = 0).
+// order the f16 dequantisation produces): a row with max |x| = m > 0 is
+// divided by 2^e = 2^ilogb(m), so that its largest element lies in [1, 2)
+// (exact: a power of two), whether m is large or small; e is kept in
+// [-100, 127] (2^-e stays finite for every fp32 row); rows of zeros and
+// rows holding inf or NaN pass unscaled (e = 0).  The activations between
+// the two GEMMs are kept divided by 2^(2e) (see k_prefill_gate_up), which
+// holds them inside f16's range whatever the row's magnitude.
 __device__ __forceinline__ int prefill_x_exp(float m) {
     int e = 0;
-    if (m > 16384.0f) e = ilogbf(m) - 13;  // m / 2^e < 2^14
-    if (!(m <= 3.0e38f)) e = 0;
+    if (m > 0.0f && m <= 3.4e38f) e = min(max(ilogbf(m), -100), 127);
     return e;
 }
 
@@ -294,6 +297,11 @@ __device__ __forceinline__ uint64_t hand_get(const uint64_t *p) {
 }
 __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t ep) { return (uint32_t)(w >> 32) == ep; }
 
+// The context's host-mapped error words (16): [0] code bits (the fused
+// kernels' timed-out waits below 0x100), [2..6] the first wait's details,
+// [8] the prefill's count of saturated f16 activations (code bit 0x100).
+constexpr uint32_t kErrCodePrefillSat = 0x100u;
+constexpr int kErrPrefillSat = 8;
 __device__ __forceinline__ void report_timeout(uint32_t *err, uint32_t code) {
     __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -410,7 +418,7 @@ hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, cons
 size_t prefill_workspace_bytes(int T, int k, int E, int F, int D);
 hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const DevTensor &Dn, const float *X, int T,
                               const float *bias, int k, int F, uint32_t act, uint32_t norm, void *ws, float *out,
-                              uint32_t *out_ids, float *out_w, hipStream_t s);
+                              uint32_t *out_ids, float *out_w, uint32_t *err, hipStream_t s);
 hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
                                      hipStream_t s);

@@ -8,18 +8,22 @@
 //      row ranges ("sorted rows"), cuts each range into chunks of at most
 //      MC = 128 rows, and scatters (token, slot) assignments into them;
 //      X is converted to f16 once (by the router kernel, or
-//      k_prefill_x_f16), each row scaled by a power of two that keeps it far
-//      inside f16's range;
+//      k_prefill_x_f16), each row t divided by r_t = 2^e, a power of two
+//      that puts its largest element in [1, 2);
 //   3. grouped gate/up GEMM: one block per (chunk, 64 output columns); its
 //      128 weight rows (64 gate + 64 up) are dequantised from Q4_K to f16
 //      in LDS once per K stage and shared by the chunk's 4 token tiles (one
 //      32-row tile per wavefront, v_mfma_f32_32x32x16_f16, fp32
 //      accumulation); gate and up of an output column sit in the same
-//      wavefront, so the epilogue act(gate) * up -> H (f16) needs no
-//      exchange;
+//      wavefront, so the epilogue h = act(gate) * up needs no exchange; it
+//      stores H = h / r_t^2 (f16), which |act(g)| <= |g| bounds by the
+//      scaled row's products whatever X's magnitude (a value still past
+//      f16's range saturates at +-65504 and is counted: the call then
+//      reports LT_ERR_DEVICE);
 //   4. grouped down GEMM: one block per (chunk, 128 output rows), the same
 //      scheme with H as the A operand -> Y (fp32, sorted rows);
-//   5. combine: out[t] = sum over slots in slot order of w[t][s] * Y[pos].
+//   5. combine: out[t] = r_t^2 * sum over slots in slot order of w[t][s] *
+//      Y[pos] (r_t^2 exact).
 // Both GEMMs run a software pipeline over K stages of 128 (half a Q4_K
 // super-block): weight loads are issued two stages ahead into registers,
 // A fragments one stage ahead, the dequantised tile is double-buffered in
@@ -441,7 +445,7 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
                                                          const int *__restrict__ n_chunks,
                                                          const int *__restrict__ offsets,
                                                          const int *__restrict__ perm, uint32_t act,
-                                                         _Float16 *__restrict__ H, int Kd) {
+                                                         _Float16 *__restrict__ H, int Kd, uint32_t *err) {
     if ((int)blockIdx.y >= *n_chunks) return;
     const int e = chunks[3 * blockIdx.y], m0 = chunks[3 * blockIdx.y + 1], mc = chunks[3 * blockIdx.y + 2];
     const int base = offsets[e];
@@ -457,17 +461,27 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
     const int *prow = perm + base + m0;
     auto row_ptr = [&](int m) { return Xh + (size_t)prow[m] * D; };
     // ct 0, 1 = gate columns n0 + [0, 64), ct 2, 3 = the matching up columns;
-    // the row scale brings gate and up back to X's scale; h is stored in
-    // kperm order (the down GEMM's K), clamped to f16's finite range
+    // with r the row's scale, gate = r v[0] and up = r v[2], and H = act(gate)
+    // * up / r^2 = act(r v[0]) * (v[2] / r) (exact scalings) is stored in
+    // kperm order (the down GEMM's K); a finite value past f16's range
+    // saturates at +-65504 and is counted (inf and NaN pass through)
+    uint32_t sat = 0;
+    auto sat16 = [&](float h) {
+        if (fabsf(h) > 65504.0f && fabsf(h) <= 3.4e38f) {
+            h = copysignf(65504.0f, h);
+            sat++;
+        }
+        return (_Float16)h;
+    };
     auto epi = [&](int t, int i, const float (&v)[4]) {
         const int m = 32 * t + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
         if (m < mc) {
-            const float r = rs[prow[m]];
+            const float r = rs[prow[m]], ri = 1.0f / r;  // (powers of two: exact)
             _Float16 *hrow = H + (size_t)(base + m0 + m) * Kd;
             const int c0 = n0 + (lane & 31);
-            const float h0 = act_apply(act, v[0] * r) * (v[2] * r), h1 = act_apply(act, v[1] * r) * (v[3] * r);
-            hrow[kperm(c0)] = (_Float16)fminf(fmaxf(h0, -65504.0f), 65504.0f);
-            hrow[kperm(c0 + 32)] = (_Float16)fminf(fmaxf(h1, -65504.0f), 65504.0f);
+            const float h0 = act_apply(act, v[0] * r) * (v[2] * ri), h1 = act_apply(act, v[1] * r) * (v[3] * ri);
+            hrow[kperm(c0)] = sat16(h0);
+            hrow[kperm(c0 + 32)] = sat16(h1);
         }
     };
     const int nt = (mc + 31) / 32, NS = 2 * nsb;
@@ -477,6 +491,10 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
         run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
     else
         run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+    if (sat) {  // (rare): the count and the error bit, reported at the next synchronising call
+        __hip_atomic_fetch_add(err + kErrPrefillSat, sat, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        report_timeout(err, kErrCodePrefillSat);
+    }
     if (blockIdx.x == 0 && Kd > F)  // zero K padding of the down product
         for (int i = tid; i < mc * (Kd - F); i += 256) {
             const int m = i / (Kd - F), col = F + i % (Kd - F);
@@ -522,10 +540,11 @@ __global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict_
 // ---------------------------------------------------------------- combine
 // Thread: 4 consecutive elements of one token's row (D % 4 == 0); every
 // slot's Y row is read with one 16-byte load per thread, all k loads in
-// flight before the sum, which runs in slot order.
+// flight before the sum, which runs in slot order; the sum times r_t^2
+// (the row scale the activations were divided by, exact).
 __global__ void __launch_bounds__(256) k_prefill_combine(const float *__restrict__ Y, const int *__restrict__ pos,
-                                                         const float *__restrict__ w, int k, int D,
-                                                         float *__restrict__ out) {
+                                                         const float *__restrict__ w, const float *__restrict__ rs,
+                                                         int k, int D, float *__restrict__ out) {
     const int t = blockIdx.y, i = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (i >= D) return;
     float4 v[16];
@@ -548,6 +567,11 @@ __global__ void __launch_bounds__(256) k_prefill_combine(const float *__restrict
             acc.w += ws[s] * v[s].w;
         }
     }
+    const float r2 = rs[t] * rs[t];
+    acc.x *= r2;
+    acc.y *= r2;
+    acc.z *= r2;
+    acc.w *= r2;
     *reinterpret_cast<float4 *>(out + (size_t)t * D + i) = acc;
 }
 
@@ -560,7 +584,7 @@ size_t prefill_workspace_bytes(int T, int k, int E, int Kd, int D) {
 
 hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const DevTensor &Dn, const float *X, int T,
                               const float *bias, int k, int F, uint32_t act, uint32_t norm, void *ws, float *out,
-                              uint32_t *out_ids, float *out_w, hipStream_t s) {
+                              uint32_t *out_ids, float *out_w, uint32_t *err, hipStream_t s) {
     const int E = (int)GU.n_experts, D = (int)GU.cols, Kd = (int)Dn.cols;
     const int TK = T * k;
     Ws w = carve(ws, T, k, E, Kd, D);
@@ -576,12 +600,13 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
     }
     const int mc = max_chunks(TK, E);
     hipLaunchKernelGGL(k_prefill_gate_up, dim3(F / BN1, mc), dim3(256), 0, s, GU.p0, GU.p1, (int)GU.blocks_per_row,
-                       F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm, act, w.H, Kd);
+                       F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm, act, w.H, Kd, err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_prefill_down, dim3(D / BN2, mc), dim3(256), 0, s, Dn.p0, Dn.p1, (int)Dn.blocks_per_row, D,
                        w.H, Kd, w.chunks, w.n_chunks, w.offsets, w.Y);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_prefill_combine, dim3((D / 4 + 255) / 256, T), dim3(256), 0, s, w.Y, w.pos, w.w, k, D, out);
+    hipLaunchKernelGGL(k_prefill_combine, dim3((D / 4 + 255) / 256, T), dim3(256), 0, s, w.Y, w.pos, w.w, w.rs, k, D,
+                       out);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (out_ids) {
         if ((e = hipMemcpyAsync(out_ids, w.ids, (size_t)TK * 4, hipMemcpyDefault, s)) != hipSuccess) return e;
