@@ -788,27 +788,12 @@ __device__ __forceinline__ void sh_down_rows(const FusedArgs &a, uint8_t *smem, 
     uint4 *la = reinterpret_cast<uint4 *>(const_cast<float *>(hs) + 16 * nv);  // [nv][2]: limbs a, b
     float *lsp = reinterpret_cast<float *>(la + 2 * nv);                       // [nv]
     float *ps = sh_row_sums(smem, nk);                                         // [64]
-    if (tid < nv) {
+    if (tid < nv) {  // (limbs16: NaN / inf groups give sp = NaN, tiny groups are scaled first)
         float v[16];
         lds_x16(hs + tid * 16, v);
-        float m = 0.0f, sum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            m = fmaxf(m, fabsf(v[i]));
-            sum += v[i];
-        }
-        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
-        float sp = m * (1.0f / 32512.0f);
-        if (!(fabsf(sum) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);  // inf / NaN propagate
-        uint32_t pa[4] = {0u, 0u, 0u, 0u}, pb[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float t = v[i] * inv;
-            const float fa = rintf(t);
-            const float fb = fminf(rintf((t - fa) * 256.0f), 127.0f);
-            pa[i >> 2] |= ((uint32_t)(int)fa & 0xffu) << (8 * (i & 3));
-            pb[i >> 2] |= ((uint32_t)(int)fb & 0xffu) << (8 * (i & 3));
-        }
+        uint32_t pa[4], pb[4];
+        float sp, xs;
+        limbs16(v, pa, pb, sp, xs);
         la[2 * tid] = make_uint4(pa[0], pa[1], pa[2], pa[3]);
         la[2 * tid + 1] = make_uint4(pb[0], pb[1], pb[2], pb[3]);
         lsp[tid] = sp;
