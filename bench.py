@@ -896,8 +896,43 @@ def bench_gemma4(args):
                                                                c["layer_output_scale"], c["eps"], pool=pool)),
             1e6, "us/token", "config-4 block tokens; oracle lto_gemma4_moe_block (quantMatvecPar rows)")
     print(json.dumps(result), flush=True)
+    if args.timeline:
+        timeline_gemma4(args, c, w, X, dense, dn)
     for a in [X, dense] + [v for v in dn.values() if v is not None]:
         a.free()
+
+
+def timeline_gemma4(args, c, w, X, dense, dn, n=200):
+    """The Gemma4 block's phase timeline: n eager launches in a context
+    created with LT_PROFILE=timeline (rotated weight copies, the bench's x
+    pool, which the block overwrites in place), each followed by lt_sync;
+    writes lt_profile_report's text to args.timeline."""
+    import llmtoy_amd as lt
+    from llmtoy_amd import lib as ltlib
+    os.environ["LT_PROFILE"] = "timeline"
+    try:
+        ctx = lt.Context(0)
+    finally:
+        del os.environ["LT_PROFILE"]
+    base = lt.upload_moe(ctx, w)
+    copies = [base] + [tuple(t.clone() for t in base) for _ in range(args.copies - 1)]
+    for i in range(n):
+        r, g, d = copies[i % len(copies)]
+        ltlib.gemma4_moe_block(ctx, X.row(i % args.xpool), dense, r, g, d, K, G4_F, dn, c["layer_output_scale"],
+                               c["eps"])
+        ctx.sync()
+    rep = ctx.profile_report()
+    head = (f"Command (GPU box, repo root): python3 {' '.join(sys.argv)}\n"
+            f"Workload: Gemma4 block (config-4 layer, router-input prep, MoE tail in the same launch), {n} eager "
+            f"launches, {len(copies)} weight copies rotated, x pool of {args.xpool}; LT_PROFILE=timeline adds one "
+            f"store per workgroup at its end.\n\n")
+    with open(args.timeline, "w") as f:
+        f.write(head + rep)
+    log("timeline report:\n" + rep)
+    for cp in copies:
+        for t in cp:
+            t.free()
+    ctx.close()
     for cp in copies:
         for tns in cp:
             tns.free()
@@ -1023,8 +1058,8 @@ def main():
     ap.add_argument("--calibrate", action="store_true",
                     help="finish with device copies of known size (for rocprofv3 --pmc scaling)")
     ap.add_argument("--timeline", metavar="PATH", default=None,
-                    help="decode: afterwards run LT_PROFILE=timeline steps in a fresh context and write the "
-                         "library's per-phase report to PATH")
+                    help="decode, cfg4, gemma4: afterwards run LT_PROFILE=timeline steps in a fresh context and "
+                         "write the library's per-phase report to PATH")
     args = ap.parse_args()
 
     if args.gpus != 1:

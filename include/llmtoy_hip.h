@@ -300,10 +300,19 @@ int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float *dense_ffn,
  * x [d_model] is updated in place; dense_ffn is the dense FFN output after
  * post_ffw_norm_1.  down_exps_scale [n_experts] may be NULL (all ones).
  * router: F32 or Q8_0; experts: Q4_K, Q3_K, Q5_0, Q5_1 or IQ4_NL (device x:
- * 16-byte aligned).  With a Q8_0 router and the default tree sums, the
- * router-input prep runs inside the router kernel.  flags: LT_HOST_IO, LT_NORM_PRECISE,
- * LT_MOE_NORM_TOPK.  out_ids / out_w (may be NULL) get the selection and its
- * probabilities (router_out at the selected ids). */
+ * 16-byte aligned).  With a Q8_0 router, Q4_K experts and the default tree
+ * sums the whole block is one launch of the single-launch MoE kernel
+ * (router-input prep in its router blocks, the expert input in its gate/up
+ * blocks, the tail in one block after the down blocks); otherwise the
+ * router-input prep runs inside the Q8_0 router kernel, or in a norm
+ * kernel, and the experts and the tail in launches of their own.  The
+ * single launch adds the experts' rows with float atomics, so the last bits
+ * of x may differ run to run (as lt_moe_forward's default combine).  flags:
+ * LT_HOST_IO, LT_NORM_PRECISE, LT_MOE_NORM_TOPK, LT_MOE_UNFUSED (separate
+ * launches), LT_MOE_DETERMINISTIC (the separate launches, whose down kernel
+ * adds in slot order: bit-identical run to run).  out_ids / out_w (may be
+ * NULL) get the selection and its probabilities (router_out at the selected
+ * ids). */
 int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn, const lt_tensor *router,
                         const lt_tensor *gate_up, const lt_tensor *down, const float *pre_ffw_norm_2,
                         const float *router_scale, const float *down_exps_scale, const float *post_ffw_norm_2,

@@ -38,7 +38,7 @@ struct SpanStat {
     size_t n = 0;
     double total_ms = 0, min_ms = 1e30, max_ms = 0;
 };
-constexpr int kRoles = 7, kPhases = lt::kStamps - 1;
+constexpr int kRoles = 8, kPhases = lt::kStamps - 1;
 struct Profile {
     int mode = 0;  // 0 off, 1 spans, 2 spans + timeline
     std::vector<PendingSpan> pending;
@@ -259,13 +259,13 @@ void prof_harvest(lt_ctx *ctx) {
         // the first harvested launch: which in-group indices (block / 8) of
         // XCD group 0 shared a CU (HW_ID bits 8-15: CU, shader array,
         // engine), with their roles
-        static const char rc[] = "-RGDCsd";
+        static const char rc[] = "-RGDCsdT";
         std::map<uint32_t, std::string> cu;
         for (int b = 0; b < lt::kFusedBlocks; b += 8) {
             const uint64_t w = st[(size_t)b * lt::kStamps + lt::kStamps - 1];
             const int role = (int)(w & 0xff);
             char item[24];
-            snprintf(item, sizeof item, " %d%c", b >> 3, role >= 0 && role < 7 ? rc[role] : '?');
+            snprintf(item, sizeof item, " %d%c", b >> 3, role >= 0 && role < 8 ? rc[role] : '?');
             cu[(uint32_t)(w >> 40) & 0xffu] += item;
         }
         P.placement = "placement, XCD group 0, one launch (in-group index + role: R router, G gate/up, D down, "
@@ -440,7 +440,8 @@ int check_fused_err(lt_ctx *ctx) {
     return fail(ctx, LT_ERR_DEVICE,
                 "single-launch kernel: a hand-over wait timed out (code 0x%x: 1 gate/up logits, 2 down logits, 4 down "
                 "h records, 8 combine, 0x10 shared-FFN logits or last h word, 0x20 shared-FFN h, 0x40 dense-FFN h, "
-                "0x80 dense-FFN start values, 0x100 prefill f16 saturation; first recorded: block %d, site 0x%x, index "
+                "0x80 dense-FFN start values, 0x100 prefill f16 saturation, 0x200 Gemma4 tail; first recorded: block %d, "
+                "site 0x%x, index "
                 "%u, saw %u, expected epoch %u); outputs of that call are NaN",
                 v, (int)d[0] - 1, d[1], d[2], d[3], d[4]);
 }
@@ -1376,7 +1377,8 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     int rc;
     if ((rc = check_router(ctx, router, n, k))) return rc;
     if ((rc = check_experts(ctx, gate_up, down, n, d_expert, router->t.total_rows, k))) return rc;
-    if ((rc = check_norm(ctx, 1, (uint32_t)n, eps, flags, LT_HOST_IO | LT_NORM_PRECISE | LT_MOE_NORM_TOPK)))
+    if ((rc = check_norm(ctx, 1, (uint32_t)n, eps, flags,
+                         LT_HOST_IO | LT_NORM_PRECISE | LT_MOE_NORM_TOPK | LT_MOE_UNFUSED | LT_MOE_DETERMINISTIC)))
         return rc;
     const DevTensor &R = router->t, &GU = gate_up->t, &D = down->t;
     const size_t E = R.total_rows, Kd = D.cols;
@@ -1398,9 +1400,41 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
         (rc = io_in(ctx, host, ar, post_ffw_norm_2, n, &dp2)) || (rc = io_in(ctx, host, ar, post_ffw_norm, n, &dp)))
         return rc;
     float *xio = const_cast<float *>(dx);
+    const float inv_sqrt_d = 1.0f / sqrtf((float)n);
+    // the whole block in one launch of the single-launch MoE kernel: Q8_0
+    // router, Q4_K experts, the tree order of the norms (LT_NORM_PRECISE
+    // keeps the reference's sequential sums, LT_MOE_DETERMINISTIC the slot
+    // order of the experts' adds: the launches below)
+    if (!(flags & (LT_NORM_PRECISE | LT_MOE_UNFUSED | LT_MOE_DETERMINISTIC)) && R.type == LT_TYPE_Q8_0 &&
+        GU.type == LT_TYPE_Q4_K &&
+        D.type == LT_TYPE_Q4_K) {
+        const lt::GemmaBlock gb{drs, dpre, dds, dd, dp2, dp, xio, inv_sqrt_d, eps, layer_output_scale};
+        lt::FusedLayer L = fused_layer(R, GU, D, nullptr, nullptr, nullptr, k, d_expert, flags);
+        L.gb = &gb;
+        const lt::FusedPlan pl = lt::plan_moe_fused(L);
+        if (pl.ok && pl.gemma) {
+            if ((rc = ensure_fused(ctx)) || (rc = ensure(ctx, ctx->ids, kMaxK * 4)) ||
+                (rc = ensure(ctx, ctx->w, kMaxK * 4)))
+                return rc;
+            ctx->prof.stamps_pending = ctx->prof.stamps != nullptr;
+            rc = launch_rc(ctx,
+                           lt::launch_moe_fused(pl, L, nullptr, dx, act, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, nullptr,
+                                                0, 0, moe, (uint32_t *)ctx->ids.p, (float *)ctx->w.p, ctx->fsc,
+                                                ctx->stream),
+                           "gemma4_block_fused");
+            if (rc) return rc;
+            if ((rc = copy_routing_out(ctx, k, out_ids, out_w, host))) return rc;
+            if (host) {
+                LT_HIP(ctx, hipMemcpyAsync(x, xio, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+                LT_HIP(ctx, hipStreamSynchronize(ctx->stream));
+                prof_harvest(ctx);
+                return check_fused_err(ctx);
+            }
+            return LT_OK;
+        }
+    }
     // gemma4/forward.zig:405-414: expert input and router input from one RMS
     // of x -- inside the Q8_0 router with the tree sum, else a kernel of its own
-    const float inv_sqrt_d = 1.0f / sqrtf((float)n);
     const bool fuse_prep = !(flags & LT_NORM_PRECISE) && R.type == LT_TYPE_Q8_0;
     const lt::RouterPrep prep{drs, dpre, moe_in, inv_sqrt_d, eps};
     const float *rin = fuse_prep ? dx : router_in;
@@ -1458,7 +1492,7 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
                  "us from the first block's start; median over launches of the block median / the last block\n",
                  P.launches);
         o += line;
-        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "sh g/u", "sh down"};
+        static const char *roles[kRoles] = {"", "router", "gate/up", "down", "combine", "sh g/u", "sh down", "tail"};
         static const char *phases[kRoles][kPhases] = {
             {},
             {"block start", "first row chunk in", "logit published", "all row terms in"},
@@ -1467,7 +1501,8 @@ extern "C" size_t lt_profile_report(lt_ctx *ctx, char *buf, size_t len) {
              "shared h slice read", "shared rows added"},
             {"block start", "rows written"},
             {"block start", "h rows out"},
-            {"block start", nullptr, nullptr, nullptr, nullptr, "h slice read", "rows added"}};
+            {"block start", nullptr, nullptr, nullptr, nullptr, "h slice read", "rows added"},
+            {"block start", "down blocks done", "x written"}};
         snprintf(line, sizeof line, "%-9s %-22s %10s %10s\n", "role", "phase", "median", "last");
         o += line;
         for (int r = 1; r < kRoles; r++)

@@ -452,18 +452,32 @@ struct FusedPlan {
     int NCg;     // combining blocks per XCD group (deterministic combine only)
     int Ewait;   // logit rows published and waited for (>= E: placeholders cover start-value blocks)
     int shared;  // a shared FFN in the launch (blocks of its own)
+    int gemma;   // the Gemma4 block around the layer (GemmaBlock; one tail block in XCD group 0)
     int NSg;     // shared gate/up blocks per XCD group (the shared down rows are in the down blocks)
     int sg_rows; // shared h rows per shared gate/up block (<= 32)
     size_t lds;  // dynamic LDS bytes per block
 };
+// The Gemma4 MoE block around the layer (gemma4/forward.zig:403-497) in the
+// same launch: router input (x * (rms_inv / sqrt(n))) * raw_scale and
+// expert input (x * rms_inv) * pre_ffw_norm_2 from one RMS of x (math.zig:
+// 51-82, the tree order of the Q8_0 router's prep), down_exps_scale per
+// expert, and the tail x = (x + rmsnorm(dense + rmsnorm(moe, w2), w)) *
+// layer_output_scale (the tree order of the tail kernel).
+struct GemmaBlock {
+    const float *raw_scale, *pre_ffw_norm_2, *down_exps_scale, *dense, *post_ffw_norm_2, *post_ffw_norm;
+    float *x;  // read as the layer's input, written by the tail
+    float raw_global_scale, eps, layer_output_scale;
+};
 // A layer for the fused kernel.  MoE: R, GU, Dn set (E experts, k > 0),
 // optionally a shared FFN SG, SU, SD (Q8_0, S rows) added to the experts'
-// combine.  Dense FFN alone: R, GU, Dn null, k = 0, SG, SU, SD set.
+// combine, or the Gemma4 block around it (gb: Q8_0 router, no shared FFN,
+// atomic combine).  Dense FFN alone: R, GU, Dn null, k = 0, SG, SU, SD set.
 struct FusedLayer {
     const DevTensor *R, *GU, *Dn;
     const DevTensor *SG, *SU, *SD;
     int E, D, F, Kd, k, S;
     int det;  // slot-order combine (combining blocks; no shared FFN)
+    const GemmaBlock *gb = nullptr;
 };
 // Device memory the fused kernel hands results over through; zeroed once
 // when allocated and never cleared again (words carry launch epochs).
@@ -481,8 +495,9 @@ struct FusedScratch {
 // writes stamps[b * kStamps + i], wall-clock ticks (100 MHz) at the end of
 // phase i of its role, and stamps[b * kStamps + kStamps - 1] = role | slot
 // << 8 | XCD << 16 | HW_ID << 32 (role 0 none, 1 router, 2 gate/up, 3 down,
-// 4 combine, 5 shared-FFN gate/up, 6 shared-FFN down; HW_ID the hardware
-// register naming the CU, shader array and engine the block ran on).
+// 4 combine, 5 shared-FFN gate/up, 6 shared-FFN down, 7 Gemma4 tail; HW_ID
+// the hardware register naming the CU, shader array and engine the block
+// ran on).
 constexpr int kStamps = 8;
 enum : int { kStampStart = 0 };
 // router: 1 first row chunk in, 2 logit published, 3 all row terms in (Q8_0
@@ -490,7 +505,8 @@ enum : int { kStampStart = 0 };
 // record published; down: 1 logits seen, 2 weight loads issued, 3 h records
 // read, 4 adds issued, with a shared FFN 5 its h slice read, 6 its rows
 // added; combine: 1 rows written; shared gate/up: 1 h rows out; shared
-// down only (a group without a slot): 5 h slice read, 6 rows added
+// down only (a group without a slot): 5 h slice read, 6 rows added; Gemma4
+// tail: 1 down blocks done, 2 x written
 // Byte layout of that hand-over memory (a context's own allocation, or the
 // library's static scratch in lt_noalloc.hip): launch counters, 8 logit
 // copies, h record lines, partial-output lines, the XCD probe's ids, and

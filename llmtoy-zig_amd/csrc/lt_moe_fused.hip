@@ -85,6 +85,7 @@ namespace lt {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kFusedMaxD = 4096;            // d_model of the single-launch kernel
 constexpr int kDownRows = 64;               // output rows per down block (16 lane groups x 4)
 constexpr int kCombRows = 8;                // output rows per combining block
 constexpr uint64_t kWaitTicks = 20000000;   // 200 ms of the 100 MHz wall clock
@@ -111,7 +112,7 @@ struct FusedArgs {
     int rb;        // logit rows per router block: 2 or 4
     int NRg, SPG, G, NDg, NCg;
     int Ewait;  // logit rows published and waited for (E)
-    // the Gemma-style instance (SH) only
+    // the Gemma-style instances (SH 1 and 2) only
     const uint8_t *rq;   // Q8_0 router: quant plane [E][nb][32] (qrouter)
     const uint16_t *rd;  //   and f16 scale plane [E][nb]
     const uint8_t *sgq, *suq, *sdq;   // shared FFN (Q8_0) quant planes: gate, up [S][D/32], down [D][S/32]
@@ -120,6 +121,13 @@ struct FusedArgs {
     int qrouter, S;      // S = 0: no shared FFN
     int NSg;             // shared gate/up blocks per XCD group
     int sg_rows;         // shared h rows per shared gate/up block
+    // the Gemma4 block (gemma; the SH 2 instance): out is the experts' sum
+    // (moe), x the block's input, overwritten by the tail block
+    const float *g_raw_scale, *g_pre, *g_dscale, *g_dense, *g_w2, *g_w;
+    float *g_x;
+    float g_raw_global, g_eps, g_out_scale;
+    int gemma;
+    uint64_t *done;      // [k * NDg] down blocks' completion words, awaited by the tail block
 };
 
 // Phase stamps (LT_PROFILE=timeline), thread 0's: held in registers and
@@ -466,6 +474,69 @@ __device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t
     if (tid == 0) (void)epoch_commit(a.counters, bid, c0);
 }
 
+// ---------------------------------------------------------------- Gemma4 block
+// s + shfl_xor(s, 32), then 16, 8, 4, 2, 1 (the butterfly of the Q8_0
+// router's prep and of the norm kernels), bit for bit, over DPP and lane
+// swaps instead of LDS permutes: after the steps over lane bits 5..3 every
+// lane's value depends only on lane % 8, so row_ror:4 reads a lane holding
+// the value of lane ^ 4.
+__device__ __forceinline__ float butterfly_sum64(float s, bool first) {
+#pragma clang fp contract(off)
+    s = s + xor32(s, first);
+    s = s + xor16(s);
+    s = s + dpp<0x128>(s);  // row_ror:8 = lane ^ 8
+    s = s + dpp<0x124>(s);  // row_ror:4
+    s = s + dpp<0x4E>(s);   // quad_perm [2,3,0,1] = lane ^ 2
+    s = s + dpp<0xB1>(s);   // quad_perm [1,0,3,2] = lane ^ 1
+    return s;
+}
+
+// rms_inv of x (the Gemma4 block's input, D floats) in the order of the Q8_0
+// router kernel's prep (k_router_q8_0, 128 threads): thread t < 128 sums
+// x^2 over float4 chunks t, t + 128, ... in order, the 64-lane xor
+// butterfly, then wavefront 0's total plus wavefront 1's; 1 / sqrt(ss / n +
+// eps) with correctly rounded division and square root.  gemma_rms_load
+// issues the (at most 8) chunks of a thread at once (indices clamped: only
+// those in range are added, in the loop's order); gemma_rms_inv, called by
+// every thread of the block (a barrier inside), returns the same bits to
+// all.
+struct RmsLoads {
+    float4 v[8];
+};
+__device__ __forceinline__ void gemma_rms_load(const FusedArgs &a, int tid, RmsLoads &r) {
+    if (tid >= 128) return;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+    const int n4 = a.D / 4;  // <= 1024
+#pragma unroll
+    for (int m = 0; m < 8; m++) r.v[m] = x4[min(tid + 128 * m, n4 - 1)];
+}
+__device__ __forceinline__ float gemma_rms_inv(const FusedArgs &a, int tid, const RmsLoads &r) {
+#pragma clang fp contract(off)
+    __shared__ float red[2];
+    if (tid < 128) {
+        const int n4 = a.D / 4;
+        float ss = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            if (tid + 128 * m < n4) {
+                ss = ss + r.v[m].x * r.v[m].x;
+                ss = ss + r.v[m].y * r.v[m].y;
+                ss = ss + r.v[m].z * r.v[m].z;
+                ss = ss + r.v[m].w * r.v[m].w;
+            }
+        }
+        ss = butterfly_sum64(ss, p32_first(tid & 63));
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+    }
+    __syncthreads();
+    return 1.0f / sqrtf((red[0] + red[1]) / (float)a.D + a.g_eps);
+}
+__device__ __forceinline__ float gemma_rms_inv(const FusedArgs &a, int tid) {
+    RmsLoads r;
+    gemma_rms_load(a, tid, r);
+    return gemma_rms_inv(a, tid, r);
+}
+
 // ---------------------------------------------------------------- Q8_0 router
 // Rows 2 bid + [0, 2) of a Q8_0 router: thread t of half h = t >> 7 takes
 // block b = t & 127 (b < nb = D / 32 <= 128) of row 2 bid + h and computes
@@ -473,6 +544,7 @@ __device__ __forceinline__ void role_router_pair_one(const FusedArgs &a, uint8_t
 // groups of 8 products, the ordered 8-lane sum, times d) into LDS; the first
 // wavefront of each half adds the nb terms in block order (the reference's
 // running total) and the bias, and lanes 0-7 publish the logit's 8 copies.
+template <int GEM>
 __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem, int bid, int tid, int lane,
                                                Stamps &S) {
 #pragma clang fp contract(off)
@@ -481,6 +553,8 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
     const int nb = a.D >> 5;
     const int row = 2 * bid + h;
     const bool valid = row < a.E;
+    RmsLoads rms;  // (the Gemma4 block: x for the RMS first, so that it is not behind the weights)
+    if (GEM && a.gemma) gemma_rms_load(a, tid, rms);
     // every load unconditional (clamped row and block)
     const size_t blk = (size_t)(valid ? row : 0) * nb + (b < nb ? b : nb - 1);
     const uint4 q0 = ld16(a.rq + blk * 32), q1 = ld16(a.rq + blk * 32 + 16);
@@ -499,6 +573,20 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
     }
     const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
     const uint32_t c0 = epoch_peek(a.counters, bid);
+    if (GEM && a.gemma) {
+        // the router input (x * (rms_inv * raw_global)) * raw_scale, as the
+        // Q8_0 router kernel's prep forms it
+        float sv[32];
+        const float4 *sp = reinterpret_cast<const float4 *>(a.g_raw_scale + (b < nb ? b : nb - 1) * 32);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 v4 = sp[t];
+            sv[4 * t] = v4.x; sv[4 * t + 1] = v4.y; sv[4 * t + 2] = v4.z; sv[4 * t + 3] = v4.w;
+        }
+        const float raw_base = gemma_rms_inv(a, tid, rms) * a.g_raw_global;
+#pragma unroll
+        for (int e = 0; e < 32; e++) xv[e] = (xv[e] * raw_base) * sv[e];
+    }
     const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     float acc[8];
 #pragma unroll
@@ -848,7 +936,9 @@ __device__ __forceinline__ void sh_down_add(const FusedArgs &a, uint8_t *smem, i
 // WIDE (rows of 9-16 super-blocks): lane position pos covers pos and pos
 // + 32; the second position's weights are loaded as the first's products
 // finish, its x limbs are read from LDS after them.
-template <int PER, int WIDE>
+// GEM (the SH 2 instance): with a.gemma the activations are the Gemma4
+// block's expert input (x * rms_inv) * pre_ffw_norm_2 (math.zig:51-82).
+template <int PER, int WIDE, int GEM>
 __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
                                              int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
                                              Stamps &S) {
@@ -866,11 +956,21 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     uint32_t *lb = la + a.D / 4;
     float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
     float *lxs = lsp + a.D / 16;
+    const bool gem = GEM && a.gemma;
+    const float grms = gem ? gemma_rms_inv(a, tid) : 0.0f;  // (a.gemma is uniform: every thread or none)
     for (int t8 = tid; t8 < a.D / 8; t8 += kThreads) {  // one pass for D <= 2048
         const float *xsrc = a.x;
         const float4 f0 = *reinterpret_cast<const float4 *>(xsrc + 8 * t8);
         const float4 f1 = *reinterpret_cast<const float4 *>(xsrc + 8 * t8 + 4);
-        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        if (gem) {
+#pragma clang fp contract(off)
+            const float4 w0 = *reinterpret_cast<const float4 *>(a.g_pre + 8 * t8);
+            const float4 w1 = *reinterpret_cast<const float4 *>(a.g_pre + 8 * t8 + 4);
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = (v[i] * grms) * wv[i];
+        }
         float m = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
@@ -1025,6 +1125,125 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
     }
 }
 
+// ---------------------------------------------------------------- Gemma4 tail
+// One block (XCD group 0, after the down blocks) waits for every down
+// block's completion word, then x = (x + rmsnorm(dense + rmsnorm(moe, w2),
+// w)) * layer_output_scale (gemma4/forward.zig:482-497) over the D
+// elements, with the tail kernel's tree order for both sums of squares
+// (lt_norm.hip k_norm<kTail>, 1024 threads: thread t of the 1024 sums
+// v[i]^2 for i = t, t + 1024, ... in order, a 64-lane xor butterfly per
+// wavefront, then the 16 wavefront totals in order).  Thread t here plays
+// threads t + 256 m of those (m < 4; their wavefronts are w + 4 m) and holds
+// element t + 256 m' in register m' (m' < 16), so the element sums and the
+// four butterflies run from registers; every thread then adds the 16 totals
+// itself (one barrier per sum, red distinct per sum).  moe is read with
+// agent-scope loads (the down blocks added into it with device atomics).  A
+// wait that times out makes x NaN (error word 0x200).  (The last down block
+// to finish running the tail instead, found with a counter of finished
+// blocks, measured 1.7 us slower per block: the increments of one word
+// queue, and the operands below are not loaded ahead.)
+constexpr int kTailT = kFusedMaxD / kThreads;  // elements per thread
+__device__ __forceinline__ float tail_sum_sq(const float (&v)[kTailT], int n, int tid, int wave, int lane,
+                                             float *red) {
+#pragma clang fp contract(off)
+    float s[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        s[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kTailT / 4; j++)
+            if (tid + kThreads * (m + 4 * j) < n) s[m] = s[m] + v[m + 4 * j] * v[m + 4 * j];
+    }
+    const bool first = p32_first(lane);
+#pragma unroll
+    for (int m = 0; m < 4; m++) s[m] = butterfly_sum64(s[m], first);
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < 4; m++) red[wave + 4 * m] = s[m];
+    }
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) t = t + red[i];
+    return t;
+}
+__device__ __forceinline__ void role_gemma_tail(const FusedArgs &a, int bid, int tid, int wave, int lane,
+                                                Stamps &S) {
+#pragma clang fp contract(off)
+    constexpr int kT = kTailT;
+    __shared__ float red[32];
+    __shared__ int t_fail;
+    // the arguments in registers: the compiler would otherwise read them
+    // again from the kernel arguments (a scalar load and its wait) after the
+    // barriers and inside the branches below
+    typedef __attribute__((address_space(1))) float gfloat;
+    const int n = a.D, nd = a.k * a.NDg;
+    float eps = a.g_eps, osc = a.g_out_scale;
+    typedef __attribute__((address_space(1))) uint64_t gword;
+    const gfloat *out = (const gfloat *)a.out;
+    const gword *done = (const gword *)a.done;
+    float *gx = a.g_x;
+    asm volatile("" : "+s"(eps), "+s"(osc), "+s"(out), "+s"(done));  // (kept in registers)
+    const uint32_t ep = epoch_peek(a.counters, bid) + 1u;
+    // the operands that do not depend on the experts, loaded while the down
+    // blocks work (indices clamped: every load unconditional)
+    float dv[kT], w2v[kT], wv[kT], xv[kT];
+#pragma unroll
+    for (int m = 0; m < kT; m++) {
+        const int i = min(tid + kThreads * m, n - 1);
+        dv[m] = a.g_dense[i];
+        w2v[m] = a.g_w2[i];
+        wv[m] = a.g_w[i];
+        xv[m] = gx[i];
+    }
+    if (tid == 0) t_fail = 0;
+    __syncthreads();
+    {
+        const uint64_t t0 = wall_clock64();
+        bool ok = true;
+        for (int i = tid; i < nd && ok; i += kThreads) {
+            while (!tag_is(__hip_atomic_load(done + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), ep)) {
+                if (wall_clock64() - t0 > kWaitTicks) {
+                    ok = false;
+                    report_detail(a.err, bid, 0x200u, (uint32_t)i, 0, ep);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        if (!ok) t_fail = 1;
+    }
+    __syncthreads();
+    S.mark(1, tid);
+    float v[kT];
+#pragma unroll
+    for (int m = 0; m < kT; m++)
+        v[m] = __hip_atomic_load(out + min(tid + kThreads * m, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float r = 1.0f / sqrtf(tail_sum_sq(v, n, tid, wave, lane, red) / (float)n + eps);
+#pragma unroll
+    for (int m = 0; m < kT; m++) v[m] = dv[m] + (v[m] * r) * w2v[m];  // dense + rmsnorm(moe, w2)
+    r = 1.0f / sqrtf(tail_sum_sq(v, n, tid, wave, lane, red + 16) / (float)n + eps);
+    const bool fail = t_fail != 0;
+#pragma unroll
+    for (int m = 0; m < kT; m++) {
+        float y = xv[m] + (v[m] * r) * wv[m];
+        if (osc != 1.0f) y = y * osc;
+        v[m] = fail ? __int_as_float(0x7fc00000) : y;
+        asm volatile("" : "+v"(v[m]));  // (computed here, not inside each store's branch)
+    }
+    // Agent-scope stores: written through, not left dirty in the L2 for the
+    // end of the kernel to write back (0.3 us per block).  The lane's global
+    // address is an opaque register value, which the compiler cannot re-derive
+    // from the kernel arguments (a scalar load and a wait) before each store.
+    gfloat *px = (gfloat *)(gx + tid);
+    asm volatile("" : "+v"(px));
+#pragma unroll
+    for (int m = 0; m < kT; m++)
+        if (tid + kThreads * m < n) __hip_atomic_store(px + kThreads * m, v[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0 && fail) report_timeout(a.err, 0x200u);
+    S.mark(2, tid);
+}
+
 // ---------------------------------------------------------------- down
 // Sums V values per lane over each aligned group of 16 lanes, transposed:
 // returns the group's total of value index (lane & 15) >> log2(16 / V).
@@ -1094,7 +1313,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     uint32_t *rec_b = rec_a + G * 4;
     float *rec_sp = reinterpret_cast<float *>(rec_b + G * 4);
     float *rec_xs = rec_sp + G;
-    const bool fill = FILL && a.S > 0 && s < 8;
+    const bool fill = FILL == 1 && a.S > 0 && s < 8;
     __shared__ int sh_fail;
     ShStage sst;
     if (fill) sh_stage_load(a, sst, bid & 7, j, tid);
@@ -1225,7 +1444,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         a.ids_out[tid] = s_ids[tid];
         a.w_out[tid] = s_w[tid];
     }
-    const float ws = s_w[s];
+    const float ws = FILL == 2 && a.gemma && a.g_dscale ? a.g_dscale[e] * s_w[s] : s_w[s];  // (down_exps_scale[e] * p_e, gemma4/forward.zig:477)
     float v[RPG];
 #pragma unroll
     for (int i = 0; i < RPG; i++) v[i] = 0.0f;
@@ -1270,6 +1489,11 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     // (the start values of these rows were awaited with the h records; the
     // row sums are behind the barrier after the records)
     if (fill) sh_down_add(a, smem, bid & 7, j, sh_fail != 0 || *s_fail != 0, tid, S);
+    if (FILL == 2 && a.gemma) {  // the Gemma4 block's tail waits for every down block's adds
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's adds acknowledged
+        __syncthreads();
+        if (tid == 0) hand_put(a.done + (size_t)s * a.NDg + j, 1u, ep);
+    }
 }
 
 // ---------------------------------------------------------------- combine
@@ -1322,12 +1546,15 @@ __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep,
     S.mark(1, tid);
 }
 
-// SH: the Gemma-style instance (Q8_0 router role, shared-FFN roles); the
-// others hold only the F32 router roles and the experts' roles, and WIDE
-// (rows over 2048) only the router variants those rows use: less code per
-// instance (the roles of a CU's four workgroups share its instruction cache).
+// SH 1: the Gemma-style instance (Q8_0 router role, shared-FFN roles); SH
+// 2: the Gemma4 block (Q8_0 router with the block's input norms, expert
+// input norm and scales, the tail role; no shared FFN); SH 0 holds only the
+// F32 router roles and the experts' roles, and WIDE (rows over 2048) only
+// the router variants those rows use: less code per instance (the roles of
+// a CU's four workgroups share its instruction cache; the Gemma4 code in the
+// SH 1 instance made config 4 0.7 us slower).
 template <int PER, int WIDE, int SH>
-// (SH: at most 128 VGPRs, four blocks per SIMD, for the whole grid to be
+// (SH 1, 2: at most 128 VGPRs, four blocks per SIMD, for the whole grid to be
 // resident; the others fit without the bound, which costs config 3 0.07 us)
 __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1358,7 +1585,7 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
     int u = i;
     if (u < a.NRg) {
         if (SH && a.qrouter)
-            role_router_q8(a, smem, bid, tid, lane, S);
+            role_router_q8<SH == 2>(a, smem, bid, tid, lane, S);
         else if (!WIDE && a.rb == 2)
             role_router_pair_one(a, smem, bid, tid, wave, lane, S);
         else if (WIDE)
@@ -1367,12 +1594,12 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
             role_router(a, smem, bid, tid, wave, lane, S);
         role = 1;
     } else if ((u -= a.NRg) < a.NSg) {
-        if (SH) role_shared_gate_up(a, smem, x, u, bid, tid, wave, lane, S);
+        if (SH == 1) role_shared_gate_up(a, smem, x, u, bid, tid, wave, lane, S);
         role = 5;
     } else if ((u -= a.NSg) < a.SPG * a.G) {
         const int s = x + 8 * (u / a.G);
         if (s < a.k) {
-            role_gate_up<PER, WIDE>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            role_gate_up<PER, WIDE, SH == 2>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, 1u);  // logits
             role = 2u | (uint32_t)s << 8;
         }
@@ -1382,7 +1609,7 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
             role_down<PER, 4, SH>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, (uint32_t)s_fail << 1);  // 2 logits, 4 h records
             role = 3u | (uint32_t)s << 8;
-        } else if (SH && a.S > 0 && u < a.NDg) {  // a group without a slot still adds its shared rows
+        } else if (SH == 1 && a.S > 0 && u < a.NDg) {  // a group without a slot still adds its shared rows
             const uint32_t ep = epoch_peek(a.counters, bid) + 1u;
             ShStage sst;
             sh_stage_load(a, sst, x, u, tid);
@@ -1399,10 +1626,13 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
         role_combine(a, &s_ep, bid, 8 * u + x, tid, S);
         role = 4;
+    } else if (SH == 2 && a.gemma && x == 0 && u == a.NCg) {  // the Gemma4 block's tail
+        role_gemma_tail(a, bid, tid, wave, lane, S);
+        role = 7;
     }
     // no role in this configuration, or a shared-FFN role: keep the counter in step
-    // (role 5 and 6 carry no slot bits; 2 and 3 do, and commit in their role)
-    if ((role == 0 || role == 5 || role == 6) && tid == 0)
+    // (roles 5-7 carry no slot bits; 2 and 3 do, and commit in their role)
+    if ((role == 0 || (role >= 5 && role <= 7)) && tid == 0)
         (void)epoch_commit(a.counters, bid, epoch_peek(a.counters, bid));
     if (S.row && tid == 0) {
         uint32_t xcc, hw;  // the XCD and the CU this block ran on
@@ -1486,6 +1716,10 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         pl.per = 2;
         pl.rb = 2;
     }
+    if (L.gb) {  // the Gemma4 block around the layer: one tail block more in XCD group 0
+        if (!moe || sh || L.det || !pl.qrouter || used + 1 > kFusedBlocks / 8) return pl;
+        pl.gemma = 1;
+    }
     if (sh) {
         // the shared FFN's gate/up rows in blocks of their own (the group's
         // blocks the experts leave free, at most 32 h rows each), its down
@@ -1560,6 +1794,21 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     fa.qrouter = pl.qrouter;
     fa.S = pl.shared ? L.S : 0;
     fa.NSg = pl.shared ? pl.NSg : 0;
+    if (pl.gemma) {
+        const GemmaBlock &g = *L.gb;
+        fa.gemma = 1;
+        fa.g_raw_scale = g.raw_scale;
+        fa.g_pre = g.pre_ffw_norm_2;
+        fa.g_dscale = g.down_exps_scale;
+        fa.g_dense = g.dense;
+        fa.g_w2 = g.post_ffw_norm_2;
+        fa.g_w = g.post_ffw_norm;
+        fa.g_x = g.x;
+        fa.g_raw_global = g.raw_global_scale;
+        fa.g_eps = g.eps;
+        fa.g_out_scale = g.layer_output_scale;
+        fa.done = sc.pl;  // (the partial lines: unused without the slot-order combine)
+    }
     fa.sg_rows = pl.sg_rows;
     fa.E = moe ? L.E : 0;
     fa.D = L.D;
@@ -1588,12 +1837,14 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // blocks' share of the grid (atomic combine) measured 0.15 us slower per
     // layer -- more h record reads and atomics -- though each block's
     // products halve
-    const bool sh = pl.shared || pl.qrouter;
+    const int mode = pl.gemma ? 2 : (pl.shared || pl.qrouter) ? 1 : 0;
     if (pl.wide) {
-        if (sh) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl, s) : launch_fused_t<4, 1, 1>(fa, pl, s);
+        if (mode == 2) return pl.per == 2 ? launch_fused_t<2, 1, 2>(fa, pl, s) : launch_fused_t<4, 1, 2>(fa, pl, s);
+        if (mode == 1) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl, s) : launch_fused_t<4, 1, 1>(fa, pl, s);
         return pl.per == 2 ? launch_fused_t<2, 1, 0>(fa, pl, s) : launch_fused_t<4, 1, 0>(fa, pl, s);
     }
-    if (sh) return pl.per == 2 ? launch_fused_t<2, 0, 1>(fa, pl, s) : launch_fused_t<4, 0, 1>(fa, pl, s);
+    if (mode == 2) return pl.per == 2 ? launch_fused_t<2, 0, 2>(fa, pl, s) : launch_fused_t<4, 0, 2>(fa, pl, s);
+    if (mode == 1) return pl.per == 2 ? launch_fused_t<2, 0, 1>(fa, pl, s) : launch_fused_t<4, 0, 1>(fa, pl, s);
     return pl.per == 2 ? launch_fused_t<2, 0, 0>(fa, pl, s) : launch_fused_t<4, 0, 0>(fa, pl, s);
 }
 

@@ -348,14 +348,17 @@ def moe_tail(ctx: Context, x, moe, dense_ffn, post_ffw_norm_2, post_ffw_norm, la
 
 def gemma4_moe_block(ctx: Context, x, dense_ffn, router: Tensor, gate_up: Tensor, down: Tensor, k: int,
                      d_expert: int, norms: dict, layer_output_scale=1.0, eps=1e-6, act=ACT_GELU_TANH,
-                     precise=False, norm_topk=False, out_ids=None, out_w=None):
+                     precise=False, norm_topk=False, out_ids=None, out_w=None, unfused=False, deterministic=False):
     """The Gemma4 MoE block of one token (gemma4/forward.zig:403-497); x is
     updated in place.  norms: pre_ffw_norm_2, router_scale, down_exps_scale
-    (or None), post_ffw_norm_2, post_ffw_norm."""
+    (or None), post_ffw_norm_2, post_ffw_norm.  unfused: separate launches
+    even where the single-launch kernel covers the block; deterministic: the
+    separate launches' slot-order adds (bit-identical run to run)."""
     ds = norms.get("down_exps_scale")
     vecs = [norms["pre_ffw_norm_2"], norms["router_scale"], ds, norms["post_ffw_norm_2"], norms["post_ffw_norm"]]
     fl = _norm_io(ctx, x, dense_ffn, *vecs, out_ids, out_w)
     fl |= (LT_NORM_PRECISE if precise else 0) | (LT_MOE_NORM_TOPK if norm_topk else 0)
+    fl |= (LT_MOE_UNFUSED if unfused else 0) | (LT_MOE_DETERMINISTIC if deterministic else 0)
     ctx._check(ctx.lib.lt_gemma4_moe_block(ctx.ptr, _ptr(x)[0], _ptr(dense_ffn)[0], router.handle, gate_up.handle,
                                            down.handle, *(_ptr(v)[0] for v in vecs), layer_output_scale, eps, k,
                                            d_expert, act, fl, _ptr(out_ids)[0], _ptr(out_w)[0]))
