@@ -490,6 +490,55 @@ def test_gpu_moe_expert_counts_and_k(ctx, pool, E, k):
         t.free()
 
 
+def test_gpu_probability_tie_selects_on_logits(ctx, pool):
+    """Two distinct logits whose probabilities are one float: the reference
+    (ops/moe.zig:48-52: softmax, then topK's strict '>' on the probabilities,
+    :80-91) keeps the lower index; the GPU selects on the logits and keeps the
+    larger logit.  x is one-hot, so each logit is exactly router[e, 0]: expert
+    7 at 4 is the maximum; experts 3 and 5 at 1 and the next float above 1
+    both give l - 4 = -3 (the odd ulp rounds to even), so both weigh 0.045.
+    The GPU returns [7, 5] with weights equal to the reference's [p7, p3]
+    (p3 == p5), on every path, and its output equals the reference's on the
+    weights with experts 3 and 5 swapped (the same expert data under the
+    same weight; with expert 3's data the output differs by far more than
+    the tolerance)."""
+    D, E, F, k = 512, 16, 256, 2
+    w = synth.moe_weights(81, D, E, F)
+    router = np.zeros((E, D), np.float32)
+    router[:, 0] = -8.0
+    router[7, 0] = 4.0
+    router[3, 0] = 1.0
+    router[5, 0] = np.nextafter(np.float32(1.0), np.float32(2.0))
+    w = dataclasses.replace(w, router=router)
+    x = np.zeros(D, np.float32)
+    x[0] = 1.0
+    _, rids, rw, agree = orc.moe_forward(w, x, k, pool=pool)
+    assert not agree and rids.tolist() == [7, 3]
+    assert np.float32(1.0) - np.float32(4.0) == router[5, 0] - np.float32(4.0) and rw[1] > 0.04
+    # the same experts under the reference's rule: 3 and 5 swapped (router rows included)
+    sw = w.gate_up.copy().reshape(E, 2 * F, -1)
+    sw[[3, 5]] = sw[[5, 3]]
+    sd = w.down.copy().reshape(E, D, -1)
+    sd[[3, 5]] = sd[[5, 3]]
+    rs = router.copy()
+    rs[[3, 5]] = rs[[5, 3]]
+    ws = dataclasses.replace(w, router=rs, gate_up=sw.reshape(w.gate_up.shape), down=sd.reshape(w.down.shape))
+    ref_sw, rids_sw, _, _ = orc.moe_forward(ws, x, k, pool=pool)
+    assert rids_sw.tolist() == [7, 3]  # expert 5's data, now at index 3
+    assert rel_l2(ref_sw, orc.moe_forward(w, x, k, pool=pool)[0]) > 10 * REL_L2
+    router_t, gate_up, down = lt.upload_moe(ctx, w)
+    for kw in ({}, {"unfused": True}, {"deterministic": True}):
+        out = np.zeros(D, np.float32)
+        ids = np.zeros(k, np.uint32)
+        wts = np.zeros(k, np.float32)
+        ctx.moe_forward(out, x, router_t, gate_up, down, k, F, out_ids=ids, out_w=wts, **kw)
+        assert ids.tolist() == [7, 5], (kw, ids)
+        assert max_rel(wts, rw) < 1e-6, (kw, wts, rw)
+        assert rel_l2(out, ref_sw) <= REL_L2, kw
+    for t in (router_t, gate_up, down):
+        t.free()
+
+
 def test_gpu_router_duplicate_rows_lowest_index_wins(ctx):
     g = np.random.default_rng(4)
     w = g.standard_normal((64, 256)).astype(np.float32) * 0.02
