@@ -110,8 +110,8 @@ __device__ __forceinline__ void role_gate_up(const FfnArgs &a, float *xs, uint32
         for (int c = 0; c < CU; c++) {
             const int u = min(lane + 64 * c, nu - 1);
             const size_t blk = (size_t)j * a.nbD + (u >> 1);
-            qg[p][c] = ldg16(a.gq + blk * 32 + (u & 1) * 16);
-            qu[p][c] = ldg16(a.uq + blk * 32 + (u & 1) * 16);
+            qg[p][c] = ldg16_nt(a.gq + blk * 32 + (u & 1) * 16);  // (non-temporal: read once)
+            qu[p][c] = ldg16_nt(a.uq + blk * 32 + (u & 1) * 16);
             dg[p][c] = a.gd[blk];
             du[p][c] = a.ud[blk];
         }
