@@ -989,8 +989,12 @@ int moe_dev(lt_ctx *ctx, float *out, const float *x, const DevTensor &R, const f
             uint32_t k, uint32_t d_expert, uint32_t act, uint32_t flags) {
     int rc;
     const size_t Kd = D.cols;
+    // (Q4_K experts, or the APEX formats: Q3_K gate/up, IQ4_NL / Q5_0 / Q5_1
+    // down; the plan checks the shapes)
     const bool fusable = !(flags & LT_MOE_UNFUSED) && (R.type == LT_TYPE_F32 || R.type == LT_TYPE_Q8_0) &&
-                         GU.type == LT_TYPE_Q4_K && D.type == LT_TYPE_Q4_K;
+                         (GU.type == LT_TYPE_Q4_K || GU.type == LT_TYPE_Q3_K) &&
+                         (D.type == LT_TYPE_Q4_K || D.type == LT_TYPE_IQ4_NL || D.type == LT_TYPE_Q5_0 ||
+                          D.type == LT_TYPE_Q5_1);
     // the shared FFN inside the same launch: Q8_0, unpadded down, atomic combine
     bool sh_in = fusable && sh_gate && shared_fusable(sh_gate->t, sh_up->t, sh_down->t) &&
                  !(flags & LT_MOE_DETERMINISTIC);
@@ -1402,12 +1406,12 @@ extern "C" int lt_gemma4_moe_block(lt_ctx *ctx, float *x, const float *dense_ffn
     float *xio = const_cast<float *>(dx);
     const float inv_sqrt_d = 1.0f / sqrtf((float)n);
     // the whole block in one launch of the single-launch MoE kernel: Q8_0
-    // router, Q4_K experts, the tree order of the norms (LT_NORM_PRECISE
+    // router, Q4_K or APEX experts, the tree order of the norms (LT_NORM_PRECISE
     // keeps the reference's sequential sums, LT_MOE_DETERMINISTIC the slot
     // order of the experts' adds: the launches below)
     if (!(flags & (LT_NORM_PRECISE | LT_MOE_UNFUSED | LT_MOE_DETERMINISTIC)) && R.type == LT_TYPE_Q8_0 &&
-        GU.type == LT_TYPE_Q4_K &&
-        D.type == LT_TYPE_Q4_K) {
+        (GU.type == LT_TYPE_Q4_K || GU.type == LT_TYPE_Q3_K) &&
+        (D.type == LT_TYPE_Q4_K || D.type == LT_TYPE_IQ4_NL || D.type == LT_TYPE_Q5_0 || D.type == LT_TYPE_Q5_1)) {
         const lt::GemmaBlock gb{drs, dpre, dds, dd, dp2, dp, xio, inv_sqrt_d, eps, layer_output_scale};
         lt::FusedLayer L = fused_layer(R, GU, D, nullptr, nullptr, nullptr, k, d_expert, flags);
         L.gb = &gb;

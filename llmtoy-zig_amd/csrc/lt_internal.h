@@ -453,6 +453,7 @@ struct FusedPlan {
     int Ewait;   // logit rows published and waited for (>= E: placeholders cover start-value blocks)
     int shared;  // a shared FFN in the launch (blocks of its own)
     int gemma;   // the Gemma4 block around the layer (GemmaBlock; one tail block in XCD group 0)
+    int fmt;     // APEX expert formats (Q3_K gate/up, IQ4_NL / Q5_0 / Q5_1 down): the format instance
     int NSg;     // shared gate/up blocks per XCD group (the shared down rows are in the down blocks)
     int sg_rows; // shared h rows per shared gate/up block (<= 32)
     size_t lds;  // dynamic LDS bytes per block

@@ -75,6 +75,7 @@
 #include "lt_internal.h"
 #include "lt_topk.h"
 #include "lt_limbs.h"
+#include "lt_fmt.h"
 
 #include <math.h>
 
@@ -128,6 +129,11 @@ struct FusedArgs {
     float g_raw_global, g_eps, g_out_scale;
     int gemma;
     uint64_t *done;      // [k * NDg] down blocks' completion words, awaited by the tail block
+    // the format instance (SH 3): the expert tensors' types and their other
+    // planes (Q3_K gate/up: qs gu_hdr, hmask gu_qs, scales gu_p2, d gu_p3;
+    // IQ4_NL / Q5_0 / Q5_1 down: qs dn_hdr, then dn_qs, dn_p2)
+    int gu_type, dn_type;
+    const uint8_t *gu_p2, *gu_p3, *dn_p2;
 };
 
 // Phase stamps (LT_PROFILE=timeline), thread 0's: held in registers and
@@ -927,35 +933,57 @@ __device__ __forceinline__ void sh_down_add(const FusedArgs &a, uint8_t *smem, i
 }
 
 // ---------------------------------------------------------------- gate/up
-// Block: slot s, h indices j0 = 16 jg + [0, 16), jg < G = Kd/16 (indices
-// >= F are the zero padding of the down K); its record is line s*G + jg.
-// Wavefront w: pairs j0 + 4w + [0, 4).  Lanes 0-31 take the gate row, lanes
-// 32-63 the up row; lane & 31 = (super-block, sub-block pair) position, so
-// a lane reads 32 bytes of quants per row and one header word (the quad's
-// four words are shared over DPP).
-// WIDE (rows of 9-16 super-blocks): lane position pos covers pos and pos
-// + 32; the second position's weights are loaded as the first's products
-// finish, its x limbs are read from LDS after them.
-// GEM (the SH 2 instance): with a.gemma the activations are the Gemma4
-// block's expert input (x * rms_inv) * pre_ffw_norm_2 (math.zig:51-82).
-template <int PER, int WIDE, int GEM>
-__device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
-                                             int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
-                                             Stamps &S) {
-    const int G = a.nsbd * 16;
-    const int g = s * G + jg;  // record line
-    const int j0 = jg * 16;
-    const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
-    const bool lane_on = pos < 4 * a.nsb;
-    const bool first = p32_first(lane);
-    const uint32_t c0 = epoch_peek(a.counters, bid);
-    // activation limbs, once per block: thread t converts elements 8t + [0, 8)
-    // (half of group t / 2) into LDS; each lane then reads its window's 4
-    // groups.  LDS: limb-a words [D/4], limb-b words [D/4], sp [D/16], xs [D/16].
-    uint32_t *la = reinterpret_cast<uint32_t *>(smem + 64);
-    uint32_t *lb = la + a.D / 4;
-    float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
-    float *lxs = lsp + a.D / 16;
+// The block's 16 h values (s_h, written by every wavefront before the call)
+// as one limb record line g: a-words, b-words, scale, sum (kRecWords words,
+// group-local hand-over words); a routing timeout publishes a NaN record.
+__device__ __forceinline__ void publish_h_record(const FusedArgs &a, const float *s_h, const int *s_fail, int g,
+                                                 uint32_t ep, int tid, int wave, int lane, Stamps &S) {
+    __syncthreads();
+    if (wave == 0) {
+        // the 16 h values as one limb record: lanes 0..15 own one value each
+        const float hv = lane < 16 ? s_h[lane] : 0.0f;
+        float m = fabsf(hv);
+        m = fmaxf(m, dpp<0x128>(m));
+        m = fmaxf(m, dpp<0x124>(m));
+        m = fmaxf(m, dpp<0x122>(m));
+        m = fmaxf(m, dpp<0x121>(m));
+        float xs = hv;
+        xs += dpp<0x128>(xs);
+        xs += dpp<0x124>(xs);
+        xs += dpp<0x122>(xs);
+        xs += dpp<0x121>(xs);
+        xs = __shfl(xs, 0, 64);
+        m = __shfl(m, 0, 64);
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        float sp = m * (1.0f / 32512.0f);
+        if (!(fabsf(xs) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);
+        const float tt = hv * inv;
+        const float fa = rintf(tt);
+        const float fb = fminf(rintf((tt - fa) * 256.0f), 127.0f);
+        uint32_t pa = ((uint32_t)(int)fa & 0xffu) << (8 * (lane & 3));
+        uint32_t pb = ((uint32_t)(int)fb & 0xffu) << (8 * (lane & 3));
+        pa |= dppw<0xB1>(pa);
+        pa |= dppw<0x4E>(pa);
+        pb |= dppw<0xB1>(pb);
+        pb |= dppw<0x4E>(pb);
+        // record word i: a-words from lanes 0,4,8,12; b-words; sp; xs
+        const int src = lane < 4 ? 4 * lane : (lane < 8 ? 4 * (lane - 4) : 0);
+        const uint32_t ga = (uint32_t)__shfl((int)pa, src, 64);
+        const uint32_t gb = (uint32_t)__shfl((int)pb, src, 64);
+        uint32_t word = lane < 4 ? ga : (lane < 8 ? gb : (lane == 8 ? __float_as_uint(sp) : __float_as_uint(xs)));
+        if (*s_fail) word = lane < 8 ? 0u : 0x7fc00000u;  // routing timed out: NaN record
+        if (lane < kRecWords) hand_put_group(a.hl + (size_t)g * 16 + lane, word, ep, a.local);
+        S.mark(4, tid);
+    }
+}
+
+// The block's activations as limb groups in LDS (la, lb [D / 4] words, lsp,
+// lxs [D / 16]): thread t converts elements 8t + [0, 8) (half of group
+// t / 2).  GEM: with a.gemma, the Gemma4 block's expert input (x * rms_inv)
+// * pre_ffw_norm_2 (math.zig:51-82) is formed first.
+template <int GEM>
+__device__ __forceinline__ void stage_x_limbs(const FusedArgs &a, uint32_t *la, uint32_t *lb, float *lsp, float *lxs,
+                                              int tid) {
     const bool gem = GEM && a.gemma;
     const float grms = gem ? gemma_rms_inv(a, tid) : 0.0f;  // (a.gemma is uniform: every thread or none)
     for (int t8 = tid; t8 < a.D / 8; t8 += kThreads) {  // one pass for D <= 2048
@@ -996,6 +1024,39 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
             lxs[t8 >> 1] = xs;
         }
     }
+}
+
+
+// Block: slot s, h indices j0 = 16 jg + [0, 16), jg < G = Kd/16 (indices
+// >= F are the zero padding of the down K); its record is line s*G + jg.
+// Wavefront w: pairs j0 + 4w + [0, 4).  Lanes 0-31 take the gate row, lanes
+// 32-63 the up row; lane & 31 = (super-block, sub-block pair) position, so
+// a lane reads 32 bytes of quants per row and one header word (the quad's
+// four words are shared over DPP).
+// WIDE (rows of 9-16 super-blocks): lane position pos covers pos and pos
+// + 32; the second position's weights are loaded as the first's products
+// finish, its x limbs are read from LDS after them.
+// GEM (the SH 2 instance): with a.gemma the activations are the Gemma4
+// block's expert input (x * rms_inv) * pre_ffw_norm_2 (math.zig:51-82).
+template <int PER, int WIDE, int GEM>
+__device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
+                                             int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
+                                             Stamps &S) {
+    const int G = a.G;  // records per slot (down K / 16)
+    const int g = s * G + jg;  // record line
+    const int j0 = jg * 16;
+    const int half = lane >> 5, pos = lane & 31, sb = pos >> 2, p = pos & 3;
+    const bool lane_on = pos < 4 * a.nsb;
+    const bool first = p32_first(lane);
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    // activation limbs, once per block: thread t converts elements 8t + [0, 8)
+    // (half of group t / 2) into LDS; each lane then reads its window's 4
+    // groups.  LDS: limb-a words [D/4], limb-b words [D/4], sp [D/16], xs [D/16].
+    uint32_t *la = reinterpret_cast<uint32_t *>(smem + 64);
+    uint32_t *lb = la + a.D / 4;
+    float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
+    float *lxs = lsp + a.D / 16;
+    stage_x_limbs<GEM>(a, la, lb, lsp, lxs, tid);
     if (tid == 0) *s_ep = epoch_commit(a.counters, bid, c0);
     __syncthreads();  // limbs (and s_ep)
     auto read_limbs = [&](Limbs &xl, int gi) {  // gi: first of the window's 4 groups
@@ -1086,43 +1147,86 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
         const int r = lane >> 3;
         s_h[wave * 4 + r] = (jb + r < a.F) ? act_apply((uint32_t)a.act, t) * u : 0.0f;
     }
-    __syncthreads();
-    if (wave == 0) {
-        // the 16 h values as one limb record: lanes 0..15 own one value each
-        const float hv = lane < 16 ? s_h[lane] : 0.0f;
-        float m = fabsf(hv);
-        m = fmaxf(m, dpp<0x128>(m));
-        m = fmaxf(m, dpp<0x124>(m));
-        m = fmaxf(m, dpp<0x122>(m));
-        m = fmaxf(m, dpp<0x121>(m));
-        float xs = hv;
-        xs += dpp<0x128>(xs);
-        xs += dpp<0x124>(xs);
-        xs += dpp<0x122>(xs);
-        xs += dpp<0x121>(xs);
-        xs = __shfl(xs, 0, 64);
-        m = __shfl(m, 0, 64);
-        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
-        float sp = m * (1.0f / 32512.0f);
-        if (!(fabsf(xs) <= 3.0e38f) || !(m <= 3.0e38f)) sp = __int_as_float(0x7fc00000);
-        const float tt = hv * inv;
-        const float fa = rintf(tt);
-        const float fb = fminf(rintf((tt - fa) * 256.0f), 127.0f);
-        uint32_t pa = ((uint32_t)(int)fa & 0xffu) << (8 * (lane & 3));
-        uint32_t pb = ((uint32_t)(int)fb & 0xffu) << (8 * (lane & 3));
-        pa |= dppw<0xB1>(pa);
-        pa |= dppw<0x4E>(pa);
-        pb |= dppw<0xB1>(pb);
-        pb |= dppw<0x4E>(pb);
-        // record word i: a-words from lanes 0,4,8,12; b-words; sp; xs
-        const int src = lane < 4 ? 4 * lane : (lane < 8 ? 4 * (lane - 4) : 0);
-        const uint32_t ga = (uint32_t)__shfl((int)pa, src, 64);
-        const uint32_t gb = (uint32_t)__shfl((int)pb, src, 64);
-        uint32_t word = lane < 4 ? ga : (lane < 8 ? gb : (lane == 8 ? __float_as_uint(sp) : __float_as_uint(xs)));
-        if (*s_fail) word = lane < 8 ? 0u : 0x7fc00000u;  // routing timed out: NaN record
-        if (lane < kRecWords) hand_put_group(a.hl + (size_t)g * 16 + lane, word, ep, a.local);
-        S.mark(4, tid);
+    publish_h_record(a, reinterpret_cast<const float *>(smem), s_fail, g, ep, tid, wave, lane, S);
+}
+
+// Q3_K gate/up rows (the format instance): the block's 16 h rows j0 + r of
+// slot s as 32 D / 128 tasks (row r, gate or up, super-block half hu: the
+// 128 weights of qs[32 h ..] with all of hmask, the scales and d); task t =
+// tid + 256 c (c < 4: D <= 4096) loads its half up front, then adds its
+// four 32-element groups against the limbs (lt_fmt.h q3k_group_dot) into
+// part[t]; thread 2r + gu sums row r's halves in order, and h = act(gate) *
+// up goes out as the record (publish_h_record).  Rows past F give h = 0.
+template <int PER, int GEM>
+__device__ __forceinline__ void role_gate_up_q3k(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
+                                                 int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
+                                                 Stamps &S) {
+    const int g = s * a.G + jg;  // record line
+    const int j0 = jg * 16;
+    const uint32_t c0 = epoch_peek(a.counters, bid);
+    uint32_t *la = reinterpret_cast<uint32_t *>(smem + 64);
+    uint32_t *lb = la + a.D / 4;
+    float *lsp = reinterpret_cast<float *>(lb + a.D / 4);
+    float *lxs = lsp + a.D / 16;
+    float *part = lxs + a.D / 16;  // [32 D / 128]
+    stage_x_limbs<GEM>(a, la, lb, lsp, lxs, tid);
+    if (tid == 0) *s_ep = epoch_commit(a.counters, bid, c0);
+    __syncthreads();  // limbs (and s_ep)
+    const uint32_t ep = *s_ep;
+    if (wave == 0) {  // only this slot's expert: s + 1 selection rounds, no softmax
+        float lv[PER];
+        const bool ok = poll_logits<PER>(a, ep, lv, lane);
+        S.mark(1, tid);
+        const int idx = topk_index_at<PER>(lv, a.E, s, lane);
+        S.mark(2, tid);
+        if (lane == 0) {
+            s_ids[0] = (uint32_t)idx;
+            if (!ok) *s_fail = 1;
+        }
     }
+    __syncthreads();  // s_ids[0], s_fail
+    uint32_t e = s_ids[0];
+    if (e >= (uint32_t)a.E) e = 0;
+    const int nh = a.D / 128, ntask = 32 * nh;
+    DevTensor W{};
+    W.p0 = a.gu_hdr;
+    W.p1 = a.gu_qs;
+    W.p2 = a.gu_p2;
+    W.p3 = a.gu_p3;
+    W.blocks_per_row = (size_t)a.nsb;
+    UnitW<LT_TYPE_Q3_K> w[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        // (clamped: every load unconditional)
+        const int t = min(tid + kThreads * c, ntask - 1);
+        const int r = t / (2 * nh), gu = (t / nh) & 1, hu = t % nh;
+        const int row = min(j0 + r, a.F - 1);
+        w[c] = load_unit<LT_TYPE_Q3_K>(W, (size_t)e * 2 * a.F + (size_t)gu * a.F + row, 4 * hu);
+    }
+    const LimbView xv{la, lb, lsp, lxs};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int t = tid + kThreads * c;
+        if (t < ntask) {
+            const int hu = t % nh;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc += dot_unit<LT_TYPE_Q3_K>(w[c], 4 * hu + j, load_ux(xv, 4 * hu + j));
+            part[t] = acc;
+        }
+    }
+    S.mark(3, tid);
+    __syncthreads();  // part
+    float *s_h = reinterpret_cast<float *>(smem);
+    if (tid < 32) {
+        const int r = tid >> 1;
+        const float *pr = part + tid * nh;  // row r, gate (tid even) or up
+        float sum = 0.0f;
+        for (int hu = 0; hu < nh; hu++) sum += pr[hu];
+        const float other = __shfl_xor(sum, 1, 64);
+        if ((tid & 1) == 0) s_h[r] = (j0 + r < a.F) ? act_apply((uint32_t)a.act, sum) * other : 0.0f;
+    }
+    publish_h_record(a, s_h, s_fail, g, ep, tid, wave, lane, S);
 }
 
 // ---------------------------------------------------------------- Gemma4 tail
@@ -1300,7 +1404,10 @@ __device__ __forceinline__ float group16_sum_transposed(const float (&v)[V], int
 // its group's K slice: sh_stage_load when it starts, sh_stage_store during
 // its logit poll, sh_read_h with its h records, sh_down_add after its own
 // rows.
-template <int PER, int RPG, int FILL>
+// DT: the down tensor's type (Q4_K, or IQ4_NL / Q5_0 / Q5_1: then lane l16
+// of a row group takes 32-element blocks l16 and l16 + 16 of its rows, K <=
+// 1024, each block's activations the two h records it spans).
+template <int PER, int RPG, int FILL, int DT = LT_TYPE_Q4_K>
 __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, float *s_w,
                                           uint32_t *s_ep, int *s_fail, int bid, int s, int j, int tid, int wave,
                                           int lane, Stamps &S) {
@@ -1308,7 +1415,8 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     const int row0 = j * 16 * RPG;
     const int rg = tid >> 4, l16 = tid & 15;
     const int sb = l16 >> 2, p = l16 & 3;
-    const bool t_on = sb < a.nsbd;
+    constexpr bool kQ4 = DT == LT_TYPE_Q4_K;
+    const bool t_on = kQ4 ? sb < a.nsbd : true;
     uint32_t *rec_a = reinterpret_cast<uint32_t *>(smem);
     uint32_t *rec_b = rec_a + G * 4;
     float *rec_sp = reinterpret_cast<float *>(rec_b + G * 4);
@@ -1349,16 +1457,32 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     S.mark(2, tid);
     uint4 q0[RPG], q1[RPG];
     uint32_t hw[RPG];
+    UnitW<DT> fw[kQ4 ? 1 : RPG][2];  // (block formats: blocks l16, l16 + 16 of each row)
+    DevTensor fW{};
+    fW.p0 = a.dn_hdr;
+    fW.p1 = a.dn_qs;
+    fW.p2 = a.dn_p2;
+    fW.blocks_per_row = (size_t)a.nsbd;
 #pragma unroll
     for (int i = 0; i < RPG; i++) {
         const int row = row0 + rg * RPG + i;
-        q0[i] = q1[i] = make_uint4(0u, 0u, 0u, 0u);
-        hw[i] = 0u;
-        if (t_on && row < a.D) {
-            const size_t blk = ((size_t)e * a.D + row) * a.nsbd + sb;
-            q0[i] = ld16(a.dn_qs + blk * 128 + 32 * p);
-            q1[i] = ld16(a.dn_qs + blk * 128 + 32 * p + 16);
-            hw[i] = *reinterpret_cast<const uint32_t *>(a.dn_hdr + blk * 16 + 4 * p);
+        if constexpr (kQ4) {
+            q0[i] = q1[i] = make_uint4(0u, 0u, 0u, 0u);
+            hw[i] = 0u;
+            if (t_on && row < a.D) {
+                const size_t blk = ((size_t)e * a.D + row) * a.nsbd + sb;
+                q0[i] = ld16(a.dn_qs + blk * 128 + 32 * p);
+                q1[i] = ld16(a.dn_qs + blk * 128 + 32 * p + 16);
+                hw[i] = *reinterpret_cast<const uint32_t *>(a.dn_hdr + blk * 16 + 4 * p);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const int u = l16 + 16 * m;
+                // (clamped: every load unconditional; a block past the row's
+                // end or a row past D is loaded but not added)
+                fw[i][m] = load_unit<DT>(fW, (size_t)e * a.D + min(row, a.D - 1), min(u, a.nsbd - 1));
+            }
         }
     }
     // the shared FFN's rows while these weights are in flight: its slice of
@@ -1377,7 +1501,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     PairScale ps[RPG];
     uint32_t nlo[2][8], nhi[2][8];
 #pragma unroll
-    for (int i = 0; i < RPG; i++) {
+    for (int i = 0; i < (kQ4 ? RPG : 0); i++) {
         uint32_t h0, h1, h2, h3;
         quad_header(hw[i], h0, h1, h2, h3);
         ps[i] = pair_scale(h0, h1, h2, h3, p);
@@ -1448,7 +1572,31 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     float v[RPG];
 #pragma unroll
     for (int i = 0; i < RPG; i++) v[i] = 0.0f;
-    if (t_on) {
+    if constexpr (!kQ4) {
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const int u = l16 + 16 * m;
+            if (u < a.nsbd) {
+                // block u's activations: records 2u (elements 0-15) and 2u + 1
+                UnitX ux;
+                const uint4 *pa = reinterpret_cast<const uint4 *>(rec_a + 8 * u);
+                const uint4 *pb = reinterpret_cast<const uint4 *>(rec_b + 8 * u);
+#pragma unroll
+                for (int g = 0; g < 2; g++) {
+                    const uint4 qa = pa[g], qb = pb[g];
+                    ux.a[4 * g] = qa.x; ux.a[4 * g + 1] = qa.y; ux.a[4 * g + 2] = qa.z; ux.a[4 * g + 3] = qa.w;
+                    ux.b[4 * g] = qb.x; ux.b[4 * g + 1] = qb.y; ux.b[4 * g + 2] = qb.z; ux.b[4 * g + 3] = qb.w;
+                }
+                ux.sp[0] = rec_sp[2 * u];
+                ux.sp[1] = rec_sp[2 * u + 1];
+                ux.xs[0] = rec_xs[2 * u];
+                ux.xs[1] = rec_xs[2 * u + 1];
+#pragma unroll
+                for (int i = 0; i < RPG; i++) v[i] += dot_unit<DT>(fw[i][m], u, ux);
+            }
+        }
+    }
+    if (kQ4 && t_on) {
         const int gi = sb * 16 + 4 * p;  // first of the window's 4 groups
         Limbs xl;
 #pragma unroll
@@ -1464,7 +1612,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
         xl.xs_lo = xs4.x + xs4.y;
         xl.xs_hi = xs4.z + xs4.w;
 #pragma unroll
-        for (int i = 0; i < RPG; i++) {
+        for (int i = 0; i < (kQ4 ? RPG : 0); i++) {
             if (i < 2) {
                 v[i] = q4k_pair_dot_nib(nlo[i], nhi[i], ps[i], xl);
             } else {
@@ -1548,7 +1696,9 @@ __device__ __forceinline__ void role_combine(const FusedArgs &a, uint32_t *s_ep,
 
 // SH 1: the Gemma-style instance (Q8_0 router role, shared-FFN roles); SH
 // 2: the Gemma4 block (Q8_0 router with the block's input norms, expert
-// input norm and scales, the tail role; no shared FFN); SH 0 holds only the
+// input norm and scales, the tail role; no shared FFN); SH 3: SH 2's roles
+// plus the APEX expert formats (Q3_K gate/up, IQ4_NL / Q5_0 / Q5_1 down),
+// with or without the Gemma4 block; SH 0 holds only the
 // F32 router roles and the experts' roles, and WIDE (rows over 2048) only
 // the router variants those rows use: less code per instance (the roles of
 // a CU's four workgroups share its instruction cache; the Gemma4 code in the
@@ -1585,7 +1735,7 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
     int u = i;
     if (u < a.NRg) {
         if (SH && a.qrouter)
-            role_router_q8<SH == 2>(a, smem, bid, tid, lane, S);
+            role_router_q8<SH >= 2>(a, smem, bid, tid, lane, S);
         else if (!WIDE && a.rb == 2)
             role_router_pair_one(a, smem, bid, tid, wave, lane, S);
         else if (WIDE)
@@ -1599,14 +1749,28 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
     } else if ((u -= a.NSg) < a.SPG * a.G) {
         const int s = x + 8 * (u / a.G);
         if (s < a.k) {
-            role_gate_up<PER, WIDE, SH == 2>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            if (SH == 3 && a.gu_type == LT_TYPE_Q3_K)
+                role_gate_up_q3k<PER, 1>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
+            else
+                role_gate_up<PER, WIDE, SH >= 2>(a, smem, s_ids, &s_ep, &s_fail, bid, s, u % a.G, tid, wave, lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, 1u);  // logits
             role = 2u | (uint32_t)s << 8;
         }
     } else if ((u -= a.SPG * a.G) < a.SPG * a.NDg) {
         const int s = x + 8 * (u / a.NDg);
         if (s < a.k) {
-            role_down<PER, 4, SH>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave, lane, S);
+            if (SH == 3 && a.dn_type == LT_TYPE_IQ4_NL)
+                role_down<PER, 4, 2, LT_TYPE_IQ4_NL>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave,
+                                                      lane, S);
+            else if (SH == 3 && a.dn_type == LT_TYPE_Q5_0)
+                role_down<PER, 4, 2, LT_TYPE_Q5_0>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave,
+                                                    lane, S);
+            else if (SH == 3 && a.dn_type == LT_TYPE_Q5_1)
+                role_down<PER, 4, 2, LT_TYPE_Q5_1>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave,
+                                                    lane, S);
+            else
+                role_down<PER, 4, SH == 3 ? 2 : SH>(a, smem, s_ids, s_w, &s_ep, &s_fail, bid, s, u % a.NDg, tid, wave,
+                                                    lane, S);
             if (tid == 0 && s_fail) report_timeout(a.err, (uint32_t)s_fail << 1);  // 2 logits, 4 h records
             role = 3u | (uint32_t)s << 8;
         } else if (SH == 1 && a.S > 0 && u < a.NDg) {  // a group without a slot still adds its shared rows
@@ -1626,7 +1790,7 @@ __global__ void __launch_bounds__(kThreads, SH ? 4 : 1) k_moe_fused(FusedArgs a)
     } else if ((u -= a.SPG * a.NDg) < a.NCg) {
         role_combine(a, &s_ep, bid, 8 * u + x, tid, S);
         role = 4;
-    } else if (SH == 2 && a.gemma && x == 0 && u == a.NCg) {  // the Gemma4 block's tail
+    } else if (SH >= 2 && a.gemma && x == 0 && u == a.NCg) {  // the Gemma4 block's tail
         role_gemma_tail(a, bid, tid, wave, lane, S);
         role = 7;
     }
@@ -1684,7 +1848,15 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
     if (moe) {
         const int E = L.E, k = L.k, Kd = L.Kd;
         if (!L.R || !L.GU || !L.Dn) return pl;
-        if (Kd % 256 != 0 || Kd < L.F || Kd > 1024) return pl;  // 16 lanes = 4 super-blocks x 4 pairs
+        const uint32_t gt = L.GU->type, dt = L.Dn->type;
+        const bool dq4 = dt == LT_TYPE_Q4_K;
+        if (gt != LT_TYPE_Q4_K && gt != LT_TYPE_Q3_K) return pl;
+        if (!dq4 && dt != LT_TYPE_IQ4_NL && dt != LT_TYPE_Q5_0 && dt != LT_TYPE_Q5_1) return pl;
+        pl.fmt = gt != LT_TYPE_Q4_K || !dq4;
+        if (pl.fmt && (sh || L.det)) return pl;  // (the format instance: no shared FFN, atomic combine)
+        // 16 lanes per down row: 4 super-blocks x 4 pairs (Q4_K), or 2 x 16
+        // blocks of 32 (the block formats)
+        if (Kd % (dq4 ? 256 : 32) != 0 || Kd < L.F || Kd > 1024) return pl;
         if (E < 1 || E > 256 || k > 16 || k > E) return pl;
         pl.per = E <= 128 ? 2 : 4;
         pl.wide = D > 2048;
@@ -1738,7 +1910,8 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
     if (moe) {
         const size_t lds_router = pl.qrouter ? (size_t)2 * 128 * 4 : (size_t)(4 * 512 + 16) * 4;
         const size_t lds_down = (size_t)pl.G * 40;
-        const size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
+        size_t lds_gu = 64 + (size_t)D / 4 * 4 * 2 + (size_t)D / 16 * 4 * 2;
+        if (L.GU->type == LT_TYPE_Q3_K) lds_gu += (size_t)D;  // the tasks' partial sums
         lds = std::max(lds, std::max(lds_router, std::max(lds_down, lds_gu)));
     }
     if (sh) lds = std::max(lds, std::max((size_t)D * 4, sh_down_lds(L.S)));  // x; shared down weights + h slice
@@ -1769,6 +1942,11 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
         fa.dn_qs = L.Dn->p1;
         fa.nsb = (int)L.GU->blocks_per_row;
         fa.nsbd = (int)L.Dn->blocks_per_row;
+        fa.gu_type = (int)L.GU->type;
+        fa.dn_type = (int)L.Dn->type;
+        fa.gu_p2 = L.GU->p2;
+        fa.gu_p3 = L.GU->p3;
+        fa.dn_p2 = L.Dn->p2;
     }
     if (L.SG) {
         fa.sgq = L.SG->p0;
@@ -1824,7 +2002,7 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // measured for this stream) after the logits are seen, in 10 ns ticks;
     // tuned on config 3 (14.2 MB: 296 ticks; 200 or 360 are 0.2-0.4 us
     // slower per layer).
-    const double gu_bytes = (double)L.k * 2.0 * L.F * fa.nsb * 144.0;
+    const double gu_bytes = moe ? (double)L.k * 2.0 * L.F * ((double)L.GU->bytes / (double)L.GU->total_rows) : 0.0;
     fa.dn_delay = 70 + (int)(0.8 * gu_bytes / 50000.0);
     fa.NRg = pl.NRg;
     fa.rb = pl.rb;
@@ -1837,12 +2015,14 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // blocks' share of the grid (atomic combine) measured 0.15 us slower per
     // layer -- more h record reads and atomics -- though each block's
     // products halve
-    const int mode = pl.gemma ? 2 : (pl.shared || pl.qrouter) ? 1 : 0;
+    const int mode = pl.fmt ? 3 : pl.gemma ? 2 : (pl.shared || pl.qrouter) ? 1 : 0;
     if (pl.wide) {
+        if (mode == 3) return pl.per == 2 ? launch_fused_t<2, 1, 3>(fa, pl, s) : launch_fused_t<4, 1, 3>(fa, pl, s);
         if (mode == 2) return pl.per == 2 ? launch_fused_t<2, 1, 2>(fa, pl, s) : launch_fused_t<4, 1, 2>(fa, pl, s);
         if (mode == 1) return pl.per == 2 ? launch_fused_t<2, 1, 1>(fa, pl, s) : launch_fused_t<4, 1, 1>(fa, pl, s);
         return pl.per == 2 ? launch_fused_t<2, 1, 0>(fa, pl, s) : launch_fused_t<4, 1, 0>(fa, pl, s);
     }
+    if (mode == 3) return pl.per == 2 ? launch_fused_t<2, 0, 3>(fa, pl, s) : launch_fused_t<4, 0, 3>(fa, pl, s);
     if (mode == 2) return pl.per == 2 ? launch_fused_t<2, 0, 2>(fa, pl, s) : launch_fused_t<4, 0, 2>(fa, pl, s);
     if (mode == 1) return pl.per == 2 ? launch_fused_t<2, 0, 1>(fa, pl, s) : launch_fused_t<4, 0, 1>(fa, pl, s);
     return pl.per == 2 ? launch_fused_t<2, 0, 0>(fa, pl, s) : launch_fused_t<4, 0, 0>(fa, pl, s);

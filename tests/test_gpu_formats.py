@@ -72,23 +72,38 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
 
-@pytest.mark.parametrize("gu,dn,F", [(ggml.Q3_K, ggml.Q5_0, 704), (ggml.Q3_K, ggml.Q5_1, 704),
-                                     (ggml.Q3_K, ggml.IQ4_NL, 704), (ggml.Q5_0, ggml.Q3_K, 768),
-                                     (ggml.IQ4_NL, ggml.Q4_K, 768), (ggml.Q4_K, ggml.IQ4_NL, 768)])
-def test_gpu_moe_forward_apex_formats(ctx, pool, gu, dn, F):
+@pytest.mark.parametrize("gu,dn,F,D", [(ggml.Q3_K, ggml.Q5_0, 704, 2816), (ggml.Q3_K, ggml.Q5_1, 704, 2816),
+                                       (ggml.Q3_K, ggml.IQ4_NL, 704, 2816), (ggml.Q5_0, ggml.Q3_K, 768, 2816),
+                                       (ggml.IQ4_NL, ggml.Q4_K, 768, 2816), (ggml.Q4_K, ggml.IQ4_NL, 768, 2816),
+                                       (ggml.Q3_K, ggml.IQ4_NL, 512, 2048), (ggml.Q3_K, ggml.Q4_K, 256, 4096),
+                                       (ggml.Q4_K, ggml.Q5_1, 1024, 1024)])
+def test_gpu_moe_forward_apex_formats(ctx, pool, gu, dn, F, D):
+    # Q3_K or Q4_K gate/up with IQ4_NL / Q5_0 / Q5_1 / Q4_K down run in the
+    # single launch (the format instance), the other mixes in separate
+    # launches; unfused forces the separate launches: both against the
+    # oracle and against each other (the single launch adds the slots' rows
+    # with float atomics and hands h over as int8 limbs, where the Q4_K down
+    # kernel of the separate launches reads fp32 h: to about 3e-5)
     import llmtoy_amd as lt
-    w = synth.moe_weights(43, 2816, 32, F, gate_up_type=gu, down_type=dn)
+    w = synth.moe_weights(43, D, 32, F, gate_up_type=gu, down_type=dn)
     R, GU, DN = lt.upload_moe(ctx, w)
-    x = synth.normal(synth.stream(43, 1), (2816,))
-    print(f"moe_forward gate_up {ggml.NAMES[gu]} down {ggml.NAMES[dn]}", flush=True)
-    out = np.zeros(2816, np.float32)
-    ids = np.zeros(8, np.uint32)
-    ctx.moe_forward(out, x, R, GU, DN, 8, F, act=lt.ACT_GELU_TANH, out_ids=ids)
-    ref, rids, _, agree = orc.moe_forward(w, x, 8, act=orc.ACT_GELU_TANH, pool=pool)
+    x = synth.normal(synth.stream(43, 1), (D,))
+    print(f"moe_forward gate_up {ggml.NAMES[gu]} down {ggml.NAMES[dn]} F {F} D {D}", flush=True)
+    ref, rids, rw, agree = orc.moe_forward(w, x, 8, act=orc.ACT_GELU_TANH, pool=pool)
+    assert agree
+    outs = []
+    for unfused in (False, True):
+        out = np.zeros(D, np.float32)
+        ids = np.zeros(8, np.uint32)
+        wts = np.zeros(8, np.float32)
+        ctx.moe_forward(out, x, R, GU, DN, 8, F, act=lt.ACT_GELU_TANH, out_ids=ids, out_w=wts, unfused=unfused)
+        assert ids.tolist() == rids.tolist(), (unfused, ids, rids)
+        assert np.max(np.abs(wts - rw)) < 1e-6, unfused
+        assert rel_l2(out, ref) < 1e-3, (unfused, rel_l2(out, ref))
+        outs.append(out)
     for t in (R, GU, DN):
         t.free()
-    assert agree and np.array_equal(np.sort(ids), np.sort(rids))
-    assert rel_l2(out, ref) < 1e-3
+    assert rel_l2(outs[0], outs[1]) < 1e-4, rel_l2(outs[0], outs[1])
 
 
 def test_gpu_gemma4_block_apex_formats(ctx, pool):
@@ -106,6 +121,34 @@ def test_gpu_gemma4_block_apex_formats(ctx, pool):
     for t in tens:
         t.free()
     assert ids.tolist() == rids.tolist() and rel_l2(got, ref) < 1e-3
+
+
+def test_gpu_gemma4_block_apex_fused_matches_launches(ctx, pool):
+    # the APEX Gemma4 block in one launch (tree-order norms) against its
+    # separate launches and the oracle: the same routing bits, the output to
+    # the order of the experts' float atomics
+    import llmtoy_amd as lt
+    from llmtoy_amd import lib as ltlib
+    w = synth.moe_weights(45, 2816, 128, 704, router_type=ggml.Q8_0, gate_up_type=ggml.Q3_K,
+                          down_type=ggml.IQ4_NL)
+    tens = lt.upload_moe(ctx, w)
+    nm = synth.gemma4_norms(45, 2816, 128)
+    for i in range(3):
+        x, dense = synth.normal(synth.stream(45, 1 + i), (2816,)), synth.normal(synth.stream(45, 9), (2816,))
+        print(f"gemma4 apex block, input {i}", flush=True)
+        ref, rids, _ = orc.gemma4_moe_block(w, x, dense, 8, nm, 0.75, 1e-6, pool=pool)
+        res = []
+        for unfused in (False, True):
+            ids, wt = np.zeros(8, np.uint32), np.zeros(8, np.float32)
+            got = ltlib.gemma4_moe_block(ctx, x.copy(), dense, *tens, 8, 704, nm, 0.75, 1e-6, out_ids=ids, out_w=wt,
+                                         unfused=unfused)
+            assert ids.tolist() == rids.tolist() and rel_l2(got, ref) < 1e-3, (i, unfused, rel_l2(got, ref))
+            res.append((got, ids, wt))
+        (a, ia, wa), (b, ib, wb) = res
+        assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
+        assert rel_l2(a, b) < 1e-5, (i, rel_l2(a, b))
+    for t in tens:
+        t.free()
 
 
 @pytest.mark.parametrize("gtype", FMTS)
