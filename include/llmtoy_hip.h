@@ -202,7 +202,12 @@ int lt_expert_down_id(lt_ctx *ctx, const lt_tensor *down, const float *h, const 
  * Replaces moeForward (ops/moe.zig:18-77) and GpuWeights.runExpertBatch
  * (gemma4/gpu_weights.zig:2748-3149).  out_ids / out_w (may be NULL)
  * receive the routing.  d_expert is the expert FFN width; down's cols may be
- * larger (zero-padded K). */
+ * larger (zero-padded K).  One launch of the single-launch kernel where the
+ * layer fits it (F32 or Q8_0 router, d_model 256..4096, down K <= 1024, <=
+ * 256 experts, k <= 16): Q4_K experts (with a Q8_0 shared FFN in the same
+ * launch), or Q3_K / Q4_K gate_up with IQ4_NL, Q5_0 or Q5_1 down (atomic
+ * combine, the shared FFN then first, as the base); other expert types and
+ * LT_MOE_UNFUSED run router, gate/up and down as separate launches. */
 int lt_moe_forward(lt_ctx *ctx, float *out, const float *x, const lt_tensor *router, const float *router_bias,
                    const lt_tensor *gate_up, const lt_tensor *down, const lt_tensor *sh_gate,
                    const lt_tensor *sh_up, const lt_tensor *sh_down, uint32_t k, uint32_t d_expert, uint32_t act,
@@ -300,8 +305,9 @@ int lt_moe_tail(lt_ctx *ctx, float *x, const float *moe, const float *dense_ffn,
  * x [d_model] is updated in place; dense_ffn is the dense FFN output after
  * post_ffw_norm_1.  down_exps_scale [n_experts] may be NULL (all ones).
  * router: F32 or Q8_0; experts: Q4_K, Q3_K, Q5_0, Q5_1 or IQ4_NL (device x:
- * 16-byte aligned).  With a Q8_0 router, Q4_K experts and the default tree
- * sums the whole block is one launch of the single-launch MoE kernel
+ * 16-byte aligned).  With a Q8_0 router, Q4_K or Q3_K gate/up, Q4_K,
+ * IQ4_NL, Q5_0 or Q5_1 down and the default tree sums the whole block is
+ * one launch of the single-launch MoE kernel
  * (router-input prep in its router blocks, the expert input in its gate/up
  * blocks, the tail in one block after the down blocks); otherwise the
  * router-input prep runs inside the Q8_0 router kernel, or in a norm

@@ -189,9 +189,13 @@ __device__ __forceinline__ float q3k_group_dot(const UnitW<LT_TYPE_Q3_K> &w, int
 #pragma unroll
     for (int g = 0; g < 2; g++) {
         uint32_t c[4];
+        // the high bit moved straight to bit 2 of each byte (a left shift for
+        // msh < 2), then one and-or with the two low bits
 #pragma unroll
-        for (int w4 = 0; w4 < 4; w4++)
-            c[w4] = ((qw[4 * g + w4] >> qsh) & 0x03030303u) | (((mw[4 * g + w4] >> msh) & 0x01010101u) << 2);
+        for (int w4 = 0; w4 < 4; w4++) {
+            const uint32_t mb = msh >= 2 ? mw[4 * g + w4] >> (msh - 2) : mw[4 * g + w4] << (2 - msh);
+            c[w4] = ((qw[4 * g + w4] >> qsh) & 0x03030303u) | (mb & 0x04040404u);
+        }
         const float dot = group_dot(c, x, g);
         total += (d * (float)(q3k_scale(w.sc[0], w.sc[1], w.sc[2], 8 * h + 2 * j + g) - 32)) * (dot - 4.f * x.xs[g]);
     }
@@ -212,6 +216,44 @@ __device__ __forceinline__ float dot_unit(const UnitW<T> &w, int u, const UnitX 
         if constexpr (T == LT_TYPE_Q5_0) return d * (dot - 16.f * s0);                   // codes - 16
         return d * dot + f16_bits_to_f32((uint16_t)(w.dm >> 16)) * s0;                    // Q5_1: d q + m
     }
+}
+
+// A 32-element block's codes as signed (IQ4_NL: the table values) or
+// unsigned (Q5_0 / Q5_1: 5-bit) bytes, words 0-3 the low half (elements
+// 4i..4i+3 in word i), 4-7 the high half, with the block's f16 d (and Q5_1
+// m) -- formed from the weights alone, before the activations are there.
+struct BlockCodes {
+    uint32_t c[8];
+    uint32_t dm;
+};
+template <int T>
+__device__ __forceinline__ BlockCodes block_codes(const UnitW<T> &w) {
+    static_assert(T == LT_TYPE_IQ4_NL || T == LT_TYPE_Q5_0 || T == LT_TYPE_Q5_1, "32-element block formats");
+    BlockCodes b;
+    const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (T == LT_TYPE_IQ4_NL) {
+            b.c[i] = iq4_lookup4(q[i] & 0x0f0f0f0fu);
+            b.c[4 + i] = iq4_lookup4((q[i] >> 4) & 0x0f0f0f0fu);
+        } else {
+            b.c[i] = (q[i] & 0x0f0f0f0fu) | spread4((w.qh >> (4 * i)) & 15u);
+            b.c[4 + i] = ((q[i] >> 4) & 0x0f0f0f0fu) | spread4((w.qh >> (16 + 4 * i)) & 15u);
+        }
+    }
+    b.dm = w.dm;
+    return b;
+}
+// The block's contribution from its codes (dot_unit's arithmetic).
+template <int T>
+__device__ __forceinline__ float block_codes_dot(const BlockCodes &b, const UnitX &x) {
+    const uint32_t lo[4] = {b.c[0], b.c[1], b.c[2], b.c[3]}, hi[4] = {b.c[4], b.c[5], b.c[6], b.c[7]};
+    const float dot = group_dot(lo, x, 0) + group_dot(hi, x, 1);
+    const float d = f16_bits_to_f32((uint16_t)b.dm);
+    if constexpr (T == LT_TYPE_IQ4_NL) return d * dot;
+    const float s0 = x.xs[0] + x.xs[1];
+    if constexpr (T == LT_TYPE_Q5_0) return d * (dot - 16.f * s0);  // codes - 16
+    return d * dot + f16_bits_to_f32((uint16_t)(b.dm >> 16)) * s0;   // Q5_1: d q + m
 }
 
 template <int T>

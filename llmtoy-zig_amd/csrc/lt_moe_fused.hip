@@ -559,15 +559,69 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
     const int nb = a.D >> 5;
     const int row = 2 * bid + h;
     const bool valid = row < a.E;
-    RmsLoads rms;  // (the Gemma4 block: x for the RMS first, so that it is not behind the weights)
-    if (GEM && a.gemma) gemma_rms_load(a, tid, rms);
-    // every load unconditional (clamped row and block)
-    const size_t blk = (size_t)(valid ? row : 0) * nb + (b < nb ? b : nb - 1);
-    const uint4 q0 = ld16(a.rq + blk * 32), q1 = ld16(a.rq + blk * 32 + 16);
-    const uint32_t d16 = a.rd[blk];
     float xv[32];
-    {
-        const float4 *xp = reinterpret_cast<const float4 *>(a.x + (b < nb ? b : nb - 1) * 32);
+    const int bc = b < nb ? b : nb - 1;
+    uint4 q0, q1;
+    uint32_t d16;
+    float bias;
+    uint32_t c0;
+    if (GEM && a.gemma) {
+        // The Gemma4 block: the router input (x * (rms_inv * raw_global)) *
+        // raw_scale, as the Q8_0 router kernel's prep forms it, once per block:
+        // x and raw_scale float4 c = tid + 256 m go to LDS (x first, for the
+        // RMS), then the prepared row replaces x there and each thread reads
+        // its block's 32 values (both rows' threads share them).
+        float4 *xs4 = reinterpret_cast<float4 *>(smem + 2 * 128 * 4);  // [D / 4], after terms
+        const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+        const float4 *s4 = reinterpret_cast<const float4 *>(a.g_raw_scale);
+        const int n4 = a.D / 4;  // <= 1024
+        float4 xr[4], sr[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) xr[m] = x4[min(tid + kThreads * m, n4 - 1)];
+        // every load unconditional (clamped row and block)
+        const size_t blk = (size_t)(valid ? row : 0) * nb + bc;
+        q0 = ld16(a.rq + blk * 32);
+        q1 = ld16(a.rq + blk * 32 + 16);
+        d16 = a.rd[blk];
+#pragma unroll
+        for (int m = 0; m < 4; m++) sr[m] = s4[min(tid + kThreads * m, n4 - 1)];
+        bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
+        c0 = epoch_peek(a.counters, bid);
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            if (tid + kThreads * m < n4) xs4[tid + kThreads * m] = xr[m];
+        __syncthreads();
+        RmsLoads rms;  // k_router_q8_0's order: thread t < 128 takes chunks t + 128 m
+        if (tid < 128)
+#pragma unroll
+            for (int m = 0; m < 8; m++) rms.v[m] = xs4[min(tid + 128 * m, n4 - 1)];
+        const float raw_base = gemma_rms_inv(a, tid, rms) * a.g_raw_global;  // (a barrier inside)
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            if (tid + kThreads * m < n4) {
+                float4 v = xr[m];
+                v.x = (v.x * raw_base) * sr[m].x;
+                v.y = (v.y * raw_base) * sr[m].y;
+                v.z = (v.z * raw_base) * sr[m].z;
+                v.w = (v.w * raw_base) * sr[m].w;
+                xs4[tid + kThreads * m] = v;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 v4 = xs4[bc * 8 + t];
+            xv[4 * t] = v4.x;
+            xv[4 * t + 1] = v4.y;
+            xv[4 * t + 2] = v4.z;
+            xv[4 * t + 3] = v4.w;
+        }
+    } else {
+        // every load unconditional (clamped row and block)
+        const size_t blk = (size_t)(valid ? row : 0) * nb + bc;
+        q0 = ld16(a.rq + blk * 32);
+        q1 = ld16(a.rq + blk * 32 + 16);
+        d16 = a.rd[blk];
+        const float4 *xp = reinterpret_cast<const float4 *>(a.x + bc * 32);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const float4 v4 = xp[t];
@@ -576,22 +630,8 @@ __device__ __forceinline__ void role_router_q8(const FusedArgs &a, uint8_t *smem
             xv[4 * t + 2] = v4.z;
             xv[4 * t + 3] = v4.w;
         }
-    }
-    const float bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
-    const uint32_t c0 = epoch_peek(a.counters, bid);
-    if (GEM && a.gemma) {
-        // the router input (x * (rms_inv * raw_global)) * raw_scale, as the
-        // Q8_0 router kernel's prep forms it
-        float sv[32];
-        const float4 *sp = reinterpret_cast<const float4 *>(a.g_raw_scale + (b < nb ? b : nb - 1) * 32);
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const float4 v4 = sp[t];
-            sv[4 * t] = v4.x; sv[4 * t + 1] = v4.y; sv[4 * t + 2] = v4.z; sv[4 * t + 3] = v4.w;
-        }
-        const float raw_base = gemma_rms_inv(a, tid, rms) * a.g_raw_global;
-#pragma unroll
-        for (int e = 0; e < 32; e++) xv[e] = (xv[e] * raw_base) * sv[e];
+        bias = *(a.bias ? a.bias + (valid ? row : 0) : a.x);
+        c0 = epoch_peek(a.counters, bid);
     }
     const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     float acc[8];
@@ -1152,11 +1192,12 @@ __device__ __forceinline__ void role_gate_up(const FusedArgs &a, uint8_t *smem, 
 
 // Q3_K gate/up rows (the format instance): the block's 16 h rows j0 + r of
 // slot s as 32 D / 128 tasks (row r, gate or up, super-block half hu: the
-// 128 weights of qs[32 h ..] with all of hmask, the scales and d); task t =
-// tid + 256 c (c < 4: D <= 4096) loads its half up front, then adds its
-// four 32-element groups against the limbs (lt_fmt.h q3k_group_dot) into
-// part[t]; thread 2r + gu sums row r's halves in order, and h = act(gate) *
-// up goes out as the record (publish_h_record).  Rows past F give h = 0.
+// 128 weights of qs[32 h ..] with all of hmask, the scales and d); a thread
+// loads up to 4 tasks of one half up front (D <= 4096), then adds each
+// task's four 32-element groups in order against the limbs (lt_fmt.h
+// q3k_group_dot; the groups' limbs read once for its tasks) into part[task];
+// thread 2r + gu sums row r's halves in order, and h = act(gate) * up goes
+// out as the record (publish_h_record).  Rows past F give h = 0.
 template <int PER, int GEM>
 __device__ __forceinline__ void role_gate_up_q3k(const FusedArgs &a, uint8_t *smem, uint32_t *s_ids, uint32_t *s_ep,
                                                  int *s_fail, int bid, int s, int jg, int tid, int wave, int lane,
@@ -1187,32 +1228,49 @@ __device__ __forceinline__ void role_gate_up_q3k(const FusedArgs &a, uint8_t *sm
     __syncthreads();  // s_ids[0], s_fail
     uint32_t e = s_ids[0];
     if (e >= (uint32_t)a.E) e = 0;
-    const int nh = a.D / 128, ntask = 32 * nh;
+    // thread tid takes super-block half hu = tid % nh of the rows and
+    // (row, gate / up) combinations cb = tid / nh + tph i (cb < 32): the
+    // half's four limb groups are read from LDS once for all of them
+    const int nh = a.D / 128, tph = kThreads / nh;
+    const int hu = tid % nh, kb = tid / nh;
     DevTensor W{};
     W.p0 = a.gu_hdr;
     W.p1 = a.gu_qs;
     W.p2 = a.gu_p2;
     W.p3 = a.gu_p3;
     W.blocks_per_row = (size_t)a.nsb;
-    UnitW<LT_TYPE_Q3_K> w[4];
+    // up to three tasks loaded at once (d_model <= 2816: every task); a
+    // fourth (d_model >= 3072) after them
+    auto task_w = [&](int cb) {
+        cb = min(cb, 31);  // (clamped: every load unconditional)
+        const int row = min(j0 + (cb >> 1), a.F - 1);
+        return load_unit<LT_TYPE_Q3_K>(W, (size_t)e * 2 * a.F + (size_t)(cb & 1) * a.F + row, 4 * hu);
+    };
+    UnitW<LT_TYPE_Q3_K> w[3];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        // (clamped: every load unconditional)
-        const int t = min(tid + kThreads * c, ntask - 1);
-        const int r = t / (2 * nh), gu = (t / nh) & 1, hu = t % nh;
-        const int row = min(j0 + r, a.F - 1);
-        w[c] = load_unit<LT_TYPE_Q3_K>(W, (size_t)e * 2 * a.F + (size_t)gu * a.F + row, 4 * hu);
-    }
+    for (int i = 0; i < 3; i++) w[i] = task_w(kb + tph * i);
     const LimbView xv{la, lb, lsp, lxs};
+    if (kb < tph) {  // (threads past nh tph have no half)
+        float acc[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int t = tid + kThreads * c;
-        if (t < ntask) {
-            const int hu = t % nh;
-            float acc = 0.0f;
+        for (int j = 0; j < 4; j++) {
+            const UnitX ux = load_ux(xv, 4 * hu + j);
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc += dot_unit<LT_TYPE_Q3_K>(w[c], 4 * hu + j, load_ux(xv, 4 * hu + j));
-            part[t] = acc;
+            for (int i = 0; i < 3; i++)
+                if (kb + tph * i < 32) acc[i] += dot_unit<LT_TYPE_Q3_K>(w[i], 4 * hu + j, ux);
+        }
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const int cb = kb + tph * i;
+            if (cb < 32) part[(cb >> 1) * 2 * nh + (cb & 1) * nh + hu] = acc[i];
+        }
+        const int cb = kb + tph * 3;
+        if (cb < 32) {
+            const UnitW<LT_TYPE_Q3_K> w3 = task_w(cb);
+            float a3 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) a3 += dot_unit<LT_TYPE_Q3_K>(w3, 4 * hu + j, load_ux(xv, 4 * hu + j));
+            part[(cb >> 1) * 2 * nh + (cb & 1) * nh + hu] = a3;
         }
     }
     S.mark(3, tid);
@@ -1498,6 +1556,19 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
     // records are awaited (the dots after their arrival are VALU-bound; all
     // four rows unpacked would exceed 128 VGPRs); the empty asm keeps the
     // compiler from sinking the unpacking to its use
+    // (block formats: each block's codes formed now, the table lookups or
+    // high bits off the path after the records)
+    BlockCodes bc[kQ4 ? 1 : RPG][2];
+    if constexpr (!kQ4) {
+#pragma unroll
+        for (int i = 0; i < RPG; i++)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                bc[i][m] = block_codes<DT>(fw[i][m]);
+#pragma unroll
+                for (int q = 0; q < 8; q++) asm volatile("" : "+v"(bc[i][m].c[q]));
+            }
+    }
     PairScale ps[RPG];
     uint32_t nlo[2][8], nhi[2][8];
 #pragma unroll
@@ -1592,7 +1663,7 @@ __device__ __forceinline__ void role_down(const FusedArgs &a, uint8_t *smem, uin
                 ux.xs[0] = rec_xs[2 * u];
                 ux.xs[1] = rec_xs[2 * u + 1];
 #pragma unroll
-                for (int i = 0; i < RPG; i++) v[i] += dot_unit<DT>(fw[i][m], u, ux);
+                for (int i = 0; i < RPG; i++) v[i] += block_codes_dot<DT>(bc[i][m], ux);
             }
         }
     }
@@ -1915,6 +1986,7 @@ FusedPlan plan_moe_fused(const FusedLayer &L) {
         lds = std::max(lds, std::max(lds_router, std::max(lds_down, lds_gu)));
     }
     if (sh) lds = std::max(lds, std::max((size_t)D * 4, sh_down_lds(L.S)));  // x; shared down weights + h slice
+    if (pl.gemma) lds = std::max(lds, (size_t)2 * 128 * 4 + (size_t)D * 4);  // router terms + the prepared x
     if (lds > 40 * 1024) return pl;  // four blocks per CU (160 KB of LDS): the whole grid resident
     pl.lds = lds;
     pl.ok = true;
