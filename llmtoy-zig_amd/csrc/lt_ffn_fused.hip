@@ -84,11 +84,15 @@ __device__ __forceinline__ void lds16(const float *p, float (&xv)[16]) {
     }
 }
 
-// Gate/up block i of group x: h rows jb + 4 p + w (p < P) of the slice,
-// wavefront w; lane l takes units l + 64 c (c < CU) of the row (16 quants
-// each).  x goes to LDS once; every load is issued before the first
-// product, unconditionally (clamped), so that each pass waits only for its
-// own data.
+// Gate/up block i of group x: h rows 32 kb0 + 4 (p NG + i) + w (p < P) of
+// the slice, wavefront w -- pass p of the NG blocks covers 4 NG consecutive
+// rows, so the rows past the slice fall to the last pass of the last
+// blocks, and with NG a multiple of 32 (blocks i and i + 32 share a CU)
+// every CU carries the same share of the stream up to one pass; lane l
+// takes units l + 64 c (c < CU) of the row (16 quants each).  x goes to LDS
+// once; every load is issued before the first product, unconditionally (a
+// row past the slice reloads the block's pass-0 row), so that each pass
+// waits only for its own data.
 template <int CU, int P>
 __device__ __forceinline__ void role_gate_up(const FfnArgs &a, float *xs, uint32_t *s_ep, int x, int i, int bid,
                                              int tid, int wave, int lane) {
@@ -96,7 +100,7 @@ __device__ __forceinline__ void role_gate_up(const FfnArgs &a, float *xs, uint32
     int kb0, kb1;
     k_slice(a.nbS, x, kb0, kb1);
     const int j_end = 32 * kb1;
-    const int jb = 32 * kb0 + i * 4 * P;
+    const int jb = 32 * kb0 + 4 * i + wave;  // pass 0's row
     // x: thread t loads float4 t and t + 256 (D <= 2048)
     const float4 x0 = *reinterpret_cast<const float4 *>(a.x + min(4 * tid, a.D - 4));
     const float4 x1 = *reinterpret_cast<const float4 *>(a.x + min(4 * (tid + kThreads), a.D - 4));
@@ -105,7 +109,8 @@ __device__ __forceinline__ void role_gate_up(const FfnArgs &a, float *xs, uint32
     uint32_t dg[P][CU], du[P][CU];
 #pragma unroll
     for (int p = 0; p < P; p++) {
-        const int j = min(jb + 4 * p + wave, j_end - 1);
+        const int jp = jb + 4 * a.NG * p;
+        const int j = jp < j_end ? jp : min(jb, j_end - 1);
 #pragma unroll
         for (int c = 0; c < CU; c++) {
             const int u = min(lane + 64 * c, nu - 1);
@@ -124,7 +129,7 @@ __device__ __forceinline__ void role_gate_up(const FfnArgs &a, float *xs, uint32
     const bool first = p32_first(lane);
 #pragma unroll
     for (int p = 0; p < P; p++) {
-        const int j = jb + 4 * p + wave;
+        const int j = jb + 4 * a.NG * p;
         float g = 0.0f, up = 0.0f;
 #pragma unroll
         for (int c = 0; c < CU; c++) {
@@ -272,10 +277,13 @@ FfnPlan plan_ffn_fused(int D, int S) {
     pl.cu = (2 * (D / 32) + 63) / 64;
     // fewest down steps first, then fewest gate/up passes (measured on
     // config 1: 3 passes / 1 step 7.3 us, 2 / 2 7.4, 4 / 1 8.4; a 2048-block
-    // grid with 1 / 1 7.6)
+    // grid with 1 / 1 7.6); the gate/up blocks rounded up to a multiple of
+    // 32 where the grid has room (every CU the same share)
     for (int Q = 1; Q <= kQMax && !pl.ok; Q++)
         for (int P = 1; P <= kPMax && !pl.ok; P++) {
-            const int NG = (rows_max + 4 * P - 1) / (4 * P), ND = (D + 16 * Q - 1) / (16 * Q);
+            const int ND = (D + 16 * Q - 1) / (16 * Q);
+            int NG = (rows_max + 4 * P - 1) / (4 * P);
+            if ((NG + 31) / 32 * 32 + ND <= kFusedBlocks / 8) NG = (NG + 31) / 32 * 32;
             if (NG + ND <= kFusedBlocks / 8 && ND <= kFfnFlags) {
                 pl.P = P;
                 pl.Q = Q;

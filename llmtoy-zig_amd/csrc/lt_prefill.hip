@@ -53,7 +53,7 @@ namespace {
 
 constexpr int MC = 128;       // sorted rows per chunk: 4 wavefronts x 32
 constexpr int KS = 128;       // K per stage: half a Q4_K super-block
-constexpr int LDK = KS + 8;   // padded LDS row (f16 elements)
+constexpr int LDK = KS;       // LDS row (f16 elements), units swizzled (bunit)
 constexpr int NB = 128;       // weight rows per block (gate/up: 64 gate + 64 up)
 constexpr int BN1 = 64;       // gate/up output columns per block
 constexpr int BN2 = 128;      // down output rows (= output columns of Y) per block
@@ -96,6 +96,20 @@ Ws carve(void *base, int T, int k, int E, int Kd, int D) {
     return w;
 }
 
+// LDS weight tiles: a row's 128 K values are 16 units of 8 f16 (16 bytes);
+// unit u of row r is stored at unit bunit(r, u) = u ^ g(r) ^ 4 (u >> 3 & 1),
+// g(r) = r & 7 | (r >> 3 ^ r >> 1 & 1) << 3.  g takes 16 distinct values over
+// 16 consecutive rows, so the MFMA operand reads (consecutive lanes: rows
+// r.., one unit) fall in distinct 16-byte bank groups; the 4 (u >> 3 & 1)
+// separates a dequantising quad's units U and 8 + U of one row, so its
+// 16-byte writes (a quad per row, four rows per 16 lanes) are conflict-free
+// too, whether the LDS serves 8 lanes over 32 banks or 16 over 64.  A
+// bijection within each row (XOR with 4 leaves bit 3 alone).  Rows r and
+// r + 32 j share g.
+__host__ __device__ __forceinline__ int bunit(int r, int u) {
+    return u ^ ((r & 7) | (((r >> 3) ^ (r >> 1)) & 1) << 3) ^ (((u >> 3) & 1) << 2);
+}
+
 // The K order of every f16 operand: within each aligned group of 4 the
 // middle two elements are swapped (an involution).
 __host__ __device__ __forceinline__ int kperm(int c) { return (c & ~3) | ((c & 1) << 1) | ((c >> 1) & 1); }
@@ -115,8 +129,8 @@ __device__ __forceinline__ void q4_pairs_to_f16(const uint32_t (&v)[4], half2v s
 
 // Q4_K 16-byte chunk cc (0..7) of a super-block with header hdr, dequantised
 // (quant/dequant.zig:157-187: (d*sc)*q - dmin*mn) to f16: elements 64p +
-// 16(cc&1) + [0, 16) at lo_dst, the same + 32 at hi_dst (p = cc / 2), each
-// run in kperm order.  Quant byte j holds element j of the low run in its
+// 16(cc&1) + [0, 8) at dst[0], + [8, 16) at dst[1], the same + 32 at dst[2],
+// dst[3] (p = cc / 2), each run in kperm order.  Quant byte j holds element j of the low run in its
 // low nibble and of the high run in its high nibble.  Under f16's exponent
 // of 1024 (0x6400) a nibble in mantissa bits 0-3 reads 1024 + q and one in
 // bits 4-7 reads 1024 + 16 q, both exact, so (w & 0x000f000f) | 0x64006400
@@ -124,7 +138,7 @@ __device__ __forceinline__ void q4_pairs_to_f16(const uint32_t (&v)[4], half2v s
 // | 0x64006400 the high-run pair, and the same of w >> 8 gives (e1, e3):
 // one v_and_or per pair (the masks kept in registers so that the compiler
 // forms it), the high run's scale divided by 16.
-__device__ __forceinline__ void q4k_chunk_to_f16(uint4 hdr, uint4 q, int cc, _Float16 *lo_dst, _Float16 *hi_dst) {
+__device__ __forceinline__ void q4k_chunk_to_f16(uint4 hdr, uint4 q, int cc, _Float16 *const (&dst)[4]) {
     const float d = f16_bits_to_f32(hdr.x), dmin = f16_bits_to_f32(hdr.x >> 16);
     const int p = cc >> 1;
     const int sh = (p & 1) * 16;
@@ -147,10 +161,10 @@ __device__ __forceinline__ void q4k_chunk_to_f16(uint4 hdr, uint4 q, int cc, _Fl
     }
     const uint32_t lo0[4] = {lo[0], lo[1], lo[2], lo[3]}, lo1[4] = {lo[4], lo[5], lo[6], lo[7]};
     const uint32_t hi0[4] = {hi[0], hi[1], hi[2], hi[3]}, hi1[4] = {hi[4], hi[5], hi[6], hi[7]};
-    q4_pairs_to_f16(lo0, half2v{d1, d1}, half2v{m1, m1}, lo_dst);
-    q4_pairs_to_f16(lo1, half2v{d1, d1}, half2v{m1, m1}, lo_dst + 8);
-    q4_pairs_to_f16(hi0, half2v{d2, d2}, half2v{m2, m2}, hi_dst);
-    q4_pairs_to_f16(hi1, half2v{d2, d2}, half2v{m2, m2}, hi_dst + 8);
+    q4_pairs_to_f16(lo0, half2v{d1, d1}, half2v{m1, m1}, dst[0]);
+    q4_pairs_to_f16(lo1, half2v{d1, d1}, half2v{m1, m1}, dst[1]);
+    q4_pairs_to_f16(hi0, half2v{d2, d2}, half2v{m2, m2}, dst[2]);
+    q4_pairs_to_f16(hi1, half2v{d2, d2}, half2v{m2, m2}, dst[3]);
 }
 
 // One thread's share of a K stage's weight tile: 2 units of (weight row r,
@@ -179,15 +193,19 @@ __device__ __forceinline__ uint32_t quad_word(uint32_t v) {
 }
 
 // Stage ks's chunk cc = 4 (ks & 1) + c lands at local K 64 (c / 2) + 16 (c & 1)
-// (low nibbles) and +32 (high nibbles).
-__device__ __forceinline__ void stage_dequant(const StageRegs &R, _Float16 (*Bs)[LDK], int r0, int ks, int c) {
-    const int cc = (ks & 1) * 4 + c, local = 64 * (c >> 1) + 16 * (c & 1);
+// (low nibbles) and +32 (high nibbles): units U, U + 1, U + 4, U + 5 with U
+// = 8 (c / 2) + 2 (c & 1), at doff[q] = 8 bunit(r0, unit) (rows r0 + 64 j
+// share r0's swizzle).
+__device__ __forceinline__ void stage_dequant(const StageRegs &R, _Float16 (*Bs)[LDK], int r0, int ks, int c,
+                                              const int (&doff)[4]) {
+    const int cc = (ks & 1) * 4 + c;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         _Float16 *row = Bs[r0 + 64 * j];
         const uint4 h = make_uint4(quad_word<0x00>(R.h[j]), quad_word<0x55>(R.h[j]), quad_word<0xAA>(R.h[j]),
                                    quad_word<0xFF>(R.h[j]));
-        q4k_chunk_to_f16(h, R.q[j], cc, row + local, row + local + 32);
+        _Float16 *const dst[4] = {row + doff[0], row + doff[1], row + doff[2], row + doff[3]};
+        q4k_chunk_to_f16(h, R.q[j], cc, dst);
     }
 }
 
@@ -205,6 +223,16 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
                                              const _Float16 *arow, bool wave_on, int kb, int tid, int lane) {
     constexpr int NK = 8 / S;
     const int c = tid & 3, r0 = tid >> 2;
+    int doff[4], boff[NK];  // this thread's swizzled LDS units (f16 offsets in a row)
+    {
+        const int U = 8 * (c >> 1) + 2 * (c & 1);
+        doff[0] = 8 * bunit(r0, U);
+        doff[1] = 8 * bunit(r0, U + 1);
+        doff[2] = 8 * bunit(r0, U + 4);
+        doff[3] = 8 * bunit(r0, U + 5);
+#pragma unroll
+        for (int i = 0; i < NK; i++) boff[i] = 8 * bunit(lane & 31, 2 * (kb + i) + (lane >> 5));
+    }
     StageRegs R[3];
     f16x8 a[2][NK];
 #pragma unroll
@@ -220,7 +248,7 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
     stage_load(R[2], hdr, qs, nsb, wrow, min(2, NS - 1), c);
 #pragma unroll
     for (int i = 0; i < NK; i++) a[0][i] = *reinterpret_cast<const f16x8 *>(arow + (kb + i) * 16);
-    stage_dequant(R[0], Bs[0], r0, 0, c);
+    stage_dequant(R[0], Bs[0], r0, 0, c, doff);
     stage_load(R[0], hdr, qs, nsb, wrow, min(3, NS - 1), c);
     __syncthreads();
     // Six stages per trip, so that the A buffers (stage parity) and the
@@ -244,12 +272,11 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
                 for (int i = 0; i < NK; i++)
 #pragma unroll
                     for (int ct = 0; ct < 4; ct++) {
-                        const f16x8 b = *reinterpret_cast<const f16x8 *>(
-                            &B[32 * ct + (lane & 31)][(kb + i) * 16 + (lane >> 5) * 8]);
+                        const f16x8 b = *reinterpret_cast<const f16x8 *>(&B[32 * ct + (lane & 31)][boff[i]]);
                         acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(acur[i], b, acc[ct], 0, 0, 0);
                     }
             }
-            if (st + 1 < NS) stage_dequant(Rn, Bs[(st + 1) & 1], r0, st + 1, c);
+            if (st + 1 < NS) stage_dequant(Rn, Bs[(st + 1) & 1], r0, st + 1, c, doff);
             stage_load(Rn, hdr, qs, nsb, wrow, min(st + 4, NS - 1), c);
             __syncthreads();
         }
