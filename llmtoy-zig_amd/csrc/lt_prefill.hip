@@ -289,10 +289,14 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
 // last stage) and are added in wavefront order, so results do not depend
 // on timing.  acc element i of a 32x32 tile is C[(i / 4) * 8 + (lane / 32) *
 // 4 + i % 4][lane % 32].
-template <int S, typename Row, typename Epi>
+// pre(t, i) gives a value epi receives with element i (the gate/up
+// kernel's row scale): all of a wavefront's pre loads are issued before its
+// first epi, so that their round trips overlap instead of queueing behind
+// each element's stores.
+template <int S, typename Row, typename Pre, typename Epi>
 __device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t *hdr, const uint8_t *qs, int nsb,
-                                          const size_t (&wrow)[2], int NS, int mc, Row row_ptr, Epi epi, int tid,
-                                          int wave, int lane) {
+                                          const size_t (&wrow)[2], int NS, int mc, Row row_ptr, Pre pre, Epi epi,
+                                          int tid, int wave, int lane) {
     constexpr int NT = 4 / S;  // token tiles handled side by side
     const int t = wave % NT, q = wave / NT;
     const int mrow = 32 * t + (lane & 31);
@@ -300,13 +304,19 @@ __device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t
     const _Float16 *arow = row_ptr(mrow < mc ? mrow : 0) + (lane >> 5) * 8;
     floatx16 acc[4];
     grouped_gemm<S>(acc, Bs, hdr, qs, nsb, wrow, NS, arow, wave_on, q * (8 / S), tid, lane);
+    constexpr int NI = 16 / S;  // elements this wavefront hands over
+    const int i0 = S == 1 ? 0 : q * NI;
+    float pv[NI];
     if (S == 1) {
-        if (wave_on)
+        if (wave_on) {
+#pragma unroll
+            for (int ii = 0; ii < NI; ii++) pv[ii] = pre(t, ii);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float v[4] = {acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
-                epi(t, i, v);
+                epi(t, i, v, pv[i]);
             }
+        }
         return;
     }
     float *red = reinterpret_cast<float *>(&Bs[0][0][0]);  // [4 waves][4 ct][16 i][64 lanes]
@@ -316,8 +326,11 @@ __device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t
         for (int i = 0; i < 16; i++) red[((wave * 4 + ct) * 16 + i) * 64 + lane] = acc[ct][i];
     __syncthreads();
     if (!wave_on) return;
-    for (int ii = 0; ii < 16 / S; ii++) {
-        const int i = q * (16 / S) + ii;
+#pragma unroll
+    for (int ii = 0; ii < NI; ii++) pv[ii] = pre(t, i0 + ii);
+#pragma unroll
+    for (int ii = 0; ii < NI; ii++) {
+        const int i = i0 + ii;
         float v[4];
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) {
@@ -326,7 +339,7 @@ __device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t
             for (int qq = 0; qq < S; qq++) sum += red[(((t + NT * qq) * 4 + ct) * 16 + i) * 64 + lane];
             v[ct] = sum;
         }
-        epi(t, i, v);
+        epi(t, i, v, pv[ii]);
     }
 }
 
@@ -460,10 +473,28 @@ __global__ void __launch_bounds__(256) k_prefill_x_f16(const float *__restrict__
 }
 
 // ---------------------------------------------------------------- gate/up
+// The activation for the f16 H, branch-free: e^x and 1 / x as one hardware
+// instruction each (v_exp_f32 on x log2 e, v_rcp_f32; about 1 ulp of fp32,
+// far below the f16 rounding of H that follows).  SiLU g / (1 + e^-g);
+// GELU (tanh form) 0.5 g (1 + tanh y) with tanh y = 1 - 2 / (1 + e^2y).
+// Limits: g -> -inf gives -0 (SiLU) or 0, +inf gives g; NaN passes.
+template <int ACT>
+__device__ __forceinline__ float prefill_act(float g) {
+    constexpr float kLog2e = 1.4426950408889634f;
+    if (ACT == 1) {
+        const float y = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+        const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(2.0f * kLog2e * y));
+        return 0.5f * g * (1.0f + t);
+    }
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * g));
+}
+
 // Block: chunk (expert e, sorted rows base + m0 + [0, mc)) x output columns
 // [n0, n0 + 64).  Weight rows 0..63 are gate rows n0.., 64..127 the up rows;
 // wavefront w computes token tile w against all 128 (ct 0,1 = gate, 2,3 =
-// up), so h = act(gate) * up is formed in registers.
+// up), so h = act(gate) * up is formed in registers.  ACT: the activation
+// (0 SiLU, 1 GELU-tanh).
+template <int ACT>
 __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restrict__ hdr,
                                                          const uint8_t *__restrict__ qs, int nsb, int F,
                                                          const _Float16 *__restrict__ Xh,
@@ -493,31 +524,33 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
     // kperm order (the down GEMM's K); a finite value past f16's range
     // saturates at +-65504 and is counted (inf and NaN pass through)
     uint32_t sat = 0;
-    auto sat16 = [&](float h) {
-        if (fabsf(h) > 65504.0f && fabsf(h) <= 3.4e38f) {
-            h = copysignf(65504.0f, h);
-            sat++;
-        }
-        return (_Float16)h;
+    auto sat16 = [&](float h) {  // (no branch: a select and a count)
+        const bool big = fabsf(h) > 65504.0f && fabsf(h) <= 3.4e38f;
+        sat += big ? 1u : 0u;
+        return (_Float16)(big ? copysignf(65504.0f, h) : h);
     };
-    auto epi = [&](int t, int i, const float (&v)[4]) {
+    auto pre = [&](int t, int i) {  // the row's scale (rows past the chunk: row 0's)
+        const int m = 32 * t + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+        return rs[prow[m < mc ? m : 0]];
+    };
+    auto epi = [&](int t, int i, const float (&v)[4], float r) {
         const int m = 32 * t + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
         if (m < mc) {
-            const float r = rs[prow[m]], ri = 1.0f / r;  // (powers of two: exact)
+            // r = 2^k exactly: frexp gives k + 1, so 1 / r = 2^(1 - (k + 1))
+            const float ri = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(r));
             _Float16 *hrow = H + (size_t)(base + m0 + m) * Kd;
             const int c0 = n0 + (lane & 31);
-            const float h0 = act_apply(act, v[0] * r) * (v[2] * ri), h1 = act_apply(act, v[1] * r) * (v[3] * ri);
-            hrow[kperm(c0)] = sat16(h0);
-            hrow[kperm(c0 + 32)] = sat16(h1);
+            hrow[kperm(c0)] = sat16(prefill_act<ACT>(v[0] * r) * (v[2] * ri));
+            hrow[kperm(c0 + 32)] = sat16(prefill_act<ACT>(v[1] * r) * (v[3] * ri));
         }
     };
     const int nt = (mc + 31) / 32, NS = 2 * nsb;
     if (nt == 1)
-        run_block<4>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+        run_block<4>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
     else if (nt == 2)
-        run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+        run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
     else
-        run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+        run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
     if (sat) {  // (rare): the count and the error bit, reported at the next synchronising call
         __hip_atomic_fetch_add(err + kErrPrefillSat, sat, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         report_timeout(err, kErrCodePrefillSat);
@@ -547,7 +580,8 @@ __global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict_
     for (int j = 0; j < 2; j++) wrow[j] = (size_t)e * D + n0 + (tid >> 2) + 64 * j;
     const _Float16 *hbase = H + (size_t)(base + m0) * Kd;
     auto row_ptr = [&](int m) { return hbase + (size_t)m * Kd; };
-    auto epi = [&](int t, int i, const float (&v)[4]) {
+    auto pre = [](int, int) { return 0.0f; };
+    auto epi = [&](int t, int i, const float (&v)[4], float) {
         const int m = 32 * t + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
         if (m < mc) {
             float *yrow = Y + (size_t)(base + m0 + m) * D + n0 + (lane & 31);
@@ -557,11 +591,11 @@ __global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict_
     };
     const int nt = (mc + 31) / 32, NS = 2 * nsb;
     if (nt == 1)
-        run_block<4>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+        run_block<4>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
     else if (nt == 2)
-        run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+        run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
     else
-        run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, epi, tid, wave, lane);
+        run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
 }
 
 // ---------------------------------------------------------------- combine
@@ -626,8 +660,9 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const int mc = max_chunks(TK, E);
-    hipLaunchKernelGGL(k_prefill_gate_up, dim3(F / BN1, mc), dim3(256), 0, s, GU.p0, GU.p1, (int)GU.blocks_per_row,
-                       F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm, act, w.H, Kd, err);
+    hipLaunchKernelGGL(act == 1u ? k_prefill_gate_up<1> : k_prefill_gate_up<0>, dim3(F / BN1, mc), dim3(256), 0, s,
+                       GU.p0, GU.p1, (int)GU.blocks_per_row, F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm,
+                       act, w.H, Kd, err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_prefill_down, dim3(D / BN2, mc), dim3(256), 0, s, Dn.p0, Dn.p1, (int)Dn.blocks_per_row, D,
                        w.H, Kd, w.chunks, w.n_chunks, w.offsets, w.Y);
