@@ -28,7 +28,8 @@ Measurement (every workload):
     algorithmic bytes per launch / that duration.  traffic = HBM bytes per
     launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs committed under
     profiles/ (scaled by the counters' reading on a copy of known size), or
-    null when no counter summary exists for the workload.
+    null when no counter summary exists for the workload; traffic_gbps =
+    those bytes over the same launch duration (the counter-side GB/s).
   * cpu_baseline: the oracle's restatement of the reference CPU path
     (quantMatvecPar row split over a persistent pool + moeForward) on this
     host, min(usable cores, 64) threads (the reference's job arrays hold 64),
@@ -122,6 +123,8 @@ def roofline(kernel: str, algo_bytes: int, mean_us: float, pmc_name: str | None,
          "timing": f"{iters} back-to-back launches, one HIP event pair on the library stream"}
     r["traffic_source"] = (f"committed counters {src} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE per dispatch, "
                            "scaled by a 256 MiB copy), not measured in this run") if traffic is not None else None
+    # the second derivation: counter bytes (FETCH + WRITE) over the same launch time
+    r["traffic_gbps"] = None if traffic is None else round(traffic / (mean_us * 1e-6) / 1e9, 1)
     return r
 
 
