@@ -440,9 +440,9 @@ int check_fused_err(lt_ctx *ctx) {
     return fail(ctx, LT_ERR_DEVICE,
                 "single-launch kernel: a hand-over wait timed out (code 0x%x: 1 gate/up logits, 2 down logits, 4 down "
                 "h records, 8 combine, 0x10 shared-FFN logits or last h word, 0x20 shared-FFN h, 0x40 dense-FFN h, "
-                "0x80 dense-FFN start values, 0x100 prefill f16 saturation, 0x200 Gemma4 tail; first recorded: block %d, "
-                "site 0x%x, index "
-                "%u, saw %u, expected epoch %u); outputs of that call are NaN",
+                "0x80 dense-FFN start values, 0x100 prefill f16 saturation, 0x200 Gemma4 tail, 0x400 prefill chunk "
+                "activations; first recorded: block %d, site 0x%x, index %u, saw %u, expected epoch or count %u); "
+                "outputs of that call are NaN (prefill: wrong)",
                 v, (int)d[0] - 1, d[1], d[2], d[3], d[4]);
 }
 
@@ -1191,7 +1191,7 @@ extern "C" int lt_moe_prefill(lt_ctx *ctx, float *out, const float *X, uint32_t 
     rc = launch_rc(ctx,
                    lt::launch_moe_prefill(router->t, gate_up->t, down->t, dX, (int)T, dbias, (int)k, (int)d_expert,
                                           act, (flags & LT_MOE_NORM_TOPK) ? 1u : 0u, ctx->pf.p, dout, dids, dw,
-                                          ctx->err_dev, ctx->stream),
+                                          ctx->err_dev, ctx->xcd_local, ctx->stream),
                    "moe_prefill");
     if (rc) return rc;
     if (host) {

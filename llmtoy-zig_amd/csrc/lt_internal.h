@@ -299,9 +299,11 @@ __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t ep) { return (uint32
 
 // The context's host-mapped error words (16): [0] code bits (the fused
 // kernels' timed-out waits below 0x100), [2..6] the first wait's details,
-// [8] the prefill's count of saturated f16 activations (code bit 0x100).
+// [8] the prefill's count of saturated f16 activations (code bit 0x100);
+// 0x400: a prefill down block's wait for its chunk's activations.
 constexpr uint32_t kErrCodePrefillSat = 0x100u;
 constexpr int kErrPrefillSat = 8;
+constexpr uint32_t kErrCodePrefillWait = 0x400u;
 __device__ __forceinline__ void report_timeout(uint32_t *err, uint32_t code) {
     __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -416,9 +418,11 @@ hipError_t launch_router_batched(const DevTensor &R, const float *X, int T, cons
 // Batched prefill MoE (Q4_K experts), see lt_prefill.hip.  ws: workspace of
 // prefill_workspace_bytes(T, k, E, F, D) bytes.
 size_t prefill_workspace_bytes(int T, int k, int E, int F, int D);
+// xcd_local (blocks with equal index % 8 share an XCD): both GEMMs in one
+// launch, H handed over in the XCD's L2; else one launch each.
 hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const DevTensor &Dn, const float *X, int T,
                               const float *bias, int k, int F, uint32_t act, uint32_t norm, void *ws, float *out,
-                              uint32_t *out_ids, float *out_w, uint32_t *err, hipStream_t s);
+                              uint32_t *out_ids, float *out_w, uint32_t *err, int xcd_local, hipStream_t s);
 hipError_t launch_expert_gate_up_q4k(const DevTensor &GU, const float *x, const uint32_t *ids, uint32_t k,
                                      uint32_t d_expert, uint32_t down_cols, uint32_t act, float *h,
                                      hipStream_t s);

@@ -6,7 +6,8 @@
 //      and per-token softmax / top-k (lt_router.hip);
 //   2. dispatch: one block counts tokens per expert, lays out per-expert
 //      row ranges ("sorted rows"), cuts each range into chunks of at most
-//      MC = 128 rows, and scatters (token, slot) assignments into them;
+//      MC = 128 rows, and places the (token, slot) assignments into them in
+//      assignment order (a stable counting sort);
 //      X is converted to f16 once (by the router kernel, or
 //      k_prefill_x_f16), each row t divided by r_t = 2^e, a power of two
 //      that puts its largest element in [1, 2);
@@ -24,13 +25,17 @@
 //      scheme with H as the A operand -> Y (fp32, sorted rows);
 //   5. combine: out[t] = r_t^2 * sum over slots in slot order of w[t][s] *
 //      Y[pos] (r_t^2 exact).
+// Steps 3 and 4 run as one launch when blocks with equal index % 8 share an
+// XCD (k_prefill_gemms: a chunk's down blocks take H from its gate/up
+// blocks through that XCD's L2), else as two.
 // Both GEMMs run a software pipeline over K stages of 128 (half a Q4_K
 // super-block): weight loads are issued two stages ahead into registers,
 // A fragments one stage ahead, the dequantised tile is double-buffered in
 // LDS, and each stage ends in one barrier.
-// A row's result does not depend on which chunk position it lands in, so
-// the atomically assigned positions leave the output bit-identical run to
-// run.
+// A row's result depends on its chunk only through the chunk's token tiles
+// (they pick the K split of the GEMMs, and with it the order of the fp32
+// sums), and the stable placement gives every row the same chunk on every
+// call, so the output is bit-identical run to run.
 //
 // f16 rather than bf16 tiles: a Q4_K nibble q becomes the exact f16 1024 + q
 // (or 1024 + 16 q) with one v_and_or (its bits in the mantissa under 1024's
@@ -73,6 +78,7 @@ struct Ws {
     _Float16 *Xh;   // [T][D] X / rs in f16, columns in kperm order
     _Float16 *H;    // [T*k][Kd], columns in kperm order
     float *Y;       // [T*k][D]
+    int *done;      // [max_chunks] finished gate/up blocks per chunk (fused GEMMs)
 };
 
 int max_chunks(int TK, int E) { return (TK + MC - 1) / MC + E; }
@@ -93,6 +99,7 @@ Ws carve(void *base, int T, int k, int E, int Kd, int D) {
     w.Xh = (_Float16 *)p; p += align256((size_t)T * D * 2);
     w.H = (_Float16 *)p; p += align256(TK * Kd * 2);
     w.Y = (float *)p; p += align256(TK * D * 4);
+    w.done = (int *)p; p += align256((size_t)max_chunks((int)TK, E) * 4);
     return w;
 }
 
@@ -217,10 +224,14 @@ __device__ __forceinline__ void stage_dequant(const StageRegs &R, _Float16 (*Bs)
 // tiles over 2 / 4 wavefronts, so a chunk with a single token tile still
 // keeps all four wavefronts' MFMA pipes busy.  arow points at this lane's A
 // row (row 32 t + lane % 32 of the chunk) plus its K half (lane / 32) * 8.
-template <int S>
+// wait() runs (in every thread) once the first weight stages are requested
+// and before the first A load: the fused kernel's down blocks wait there
+// for their chunk's activations.
+template <int S, typename Wait>
 __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[NB][LDK], const uint8_t *hdr,
                                              const uint8_t *qs, int nsb, const size_t (&wrow)[2], int NS,
-                                             const _Float16 *arow, bool wave_on, int kb, int tid, int lane) {
+                                             const _Float16 *arow, bool wave_on, int kb, int tid, int lane,
+                                             Wait wait) {
     constexpr int NK = 8 / S;
     const int c = tid & 3, r0 = tid >> 2;
     int doff[4], boff[NK];  // this thread's swizzled LDS units (f16 offsets in a row)
@@ -246,6 +257,7 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
     stage_load(R[0], hdr, qs, nsb, wrow, 0, c);
     stage_load(R[1], hdr, qs, nsb, wrow, 1, c);  // NS = 2 * super-blocks >= 2
     stage_load(R[2], hdr, qs, nsb, wrow, min(2, NS - 1), c);
+    wait();
 #pragma unroll
     for (int i = 0; i < NK; i++) a[0][i] = *reinterpret_cast<const f16x8 *>(arow + (kb + i) * 16);
     stage_dequant(R[0], Bs[0], r0, 0, c, doff);
@@ -293,17 +305,17 @@ __device__ __forceinline__ void grouped_gemm(floatx16 (&acc)[4], _Float16 (*Bs)[
 // kernel's row scale): all of a wavefront's pre loads are issued before its
 // first epi, so that their round trips overlap instead of queueing behind
 // each element's stores.
-template <int S, typename Row, typename Pre, typename Epi>
+template <int S, typename Row, typename Pre, typename Epi, typename Wait>
 __device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t *hdr, const uint8_t *qs, int nsb,
                                           const size_t (&wrow)[2], int NS, int mc, Row row_ptr, Pre pre, Epi epi,
-                                          int tid, int wave, int lane) {
+                                          Wait wait, int tid, int wave, int lane) {
     constexpr int NT = 4 / S;  // token tiles handled side by side
     const int t = wave % NT, q = wave / NT;
     const int mrow = 32 * t + (lane & 31);
     const bool wave_on = 32 * t < mc;
     const _Float16 *arow = row_ptr(mrow < mc ? mrow : 0) + (lane >> 5) * 8;
     floatx16 acc[4];
-    grouped_gemm<S>(acc, Bs, hdr, qs, nsb, wrow, NS, arow, wave_on, q * (8 / S), tid, lane);
+    grouped_gemm<S>(acc, Bs, hdr, qs, nsb, wrow, NS, arow, wave_on, q * (8 / S), tid, lane, wait);
     constexpr int NI = 16 / S;  // elements this wavefront hands over
     const int i0 = S == 1 ? 0 : q * NI;
     float pv[NI];
@@ -346,67 +358,145 @@ __device__ __forceinline__ void run_block(_Float16 (*Bs)[NB][LDK], const uint8_t
 }  // namespace
 
 // ---------------------------------------------------------------- dispatch
+// The lanes of the wavefront whose id equals this lane's (ids below 2^nb,
+// invalid ids >= E in a group of their own): one ballot per id bit.
+__device__ __forceinline__ uint64_t match_ids(uint32_t x, bool valid, int nb) {
+    uint64_t m = __ballot(1);  // the active lanes
+    const uint64_t v = __ballot(valid);
+    m &= valid ? v : ~v;
+    for (int b = 0; b < nb; b++) {
+        const bool on = (x >> b) & 1u;
+        const uint64_t bb = __ballot(on);
+        m &= on ? bb : ~bb;
+    }
+    return m;
+}
+
+// Lanes of m below this lane.
+__device__ __forceinline__ int rank_in(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// One block of 1024 threads.  Assignment i = t k + s goes to sorted row
+// offsets[e] + (the number of assignments before i with the same expert e):
+// a stable counting sort, so every row's chunk, and with it the row's
+// result (the chunk's token tiles pick the GEMM's K split), is the same on
+// every call.  Assignments are taken in rounds of 1024 (i = 1024 r + tid),
+// a round in 16 segments of 64 (its wavefronts).  Within a wavefront the
+// lanes with equal ids find each other with one ballot per id bit
+// (match_ids); the first lane of each group adds the group's size to its
+// expert's count and, for the placement, writes it to the segment's entry
+// of a [segment][expert] table, which P = 1024 / E threads per expert
+// turn into each segment's first row (an exclusive scan over segments, the
+// experts' running rows carried from one batch of rounds to the next).
+// Per expert e (thread e): v[0] = its row count, v[1] = its full chunks,
+// v[2 + c] = 1 if its last chunk is partial with c + 1 token tiles.  An
+// inclusive scan over experts (wavefront scans, then the wavefront totals)
+// gives every expert its row offset and the positions of its chunks in a
+// list ordered by token tiles, largest first: the blocks with the most
+// MFMA work are dispatched first and the short ones fill in behind them.
+// Up to kIdsPer ids per thread are loaded once, all in flight together,
+// and kept with their ranks for the placement; longer batches read them
+// again.
 __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__restrict__ ids, int TK, int k, int E,
                                                            int *__restrict__ offsets, int *__restrict__ chunks,
                                                            int *__restrict__ n_chunks, int *__restrict__ perm,
-                                                           int *__restrict__ pos) {
-    // Per expert e (thread e): v[0] = its row count, v[1] = its full chunks,
-    // v[2 + c] = 1 if its last chunk is partial with c + 1 token tiles.  An
-    // inclusive scan over experts gives every expert its row offset and the
-    // positions of its chunks in a list ordered by token tiles, largest
-    // first: the blocks with the most MFMA work are dispatched first and
-    // the short ones fill in behind them.
-    // Up to kIdsPer ids per thread are loaded once, all in flight together,
-    // and kept for the scatter; longer batches read them again.
-    constexpr int kIdsPer = 8;
-    __shared__ int cnt[1024], cur[1024];
-    __shared__ int scan[2][6][1024];
-    const int e = threadIdx.x;
-    const bool cached = TK <= kIdsPer * (int)blockDim.x;
+                                                           int *__restrict__ pos, int *__restrict__ done, int maxc) {
+    constexpr int kIdsPer = 8, kTab = 16384;
+    __shared__ int cnt[1024], cur[1024], psum[1024];
+    __shared__ int tab[kTab];  // [segment][E]: group sizes, then the segment's first rows
+    __shared__ int wsum[6][16];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nb = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
+    const bool cached = TK <= kIdsPer * 1024;
+    const int rounds = (TK + 1023) / 1024;
     uint32_t xc[kIdsPer];
+    int rk[kIdsPer], gs[kIdsPer];  // cached: rank in the wavefront's group, group size (0: not the group's first)
 #pragma unroll
     for (int j = 0; j < kIdsPer; j++) {
-        const int i = threadIdx.x + j * blockDim.x;
+        const int i = tid + j * 1024;
         xc[j] = cached && i < TK ? ids[i] : 0xffffffffu;
     }
-    if (e < E) cnt[e] = 0;
+    if (tid < E) cnt[tid] = 0;
+    for (int i = tid; i < maxc; i += 1024) done[i] = 0;  // the fused GEMMs' per-chunk counts
     __syncthreads();
+    auto group = [&](uint32_t x, int &rank, int &size) {
+        const bool valid = x < (uint32_t)E;
+        const uint64_t m = match_ids(x, valid, nb);
+        rank = rank_in(m);
+        size = valid && rank == 0 ? __popcll(m) : 0;
+    };
+    // assignment tid + 1024 r: id, rank, group size
+    auto get = [&](int r, uint32_t &x, int &rank, int &size) {
+        if (cached) {
+            x = 0xffffffffu;
+            rank = size = 0;
+#pragma unroll
+            for (int j = 0; j < kIdsPer; j++)
+                if (j == r) {
+                    x = xc[j];
+                    rank = rk[j];
+                    size = gs[j];
+                }
+        } else {
+            const int i = tid + 1024 * r;
+            x = i < TK ? ids[i] : 0xffffffffu;
+            group(x, rank, size);
+        }
+    };
     if (cached) {
 #pragma unroll
-        for (int j = 0; j < kIdsPer; j++)
-            if (xc[j] < (uint32_t)E) atomicAdd(&cnt[xc[j]], 1);
+        for (int j = 0; j < kIdsPer; j++) {
+            if (j < rounds) {
+                group(xc[j], rk[j], gs[j]);
+                if (gs[j]) atomicAdd(&cnt[xc[j]], gs[j]);
+            }
+        }
     } else {
-        for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+        for (int i = tid; i < TK; i += 1024) {
             const uint32_t x = ids[i];
             if (x < (uint32_t)E) atomicAdd(&cnt[x], 1);
         }
     }
     __syncthreads();
+    const int e = tid;
     const int n = e < E ? cnt[e] : 0, full = n / MC, rem = n % MC, cls = rem ? (rem + 31) / 32 : 0;
     int v[6] = {n, full, cls == 1, cls == 2, cls == 3, cls == 4};
 #pragma unroll
-    for (int a = 0; a < 6; a++) scan[0][a][e] = v[a];
-    __syncthreads();
-    int b = 0;
-    for (int d = 1; d < (int)blockDim.x; d <<= 1, b ^= 1) {
+    for (int d = 1; d < 64; d <<= 1)
 #pragma unroll
-        for (int a = 0; a < 6; a++)
-            scan[b ^ 1][a][e] = scan[b][a][e] + (e >= d ? scan[b][a][e - d] : 0);
-        __syncthreads();
+        for (int a = 0; a < 6; a++) {
+            const int t = __shfl_up(v[a], d, 64);
+            if (lane >= d) v[a] += t;
+        }
+    if (lane == 63)
+#pragma unroll
+        for (int a = 0; a < 6; a++) wsum[a][wave] = v[a];
+    __syncthreads();
+    int tot[6];
+#pragma unroll
+    for (int a = 0; a < 6; a++) {
+        int before = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < 16; w++) {
+            const int s = wsum[a][w];
+            before += w < wave ? s : 0;
+            all += s;
+        }
+        v[a] += before;  // inclusive scan over experts
+        tot[a] = all;
     }
-    const int last = blockDim.x - 1;
-    const int tot_full = scan[b][1][last];
-    const int tot_p4 = scan[b][5][last], tot_p3 = scan[b][4][last], tot_p2 = scan[b][3][last];
+    const int tot_full = tot[1], tot_p4 = tot[5], tot_p3 = tot[4], tot_p2 = tot[3];
     if (e < E) {
-        const int off = scan[b][0][e] - n;
+        const int off = v[0] - n;
         offsets[e] = off;
         cur[e] = off;
         if (e == E - 1) {
             offsets[E] = off + n;
-            *n_chunks = tot_full + tot_p4 + tot_p3 + tot_p2 + scan[b][2][last];
+            *n_chunks = tot_full + tot_p4 + tot_p3 + tot_p2 + tot[2];
         }
         for (int j = 0; j < full; j++) {
-            int *ch = chunks + 3 * (scan[b][1][e] - full + j);
+            int *ch = chunks + 3 * (v[1] - full + j);
             ch[0] = e;
             ch[1] = j * MC;
             ch[2] = MC;
@@ -415,30 +505,67 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
             const int start = cls == 4 ? tot_full : cls == 3 ? tot_full + tot_p4
                                                   : cls == 2 ? tot_full + tot_p4 + tot_p3
                                                              : tot_full + tot_p4 + tot_p3 + tot_p2;
-            int *ch = chunks + 3 * (start + scan[b][1 + cls][e] - 1);
+            int *ch = chunks + 3 * (start + v[1 + cls] - 1);
             ch[0] = e;
             ch[1] = full * MC;
             ch[2] = rem;
         }
     }
-    __syncthreads();
-    auto place = [&](int i, uint32_t x) {
-        if (x < (uint32_t)E) {
-            const int p = atomicAdd(&cur[x], 1);
-            perm[p] = i / k;
-            pos[i] = p;
-        } else {
-            pos[i] = -1;
-        }
-    };
-    if (cached) {
+    // placement, in batches of RB rounds (16 RB segments x E in the table)
+    const int P = min(32, 1024 / E), pe = tid % E, pp = tid / E;  // thread pp < P of expert pe
+    const int RB = max(1, min(kIdsPer, kTab / (16 * E)));
+    for (int r0 = 0; r0 < rounds; r0 += RB) {
+        const int nr = min(RB, rounds - r0), SB = 16 * nr;
+        uint32_t xb[kIdsPer];
+        int rkb[kIdsPer];
+        for (int q = tid; q < SB * E; q += 1024) tab[q] = 0;
+        __syncthreads();  // (also: the previous batch's reads of the table and cur's update are done)
 #pragma unroll
-        for (int j = 0; j < kIdsPer; j++) {
-            const int i = threadIdx.x + j * blockDim.x;
-            if (i < TK) place(i, xc[j]);
+        for (int rr = 0; rr < kIdsPer; rr++) {
+            if (rr < nr) {
+                int size;
+                get(r0 + rr, xb[rr], rkb[rr], size);
+                if (size) tab[(16 * rr + wave) * E + xb[rr]] = size;
+            }
         }
-    } else {
-        for (int i = threadIdx.x; i < TK; i += blockDim.x) place(i, ids[i]);
+        __syncthreads();
+        const int SP = (SB + P - 1) / P, s0 = pp * SP, s1 = min(SB, s0 + SP);
+        if (pp < P) {
+            int loc = 0;
+            for (int sg = s0; sg < s1; sg++) loc += tab[sg * E + pe];
+            psum[pp * E + pe] = loc;
+        }
+        __syncthreads();
+        int total = 0;
+        if (pp < P) {
+            int base = cur[pe];
+            for (int p2 = 0; p2 < P; p2++) {
+                const int ps = psum[p2 * E + pe];
+                base += p2 < pp ? ps : 0;
+                total += ps;
+            }
+            for (int sg = s0; sg < s1; sg++) {
+                const int c = tab[sg * E + pe];
+                tab[sg * E + pe] = base;
+                base += c;
+            }
+        }
+        __syncthreads();
+        if (pp == 0) cur[pe] += total;  // (read again only after the next batch's first barrier)
+#pragma unroll
+        for (int rr = 0; rr < kIdsPer; rr++) {
+            const int i = tid + 1024 * (r0 + rr);
+            if (rr < nr && i < TK) {
+                const uint32_t x = xb[rr];
+                if (x < (uint32_t)E) {
+                    const int p = tab[(16 * rr + wave) * E + x] + rkb[rr];
+                    perm[p] = i / k;
+                    pos[i] = p;
+                } else {
+                    pos[i] = -1;
+                }
+            }
+        }
     }
 }
 
@@ -489,26 +616,42 @@ __device__ __forceinline__ float prefill_act(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * g));
 }
 
+namespace {
+
+// Arguments of both grouped GEMMs (shared by their separate kernels and the
+// fused one).
+struct PfArgs {
+    const uint8_t *gu_hdr, *gu_qs;  // gate/up planes: [E][2F] rows of gu_nsb super-blocks
+    int gu_nsb, F;
+    const _Float16 *Xh;
+    const float *rs;
+    int D;
+    const int *chunks, *n_chunks, *offsets, *perm;
+    _Float16 *H;
+    int Kd;
+    const uint8_t *dn_hdr, *dn_qs;  // down planes: [E][D] rows of dn_nsb super-blocks
+    int dn_nsb;
+    float *Y;
+    uint32_t *err;
+    int *done;  // fused kernel: finished gate/up blocks per chunk (zeroed by the dispatch)
+    int CG;     // fused kernel: chunk slots per XCD group
+};
+
+struct NoWait {
+    __device__ __forceinline__ void operator()() const {}
+};
+
 // Block: chunk (expert e, sorted rows base + m0 + [0, mc)) x output columns
 // [n0, n0 + 64).  Weight rows 0..63 are gate rows n0.., 64..127 the up rows;
 // wavefront w computes token tile w against all 128 (ct 0,1 = gate, 2,3 =
 // up), so h = act(gate) * up is formed in registers.  ACT: the activation
-// (0 SiLU, 1 GELU-tanh).
+// (0 SiLU, 1 GELU-tanh).  False when the chunk does not exist.
 template <int ACT>
-__global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restrict__ hdr,
-                                                         const uint8_t *__restrict__ qs, int nsb, int F,
-                                                         const _Float16 *__restrict__ Xh,
-                                                         const float *__restrict__ rs, int D,
-                                                         const int *__restrict__ chunks,
-                                                         const int *__restrict__ n_chunks,
-                                                         const int *__restrict__ offsets,
-                                                         const int *__restrict__ perm, uint32_t act,
-                                                         _Float16 *__restrict__ H, int Kd, uint32_t *err) {
-    if ((int)blockIdx.y >= *n_chunks) return;
-    const int e = chunks[3 * blockIdx.y], m0 = chunks[3 * blockIdx.y + 1], mc = chunks[3 * blockIdx.y + 2];
-    const int base = offsets[e];
-    const int n0 = blockIdx.x * BN1;
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
+__device__ __forceinline__ bool gate_up_body(const PfArgs &a, int bx, int by, _Float16 (*Bs)[NB][LDK]) {
+    if (by >= *a.n_chunks) return false;
+    const int e = a.chunks[3 * by], m0 = a.chunks[3 * by + 1], mc = a.chunks[3 * by + 2];
+    const int base = a.offsets[e];
+    const int n0 = bx * BN1, F = a.F, D = a.D, Kd = a.Kd;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     size_t wrow[2];
 #pragma unroll
@@ -516,7 +659,10 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
         const int r = (tid >> 2) + 64 * j;
         wrow[j] = (size_t)e * 2 * F + (r < BN1 ? n0 + r : F + n0 + (r - BN1));
     }
-    const int *prow = perm + base + m0;
+    const int *prow = a.perm + base + m0;
+    const _Float16 *Xh = a.Xh;
+    const float *rs = a.rs;
+    _Float16 *H = a.H;
     auto row_ptr = [&](int m) { return Xh + (size_t)prow[m] * D; };
     // ct 0, 1 = gate columns n0 + [0, 64), ct 2, 3 = the matching up columns;
     // with r the row's scale, gate = r v[0] and up = r v[2], and H = act(gate)
@@ -544,41 +690,38 @@ __global__ void __launch_bounds__(256) k_prefill_gate_up(const uint8_t *__restri
             hrow[kperm(c0 + 32)] = sat16(prefill_act<ACT>(v[1] * r) * (v[3] * ri));
         }
     };
-    const int nt = (mc + 31) / 32, NS = 2 * nsb;
+    const int nt = (mc + 31) / 32, NS = 2 * a.gu_nsb;
     if (nt == 1)
-        run_block<4>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
+        run_block<4>(Bs, a.gu_hdr, a.gu_qs, a.gu_nsb, wrow, NS, mc, row_ptr, pre, epi, NoWait{}, tid, wave, lane);
     else if (nt == 2)
-        run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
+        run_block<2>(Bs, a.gu_hdr, a.gu_qs, a.gu_nsb, wrow, NS, mc, row_ptr, pre, epi, NoWait{}, tid, wave, lane);
     else
-        run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
+        run_block<1>(Bs, a.gu_hdr, a.gu_qs, a.gu_nsb, wrow, NS, mc, row_ptr, pre, epi, NoWait{}, tid, wave, lane);
     if (sat) {  // (rare): the count and the error bit, reported at the next synchronising call
-        __hip_atomic_fetch_add(err + kErrPrefillSat, sat, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        report_timeout(err, kErrCodePrefillSat);
+        __hip_atomic_fetch_add(a.err + kErrPrefillSat, sat, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        report_timeout(a.err, kErrCodePrefillSat);
     }
-    if (blockIdx.x == 0 && Kd > F)  // zero K padding of the down product
+    if (bx == 0 && Kd > F)  // zero K padding of the down product
         for (int i = tid; i < mc * (Kd - F); i += 256) {
             const int m = i / (Kd - F), col = F + i % (Kd - F);
             H[(size_t)(base + m0 + m) * Kd + col] = (_Float16)0.f;  // (kperm keeps [F, Kd): F % 4 == 0)
         }
+    return true;
 }
 
-// ---------------------------------------------------------------- down
 // Block: chunk x output rows [n0, n0 + 128) of the expert's down matrix
 // (= columns of Y); wavefront w computes token tile w, A = H rows (f16).
-__global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict__ hdr, const uint8_t *__restrict__ qs,
-                                                      int nsb, int D, const _Float16 *__restrict__ H, int Kd,
-                                                      const int *__restrict__ chunks, const int *__restrict__ n_chunks,
-                                                      const int *__restrict__ offsets, float *__restrict__ Y) {
-    if ((int)blockIdx.y >= *n_chunks) return;
-    const int e = chunks[3 * blockIdx.y], m0 = chunks[3 * blockIdx.y + 1], mc = chunks[3 * blockIdx.y + 2];
-    const int base = offsets[e];
-    const int n0 = blockIdx.x * BN2;
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
+template <typename Wait>
+__device__ __forceinline__ void down_body(const PfArgs &a, int bx, int by, _Float16 (*Bs)[NB][LDK], Wait wait) {
+    const int e = a.chunks[3 * by], m0 = a.chunks[3 * by + 1], mc = a.chunks[3 * by + 2];
+    const int base = a.offsets[e];
+    const int n0 = bx * BN2, D = a.D, Kd = a.Kd;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     size_t wrow[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) wrow[j] = (size_t)e * D + n0 + (tid >> 2) + 64 * j;
-    const _Float16 *hbase = H + (size_t)(base + m0) * Kd;
+    const _Float16 *hbase = a.H + (size_t)(base + m0) * Kd;
+    float *Y = a.Y;
     auto row_ptr = [&](int m) { return hbase + (size_t)m * Kd; };
     auto pre = [](int, int) { return 0.0f; };
     auto epi = [&](int t, int i, const float (&v)[4], float) {
@@ -589,13 +732,80 @@ __global__ void __launch_bounds__(256) k_prefill_down(const uint8_t *__restrict_
             for (int ct = 0; ct < 4; ct++) yrow[32 * ct] = v[ct];
         }
     };
-    const int nt = (mc + 31) / 32, NS = 2 * nsb;
+    const int nt = (mc + 31) / 32, NS = 2 * a.dn_nsb;
     if (nt == 1)
-        run_block<4>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
+        run_block<4>(Bs, a.dn_hdr, a.dn_qs, a.dn_nsb, wrow, NS, mc, row_ptr, pre, epi, wait, tid, wave, lane);
     else if (nt == 2)
-        run_block<2>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
+        run_block<2>(Bs, a.dn_hdr, a.dn_qs, a.dn_nsb, wrow, NS, mc, row_ptr, pre, epi, wait, tid, wave, lane);
     else
-        run_block<1>(Bs, hdr, qs, nsb, wrow, NS, mc, row_ptr, pre, epi, tid, wave, lane);
+        run_block<1>(Bs, a.dn_hdr, a.dn_qs, a.dn_nsb, wrow, NS, mc, row_ptr, pre, epi, wait, tid, wave, lane);
+}
+
+constexpr uint64_t kPfWaitTicks = 20000000;  // 200 ms of the 100 MHz wall clock
+
+}  // namespace
+
+template <int ACT>
+__global__ void __launch_bounds__(256) k_prefill_gate_up(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
+    gate_up_body<ACT>(a, blockIdx.x, blockIdx.y, Bs);
+}
+
+// ---------------------------------------------------------------- down
+__global__ void __launch_bounds__(256) k_prefill_down(PfArgs a) {
+    if ((int)blockIdx.y >= *a.n_chunks) return;
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
+    down_body(a, blockIdx.x, blockIdx.y, Bs, NoWait{});
+}
+
+// ---------------------------------------------------------------- both GEMMs in one launch
+// Block b of XCD group g = b % 8 (blocks with equal b % 8 share an XCD, as
+// probed once per context), in-group index s = b / 8: the first
+// (F / 64) CG indices are the gate/up blocks of the group's chunks
+// y = g + 8c (c = s / (F / 64), column block s % (F / 64)), the next
+// (D / 128) CG the down blocks of the same chunks, in the same chunk order.
+// A gate/up block's H rows are ordinary stores that stay in its XCD's L2;
+// once they are acknowledged it adds 1 to done[y].  A down block requests
+// its first weight stages, then waits until done[y] = F / 64 and reads H
+// through the same L2.  So the down blocks of the first chunks run while
+// the last gate/up blocks finish, instead of behind the whole gate/up grid.
+// A down block only waits for blocks with smaller indices, which are
+// dispatched first; the wait is bounded by the wall clock (on expiry the
+// error word is set and that call's outputs are wrong).
+template <int ACT>
+__global__ void __launch_bounds__(256) k_prefill_gemms(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
+    const int g = blockIdx.x & 7, s = blockIdx.x >> 3;
+    const int ngx = a.F / BN1, ngu = ngx * a.CG;
+    if (s < ngu) {
+        const int y = g + 8 * (s / ngx);
+        if (!gate_up_body<ACT>(a, s % ngx, y, Bs)) return;
+        // every thread's H stores acknowledged by the L2 before the count
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(a.done + y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const int ndx = a.D / BN2, s2 = s - ngu;
+    const int y = g + 8 * (s2 / ndx);
+    if (y >= *a.n_chunks) return;
+    auto wait = [&] {
+        if (threadIdx.x == 0) {
+            const uint64_t t0 = wall_clock64();
+            int seen;
+            while ((seen = __hip_atomic_load(a.done + y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < ngx) {
+                if (wall_clock64() - t0 > kPfWaitTicks) {
+                    report_timeout(a.err, kErrCodePrefillWait);
+                    report_detail(a.err, (int)blockIdx.x, kErrCodePrefillWait, (uint32_t)y, (uint32_t)seen,
+                                  (uint32_t)ngx);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        __syncthreads();
+    };
+    down_body(a, s2 % ndx, y, Bs, wait);
 }
 
 // ---------------------------------------------------------------- combine
@@ -640,33 +850,59 @@ size_t prefill_workspace_bytes(int T, int k, int E, int Kd, int D) {
     const size_t TK = (size_t)T * k;
     return align256((size_t)T * E * 4) + 2 * align256(TK * 4) + align256((size_t)(E + 1) * 4) +
            align256((size_t)max_chunks((int)TK, E) * 12) + 256 + 2 * align256(TK * 4) + align256((size_t)T * 4) +
-           align256((size_t)T * D * 2) + align256(TK * Kd * 2) + align256(TK * D * 4);
+           align256((size_t)T * D * 2) + align256(TK * Kd * 2) + align256(TK * D * 4) +
+           align256((size_t)max_chunks((int)TK, E) * 4);
 }
 
 hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const DevTensor &Dn, const float *X, int T,
                               const float *bias, int k, int F, uint32_t act, uint32_t norm, void *ws, float *out,
-                              uint32_t *out_ids, float *out_w, uint32_t *err, hipStream_t s) {
+                              uint32_t *out_ids, float *out_w, uint32_t *err, int xcd_local, hipStream_t s) {
     const int E = (int)GU.n_experts, D = (int)GU.cols, Kd = (int)Dn.cols;
     const int TK = T * k;
     Ws w = carve(ws, T, k, E, Kd, D);
     bool x_done = false;
     hipError_t e = launch_router_batched(R, X, T, bias, w.logits, k, norm, w.ids, w.w, w.Xh, w.rs, &x_done, s);
     if (e != hipSuccess) return e;
+    const int mc = max_chunks(TK, E);
     hipLaunchKernelGGL(k_prefill_dispatch, dim3(1), dim3(1024), 0, s, w.ids, TK, k, E, w.offsets, w.chunks,
-                       w.n_chunks, w.perm, w.pos);
+                       w.n_chunks, w.perm, w.pos, w.done, mc);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (!x_done) {
         hipLaunchKernelGGL(k_prefill_x_f16, dim3((unsigned)T), dim3(256), 0, s, X, w.Xh, w.rs, D);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    const int mc = max_chunks(TK, E);
-    hipLaunchKernelGGL(act == 1u ? k_prefill_gate_up<1> : k_prefill_gate_up<0>, dim3(F / BN1, mc), dim3(256), 0, s,
-                       GU.p0, GU.p1, (int)GU.blocks_per_row, F, w.Xh, w.rs, D, w.chunks, w.n_chunks, w.offsets, w.perm,
-                       act, w.H, Kd, err);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_prefill_down, dim3(D / BN2, mc), dim3(256), 0, s, Dn.p0, Dn.p1, (int)Dn.blocks_per_row, D,
-                       w.H, Kd, w.chunks, w.n_chunks, w.offsets, w.Y);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    PfArgs pa{};
+    pa.gu_hdr = (const uint8_t *)GU.p0;
+    pa.gu_qs = (const uint8_t *)GU.p1;
+    pa.gu_nsb = (int)GU.blocks_per_row;
+    pa.F = F;
+    pa.Xh = w.Xh;
+    pa.rs = w.rs;
+    pa.D = D;
+    pa.chunks = w.chunks;
+    pa.n_chunks = w.n_chunks;
+    pa.offsets = w.offsets;
+    pa.perm = w.perm;
+    pa.H = w.H;
+    pa.Kd = Kd;
+    pa.dn_hdr = (const uint8_t *)Dn.p0;
+    pa.dn_qs = (const uint8_t *)Dn.p1;
+    pa.dn_nsb = (int)Dn.blocks_per_row;
+    pa.Y = w.Y;
+    pa.err = err;
+    pa.done = w.done;
+    pa.CG = (mc + 7) / 8;
+    if (xcd_local) {
+        const unsigned nb = 8u * (unsigned)((F / BN1 + D / BN2) * pa.CG);
+        hipLaunchKernelGGL(act == 1u ? k_prefill_gemms<1> : k_prefill_gemms<0>, dim3(nb), dim3(256), 0, s, pa);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    } else {
+        hipLaunchKernelGGL(act == 1u ? k_prefill_gate_up<1> : k_prefill_gate_up<0>, dim3(F / BN1, mc), dim3(256), 0,
+                           s, pa);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_prefill_down, dim3(D / BN2, mc), dim3(256), 0, s, pa);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(k_prefill_combine, dim3((D / 4 + 255) / 256, T), dim3(256), 0, s, w.Y, w.pos, w.w, w.rs, k, D,
                        out);
     if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -845,6 +845,62 @@ def test_gpu_prefill_deterministic(ctx, cfg3):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,E,k", [
+    (1100, 128, 8),   # 8,800 assignments: ids read again for the placement
+    (300, 600, 4),    # 600 experts: the placement table holds one round at a time
+])
+def test_gpu_prefill_large_batches(ctx, pool, T, E, k):
+    # the dispatch's other placement paths, against the oracle on a sample
+    # of the tokens (each token's result is its own)
+    w = synth.moe_weights(80 + E % 7, 256, E, 64, down_cols=256)
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    X = synth.normal(synth.stream(81, T), (T, 256))
+    bias = synth.zipf_bias(synth.stream(82, E), E)
+    out = np.zeros((T, 256), np.float32)
+    ids = np.zeros((T, k), np.uint32)
+    for _ in range(2):
+        prev = out.copy()
+        ctx.moe_prefill(out, X, router, gate_up, down, k, 64, norm_topk=True, bias=bias, out_ids=ids)
+    assert np.array_equal(prev.view(np.uint32), out.view(np.uint32))
+    sel = np.arange(0, T, 7)
+    ref, rids, _ = orc.moe_prefill(w, X[sel], k, norm_topk=True, bias=bias, pool=pool)
+    assert np.array_equal(ids[sel], rids)
+    assert rel_l2(out[sel], ref) <= PREFILL_REL_L2
+    for t in (router, gate_up, down):
+        t.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [512, 37])
+def test_gpu_prefill_one_launch_matches_two(ctx, cfg3, T):
+    # both grouped GEMMs in one launch (the activations handed over in an
+    # XCD's L2, used when blocks with equal index % 8 share an XCD) and in
+    # two launches (forced in a second context): every row is computed the
+    # same way, so the outputs carry the same bits
+    c, _ = cfg3
+    w = c["weights"]
+    os.environ["LT_FUSED_AGENT_HANDOVER"] = "1"
+    try:
+        ctx2 = lt.Context(0)
+    finally:
+        del os.environ["LT_FUSED_AGENT_HANDOVER"]
+    try:
+        t1 = lt.upload_moe(ctx, w)
+        t2 = lt.upload_moe(ctx2, w)
+        p = synth.config5(T, weights=w)
+        a = np.zeros((T, w.d_model), np.float32)
+        b = np.zeros((T, w.d_model), np.float32)
+        for _ in range(2):
+            ctx.moe_prefill(a, p["X"], *t1, 8, w.d_expert, norm_topk=True, bias=p["bias"])
+            ctx2.moe_prefill(b, p["X"], *t2, 8, w.d_expert, norm_topk=True, bias=p["bias"])
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        for t in t1 + t2:
+            t.free()
+    finally:
+        ctx2.close()
+
+
 # ------------------------------------------------------------------ single-launch kernel
 # lt_moe_forward runs the whole layer in one launch when the shape fits
 # (F32 router, Q4_K experts, d_model <= 2048); LT_MOE_UNFUSED forces the
