@@ -405,7 +405,6 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
     constexpr int kIdsPer = 8, kTab = 16384;
     __shared__ int cnt[1024], cur[1024], psum[1024];
     __shared__ int tab[kTab];  // [segment][E]: group sizes, then the segment's first rows
-    __shared__ int wsum[6][16];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
     const bool cached = TK <= kIdsPer * 1024;
@@ -417,8 +416,11 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
         const int i = tid + j * 1024;
         xc[j] = cached && i < TK ? ids[i] : 0xffffffffu;
     }
+    // placement in batches of RB rounds (16 RB segments x E in the table)
+    const int RB = max(1, min(kIdsPer, kTab / (16 * E)));
     if (tid < E) cnt[tid] = 0;
     for (int i = tid; i < maxc; i += 1024) done[i] = 0;  // the fused GEMMs' per-chunk counts
+    for (int q = tid; q < 16 * min(RB, rounds) * E; q += 1024) tab[q] = 0;  // (the first batch's table)
     __syncthreads();
     auto group = [&](uint32_t x, int &rank, int &size) {
         const bool valid = x < (uint32_t)E;
@@ -459,67 +461,81 @@ __global__ void __launch_bounds__(1024) k_prefill_dispatch(const uint32_t *__res
         }
     }
     __syncthreads();
-    const int e = tid;
-    const int n = e < E ? cnt[e] : 0, full = n / MC, rem = n % MC, cls = rem ? (rem + 31) / 32 : 0;
-    int v[6] = {n, full, cls == 1, cls == 2, cls == 3, cls == 4};
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
-#pragma unroll
-        for (int a = 0; a < 6; a++) {
-            const int t = __shfl_up(v[a], d, 64);
-            if (lane >= d) v[a] += t;
+    // Experts in order, by wavefront 0: lane l takes experts CH l + [0, CH)
+    // (CH = ceil(E / 64)); the lanes' totals of rows, full chunks and
+    // partial chunks of each tile count (two 16-bit counts per word) are
+    // scanned over the lanes, then each lane lays out its experts' rows and
+    // chunks -- full chunks first, then the partial ones by token tiles,
+    // largest first: the blocks with the most MFMA work are dispatched
+    // first and the short ones fill in behind them.
+    if (wave == 0) {
+        const int CH = (E + 63) >> 6;
+        int t0 = 0, t1 = 0, t12 = 0, t34 = 0;  // rows, full chunks, partial chunks of 1 | 2 << 16, 3 | 4 << 16 tiles
+        for (int q = 0; q < CH; q++) {
+            const int e = CH * lane + q;
+            const int n = e < E ? cnt[e] : 0, rem = n % MC, cls = rem ? (rem + 31) / 32 : 0;
+            t0 += n;
+            t1 += n / MC;
+            t12 += (cls == 1 ? 1 : 0) + (cls == 2 ? 0x10000 : 0);
+            t34 += (cls == 3 ? 1 : 0) + (cls == 4 ? 0x10000 : 0);
         }
-    if (lane == 63)
+        int i0 = t0, i1 = t1, i12 = t12, i34 = t34;  // inclusive scans over the lanes
 #pragma unroll
-        for (int a = 0; a < 6; a++) wsum[a][wave] = v[a];
+        for (int d = 1; d < 64; d <<= 1) {
+            const int a0 = __shfl_up(i0, d, 64), a1 = __shfl_up(i1, d, 64);
+            const int a12 = __shfl_up(i12, d, 64), a34 = __shfl_up(i34, d, 64);
+            if (lane >= d) {
+                i0 += a0;
+                i1 += a1;
+                i12 += a12;
+                i34 += a34;
+            }
+        }
+        const int T1 = __shfl(i1, 63, 64), T12 = __shfl(i12, 63, 64), T34 = __shfl(i34, 63, 64);
+        const int tot_full = T1, tot_p4 = T34 >> 16, tot_p3 = T34 & 0xffff, tot_p2 = T12 >> 16, tot_p1 = T12 & 0xffff;
+        // first chunk index of each partial class, then this lane's running positions
+        int off = i0 - t0, fc = i1 - t1;
+        int pc[4] = {tot_full + tot_p4 + tot_p3 + tot_p2 + ((i12 - t12) & 0xffff),
+                     tot_full + tot_p4 + tot_p3 + ((i12 - t12) >> 16), tot_full + tot_p4 + ((i34 - t34) & 0xffff),
+                     tot_full + ((i34 - t34) >> 16)};
+        for (int q = 0; q < CH; q++) {
+            const int e = CH * lane + q;
+            if (e >= E) break;
+            const int n = cnt[e], full = n / MC, rem = n % MC, cls = rem ? (rem + 31) / 32 : 0;
+            offsets[e] = off;
+            cur[e] = off;
+            for (int j = 0; j < full; j++) {
+                int *ch = chunks + 3 * (fc + j);
+                ch[0] = e;
+                ch[1] = j * MC;
+                ch[2] = MC;
+            }
+            fc += full;
+            if (cls) {
+                int *ch = chunks + 3 * pc[cls - 1];
+                ch[0] = e;
+                ch[1] = full * MC;
+                ch[2] = rem;
+                pc[cls - 1]++;
+            }
+            off += n;
+            if (e == E - 1) {
+                offsets[E] = off;
+                *n_chunks = tot_full + tot_p4 + tot_p3 + tot_p2 + tot_p1;
+            }
+        }
+    }
     __syncthreads();
-    int tot[6];
-#pragma unroll
-    for (int a = 0; a < 6; a++) {
-        int before = 0, all = 0;
-#pragma unroll
-        for (int w = 0; w < 16; w++) {
-            const int s = wsum[a][w];
-            before += w < wave ? s : 0;
-            all += s;
-        }
-        v[a] += before;  // inclusive scan over experts
-        tot[a] = all;
-    }
-    const int tot_full = tot[1], tot_p4 = tot[5], tot_p3 = tot[4], tot_p2 = tot[3];
-    if (e < E) {
-        const int off = v[0] - n;
-        offsets[e] = off;
-        cur[e] = off;
-        if (e == E - 1) {
-            offsets[E] = off + n;
-            *n_chunks = tot_full + tot_p4 + tot_p3 + tot_p2 + tot[2];
-        }
-        for (int j = 0; j < full; j++) {
-            int *ch = chunks + 3 * (v[1] - full + j);
-            ch[0] = e;
-            ch[1] = j * MC;
-            ch[2] = MC;
-        }
-        if (cls) {
-            const int start = cls == 4 ? tot_full : cls == 3 ? tot_full + tot_p4
-                                                  : cls == 2 ? tot_full + tot_p4 + tot_p3
-                                                             : tot_full + tot_p4 + tot_p3 + tot_p2;
-            int *ch = chunks + 3 * (start + v[1 + cls] - 1);
-            ch[0] = e;
-            ch[1] = full * MC;
-            ch[2] = rem;
-        }
-    }
-    // placement, in batches of RB rounds (16 RB segments x E in the table)
+    // placement: cur[e] = the expert's next free row
     const int P = min(32, 1024 / E), pe = tid % E, pp = tid / E;  // thread pp < P of expert pe
-    const int RB = max(1, min(kIdsPer, kTab / (16 * E)));
     for (int r0 = 0; r0 < rounds; r0 += RB) {
         const int nr = min(RB, rounds - r0), SB = 16 * nr;
         uint32_t xb[kIdsPer];
         int rkb[kIdsPer];
-        for (int q = tid; q < SB * E; q += 1024) tab[q] = 0;
-        __syncthreads();  // (also: the previous batch's reads of the table and cur's update are done)
+        if (r0 > 0) {  // (the first batch's table was cleared at the start)
+            for (int q = tid; q < SB * E; q += 1024) tab[q] = 0;
+            __syncthreads();  // (also: the previous batch's reads of the table and cur's update are done)
+        }
 #pragma unroll
         for (int rr = 0; rr < kIdsPer; rr++) {
             if (rr < nr) {
