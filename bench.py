@@ -811,6 +811,15 @@ def bench_prefill(args):
                       "kernel": "whole prefill call (device time per call; f16 dense MFMA peak)",
                       "algorithmic_flops": PREFILL_FLOP},
          "parity": parity})
+    if not args.no_cpu:
+        # the reference prefills token by token: the oracle's per-token MoE
+        # layer on the first 16 prompt rows per call
+        X16 = np.ascontiguousarray(p["X"][:16])
+        result["cpu_baseline"] = cpu_baseline_record(
+            args, lambda pool: (lambda i: orc.moe_prefill(w, X16, K, norm_topk=True, bias=p["bias"], pool=pool)),
+            1e6 / 16, "us/token", "oracle moe_prefill on 16 of the 512 tokens per call (per-token moeForward, "
+            "quantMatvecPar)")
+        result["cpu_baseline"]["tokens_per_s"] = round(1e6 / result["cpu_baseline"]["value"])
     if args.calibrate:
         calibrate_copy(ctx)
     print(json.dumps(result), flush=True)
