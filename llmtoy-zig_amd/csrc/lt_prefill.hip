@@ -27,7 +27,9 @@
 //      Y[pos] (r_t^2 exact).
 // Steps 3 and 4 run as one launch when blocks with equal index % 8 share an
 // XCD (k_prefill_gemms: a chunk's down blocks take H from its gate/up
-// blocks through that XCD's L2), else as two.
+// blocks through that XCD's L2), else as two.  Chunks of a single token
+// skip the tiles: their blocks stream the weights against int8 limbs of the
+// token like the decode kernels (gate_up_tiny, down_tiny).
 // Both GEMMs run a software pipeline over K stages of 128 (half a Q4_K
 // super-block): weight loads are issued two stages ahead into registers,
 // A fragments one stage ahead, the dequantised tile is double-buffered in
@@ -47,6 +49,7 @@
 // swapped (kperm): X and H are written in that order, and the MFMA sums the
 // same products.
 #include "lt_internal.h"
+#include "lt_limbs.h"
 
 namespace lt {
 
@@ -651,11 +654,176 @@ struct PfArgs {
     uint32_t *err;
     int *done;  // fused kernel: finished gate/up blocks per chunk (zeroed by the dispatch)
     int CG;     // fused kernel: chunk slots per XCD group
+    const float *X;  // the fp32 input rows (one-token chunks)
+    int tiny;        // one-token chunks take the decode-style stream (gate/up rows <= 8, down rows <= 4 super-blocks)
 };
 
 struct NoWait {
     __device__ __forceinline__ void operator()() const {}
 };
+
+// ---------------------------------------------------------------- chunks of one token
+// A chunk of one token streams its weights like the decode path instead of
+// dequantising them to f16 tiles for a 32-row MFMA: the f16 tile costs the
+// same whatever the chunk's rows, and many one-tile chunks of a skewed
+// routing hold a single token (22 of config 5's 63).  (NT = 2 as well
+// needed more registers than two waves per SIMD allow.)  A lane owns one Q4_K sub-block pair
+// window (position 4 sb + p of a row: K elements 256 sb + 64 p + [0, 64)),
+// whose activations it turns into int8 limbs in registers once (limbs16);
+// per row it loads the window's 32 quant bytes and its quad's header word
+// and meets them with each token's limbs on v_dot4 (q4k_pair_dot); a row's
+// window dots meet in LDS and one lane adds them in position order, so
+// results do not depend on timing.
+
+struct WinW {
+    uint4 q0, q1;
+    uint32_t h;
+};
+
+__device__ __forceinline__ WinW load_window(const uint8_t *hdr, const uint8_t *qs, size_t blk, int p) {
+    WinW w;
+    w.q0 = ldg16(qs + blk * 128 + 32 * p);
+    w.q1 = ldg16(qs + blk * 128 + 32 * p + 16);
+    w.h = *reinterpret_cast<const uint32_t *>(hdr + blk * 16 + 4 * p);
+    return w;
+}
+
+__device__ __forceinline__ float window_dot(const WinW &w, int p, const Limbs &xl) {
+    uint32_t h0, h1, h2, h3;
+    quad_header(w.h, h0, h1, h2, h3);
+    const PairScale ps = pair_scale(h0, h1, h2, h3, p);
+    const uint32_t w8[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    return q4k_pair_dot(w8, ps, xl);
+}
+
+// Gate/up of a chunk of NT tokens (one in use), columns n0 + [0, 64): wavefront
+// w takes columns n0 + 16 w + c, one per pass c; lanes 0-31 the gate row,
+// 32-63 the up row, lane l & 31 = window position (rows of at most 8
+// super-blocks).  Weights two passes ahead; each lane's window dots go to
+// LDS (red: [wave][pass][token][lane], the f16 tile's space) and lane c +
+// 16 t + 32 half sums the 32 positions of (pass c, token t, gate or up) in
+// position order.
+template <int ACT, int NT>
+__device__ __forceinline__ uint32_t gate_up_tiny(const PfArgs &a, float *red, const int *prow, int e, int row0,
+                                                 int n0, int wave, int lane) {
+    const int F = a.F, nsb = a.gu_nsb, Kd = a.Kd;
+    const int pos = lane & 31, sb = min(pos >> 2, nsb - 1), p = pos & 3;
+    const bool on = (pos >> 2) < nsb;
+    const int half = lane >> 5;
+    Limbs xl[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float *xr = a.X + (size_t)prow[t] * a.D + 256 * sb + 64 * p;
+        float xs[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {  // group by group: 16 values live at a time
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const float4 f = ldg16f(xr + 16 * g + i);
+                v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+            }
+            limbs16(v, xl[t].a[g], xl[t].b[g], xl[t].sp[g], xs[g]);
+        }
+        xl[t].xs_lo = xs[0] + xs[1];
+        xl[t].xs_hi = xs[2] + xs[3];
+    }
+    auto blk_of = [&](int c) {
+        const int col = n0 + 16 * wave + c;
+        return ((size_t)e * 2 * F + (half ? F + col : col)) * nsb + sb;
+    };
+    WinW w[16];
+#pragma unroll
+    for (int c = 0; c < 2; c++) w[c] = load_window(a.gu_hdr, a.gu_qs, blk_of(c), p);
+    float *rw = red + wave * (16 * NT * 64);
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        if (c + 2 < 16) w[c + 2] = load_window(a.gu_hdr, a.gu_qs, blk_of(c + 2), p);
+#pragma unroll
+        for (int t = 0; t < NT; t++) rw[(c * NT + t) * 64 + lane] = on ? window_dot(w[c], p, xl[t]) : 0.0f;
+    }
+    __syncthreads();
+    const int c = lane & 15, t = (lane >> 4) & 1;
+    float v = 0.0f;
+    if (t < NT) {
+        const float *src = rw + (c * NT + t) * 64 + 32 * half;
+#pragma unroll
+        for (int q = 0; q < 32; q++) v += src[q];
+    }
+    const float up = __shfl(v, lane + 32, 64);  // (lanes 0-31: the up row's sum)
+    uint32_t sat = 0;
+    if (!half && t < NT) {
+        // H = act(gate) * up / r^2 (r = 2^k exactly)
+        const float r = a.rs[prow[t]];
+        const float ri = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(r));
+        const float h = prefill_act<ACT>(v) * up * ri * ri;
+        const bool big = fabsf(h) > 65504.0f && fabsf(h) <= 3.4e38f;
+        sat = big ? 1u : 0u;
+        a.H[(size_t)(row0 + t) * Kd + kperm(n0 + 16 * wave + c)] = (_Float16)(big ? copysignf(65504.0f, h) : h);
+    }
+    return sat;
+}
+
+// Down of a chunk of NT tokens (one in use), output rows n0 + [0, 128): lanes
+// l & 15 = window position (K of at most 4 super-blocks), lane >> 4 = row
+// of the pass; wavefront w takes rows n0 + 32 w + 4 c + (lane >> 4), pass
+// c < 8.  The activations are the H rows (f16, K in kperm order).  Lane
+// c + 8 rr + 32 t then sums the 16 positions of (pass c, row rr, token t).
+template <int NT, typename Wait>
+__device__ __forceinline__ void down_tiny(const PfArgs &a, float *red, int e, int row0, int n0, Wait wait, int wave,
+                                          int lane) {
+    const int nsb = a.dn_nsb, D = a.D, Kd = a.Kd;
+    const int pos = lane & 15, sb = min(pos >> 2, nsb - 1), p = pos & 3;
+    const bool on = (pos >> 2) < nsb;
+    const int rr = lane >> 4;
+    auto blk_of = [&](int c) { return ((size_t)e * D + n0 + 32 * wave + 4 * c + rr) * nsb + sb; };
+    WinW w[8];
+#pragma unroll
+    for (int c = 0; c < 2; c++) w[c] = load_window(a.dn_hdr, a.dn_qs, blk_of(c), p);
+    wait();
+    Limbs xl[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const _Float16 *hr = a.H + (size_t)(row0 + t) * Kd + 256 * sb + 64 * p;
+        float xs[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {  // group by group: 16 values live at a time
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i += 8) {
+                const uint4 u = *reinterpret_cast<const uint4 *>(hr + 16 * g + i);  // h[kperm(.. + j)], j < 8
+                const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+                _Float16 f[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    f[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(wd[j] & 0xffffu));
+                    f[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(wd[j] >> 16));
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[i + kperm(j)] = (float)f[j];
+            }
+            limbs16(v, xl[t].a[g], xl[t].b[g], xl[t].sp[g], xs[g]);
+        }
+        xl[t].xs_lo = xs[0] + xs[1];
+        xl[t].xs_hi = xs[2] + xs[3];
+    }
+    float *rw = red + wave * (8 * NT * 64);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        if (c + 2 < 8) w[c + 2] = load_window(a.dn_hdr, a.dn_qs, blk_of(c + 2), p);
+#pragma unroll
+        for (int t = 0; t < NT; t++) rw[(c * NT + t) * 64 + lane] = on ? window_dot(w[c], p, xl[t]) : 0.0f;
+    }
+    __syncthreads();
+    const int c = lane & 7, r4 = (lane >> 3) & 3, t = lane >> 5;
+    if (t < NT) {
+        const float *src = rw + (c * NT + t) * 64 + 16 * r4;
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) v += src[q];
+        a.Y[(size_t)(row0 + t) * D + n0 + 32 * wave + 4 * c + r4] = v;
+    }
+}
 
 // Block: chunk (expert e, sorted rows base + m0 + [0, mc)) x output columns
 // [n0, n0 + 64).  Weight rows 0..63 are gate rows n0.., 64..127 the up rows;
@@ -707,7 +875,10 @@ __device__ __forceinline__ bool gate_up_body(const PfArgs &a, int bx, int by, _F
         }
     };
     const int nt = (mc + 31) / 32, NS = 2 * a.gu_nsb;
-    if (nt == 1)
+    float *red = reinterpret_cast<float *>(&Bs[0][0][0]);
+    if (a.tiny && mc == 1)
+        sat = gate_up_tiny<ACT, 1>(a, red, prow, e, base + m0, n0, wave, lane);
+    else if (nt == 1)
         run_block<4>(Bs, a.gu_hdr, a.gu_qs, a.gu_nsb, wrow, NS, mc, row_ptr, pre, epi, NoWait{}, tid, wave, lane);
     else if (nt == 2)
         run_block<2>(Bs, a.gu_hdr, a.gu_qs, a.gu_nsb, wrow, NS, mc, row_ptr, pre, epi, NoWait{}, tid, wave, lane);
@@ -749,7 +920,10 @@ __device__ __forceinline__ void down_body(const PfArgs &a, int bx, int by, _Floa
         }
     };
     const int nt = (mc + 31) / 32, NS = 2 * a.dn_nsb;
-    if (nt == 1)
+    float *red = reinterpret_cast<float *>(&Bs[0][0][0]);
+    if (a.tiny && mc == 1)
+        down_tiny<1>(a, red, e, base + m0, n0, wait, wave, lane);
+    else if (nt == 1)
         run_block<4>(Bs, a.dn_hdr, a.dn_qs, a.dn_nsb, wrow, NS, mc, row_ptr, pre, epi, wait, tid, wave, lane);
     else if (nt == 2)
         run_block<2>(Bs, a.dn_hdr, a.dn_qs, a.dn_nsb, wrow, NS, mc, row_ptr, pre, epi, wait, tid, wave, lane);
@@ -762,13 +936,13 @@ constexpr uint64_t kPfWaitTicks = 20000000;  // 200 ms of the 100 MHz wall clock
 }  // namespace
 
 template <int ACT>
-__global__ void __launch_bounds__(256) k_prefill_gate_up(PfArgs a) {
+__global__ void __launch_bounds__(256, 2) k_prefill_gate_up(PfArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
     gate_up_body<ACT>(a, blockIdx.x, blockIdx.y, Bs);
 }
 
 // ---------------------------------------------------------------- down
-__global__ void __launch_bounds__(256) k_prefill_down(PfArgs a) {
+__global__ void __launch_bounds__(256, 2) k_prefill_down(PfArgs a) {
     if ((int)blockIdx.y >= *a.n_chunks) return;
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
     down_body(a, blockIdx.x, blockIdx.y, Bs, NoWait{});
@@ -789,7 +963,7 @@ __global__ void __launch_bounds__(256) k_prefill_down(PfArgs a) {
 // dispatched first; the wait is bounded by the wall clock (on expiry the
 // error word is set and that call's outputs are wrong).
 template <int ACT>
-__global__ void __launch_bounds__(256) k_prefill_gemms(PfArgs a) {
+__global__ void __launch_bounds__(256, 2) k_prefill_gemms(PfArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB][LDK];
     const int g = blockIdx.x & 7, s = blockIdx.x >> 3;
     const int ngx = a.F / BN1, ngu = ngx * a.CG;
@@ -908,6 +1082,8 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
     pa.err = err;
     pa.done = w.done;
     pa.CG = (mc + 7) / 8;
+    pa.X = X;
+    pa.tiny = GU.blocks_per_row <= 8 && Dn.blocks_per_row <= 4 && !getenv("LT_PREFILL_NO_TINY");
     if (xcd_local) {
         const unsigned nb = 8u * (unsigned)((F / BN1 + D / BN2) * pa.CG);
         hipLaunchKernelGGL(act == 1u ? k_prefill_gemms<1> : k_prefill_gemms<0>, dim3(nb), dim3(256), 0, s, pa);

@@ -872,6 +872,34 @@ def test_gpu_prefill_large_batches(ctx, pool, T, E, k):
 
 
 @pytest.mark.gpu
+def test_gpu_prefill_one_token_chunks(ctx, cfg3, pool):
+    # experts that get one token of the batch stream their weights against
+    # the token's int8 limbs instead of an f16 tile; LT_PREFILL_NO_TINY
+    # (read at each call) sends them through the tile path: both within
+    # the prefill bound of the oracle, and close to each other
+    c, (router, gate_up, down) = cfg3
+    w = c["weights"]
+    p = synth.config5(512, weights=w)
+    ids = np.zeros((512, 8), np.uint32)
+    a = np.zeros((512, w.d_model), np.float32)
+    b = np.zeros((512, w.d_model), np.float32)
+    ctx.moe_prefill(a, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"], out_ids=ids)
+    os.environ["LT_PREFILL_NO_TINY"] = "1"
+    try:
+        ctx.moe_prefill(b, p["X"], router, gate_up, down, 8, w.d_expert, norm_topk=True, bias=p["bias"])
+    finally:
+        del os.environ["LT_PREFILL_NO_TINY"]
+    counts = np.bincount(ids.ravel(), minlength=w.n_experts)
+    assert ((counts % 128) == 1).sum() >= 10  # the routing has one-token chunks
+    ones = np.isin(ids, np.nonzero(counts % 128 == 1)[0]).any(axis=1)  # tokens with a slot in one
+    ref, _, _ = orc.moe_prefill(w, p["X"][ones], 8, norm_topk=True, bias=p["bias"], pool=pool)
+    assert rel_l2(a[ones], ref) <= PREFILL_REL_L2
+    assert rel_l2(b[ones], ref) <= PREFILL_REL_L2
+    assert rel_l2(a, b) <= 2e-3
+    assert not np.array_equal(a[ones].view(np.uint32), b[ones].view(np.uint32))  # the two paths did run
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("T", [512, 37])
 def test_gpu_prefill_one_launch_matches_two(ctx, cfg3, T):
     # both grouped GEMMs in one launch (the activations handed over in an
