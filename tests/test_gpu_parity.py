@@ -900,6 +900,25 @@ def test_gpu_prefill_one_token_chunks(ctx, cfg3, pool):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 2, 3])
+def test_gpu_prefill_few_tokens_gelu_padded_k(ctx, pool, T):
+    # a batch of one to three tokens: (nearly) every chunk holds one token,
+    # so the streams carry the layer, here with GELU and a down K padded
+    # past d_expert (704 -> 768)
+    w = synth.moe_weights(45, 2048, 16, 704, down_cols=768)
+    X = synth.normal(synth.stream(45, T), (T, 2048))
+    router, gate_up, down = lt.upload_moe(ctx, w)
+    out = np.zeros((T, 2048), np.float32)
+    ids = np.zeros((T, 4), np.uint32)
+    ctx.moe_prefill(out, X, router, gate_up, down, 4, 704, act=lt.ACT_GELU_TANH, out_ids=ids)
+    ref, rids, _ = orc.moe_prefill(w, X, 4, act=orc.ACT_GELU_TANH, pool=pool)
+    assert np.array_equal(ids, rids)
+    assert rel_l2(out, ref) <= 2e-3  # int8 limbs; H between the GEMMs is still f16
+    for t in (router, gate_up, down):
+        t.free()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("T", [512, 37])
 def test_gpu_prefill_one_launch_matches_two(ctx, cfg3, T):
     # both grouped GEMMs in one launch (the activations handed over in an
