@@ -51,6 +51,8 @@
 #include "lt_internal.h"
 #include "lt_limbs.h"
 
+#include <stdlib.h>
+
 namespace lt {
 
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
@@ -666,9 +668,10 @@ struct NoWait {
 // A chunk of one token streams its weights like the decode path instead of
 // dequantising them to f16 tiles for a 32-row MFMA: the f16 tile costs the
 // same whatever the chunk's rows, and many one-tile chunks of a skewed
-// routing hold a single token (22 of config 5's 63).  (NT = 2 as well
-// needed more registers than two waves per SIMD allow.)  A lane owns one Q4_K sub-block pair
-// window (position 4 sb + p of a row: K elements 256 sb + 64 p + [0, 64)),
+// routing hold a single token (22 of the 63 in a 512-token batch with
+// Zipf-biased logits).  (NT = 2 as well needed more registers than two
+// waves per SIMD allow.)  A lane owns one Q4_K sub-block pair window
+// (position 4 sb + p of a row: K elements 256 sb + 64 p + [0, 64)),
 // whose activations it turns into int8 limbs in registers once (limbs16);
 // per row it loads the window's 32 quant bytes and its quad's header word
 // and meets them with each token's limbs on v_dot4 (q4k_pair_dot); a row's
@@ -1083,6 +1086,7 @@ hipError_t launch_moe_prefill(const DevTensor &R, const DevTensor &GU, const Dev
     pa.done = w.done;
     pa.CG = (mc + 7) / 8;
     pa.X = X;
+    // (LT_PREFILL_NO_TINY, read at each call: every chunk on the tiles, for testing)
     pa.tiny = GU.blocks_per_row <= 8 && Dn.blocks_per_row <= 4 && !getenv("LT_PREFILL_NO_TINY");
     if (xcd_local) {
         const unsigned nb = 8u * (unsigned)((F / BN1 + D / BN2) * pa.CG);
