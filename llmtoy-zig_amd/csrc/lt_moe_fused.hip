@@ -2074,9 +2074,12 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // measured for this stream) after the logits are seen, in 10 ns ticks;
     // tuned on config 3 (14.2 MB: 296 ticks; 200 or 360 are 0.2-0.4 us
     // slower per layer; re-measured on the current kernel, 60% and 100% of
-    // the stream instead of 80%: +0.17 and +0.36 us).
+    // the stream instead of 80%: +0.17 and +0.36 us).  With the shared FFN
+    // in the launch (its streams run before the experts') 55% is best: on
+    // config 4 (17.8 MB) 50-60% measured 0.1-0.2 us faster than 80%, 40%
+    // and 100% slower.
     const double gu_bytes = moe ? (double)L.k * 2.0 * L.F * ((double)L.GU->bytes / (double)L.GU->total_rows) : 0.0;
-    fa.dn_delay = 70 + (int)(0.8 * gu_bytes / 50000.0);
+    fa.dn_delay = 70 + (int)((pl.shared ? 0.55 : 0.8) * gu_bytes / 50000.0);
     fa.NRg = pl.NRg;
     fa.rb = pl.rb;
     fa.SPG = pl.SPG;
