@@ -2077,7 +2077,8 @@ hipError_t launch_moe_fused(const FusedPlan &pl, const FusedLayer &L, const floa
     // the stream instead of 80%: +0.17 and +0.36 us).  With the shared FFN
     // in the launch (its streams run before the experts') 55% is best: on
     // config 4 (17.8 MB) 50-60% measured 0.1-0.2 us faster than 80%, 40%
-    // and 100% slower.
+    // and 100% slower (the Gemma4 block and the APEX instance, whose
+    // launches hold no shared FFN, were 0.15 us slower at 55%).
     const double gu_bytes = moe ? (double)L.k * 2.0 * L.F * ((double)L.GU->bytes / (double)L.GU->total_rows) : 0.0;
     fa.dn_delay = 70 + (int)((pl.shared ? 0.55 : 0.8) * gu_bytes / 50000.0);
     fa.NRg = pl.NRg;
