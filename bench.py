@@ -1075,8 +1075,9 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "sharding of this path is described in DESIGN.md and not run", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); sharding the layer "
+              "over several GPUs (experts split across them, one all-to-all of the routed activations each way) "
+              "is a design, not something this build runs", file=sys.stderr)
         sys.exit(2)
     if args.warmup is None:
         args.warmup = 5 if args.workload == "prefill" else 64
